@@ -1,0 +1,270 @@
+/*
+ * velokv.h -- C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * This library replaces the KV half of Velo-Core's Metal device runtime: the
+ * K/V pools and block table owned by MetalMemoryRuntime / MetalKvStore and the
+ * five KV kernels in kernels.metal. Everything above it (VeloEngine,
+ * VeloScheduler, RadixCache, PagedAttentionBlockManager) stays in the host
+ * program and talks to this ABI with plain pointers and sizes.
+ *
+ * Conventions
+ *  - Every function returns an int32 status: VK_OK (0) or a negative VK_ERR_*.
+ *    The message for the last failure on the calling thread is returned by
+ *    vk_last_error(). Mirrors the Result<_, SpeculativeError::Model(String)>
+ *    convention of the reference (speculative.rs, metal/runtime.rs:141-239).
+ *  - Device pointers ("dev") are caller-owned unless a function says otherwise.
+ *    The pool owns its HBM (K/V codes, scales, block table).
+ *  - Compute entry points are asynchronous on the given stream (a hipStream_t
+ *    passed as void*; NULL = the null stream). The reference blocks on every
+ *    command buffer (metal/model.rs:141-142); callers that want that behaviour
+ *    call vk_stream_sync().
+ *  - The compute path is HIP only. There is no CPU fallback: a context whose
+ *    code object is missing fails vk_ctx_create with VK_ERR_NOT_WIRED.
+ *
+ * Layout of one layer of a pool in HBM ("build layout"; the reference layout
+ * is [blk][tok][head][D(+4)], kernels.metal:474,700):
+ *    K codes   [n_blocks][n_kv_heads][block_size][head_dim]
+ *    V codes   [n_blocks][n_kv_heads][block_size/2][head_dim][2]   (token pairs interleaved)
+ *    K scales  I8_BLK: fp16 [n_blocks][n_kv_heads]; I8_REF: fp32 [n_blocks][n_kv_heads][block_size]
+ *    V scales  same as K scales
+ * Element size: F32 4, F16 2, I8_* 1 byte.
+ */
+#ifndef VELOKV_H
+#define VELOKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------
+ * Each host-forcible failure of the reference boundary has its own code.    */
+#define VK_OK                      0
+#define VK_ERR_BAD_ARG            -1  /* argument out of range / null        */
+#define VK_ERR_INVALID_BLOCK_SIZE -2  /* paged_attention.rs:104-106          */
+#define VK_ERR_OUT_OF_PAGES       -3  /* paged_attention.rs:164-169          */
+#define VK_ERR_TOO_MANY_PAGES     -4  /* metal/runtime.rs:296-302            */
+#define VK_ERR_NO_FREE_SLOTS      -5  /* engine.rs:248-252                   */
+#define VK_ERR_NOT_WIRED          -6  /* metal/backend.rs:79-83,130-140      */
+#define VK_ERR_NO_DEVICE          -7  /* metal/runtime.rs:164 (no device)    */
+#define VK_ERR_HIP                -8  /* a HIP runtime call failed           */
+#define VK_ERR_UNSUPPORTED        -9  /* shape/dtype with no kernel          */
+#define VK_ERR_UNKNOWN_HANDLE    -10  /* paged_attention.rs:189-192          */
+
+/* ---- KV storage types ----------------------------------------------------
+ * KvCacheType (paged_attention.rs:27-35) has Fp32 / Int8 / Fp8; Fp8 is routed
+ * to the Int8 kernels (metal/model.rs:404,442), so it maps to VK_KV_I8_REF.  */
+#define VK_KV_F32     0  /* KvCacheType::Fp32, kernels.metal:619-645 / 440-501 */
+#define VK_KV_F16     1  /* fp16 KV (BASELINE configs 2 and 5)                 */
+#define VK_KV_I8_REF  2  /* KvCacheType::Int8: per-(token, head) fp32 scale,
+                            truncating codes, kernels.metal:753-802           */
+#define VK_KV_I8_BLK  3  /* per-(block, head) fp16 scale, round-half-even codes
+                            clamped to +-127             */
+
+/* element types of caller tensors (q, new K/V) */
+#define VK_DT_F32 0
+#define VK_DT_F16 1
+
+typedef struct vk_ctx vk_ctx;
+typedef struct vk_pool vk_pool;
+typedef struct vk_block_manager vk_block_manager;
+
+/* ---- context -------------------------------------------------------------- */
+
+/* Last error message of the calling thread ("" if none). */
+const char* vk_last_error(void);
+
+/* Open `device`, load the gfx950 code object (NULL = velokv_gfx950.co next to
+ * this library) and resolve every kernel.
+ * Replaces MetalMemoryRuntime::new's device/queue/library setup
+ * (metal/runtime.rs:141-186) and load_metal_library (metal/runtime.rs:29-60). */
+int vk_ctx_create(int device, const char* code_object_path, vk_ctx** out);
+int vk_ctx_destroy(vk_ctx* ctx);
+/* Name of the GPU architecture the context runs on (e.g. "gfx950"). */
+int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
+
+/* ---- pools ---------------------------------------------------------------- */
+
+typedef struct vk_pool_desc {
+  int32_t n_layer;        /* MemoryRuntimeConfig::n_layer (runtime.rs:55)          */
+  int32_t n_blocks;       /* MemoryRuntimeConfig::paged_total_pages (runtime.rs:53) */
+  int32_t block_size;     /* MemoryRuntimeConfig::paged_block_size (runtime.rs:51)  */
+  int32_t n_kv_heads;     /* ModelMeta::n_head_kv                                  */
+  int32_t head_dim;       /* ModelMeta::head_dim                                   */
+  int32_t kv_type;        /* VK_KV_*  (MemoryRuntimeConfig::kv_type)               */
+  int32_t max_slots;      /* MemoryRuntimeConfig::max_slots (runtime.rs:59)        */
+  int32_t max_pages_per_slot; /* row length of the slot block table; 0 = n_blocks
+                                 (the reference sizes rows by paged_total_pages,
+                                 metal/runtime.rs:222-223)                         */
+} vk_pool_desc;
+
+/* Device addresses of one layer, for callers that read or write the pool
+ * directly (tests, KV migration). */
+typedef struct vk_layer_view {
+  void* k_codes;  void* v_codes;
+  void* k_scales; void* v_scales;   /* NULL for F32 / F16 */
+  uint64_t codes_bytes;             /* bytes of each of k_codes / v_codes  */
+  uint64_t scales_bytes;            /* bytes of each of k_scales / v_scales */
+} vk_layer_view;
+
+/* Allocate and zero the K and V pools of all layers plus the slot block table
+ * (u32[max_slots][max_pages_per_slot], zero-filled).
+ * Replaces MetalKvStore::new (metal/kv_store.rs:36-57) and the slot-mapping
+ * buffer allocation (metal/runtime.rs:221-229), with one layer offset per layer
+ * (the reference binds every layer at offset 0, metal/model.rs:409-410). */
+int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* desc, vk_pool** out);
+int vk_pool_destroy(vk_pool* pool);
+int vk_pool_get_desc(const vk_pool* pool, vk_pool_desc* out);
+int vk_pool_layer_view(const vk_pool* pool, int32_t layer, vk_layer_view* out);
+/* Device pointer of the slot block table and its row stride (in entries). */
+int vk_pool_block_table(const vk_pool* pool, int32_t** table_dev, int32_t* row_stride);
+/* Total HBM held by the pool. */
+int vk_pool_bytes(const vk_pool* pool, uint64_t* out);
+
+/* Write `pages` into row `slot` of the pool's block table and zero the rest of
+ * the row; synchronous, like the reference's memcpy into shared memory.
+ * MemoryRuntime::bind_slot (runtime.rs:34) / MetalMemoryRuntime::bind_slot
+ * (metal/runtime.rs:294-319). Errors: VK_ERR_TOO_MANY_PAGES when n_pages
+ * exceeds the row length, VK_ERR_BAD_ARG for a slot >= max_slots or a page id
+ * >= n_blocks. */
+int vk_bind_slot(vk_pool* pool, uint32_t slot, const uint32_t* pages, int32_t n_pages);
+
+/* ---- hot path ------------------------------------------------------------- */
+
+/* Per-token flat slot = table[row][pos / bs] * bs + pos % bs, where row is
+ * seq_rows[i] (or i when seq_rows is NULL). All pointers are device pointers.
+ * The slot derivation the reference performs inside kv_update
+ * (kernels.metal:637-640, 770-774). */
+int vk_slot_mapping(vk_ctx* ctx, vk_pool* pool, const int32_t* block_tables,
+                    int32_t bt_stride, const int32_t* seq_rows,
+                    const int32_t* positions, int32_t n_tok,
+                    int64_t* slot_mapping_out, void* stream);
+
+/* Append n_tok new tokens of one layer: k, v are dev [n_tok][n_kv_heads][head_dim]
+ * of type in_dtype (VK_DT_*); slot_mapping is dev int64 [n_tok] (negative =
+ * skip). Quantizes on the way in for the I8 types.
+ * kv_update (kernels.metal:619-645) and kv_update_int8 (kernels.metal:753-802),
+ * dispatched at metal/model.rs:399-434.
+ * Order rule: tokens of one call are applied in index order. For VK_KV_I8_BLK a
+ * token at block offset 0 starts a fresh block scale; a later token whose absmax
+ * needs a larger scale re-quantizes the codes already in the block. Tokens of
+ * one call that fall in the same block must be adjacent in the call (padding
+ * slots may sit between them) and in increasing offset order. */
+int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* k,
+              const void* v, int32_t in_dtype, const int64_t* slot_mapping,
+              int32_t n_tok, void* stream);
+
+typedef struct vk_decode_args {
+  int32_t layer;
+  const void* q;              /* dev [S][n_heads][head_dim] of q_dtype         */
+  int32_t q_dtype;            /* VK_DT_F16: packed fp16 math; VK_DT_F32: fp32 math */
+  float* out;                 /* dev fp32 [S][n_heads][head_dim]               */
+  const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = the pool's slot table */
+  int32_t bt_stride;          /* ignored when block_tables is NULL             */
+  const int32_t* seq_rows;    /* dev [S] row of each sequence; NULL = 0..S-1   */
+  const int32_t* context_lens;/* dev [S] tokens to attend (incl. the new one)  */
+  int32_t n_seqs;             /* S                                             */
+  int32_t n_heads;            /* query heads H (multiple of n_kv_heads)        */
+  int32_t max_context_len;    /* host upper bound of context_lens              */
+  float scale;                /* softmax scale; 0 = 1/sqrt(head_dim)           */
+  int32_t partition_tokens;   /* split-K partition size in tokens; 0 = auto    */
+  void* workspace;            /* dev scratch for split-K partials; NULL = owned by ctx */
+  uint64_t workspace_bytes;
+} vk_decode_args;
+
+/* Bytes of workspace vk_paged_decode needs for these arguments. */
+int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes);
+
+/* Single-query paged decode attention for S sequences, with split-K over
+ * context partitions and an online-softmax merge.
+ * paged_attention_flash (kernels.metal:440-501), paged_attention_flash_int8
+ * (kernels.metal:672-732); GQA map kv_head = h / (H / Hkv) (kernels.metal:456);
+ * math of llama_cpu.rs:251-284. */
+int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream);
+
+typedef struct vk_tree_args {
+  int32_t layer;
+  const void* q;              /* dev [S][n_nodes][n_heads][head_dim] of q_dtype */
+  int32_t q_dtype;
+  float* out;                 /* dev fp32 [S][n_nodes][n_heads][head_dim]       */
+  const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = slot table        */
+  int32_t bt_stride;
+  const int32_t* seq_rows;    /* dev [S] or NULL                                 */
+  const int32_t* context_lens;/* dev [S] committed tokens before the tree        */
+  const uint32_t* tree_mask;  /* dev [S][n_nodes]: bit j of row i = node i sees node j */
+  int32_t n_seqs;
+  int32_t n_nodes;            /* <= 32; node j's K/V sit at position context_len + j */
+  int32_t n_heads;
+  int32_t max_context_len;
+  float scale;
+} vk_tree_args;
+
+/* Multi-query tree-verify attention: node i attends to the committed context
+ * and to the tree nodes its mask row selects.
+ * paged_attention_tree (kernels.metal:512-599) / forward_tree
+ * (metal/model.rs:574-731), with the mask semantics defined here. */
+int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a, void* stream);
+
+/* Copy-on-write block copy: for each (src, dst) pair in the HOST array
+ * src_dst_pairs[2*n_pairs], copy the K/V codes and scales of block src to block
+ * dst in every layer. dst blocks must be distinct and must not appear as a src.
+ * No counterpart in the reference (it has no COW); serves the prefix sharing of
+ * RadixCache (radix_cache.rs:73-140). */
+int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* src_dst_pairs,
+                   int32_t n_pairs, void* stream);
+
+/* ---- host block manager ----------------------------------------------------
+ * PagedAttentionBlockManager (paged_attention.rs:92-212): FIFO free list,
+ * pages_for_tokens = ceil(len / bs), plus per-page reference counts for
+ * prefix sharing (the reference has none; used by vk_bm_fork / vk_bm_cow). */
+int vk_bm_create(int32_t block_size, int32_t total_pages, vk_block_manager** out);
+int vk_bm_destroy(vk_block_manager* bm);
+int vk_bm_free_pages(const vk_block_manager* bm, int32_t* out);
+/* allocate(handle, token_len): pops ceil(token_len/bs) pages; pages_out gets them. */
+int vk_bm_allocate(vk_block_manager* bm, uint64_t handle, int64_t token_len,
+                   uint32_t* pages_out, int32_t cap, int32_t* n_out);
+/* release(handle): drops one reference of each page; pages reaching zero go
+ * back to the free list in order. */
+int vk_bm_release(vk_block_manager* bm, uint64_t handle);
+/* materialize_span(handle). */
+int vk_bm_pages(const vk_block_manager* bm, uint64_t handle, uint32_t* pages_out,
+                int32_t cap, int32_t* n_out);
+/* New handle `child` that shares the first ceil(shared_tokens/bs) pages of
+ * `parent` (refcount + 1) and owns fresh pages for the rest of token_len. */
+int vk_bm_fork(vk_block_manager* bm, uint64_t parent, uint64_t child,
+               int64_t shared_tokens, int64_t token_len, uint32_t* pages_out,
+               int32_t cap, int32_t* n_out);
+/* Before writing into page index `page_idx` of `handle`: if that page is
+ * shared, replace it by a fresh page and report the (src, dst) copy to issue
+ * through vk_copy_blocks; *copied = 0 when the page was already private. */
+int vk_bm_cow(vk_block_manager* bm, uint64_t handle, int32_t page_idx,
+              int32_t* src, int32_t* dst, int32_t* copied);
+int vk_bm_refcount(const vk_block_manager* bm, uint32_t page, int32_t* out);
+
+/* ---- device memory and stream helpers for hosts without their own HIP ----- */
+int vk_dev_alloc(vk_ctx* ctx, uint64_t bytes, void** out);
+int vk_dev_free(vk_ctx* ctx, void* p);
+int vk_memcpy_h2d(vk_ctx* ctx, void* dst, const void* src, uint64_t bytes);
+int vk_memcpy_d2h(vk_ctx* ctx, void* dst, const void* src, uint64_t bytes);
+int vk_memset_d(vk_ctx* ctx, void* dst, int value, uint64_t bytes);
+int vk_stream_create(vk_ctx* ctx, void** out);
+int vk_stream_destroy(vk_ctx* ctx, void* stream);
+int vk_stream_sync(vk_ctx* ctx, void* stream);
+int vk_event_create(vk_ctx* ctx, void** out);
+int vk_event_destroy(vk_ctx* ctx, void* ev);
+int vk_event_record(vk_ctx* ctx, void* ev, void* stream);
+int vk_event_elapsed_ms(vk_ctx* ctx, void* start, void* end, float* ms);
+
+/* ---- synthetic-data utilities (benchmarks and full-size tests) ------------ */
+/* dev[i] = fp16(N(0,1) * (outlier channel ? outlier_scale : 1)) from a
+ * counter-based SplitMix64 stream; channel = i % row_len; a channel is an
+ * outlier when SplitMix64(seed ^ OUTLIER_SALT ^ channel) % 100 == 0. */
+int vk_fill_normal_f16(vk_ctx* ctx, void* dev, uint64_t n, uint64_t seed,
+                       int32_t row_len, float outlier_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VELOKV_H */

@@ -1,0 +1,217 @@
+"""ctypes wrapper of the CPU oracle (oracle/velokv_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker or the timed CPU baseline. The
+product (velokv) never imports it.
+
+Layer arrays use the build layout (see include/velokv.h) as numpy uint8 buffers
+so GPU pools can be compared byte for byte.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libvelokv_oracle.so")
+
+F32, F16, I8_REF, I8_BLK = 0, 1, 2, 3
+ESZ = {F32: 4, F16: 2, I8_REF: 1, I8_BLK: 1}
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.vko_f16_to_f32.argtypes = [C.c_uint16]
+        L.vko_f16_to_f32.restype = C.c_float
+        L.vko_f32_to_f16.argtypes = [C.c_float]
+        L.vko_f32_to_f16.restype = C.c_uint16
+        L.vko_append.restype = C.c_int
+        L.vko_splitmix64.argtypes = [C.c_uint64]
+        L.vko_splitmix64.restype = C.c_uint64
+        L.vko_load_elem.restype = C.c_float
+        L.vko_get_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+class VkoLayer(C.Structure):
+    _fields_ = [("n_blocks", C.c_int32), ("n_kv_heads", C.c_int32), ("block_size", C.c_int32),
+                ("head_dim", C.c_int32), ("kv_type", C.c_int32),
+                ("k", C.c_void_p), ("v", C.c_void_p), ("ks", C.c_void_p), ("vs", C.c_void_p)]
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+class Layer:
+    """One layer of a KV pool in host memory, build layout."""
+
+    def __init__(self, n_blocks, n_kv_heads, block_size, head_dim, kv_type):
+        self.n_blocks, self.n_kv_heads, self.block_size, self.head_dim, self.kv_type = (
+            n_blocks, n_kv_heads, block_size, head_dim, kv_type)
+        codes = n_blocks * n_kv_heads * block_size * head_dim * ESZ[kv_type]
+        self.k = np.zeros(codes, np.uint8)
+        self.v = np.zeros(codes, np.uint8)
+        sb = {I8_BLK: 2, I8_REF: 4 * block_size}.get(kv_type, 0) * n_blocks * n_kv_heads
+        self.ks = np.zeros(sb, np.uint8) if sb else None
+        self.vs = np.zeros(sb, np.uint8) if sb else None
+
+    def struct(self):
+        return VkoLayer(self.n_blocks, self.n_kv_heads, self.block_size, self.head_dim, self.kv_type,
+                        _ptr(self.k), _ptr(self.v), _ptr(self.ks), _ptr(self.vs))
+
+    def copy(self):
+        o = Layer(self.n_blocks, self.n_kv_heads, self.block_size, self.head_dim, self.kv_type)
+        o.k[:] = self.k
+        o.v[:] = self.v
+        if self.ks is not None:
+            o.ks[:] = self.ks
+            o.vs[:] = self.vs
+        return o
+
+    def elem(self, is_v, blk, h, tok, d):
+        s = self.struct()
+        return lib().vko_load_elem(C.byref(s), int(is_v), C.c_int64(blk), h, tok, d)
+
+
+def f16_to_f32(bits):
+    return lib().vko_f16_to_f32(int(bits))
+
+
+def f32_to_f16(x):
+    return lib().vko_f32_to_f16(float(x))
+
+
+def splitmix64(x):
+    return lib().vko_splitmix64(C.c_uint64(x & 0xFFFFFFFFFFFFFFFF))
+
+
+def _in_dtype(a):
+    if a.dtype == np.float16:
+        return F16
+    assert a.dtype == np.float32
+    return F32
+
+
+def append(layer: Layer, k, v, slot_mapping):
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    sm = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    s = layer.struct()
+    rc = lib().vko_append(C.byref(s), _ptr(k), _ptr(v), _in_dtype(k), _ptr(sm), C.c_int(len(sm)))
+    if rc != 0:
+        raise ValueError("slot outside the pool")
+
+
+def paged_decode(layer: Layer, q, block_tables, ctx_lens, scale=None):
+    q = np.ascontiguousarray(q)
+    S, H, D = q.shape
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    out = np.zeros((S, H, D), np.float32)
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    s = layer.struct()
+    lib().vko_paged_decode(C.byref(s), _ptr(q), _in_dtype(q), _ptr(out), _ptr(bt), C.c_int(bt.shape[1]),
+                           _ptr(cl), C.c_int(S), C.c_int(H), C.c_float(scale))
+    return out
+
+
+def paged_decode_f64(layer: Layer, q, block_tables, ctx_lens, scale=None):
+    q = np.ascontiguousarray(q)
+    S, H, D = q.shape
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    out = np.zeros((S, H, D), np.float64)
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    s = layer.struct()
+    lib().vko_paged_decode_f64(C.byref(s), _ptr(q), _in_dtype(q), _ptr(out), _ptr(bt), C.c_int(bt.shape[1]),
+                               _ptr(cl), C.c_int(S), C.c_int(H), C.c_double(scale))
+    return out
+
+
+def tree_verify(layer: Layer, q, block_tables, ctx_lens, mask, scale=None):
+    q = np.ascontiguousarray(q)
+    S, N, H, D = q.shape
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    mk = np.ascontiguousarray(mask, dtype=np.uint32)
+    out = np.zeros((S, N, H, D), np.float32)
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    s = layer.struct()
+    lib().vko_tree_verify(C.byref(s), _ptr(q), _in_dtype(q), _ptr(out), _ptr(bt), C.c_int(bt.shape[1]),
+                          _ptr(cl), _ptr(mk), C.c_int(S), C.c_int(N), C.c_int(H), C.c_float(scale))
+    return out
+
+
+def copy_blocks(layer: Layer, pairs):
+    p = np.ascontiguousarray(pairs, dtype=np.int32).reshape(-1)
+    s = layer.struct()
+    lib().vko_copy_blocks(C.byref(s), _ptr(p), C.c_int(len(p) // 2))
+
+
+def to_reference_layout(layer: Layer, is_v):
+    D = layer.head_dim
+    row = 4 * D if layer.kv_type == F32 else D + 4
+    dst = np.zeros(layer.n_blocks * layer.block_size * layer.n_kv_heads * row, np.uint8)
+    s = layer.struct()
+    lib().vko_to_reference_layout(C.byref(s), C.c_int(int(is_v)), _ptr(dst))
+    return dst
+
+
+# ---- reference-layout restatements ------------------------------------------
+
+def ref_kv_update(k_cache, v_cache, k_in, v_in, slot_id, table, max_pages, block_size, n_head, head_dim, pos):
+    lib().vko_ref_kv_update(_ptr(k_cache), _ptr(v_cache), _ptr(k_in), _ptr(v_in), C.c_uint32(slot_id), _ptr(table),
+                            C.c_uint32(max_pages), C.c_uint32(block_size), C.c_uint32(n_head),
+                            C.c_uint32(head_dim), C.c_uint32(pos))
+
+
+def ref_kv_update_int8(k_cache, v_cache, k_in, v_in, slot_id, table, max_pages, block_size, n_head, head_dim, pos):
+    lib().vko_ref_kv_update_int8(_ptr(k_cache), _ptr(v_cache), _ptr(k_in), _ptr(v_in), C.c_uint32(slot_id),
+                                 _ptr(table), C.c_uint32(max_pages), C.c_uint32(block_size), C.c_uint32(n_head),
+                                 C.c_uint32(head_dim), C.c_uint32(pos))
+
+
+def ref_paged_attention_flash(q, k_cache, v_cache, int8, head_dim, pos, slot_id, table, max_pages, block_size,
+                              n_head_kv, n_head):
+    out = np.zeros(n_head * head_dim, np.float32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    lib().vko_ref_paged_attention_flash(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), C.c_int(int(int8)),
+                                        C.c_uint32(head_dim), C.c_uint32(pos), C.c_uint32(slot_id), _ptr(table),
+                                        C.c_uint32(max_pages), C.c_uint32(block_size), C.c_uint32(n_head_kv),
+                                        C.c_uint32(n_head))
+    return out.reshape(n_head, head_dim)
+
+
+def ref_cpu_attention(q, k, v, n_head, n_head_kv, head_dim):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    n_seq = k.size // (n_head_kv * head_dim)
+    out = np.zeros(n_head * head_dim, np.float32)
+    lib().vko_ref_cpu_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), C.c_uint32(n_seq), C.c_uint32(n_head),
+                                C.c_uint32(n_head_kv), C.c_uint32(head_dim))
+    return out.reshape(n_head, head_dim)
+
+
+def set_threads(n):
+    lib().vko_set_threads(C.c_int(n))
+
+
+def get_threads():
+    return lib().vko_get_threads()

@@ -1,0 +1,172 @@
+"""GPU parity of the append (kv_update / kv_update_int8 and the per-block INT8
+mode) and of the copy-on-write block copy: pool bytes must equal the oracle's
+bit for bit."""
+import numpy as np
+import pytest
+
+import pyoracle as O
+import velokv
+from cases import BS, HD, make_case, oracle_layer
+from velokv import synth
+
+pytestmark = pytest.mark.gpu
+
+KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
+
+
+def gpu_pool(ctx, case, n_layer=1, layer=0, in_dtype=np.float16, with_last=True):
+    pool = velokv.Pool(ctx, n_layer, case.n_blocks, BS, case.n_kv_heads, HD, case.kv_type)
+    sl, kk, vv = case.prefill_slots()
+    if len(sl):
+        ctx.append(pool, layer, ctx.upload(kk.astype(in_dtype)), ctx.upload(vv.astype(in_dtype)),
+                   velokv.DT_F16 if in_dtype == np.float16 else velokv.DT_F32, ctx.upload(sl), len(sl))
+    if with_last:
+        sl, kk, vv = case.last_slots()
+        ctx.append(pool, layer, ctx.upload(kk.astype(in_dtype)), ctx.upload(vv.astype(in_dtype)),
+                   velokv.DT_F16 if in_dtype == np.float16 else velokv.DT_F32, ctx.upload(sl), len(sl))
+    ctx.sync()
+    return pool
+
+
+def assert_layer_equal(pool, layer_idx, ref: O.Layer):
+    got = pool.download_layer(layer_idx)
+    for key in ("k", "v", "ks", "vs"):
+        r = getattr(ref, key)
+        if r is None:
+            assert got[key] is None
+            continue
+        if not np.array_equal(got[key], r):
+            bad = np.nonzero(got[key] != r)[0]
+            raise AssertionError(f"{key}: {len(bad)} bytes differ, first at {bad[:8]}")
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+def test_append_bit_exact_config1(ctx, kv):
+    print(f"append config1 kv={kv}", flush=True)
+    # 32 blocks permuted within a 64-block pool, context 512
+    case = make_case(kv, [512], n_blocks=64, seed=101)
+    ref = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    assert_layer_equal(pool, 0, ref)
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+def test_append_bit_exact_ragged_batch_with_outliers(ctx, kv):
+    print(f"append ragged kv={kv}", flush=True)
+    lens = [1, 2, 15, 16, 17, 31, 33, 200, 257]
+    case = make_case(kv, lens, seed=102, outlier_scale=8.0)
+    ref = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    assert_layer_equal(pool, 0, ref)
+
+
+@pytest.mark.parametrize("kv", [O.F32, O.I8_REF, O.I8_BLK, O.F16])
+def test_append_fp32_input(ctx, kv):
+    # the reference's kv_update / kv_update_int8 take fp32 K/V
+    print(f"append fp32-in kv={kv}", flush=True)
+    case = make_case(kv, [40, 70], seed=103)
+    r = np.random.default_rng(5)
+    case.k = [(r.standard_normal(k.shape) * 3).astype(np.float32) for k in case.k]
+    case.v = [(r.standard_normal(v.shape) * 3).astype(np.float32) for v in case.v]
+    ref = oracle_layer(case)
+    pool = gpu_pool(ctx, case, in_dtype=np.float32)
+    assert_layer_equal(pool, 0, ref)
+
+
+def test_append_blk_token_by_token_equals_one_call(ctx):
+    """Sequential semantics: one call with all tokens == one call per token."""
+    print("append blk split", flush=True)
+    case = make_case(O.I8_BLK, [77], seed=104, outlier_scale=8.0)
+    pool_a = gpu_pool(ctx, case)
+    pool_b = velokv.Pool(ctx, 1, case.n_blocks, BS, 8, HD, O.I8_BLK)
+    sl = synth.slots_for_positions(case.block_tables, np.arange(77), BS, np.zeros(77, int))
+    for t in range(77):
+        ctx.append(pool_b, 0, ctx.upload(case.k[0][t:t + 1]), ctx.upload(case.v[0][t:t + 1]), velokv.DT_F16,
+                   ctx.upload(sl[t:t + 1]), 1)
+    ctx.sync()
+    a, b = pool_a.download_layer(0), pool_b.download_layer(0)
+    for key in ("k", "v", "ks", "vs"):
+        assert np.array_equal(a[key], b[key])
+
+
+def test_append_skips_negative_slots_and_layers_are_separate(ctx):
+    print("append negative slots / layers", flush=True)
+    case = make_case(O.I8_BLK, [20], seed=105)
+    pool = velokv.Pool(ctx, 3, case.n_blocks, BS, 8, HD, O.I8_BLK)
+    sl, kk, vv = case.prefill_slots()
+    sl = sl.copy()
+    sl[3] = -1
+    ctx.append(pool, 1, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+    ctx.sync()
+    ref = O.Layer(case.n_blocks, 8, BS, HD, O.I8_BLK)
+    O.append(ref, kk, vv, sl)
+    assert_layer_equal(pool, 1, ref)
+    for other in (0, 2):
+        got = pool.download_layer(other)
+        assert not got["k"].any() and not got["ks"].any()
+
+
+def test_slot_mapping_kernel(ctx):
+    print("slot mapping", flush=True)
+    case = make_case(O.F16, [50, 90, 3], seed=106)
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, 8, HD, O.F16)
+    rows = np.array([0, 1, 1, 2, 0, 1], np.int32)
+    pos = np.array([0, 89, 16, 2, 49, 31], np.int32)
+    bt = ctx.upload(case.block_tables)
+    out = ctx.slot_mapping(pool, ctx.upload(pos), block_tables=bt, bt_stride=case.block_tables.shape[1],
+                           seq_rows=ctx.upload(rows))
+    got = out.download((6,), np.int64)
+    ref = synth.slots_for_positions(case.block_tables, pos, BS, rows)
+    assert np.array_equal(got, ref)
+
+
+def test_bind_slot_writes_table_rows(ctx):
+    print("bind_slot", flush=True)
+    pool = velokv.Pool(ctx, 1, 64, BS, 8, HD, O.F16, max_slots=4, max_pages_per_slot=10)
+    pool.bind_slot(2, [5, 9, 1])
+    pool.bind_slot(0, list(range(10)))
+    ptr, stride = pool.block_table()
+    tb = velokv.DeviceBuffer(ctx, 4 * 10 * 4, ptr=ptr, owned=False).download((4, 10), np.int32)
+    assert stride == 10
+    assert tb[2].tolist() == [5, 9, 1] + [0] * 7
+    assert tb[0].tolist() == list(range(10))
+    with pytest.raises(velokv.VkError) as e:
+        pool.bind_slot(1, list(range(11)))
+    assert e.value.code == velokv.ERR_TOO_MANY_PAGES
+    with pytest.raises(velokv.VkError):
+        pool.bind_slot(4, [1])
+    with pytest.raises(velokv.VkError):
+        pool.bind_slot(1, [64])
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+def test_copy_blocks_bit_exact_all_layers(ctx, kv):
+    print(f"copy_blocks kv={kv}", flush=True)
+    case = make_case(kv, [100, 60], seed=107, n_blocks=40)
+    n_layer = 3
+    pool = velokv.Pool(ctx, n_layer, case.n_blocks, BS, 8, HD, kv)
+    refs = []
+    sl, kk, vv = case.prefill_slots()
+    for layer in range(n_layer):
+        k = (kk.astype(np.float32) * (layer + 1)).astype(np.float16)
+        ctx.append(pool, layer, ctx.upload(k), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+        r = O.Layer(case.n_blocks, 8, BS, HD, kv)
+        O.append(r, k, vv, sl)
+        refs.append(r)
+    used = set(case.block_tables[0, :7].tolist()) | set(case.block_tables[1, :4].tolist())
+    free = [b for b in range(case.n_blocks) if b not in used]
+    pairs = np.array([[case.block_tables[0, 6], free[0]], [case.block_tables[1, 3], free[1]],
+                      [case.block_tables[0, 0], free[2]]], np.int32)
+    ctx.copy_blocks(pool, pairs)
+    ctx.sync()
+    for layer in range(n_layer):
+        O.copy_blocks(refs[layer], pairs)
+        assert_layer_equal(pool, layer, refs[layer])
+
+
+def test_copy_blocks_rejects_bad_pairs(ctx):
+    pool = velokv.Pool(ctx, 1, 8, BS, 8, HD, O.F16)
+    for bad in ([[0, 8]], [[0, 1], [2, 1]], [[0, 1], [1, 2]], [[-1, 2]]):
+        with pytest.raises(velokv.VkError) as e:
+            ctx.copy_blocks(pool, bad)
+        assert e.value.code == velokv.ERR_BAD_ARG

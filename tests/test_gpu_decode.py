@@ -1,0 +1,168 @@
+"""GPU parity of paged decode attention against the oracle, within the north-star
+tolerance (|err| <= 2e-3 + 1e-2 |ref|, fp32-accumulated oracle), for every KV
+type, query dtype, GQA group size and split-K partition size."""
+import numpy as np
+import pytest
+
+import pyoracle as O
+import velokv
+from cases import BS, HD, make_case, oracle_layer, tol_check
+from test_gpu_append_copy import gpu_pool
+
+pytestmark = pytest.mark.gpu
+
+KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
+
+
+def run_decode(ctx, pool, case, q=None, q_dtype=np.float16, partition_tokens=0, layer=0, seq_rows=None,
+               block_tables=None, n_seqs=None):
+    q = case.q if q is None else q
+    q = q.astype(q_dtype)
+    S = q.shape[0] if n_seqs is None else n_seqs
+    out = ctx.alloc(S * case.n_heads * HD * 4)
+    bt = case.block_tables if block_tables is None else block_tables
+    ctx.paged_decode(pool, layer, ctx.upload(q), velokv.DT_F16 if q_dtype == np.float16 else velokv.DT_F32, out,
+                     ctx.upload(case.ctx_lens[:S]), S, case.n_heads, int(case.ctx_lens[:S].max()),
+                     block_tables=ctx.upload(bt), bt_stride=bt.shape[1],
+                     seq_rows=ctx.upload(seq_rows) if seq_rows is not None else None,
+                     partition_tokens=partition_tokens)
+    ctx.sync()
+    return out.download((S, case.n_heads, HD), np.float32)
+
+
+def check(got, ref, what):
+    ok, err, nbad = tol_check(got, ref)
+    assert ok, f"{what}: max err {err:.3g}, {nbad} elements out of tolerance"
+    return err
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+@pytest.mark.parametrize("qd", [np.float16, np.float32])
+def test_decode_config1(ctx, kv, qd):
+    print(f"decode config1 kv={kv} q={np.dtype(qd).name}", flush=True)
+    case = make_case(kv, [512], n_blocks=64, seed=201)
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    got = run_decode(ctx, pool, case, q_dtype=qd)
+    ref = O.paged_decode(ref_layer, case.q.astype(qd), case.block_tables, case.ctx_lens)
+    check(got, ref, "config1")
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_decode_gqa_groups_ragged(ctx, kv, G):
+    print(f"decode gqa kv={kv} G={G}", flush=True)
+    Hkv = 2 if G == 8 else 4
+    lens = [1, 16, 17, 100, 255, 256, 257, 600]
+    case = make_case(kv, lens, n_kv_heads=Hkv, n_heads=Hkv * G, seed=202 + G, outlier_scale=8.0)
+    ref_layer = oracle_layer(case)
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, Hkv, HD, kv)
+    sl, kk, vv = case.prefill_slots()
+    ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+    sl, kk, vv = case.last_slots()
+    ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+    for qd in (np.float16, np.float32):
+        got = run_decode(ctx, pool, case, q_dtype=qd)
+        ref = O.paged_decode(ref_layer, case.q.astype(qd), case.block_tables, case.ctx_lens)
+        check(got, ref, f"G={G} q={np.dtype(qd).name}")
+
+
+@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
+@pytest.mark.parametrize("P", [16, 256, 512, 1024, 4096, 0])
+def test_decode_split_k_partitions(ctx, kv, P):
+    print(f"decode split kv={kv} P={P}", flush=True)
+    lens = [3000, 1024, 2049, 777]
+    case = make_case(kv, lens, seed=210, outlier_scale=8.0)
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    got = run_decode(ctx, pool, case, partition_tokens=P)
+    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+    check(got, ref, f"P={P}")
+
+
+@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
+def test_decode_config2_3_shapes_reduced_batch(ctx, kv):
+    """Configs 2 / 3: L ~ U[1024, 8192], 40k-block pool, GQA 4 (8 of the 64 sequences)."""
+    print(f"decode config2/3 kv={kv}", flush=True)
+    r = np.random.default_rng(301)
+    lens = r.integers(1024, 8193, 8)
+    case = make_case(kv, lens, n_blocks=40000, seed=302, outlier_scale=8.0 if kv == O.I8_BLK else 1.0,
+                     stride=512)
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    got = run_decode(ctx, pool, case)
+    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+    err = check(got, ref, "config2/3")
+    print(f"  max abs err {err:.3g}")
+
+
+def test_decode_seq_rows_and_pool_slot_table(ctx):
+    """Rows chosen through seq_rows, and the pool's own slot table (bind_slot)."""
+    print("decode seq_rows / slot table", flush=True)
+    case = make_case(O.I8_BLK, [300, 45, 129], seed=303)
+    ref_layer = oracle_layer(case)
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, 8, HD, O.I8_BLK, max_slots=8,
+                       max_pages_per_slot=case.block_tables.shape[1])
+    sl, kk, vv = case.prefill_slots()
+    ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+    sl, kk, vv = case.last_slots()
+    ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+    slots = [5, 0, 7]
+    for s, slot in enumerate(slots):
+        n = -(-int(case.ctx_lens[s]) // BS)
+        pool.bind_slot(slot, case.block_tables[s, :n])
+    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+    out = ctx.alloc(3 * 32 * HD * 4)
+    ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, out, ctx.upload(case.ctx_lens), 3, 32,
+                     int(case.ctx_lens.max()), seq_rows=ctx.upload(np.array(slots, np.int32)))
+    got = out.download((3, 32, HD), np.float32)
+    check(got, ref, "slot table")
+
+
+def test_decode_deterministic_and_block_permutation_invariant(ctx):
+    print("decode determinism", flush=True)
+    case = make_case(O.I8_BLK, [700, 1500], seed=304)
+    pool = gpu_pool(ctx, case)
+    a = run_decode(ctx, pool, case)
+    b = run_decode(ctx, pool, case)
+    assert np.array_equal(a, b)
+    # the same data under another physical block assignment gives the same bits
+    case2 = make_case(O.I8_BLK, [700, 1500], seed=304)
+    perm = np.random.default_rng(9).permutation(case2.n_blocks).astype(np.int32)
+    case2.block_tables = perm[case2.block_tables]
+    pool2 = gpu_pool(ctx, case2)
+    c = run_decode(ctx, pool2, case2)
+    assert np.array_equal(a, c)
+
+
+def test_decode_empty_and_single_token(ctx):
+    print("decode empty / single", flush=True)
+    case = make_case(O.F16, [1, 5], seed=305)
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    got = run_decode(ctx, pool, case)
+    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+    assert np.array_equal(got[0], ref[0])  # one token: out = v_0 exactly
+    check(got, ref, "single")
+    case.ctx_lens = np.array([0, 5], np.int32)
+    got = run_decode(ctx, pool, case)
+    assert not got[0].any()
+
+
+def test_decode_rejects_bad_arguments(ctx):
+    case = make_case(O.F16, [20], seed=306)
+    pool = gpu_pool(ctx, case)
+    with pytest.raises(velokv.VkError) as e:
+        ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
+                         ctx.upload(case.ctx_lens), 1, 24, 20, block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1])
+    assert e.value.code == velokv.ERR_UNSUPPORTED  # 24 / 8 = 3 is not a supported group size
+    with pytest.raises(velokv.VkError) as e:
+        ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
+                         ctx.upload(case.ctx_lens), 1, 32, 10 ** 6, block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1])
+    assert e.value.code == velokv.ERR_BAD_ARG
+    with pytest.raises(velokv.VkError):
+        ctx.paged_decode(pool, 5, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
+                         ctx.upload(case.ctx_lens), 1, 32, 20, block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1])

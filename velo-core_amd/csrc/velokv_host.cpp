@@ -1,0 +1,796 @@
+// velokv_host.cpp -- C ABI (include/velokv.h) over the gfx950 code object.
+//
+// Host side of the KV hot path: context (device + code object), pools (HBM
+// layout, slot block table), argument validation, kernel launches through
+// hipModuleLaunchKernel, and the host block manager. Plain C++17 over the HIP
+// runtime API; no kernels are compiled into this library.
+#include "velokv.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "velokv_params.h"
+
+using namespace velokv;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                              \
+  do {                                                                             \
+    hipError_t _e = (expr);                                                        \
+    if (_e != hipSuccess)                                                          \
+      return fail(VK_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));     \
+  } while (0)
+
+constexpr int kBS = 16;   // block size the kernels are built for
+constexpr int kHD = 128;  // head_dim the kernels are built for
+constexpr int kChunkTokens = 256;
+
+uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+
+int kv_esz(int kv) {
+  switch (kv) {
+    case VK_KV_F32: return 4;
+    case VK_KV_F16: return 2;
+    case VK_KV_I8_REF:
+    case VK_KV_I8_BLK: return 1;
+    default: return 0;
+  }
+}
+int kv_stile(int kv, int bs) {
+  if (kv == VK_KV_I8_BLK) return 2;
+  if (kv == VK_KV_I8_REF) return 4 * bs;
+  return 0;
+}
+
+std::string default_code_object_path() {
+  Dl_info info;
+  if (dladdr(reinterpret_cast<void*>(&vk_ctx_create), &info) && info.dli_fname) {
+    std::string p(info.dli_fname);
+    const size_t slash = p.find_last_of('/');
+    return (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) + "/velokv_gfx950.co";
+  }
+  return "velokv_gfx950.co";
+}
+
+}  // namespace
+
+struct vk_ctx {
+  int device = 0;
+  std::string arch;
+  hipModule_t module = nullptr;
+  std::unordered_map<std::string, hipFunction_t> fns;
+  std::mutex ws_mu;
+  void* ws = nullptr;
+  uint64_t ws_bytes = 0;
+
+  hipFunction_t fn(const std::string& name) const {
+    auto it = fns.find(name);
+    return it == fns.end() ? nullptr : it->second;
+  }
+};
+
+struct vk_pool {
+  vk_ctx* ctx = nullptr;
+  vk_pool_desc desc{};
+  PoolGeom geom{};
+  uint8_t* base = nullptr;
+  uint64_t bytes = 0;
+  int32_t* table = nullptr;  // [max_slots][max_pages_per_slot]
+  uint64_t table_bytes = 0;
+};
+
+namespace {
+
+const char* const kKernelNames[] = {
+    "vk_decode_merge", "vk_append_kv0", "vk_append_kv1", "vk_append_kv2", "vk_append_kv3",
+    "vk_slot_mapping", "vk_copy_blocks", "vk_fill_normal_f16",
+};
+
+std::string decode_name(int kv, int g, int qt) {
+  return "vk_decode_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
+}
+
+int set_device(const vk_ctx* ctx) {
+  HIP_TRY(hipSetDevice(ctx->device));
+  return VK_OK;
+}
+
+template <typename P>
+int launch(const vk_ctx* ctx, const char* name, dim3 grid, dim3 block, const P& params, void* stream) {
+  hipFunction_t f = ctx->fn(name);
+  if (!f) return fail(VK_ERR_NOT_WIRED, "kernel %s is not in the code object", name);
+  void* args[] = {const_cast<P*>(&params)};
+  HIP_TRY(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
+                                reinterpret_cast<hipStream_t>(stream), args, nullptr));
+  return VK_OK;
+}
+
+int check_pool(const vk_ctx* ctx, const vk_pool* pool) {
+  if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
+  if (!pool) return fail(VK_ERR_NOT_WIRED, "pool is null");
+  if (pool->ctx != ctx) return fail(VK_ERR_BAD_ARG, "pool belongs to another context");
+  return VK_OK;
+}
+
+}  // namespace
+
+// ============================================================================
+// context
+// ============================================================================
+extern "C" const char* vk_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** out) {
+  if (!out) return fail(VK_ERR_BAD_ARG, "out is null");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) return fail(VK_ERR_NO_DEVICE, "no HIP device visible (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n) return fail(VK_ERR_NO_DEVICE, "device %d out of range (0..%d)", device, n - 1);
+  HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device));
+  std::string arch = prop.gcnArchName;
+  const size_t colon = arch.find(':');
+  if (colon != std::string::npos) arch = arch.substr(0, colon);
+  if (arch != "gfx950")
+    return fail(VK_ERR_UNSUPPORTED, "device %d is %s; the code object is built for gfx950", device, arch.c_str());
+
+  const std::string path = code_object_path ? std::string(code_object_path) : default_code_object_path();
+  FILE* fp = fopen(path.c_str(), "rb");
+  if (!fp) return fail(VK_ERR_NOT_WIRED, "code object %s not found (build the extension first)", path.c_str());
+  fclose(fp);
+
+  auto* ctx = new vk_ctx();
+  ctx->device = device;
+  ctx->arch = arch;
+  e = hipModuleLoad(&ctx->module, path.c_str());
+  if (e != hipSuccess) {
+    delete ctx;
+    return fail(VK_ERR_NOT_WIRED, "hipModuleLoad(%s) failed: %s", path.c_str(), hipGetErrorString(e));
+  }
+  std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
+  for (int kv = 0; kv < 4; ++kv)
+    for (int g : {1, 2, 4, 8})
+      for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
+  for (const auto& nm : names) {
+    hipFunction_t f = nullptr;
+    e = hipModuleGetFunction(&f, ctx->module, nm.c_str());
+    if (e != hipSuccess) {
+      hipModuleUnload(ctx->module);
+      delete ctx;
+      return fail(VK_ERR_NOT_WIRED, "kernel %s missing from %s: %s", nm.c_str(), path.c_str(), hipGetErrorString(e));
+    }
+    ctx->fns[nm] = f;
+  }
+  *out = ctx;
+  return VK_OK;
+}
+
+extern "C" int vk_ctx_destroy(vk_ctx* ctx) {
+  if (!ctx) return VK_OK;
+  hipSetDevice(ctx->device);
+  if (ctx->ws) {
+    hipDeviceSynchronize();
+    hipFree(ctx->ws);
+  }
+  if (ctx->module) hipModuleUnload(ctx->module);
+  delete ctx;
+  return VK_OK;
+}
+
+extern "C" int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap) {
+  if (!ctx || !buf || cap == 0) return fail(VK_ERR_BAD_ARG, "bad argument");
+  snprintf(buf, cap, "%s", ctx->arch.c_str());
+  return VK_OK;
+}
+
+// ============================================================================
+// pools
+// ============================================================================
+extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out) {
+  if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
+  if (!d || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  *out = nullptr;
+  if (d->block_size <= 0) return fail(VK_ERR_INVALID_BLOCK_SIZE, "block size must be greater than zero");
+  if (d->n_layer <= 0 || d->n_blocks <= 0 || d->n_kv_heads <= 0 || d->head_dim <= 0 || d->max_slots < 0 ||
+      d->max_pages_per_slot < 0)
+    return fail(VK_ERR_BAD_ARG, "pool sizes must be positive");
+  if (kv_esz(d->kv_type) == 0) return fail(VK_ERR_BAD_ARG, "unknown kv_type %d", d->kv_type);
+  if (d->block_size != kBS || d->head_dim != kHD)
+    return fail(VK_ERR_UNSUPPORTED, "kernels are built for block_size %d and head_dim %d (got %d, %d)", kBS, kHD,
+                d->block_size, d->head_dim);
+  auto* p = new vk_pool();
+  p->ctx = ctx;
+  p->desc = *d;
+  if (p->desc.max_pages_per_slot == 0) p->desc.max_pages_per_slot = d->n_blocks;
+  const int esz = kv_esz(d->kv_type);
+  PoolGeom& g = p->geom;
+  g.tile_bytes = (uint32_t)(d->block_size * d->head_dim * esz);
+  g.stile_bytes = (uint32_t)kv_stile(d->kv_type, d->block_size);
+  g.n_blocks = d->n_blocks;
+  g.n_kv_heads = d->n_kv_heads;
+  g.block_size = d->block_size;
+  g.head_dim = d->head_dim;
+  g.kv_type = d->kv_type;
+  g.n_layer = d->n_layer;
+  const uint64_t codes = (uint64_t)d->n_blocks * d->n_kv_heads * g.tile_bytes;
+  const uint64_t scales = (uint64_t)d->n_blocks * d->n_kv_heads * g.stile_bytes;
+  g.k_off = 0;
+  g.v_off = align_up(codes, 256);
+  g.ks_off = g.v_off + align_up(codes, 256);
+  g.vs_off = g.ks_off + align_up(scales, 256);
+  g.layer_stride = g.vs_off + align_up(scales, 256);
+  p->bytes = g.layer_stride * (uint64_t)d->n_layer;
+  int rc = set_device(ctx);
+  if (rc) { delete p; return rc; }
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->base), p->bytes);
+  if (e != hipSuccess) {
+    delete p;
+    return fail(VK_ERR_HIP, "hipMalloc of %.3f GB for the KV pool failed: %s", p->bytes / 1e9, hipGetErrorString(e));
+  }
+  e = hipMemset(p->base, 0, p->bytes);
+  if (e == hipSuccess && d->max_slots > 0) {
+    p->table_bytes = (uint64_t)d->max_slots * p->desc.max_pages_per_slot * sizeof(int32_t);
+    e = hipMalloc(reinterpret_cast<void**>(&p->table), p->table_bytes);
+    if (e == hipSuccess) e = hipMemset(p->table, 0, p->table_bytes);
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    hipFree(p->base);
+    if (p->table) hipFree(p->table);
+    delete p;
+    return fail(VK_ERR_HIP, "pool initialisation failed: %s", hipGetErrorString(e));
+  }
+  *out = p;
+  return VK_OK;
+}
+
+extern "C" int vk_pool_destroy(vk_pool* pool) {
+  if (!pool) return VK_OK;
+  hipSetDevice(pool->ctx->device);
+  hipDeviceSynchronize();
+  hipFree(pool->base);
+  if (pool->table) hipFree(pool->table);
+  delete pool;
+  return VK_OK;
+}
+
+extern "C" int vk_pool_get_desc(const vk_pool* pool, vk_pool_desc* out) {
+  if (!pool || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  *out = pool->desc;
+  return VK_OK;
+}
+
+extern "C" int vk_pool_layer_view(const vk_pool* pool, int32_t layer, vk_layer_view* out) {
+  if (!pool || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  if (layer < 0 || layer >= pool->desc.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", layer);
+  const PoolGeom& g = pool->geom;
+  uint8_t* L = pool->base + g.layer_stride * (uint64_t)layer;
+  out->k_codes = L + g.k_off;
+  out->v_codes = L + g.v_off;
+  out->codes_bytes = (uint64_t)g.n_blocks * g.n_kv_heads * g.tile_bytes;
+  out->scales_bytes = (uint64_t)g.n_blocks * g.n_kv_heads * g.stile_bytes;
+  out->k_scales = g.stile_bytes ? L + g.ks_off : nullptr;
+  out->v_scales = g.stile_bytes ? L + g.vs_off : nullptr;
+  return VK_OK;
+}
+
+extern "C" int vk_pool_block_table(const vk_pool* pool, int32_t** table_dev, int32_t* row_stride) {
+  if (!pool || !table_dev || !row_stride) return fail(VK_ERR_BAD_ARG, "null argument");
+  *table_dev = pool->table;
+  *row_stride = pool->desc.max_pages_per_slot;
+  return VK_OK;
+}
+
+extern "C" int vk_pool_bytes(const vk_pool* pool, uint64_t* out) {
+  if (!pool || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  *out = pool->bytes + pool->table_bytes;
+  return VK_OK;
+}
+
+extern "C" int vk_bind_slot(vk_pool* pool, uint32_t slot, const uint32_t* pages, int32_t n_pages) {
+  if (!pool) return fail(VK_ERR_NOT_WIRED, "pool is null");
+  if (n_pages < 0 || (n_pages > 0 && !pages)) return fail(VK_ERR_BAD_ARG, "bad page list");
+  const int32_t maxp = pool->desc.max_pages_per_slot;
+  if (n_pages > maxp)
+    return fail(VK_ERR_TOO_MANY_PAGES, "Request pages (%d) exceed max pages per slot (%d)", n_pages, maxp);
+  if ((int64_t)slot >= pool->desc.max_slots)
+    return fail(VK_ERR_BAD_ARG, "slot %u out of range (max_slots %d)", slot, pool->desc.max_slots);
+  std::vector<int32_t> row((size_t)maxp, 0);
+  for (int32_t i = 0; i < n_pages; ++i) {
+    if (pages[i] >= (uint32_t)pool->desc.n_blocks)
+      return fail(VK_ERR_BAD_ARG, "page id %u out of range (n_blocks %d)", pages[i], pool->desc.n_blocks);
+    row[(size_t)i] = (int32_t)pages[i];
+  }
+  int rc = set_device(pool->ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpy(pool->table + (uint64_t)slot * maxp, row.data(), row.size() * sizeof(int32_t),
+                    hipMemcpyHostToDevice));
+  return VK_OK;
+}
+
+// ============================================================================
+// hot path
+// ============================================================================
+extern "C" int vk_slot_mapping(vk_ctx* ctx, vk_pool* pool, const int32_t* block_tables, int32_t bt_stride,
+                               const int32_t* seq_rows, const int32_t* positions, int32_t n_tok,
+                               int64_t* slot_mapping_out, void* stream) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  if (n_tok < 0) return fail(VK_ERR_BAD_ARG, "n_tok < 0");
+  if (n_tok == 0) return VK_OK;
+  if (!positions || !slot_mapping_out) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  if (!block_tables) {
+    if (!pool->table) return fail(VK_ERR_BAD_ARG, "pool has no slot table (max_slots = 0)");
+    block_tables = pool->table;
+    bt_stride = pool->desc.max_pages_per_slot;
+  }
+  if (bt_stride <= 0) return fail(VK_ERR_BAD_ARG, "bt_stride must be positive");
+  SlotMapParams p{block_tables, seq_rows, positions, slot_mapping_out, bt_stride, pool->desc.block_size, n_tok,
+                  pool->desc.n_blocks};
+  if ((rc = set_device(ctx))) return rc;
+  return launch(ctx, "vk_slot_mapping", dim3((n_tok + 255) / 256), dim3(256), p, stream);
+}
+
+extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* k, const void* v, int32_t in_dtype,
+                         const int64_t* slot_mapping, int32_t n_tok, void* stream) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  if (layer < 0 || layer >= pool->desc.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", layer);
+  if (in_dtype != VK_DT_F32 && in_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "in_dtype %d", in_dtype);
+  if (n_tok < 0) return fail(VK_ERR_BAD_ARG, "n_tok < 0");
+  if (n_tok == 0) return VK_OK;
+  if (!k || !v || !slot_mapping) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  AppendParams p{};
+  p.base = pool->base;
+  p.g = pool->geom;
+  p.layer = layer;
+  p.in_dtype = in_dtype;
+  p.k = k;
+  p.v = v;
+  p.slot_mapping = slot_mapping;
+  p.n_tok = n_tok;
+  const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
+  if ((rc = set_device(ctx))) return rc;
+  return launch(ctx, name.c_str(), dim3((unsigned)n_tok, (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
+}
+
+namespace {
+
+struct DecodePlan {
+  const int32_t* bt;
+  int32_t bt_stride;
+  int32_t bt_rows;
+  int32_t part_tokens;
+  int32_t max_parts;
+  uint64_t acc_bytes, ml_bytes;
+};
+
+int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl) {
+  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
+  const vk_pool_desc& d = pool->desc;
+  if (a->layer < 0 || a->layer >= d.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", a->layer);
+  if (a->n_seqs < 0 || a->n_heads <= 0 || a->max_context_len < 0) return fail(VK_ERR_BAD_ARG, "bad sizes");
+  if (a->n_heads % d.n_kv_heads) return fail(VK_ERR_BAD_ARG, "n_heads %d not a multiple of n_kv_heads %d", a->n_heads, d.n_kv_heads);
+  const int G = a->n_heads / d.n_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (supported 1, 2, 4, 8)", G);
+  if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
+  pl->bt = a->block_tables;
+  pl->bt_stride = a->bt_stride;
+  pl->bt_rows = 0;
+  if (!pl->bt) {
+    if (!pool->table) return fail(VK_ERR_BAD_ARG, "no block table given and the pool has no slot table");
+    pl->bt = pool->table;
+    pl->bt_stride = d.max_pages_per_slot;
+    pl->bt_rows = d.max_slots;
+  }
+  if (pl->bt_stride <= 0) return fail(VK_ERR_BAD_ARG, "bt_stride must be positive");
+  if ((int64_t)a->max_context_len > (int64_t)pl->bt_stride * d.block_size)
+    return fail(VK_ERR_BAD_ARG, "max_context_len %d exceeds the block-table row (%d pages)", a->max_context_len, pl->bt_stride);
+  int P = a->partition_tokens;
+  if (P < 0 || P % d.block_size) return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size");
+  if (P == 0) {
+    // Enough units to fill the chip several times over; long partitions keep the
+    // split-K partial traffic small.
+    const int64_t ctx = std::max(1, a->max_context_len);
+    const int64_t pairs = std::max<int64_t>(1, (int64_t)a->n_seqs * d.n_kv_heads);
+    const int64_t target_units = 8192;
+    int64_t want = (ctx * pairs + target_units - 1) / target_units;
+    P = kChunkTokens;
+    while (P < want && P < 8192) P *= 2;
+  }
+  pl->part_tokens = P;
+  pl->max_parts = std::max(1, (a->max_context_len + P - 1) / P);
+  pl->acc_bytes = align_up((uint64_t)a->n_seqs * a->n_heads * pl->max_parts * kHD * sizeof(float), 256);
+  pl->ml_bytes = align_up((uint64_t)a->n_seqs * a->n_heads * pl->max_parts * 2 * sizeof(float), 256);
+  return VK_OK;
+}
+
+}  // namespace
+
+extern "C" int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes) {
+  if (!pool || !bytes) return fail(VK_ERR_BAD_ARG, "null argument");
+  DecodePlan pl;
+  int rc = plan_decode(pool, a, &pl);
+  if (rc) return rc;
+  *bytes = pl.acc_bytes + pl.ml_bytes;
+  return VK_OK;
+}
+
+extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  DecodePlan pl;
+  if ((rc = plan_decode(pool, a, &pl))) return rc;
+  if (a->n_seqs == 0) return VK_OK;
+  if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  if ((rc = set_device(ctx))) return rc;
+  const uint64_t need = pl.acc_bytes + pl.ml_bytes;
+  uint8_t* ws = reinterpret_cast<uint8_t*>(a->workspace);
+  if (ws) {
+    if (a->workspace_bytes < need)
+      return fail(VK_ERR_BAD_ARG, "workspace of %llu bytes, need %llu", (unsigned long long)a->workspace_bytes,
+                  (unsigned long long)need);
+  } else {
+    std::lock_guard<std::mutex> lk(ctx->ws_mu);
+    if (ctx->ws_bytes < need) {
+      if (ctx->ws) {
+        HIP_TRY(hipDeviceSynchronize());
+        HIP_TRY(hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+      }
+      HIP_TRY(hipMalloc(&ctx->ws, need));
+      ctx->ws_bytes = need;
+    }
+    ws = reinterpret_cast<uint8_t*>(ctx->ws);
+  }
+  const vk_pool_desc& d = pool->desc;
+  const PoolGeom& g = pool->geom;
+  const uint8_t* L = pool->base + g.layer_stride * (uint64_t)a->layer;
+  const int G = a->n_heads / d.n_kv_heads;
+  const float scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)d.head_dim);
+
+  DecodeParams p{};
+  p.kc = L + g.k_off;
+  p.vc = L + g.v_off;
+  p.ks = g.stile_bytes ? L + g.ks_off : nullptr;
+  p.vs = g.stile_bytes ? L + g.vs_off : nullptr;
+  p.q = a->q;
+  p.out = a->out;
+  p.part_acc = reinterpret_cast<float*>(ws);
+  p.part_ml = reinterpret_cast<float*>(ws + pl.acc_bytes);
+  p.block_tables = pl.bt;
+  p.seq_rows = a->seq_rows;
+  p.context_lens = a->context_lens;
+  p.tile_bytes = g.tile_bytes;
+  p.stile_bytes = g.stile_bytes;
+  p.bt_stride = pl.bt_stride;
+  p.bt_rows = pl.bt_rows;
+  p.n_seqs = a->n_seqs;
+  p.n_heads = a->n_heads;
+  p.n_kv_heads = d.n_kv_heads;
+  p.n_blocks = d.n_blocks;
+  p.max_parts = pl.max_parts;
+  p.part_tokens = pl.part_tokens;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
+  if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
+  const std::string name = decode_name(d.kv_type, G, a->q_dtype);
+  if ((rc = launch(ctx, name.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
+
+  MergeParams m{};
+  m.part_acc = p.part_acc;
+  m.part_ml = p.part_ml;
+  m.context_lens = a->context_lens;
+  m.out = a->out;
+  m.n_seqs = a->n_seqs;
+  m.n_heads = a->n_heads;
+  m.max_parts = pl.max_parts;
+  m.part_tokens = pl.part_tokens;
+  const uint64_t rows = (uint64_t)a->n_seqs * a->n_heads;
+  return launch(ctx, "vk_decode_merge", dim3((unsigned)((rows + 3) / 4)), dim3(256), m, stream);
+}
+
+extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a, void* stream) {
+  (void)stream;
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
+  return fail(VK_ERR_UNSUPPORTED, "tree verify kernel is not built yet");
+}
+
+extern "C" int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* pairs, int32_t n_pairs, void* stream) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  if (n_pairs < 0 || (n_pairs > 0 && !pairs)) return fail(VK_ERR_BAD_ARG, "bad pair list");
+  if (n_pairs == 0) return VK_OK;
+  const int nb = pool->desc.n_blocks;
+  std::vector<char> is_dst((size_t)nb, 0), is_src((size_t)nb, 0);
+  for (int i = 0; i < n_pairs; ++i) {
+    const int s = pairs[2 * i], t = pairs[2 * i + 1];
+    if (s < 0 || s >= nb || t < 0 || t >= nb) return fail(VK_ERR_BAD_ARG, "pair %d (%d -> %d) out of range", i, s, t);
+    if (is_dst[(size_t)t]) return fail(VK_ERR_BAD_ARG, "block %d is the destination of two pairs", t);
+    is_dst[(size_t)t] = 1;
+    is_src[(size_t)s] = 1;
+  }
+  for (int i = 0; i < n_pairs; ++i)
+    if (is_src[(size_t)pairs[2 * i + 1]]) return fail(VK_ERR_BAD_ARG, "block %d is both a source and a destination", pairs[2 * i + 1]);
+  if ((rc = set_device(ctx))) return rc;
+  for (int i0 = 0; i0 < n_pairs; i0 += kMaxCopyPairs) {
+    CopyParams p{};
+    p.base = pool->base;
+    p.g = pool->geom;
+    p.n_pairs = std::min(kMaxCopyPairs, n_pairs - i0);
+    memcpy(p.pairs, pairs + 2 * i0, sizeof(int32_t) * 2 * (size_t)p.n_pairs);
+    if ((rc = launch(ctx, "vk_copy_blocks", dim3((unsigned)p.n_pairs, (unsigned)pool->desc.n_layer, 2), dim3(256), p,
+                     stream)))
+      return rc;
+  }
+  return VK_OK;
+}
+
+// ============================================================================
+// host block manager: PagedAttentionBlockManager (paged_attention.rs:92-212)
+// plus per-page reference counts.
+// ============================================================================
+struct vk_block_manager {
+  int32_t block_size = 0;
+  int32_t total_pages = 0;
+  std::deque<uint32_t> free_pages;                    // FIFO (paged_attention.rs:130-133)
+  std::map<uint64_t, std::vector<uint32_t>> mappings; // handle -> pages
+  std::vector<int32_t> refs;                          // per-page reference count
+  int64_t pages_for(int64_t tokens) const { return (tokens + block_size - 1) / block_size; }
+};
+
+namespace {
+int copy_pages(const std::vector<uint32_t>& v, uint32_t* out, int32_t cap, int32_t* n_out) {
+  if (n_out) *n_out = (int32_t)v.size();
+  if (out) {
+    if ((int64_t)v.size() > cap) return fail(VK_ERR_BAD_ARG, "output capacity %d < %zu pages", cap, v.size());
+    std::copy(v.begin(), v.end(), out);
+  }
+  return VK_OK;
+}
+int take_pages(vk_block_manager* bm, int64_t n, std::vector<uint32_t>* pages) {
+  if (n > (int64_t)bm->free_pages.size())
+    return fail(VK_ERR_OUT_OF_PAGES, "requested %lld pages but only %zu are available", (long long)n,
+                bm->free_pages.size());
+  for (int64_t i = 0; i < n; ++i) {
+    const uint32_t pg = bm->free_pages.front();
+    bm->free_pages.pop_front();
+    bm->refs[pg] = 1;
+    pages->push_back(pg);
+  }
+  return VK_OK;
+}
+}  // namespace
+
+extern "C" int vk_bm_create(int32_t block_size, int32_t total_pages, vk_block_manager** out) {
+  if (!out) return fail(VK_ERR_BAD_ARG, "out is null");
+  *out = nullptr;
+  if (block_size <= 0) return fail(VK_ERR_INVALID_BLOCK_SIZE, "block size must be greater than zero");
+  if (total_pages < 0) return fail(VK_ERR_BAD_ARG, "total_pages < 0");
+  auto* bm = new vk_block_manager();
+  bm->block_size = block_size;
+  bm->total_pages = total_pages;
+  bm->refs.assign((size_t)total_pages, 0);
+  for (int32_t i = 0; i < total_pages; ++i) bm->free_pages.push_back((uint32_t)i);
+  *out = bm;
+  return VK_OK;
+}
+
+extern "C" int vk_bm_destroy(vk_block_manager* bm) {
+  delete bm;
+  return VK_OK;
+}
+
+extern "C" int vk_bm_free_pages(const vk_block_manager* bm, int32_t* out) {
+  if (!bm || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  *out = (int32_t)bm->free_pages.size();
+  return VK_OK;
+}
+
+extern "C" int vk_bm_allocate(vk_block_manager* bm, uint64_t handle, int64_t token_len, uint32_t* pages_out,
+                              int32_t cap, int32_t* n_out) {
+  if (!bm) return fail(VK_ERR_BAD_ARG, "null manager");
+  if (token_len < 0) return fail(VK_ERR_BAD_ARG, "token_len < 0");
+  if (bm->mappings.count(handle)) return fail(VK_ERR_BAD_ARG, "handle %llu already mapped", (unsigned long long)handle);
+  std::vector<uint32_t> pages;
+  int rc = take_pages(bm, bm->pages_for(token_len), &pages);
+  if (rc) return rc;
+  bm->mappings[handle] = pages;
+  return copy_pages(pages, pages_out, cap, n_out);
+}
+
+extern "C" int vk_bm_release(vk_block_manager* bm, uint64_t handle) {
+  if (!bm) return fail(VK_ERR_BAD_ARG, "null manager");
+  auto it = bm->mappings.find(handle);
+  if (it == bm->mappings.end()) return fail(VK_ERR_UNKNOWN_HANDLE, "unknown KV handle %llu", (unsigned long long)handle);
+  for (uint32_t pg : it->second)
+    if (--bm->refs[pg] == 0) bm->free_pages.push_back(pg);
+  bm->mappings.erase(it);
+  return VK_OK;
+}
+
+extern "C" int vk_bm_pages(const vk_block_manager* bm, uint64_t handle, uint32_t* pages_out, int32_t cap,
+                           int32_t* n_out) {
+  if (!bm) return fail(VK_ERR_BAD_ARG, "null manager");
+  auto it = bm->mappings.find(handle);
+  if (it == bm->mappings.end()) return fail(VK_ERR_UNKNOWN_HANDLE, "unknown KV handle %llu", (unsigned long long)handle);
+  return copy_pages(it->second, pages_out, cap, n_out);
+}
+
+extern "C" int vk_bm_fork(vk_block_manager* bm, uint64_t parent, uint64_t child, int64_t shared_tokens,
+                          int64_t token_len, uint32_t* pages_out, int32_t cap, int32_t* n_out) {
+  if (!bm) return fail(VK_ERR_BAD_ARG, "null manager");
+  auto it = bm->mappings.find(parent);
+  if (it == bm->mappings.end()) return fail(VK_ERR_UNKNOWN_HANDLE, "unknown KV handle %llu", (unsigned long long)parent);
+  if (bm->mappings.count(child)) return fail(VK_ERR_BAD_ARG, "handle %llu already mapped", (unsigned long long)child);
+  if (shared_tokens < 0 || token_len < shared_tokens) return fail(VK_ERR_BAD_ARG, "need 0 <= shared_tokens <= token_len");
+  const int64_t n_shared = bm->pages_for(shared_tokens);
+  if (n_shared > (int64_t)it->second.size()) return fail(VK_ERR_BAD_ARG, "parent holds only %zu pages", it->second.size());
+  std::vector<uint32_t> pages(it->second.begin(), it->second.begin() + n_shared);
+  const int64_t n_new = bm->pages_for(token_len) - n_shared;
+  std::vector<uint32_t> fresh;
+  int rc = take_pages(bm, n_new, &fresh);
+  if (rc) return rc;
+  for (uint32_t pg : pages) ++bm->refs[pg];
+  pages.insert(pages.end(), fresh.begin(), fresh.end());
+  bm->mappings[child] = pages;
+  return copy_pages(pages, pages_out, cap, n_out);
+}
+
+extern "C" int vk_bm_cow(vk_block_manager* bm, uint64_t handle, int32_t page_idx, int32_t* src, int32_t* dst,
+                         int32_t* copied) {
+  if (!bm || !src || !dst || !copied) return fail(VK_ERR_BAD_ARG, "null argument");
+  auto it = bm->mappings.find(handle);
+  if (it == bm->mappings.end()) return fail(VK_ERR_UNKNOWN_HANDLE, "unknown KV handle %llu", (unsigned long long)handle);
+  if (page_idx < 0 || page_idx >= (int32_t)it->second.size()) return fail(VK_ERR_BAD_ARG, "page index %d out of range", page_idx);
+  const uint32_t old = it->second[(size_t)page_idx];
+  *copied = 0;
+  *src = *dst = (int32_t)old;
+  if (bm->refs[old] <= 1) return VK_OK;
+  std::vector<uint32_t> fresh;
+  int rc = take_pages(bm, 1, &fresh);
+  if (rc) return rc;
+  --bm->refs[old];
+  it->second[(size_t)page_idx] = fresh[0];
+  *dst = (int32_t)fresh[0];
+  *copied = 1;
+  return VK_OK;
+}
+
+extern "C" int vk_bm_refcount(const vk_block_manager* bm, uint32_t page, int32_t* out) {
+  if (!bm || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  if (page >= (uint32_t)bm->total_pages) return fail(VK_ERR_BAD_ARG, "page %u out of range", page);
+  *out = bm->refs[page];
+  return VK_OK;
+}
+
+// ============================================================================
+// device memory / stream helpers
+// ============================================================================
+extern "C" int vk_dev_alloc(vk_ctx* ctx, uint64_t bytes, void** out) {
+  if (!ctx || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMalloc(out, std::max<uint64_t>(bytes, 1)));
+  return VK_OK;
+}
+extern "C" int vk_dev_free(vk_ctx* ctx, void* p) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipFree(p));
+  return VK_OK;
+}
+extern "C" int vk_memcpy_h2d(vk_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  if (!bytes) return VK_OK;
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  return VK_OK;
+}
+extern "C" int vk_memcpy_d2h(vk_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  if (!bytes) return VK_OK;
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  return VK_OK;
+}
+extern "C" int vk_memset_d(vk_ctx* ctx, void* dst, int value, uint64_t bytes) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipMemset(dst, value, bytes));
+  return VK_OK;
+}
+extern "C" int vk_stream_create(vk_ctx* ctx, void** out) {
+  if (!ctx || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  hipStream_t s;
+  HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = s;
+  return VK_OK;
+}
+extern "C" int vk_stream_destroy(vk_ctx* ctx, void* stream) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  HIP_TRY(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)));
+  return VK_OK;
+}
+extern "C" int vk_stream_sync(vk_ctx* ctx, void* stream) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  return VK_OK;
+}
+extern "C" int vk_event_create(vk_ctx* ctx, void** out) {
+  if (!ctx || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  hipEvent_t e;
+  HIP_TRY(hipEventCreate(&e));
+  *out = e;
+  return VK_OK;
+}
+extern "C" int vk_event_destroy(vk_ctx* ctx, void* ev) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)));
+  return VK_OK;
+}
+extern "C" int vk_event_record(vk_ctx* ctx, void* ev, void* stream) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), reinterpret_cast<hipStream_t>(stream)));
+  return VK_OK;
+}
+extern "C" int vk_event_elapsed_ms(vk_ctx* ctx, void* start, void* end, float* ms) {
+  if (!ctx || !ms) return fail(VK_ERR_BAD_ARG, "null argument");
+  HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(end)));
+  HIP_TRY(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(end)));
+  return VK_OK;
+}
+
+extern "C" int vk_fill_normal_f16(vk_ctx* ctx, void* dev, uint64_t n, uint64_t seed, int32_t row_len,
+                                  float outlier_scale, void* stream) {
+  if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
+  if (!dev && n) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  if (row_len <= 0) return fail(VK_ERR_BAD_ARG, "row_len must be positive");
+  if (n == 0) return VK_OK;
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  FillParams p{reinterpret_cast<uint16_t*>(dev), n, seed, row_len, outlier_scale};
+  const uint64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7FFFFFFFull) return fail(VK_ERR_BAD_ARG, "fill too large");
+  return launch(ctx, "vk_fill_normal_f16", dim3((unsigned)blocks), dim3(256), p, stream);
+}

@@ -1,0 +1,105 @@
+// Kernel argument blocks shared by the host library and the gfx950 code object.
+// Each kernel takes exactly one of these structs by value, so the host packs
+// one pointer into hipModuleLaunchKernel's kernelParams.
+#pragma once
+#include <stdint.h>
+
+namespace velokv {
+
+enum KvType : int32_t { KV_F32 = 0, KV_F16 = 1, KV_I8_REF = 2, KV_I8_BLK = 3 };
+enum DType : int32_t { DT_F32 = 0, DT_F16 = 1 };
+
+// Geometry of one layer of a pool (see include/velokv.h for the layout).
+struct PoolGeom {
+  uint64_t layer_stride;   // bytes between layers
+  uint64_t k_off, v_off;   // byte offsets of K / V codes inside a layer
+  uint64_t ks_off, vs_off; // byte offsets of K / V scales inside a layer
+  uint32_t tile_bytes;     // codes of one (block, head): block_size * head_dim * esz
+  uint32_t stile_bytes;    // scales of one (block, head): 2 (I8_BLK), 4*bs (I8_REF), 0
+  int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
+};
+
+struct AppendParams {
+  uint8_t* base;            // pool base (all layers)
+  PoolGeom g;
+  int32_t layer;
+  int32_t in_dtype;
+  const void* k;            // [n_tok][Hkv][D]
+  const void* v;
+  const int64_t* slot_mapping;
+  int32_t n_tok;
+};
+
+struct SlotMapParams {
+  const int32_t* block_tables;
+  const int32_t* seq_rows;
+  const int32_t* positions;
+  int64_t* out;
+  int32_t bt_stride, block_size, n_tok, n_blocks;
+};
+
+struct DecodeParams {
+  const uint8_t* kc;        // K codes of the layer
+  const uint8_t* vc;        // V codes of the layer
+  const uint8_t* ks;        // K scales of the layer (or null)
+  const uint8_t* vs;        // V scales
+  const void* q;            // [S][H][D]
+  float* out;               // [S][H][D]
+  float* part_acc;          // [S][H][max_parts][D]
+  float* part_ml;           // [S][H][max_parts][2] (running max in log2 units, sum)
+  const int32_t* block_tables;
+  const int32_t* seq_rows;
+  const int32_t* context_lens;
+  uint32_t tile_bytes;
+  uint32_t stile_bytes;
+  int32_t bt_stride;
+  int32_t bt_rows;          // rows of the block table when known (pool slot table), else 0
+  int32_t n_seqs, n_heads, n_kv_heads, n_blocks;
+  int32_t max_parts;        // partitions per sequence in the grid
+  int32_t part_tokens;      // tokens per partition (multiple of the block size)
+  float scale_log2;         // softmax scale * log2(e)
+};
+
+struct MergeParams {
+  const float* part_acc;
+  const float* part_ml;
+  const int32_t* context_lens;
+  float* out;
+  int32_t n_seqs, n_heads, max_parts, part_tokens;
+};
+
+struct TreeParams {
+  const uint8_t* kc;
+  const uint8_t* vc;
+  const uint8_t* ks;
+  const uint8_t* vs;
+  const void* q;            // [S][N][H][D]
+  float* out;               // [S][N][H][D]
+  const int32_t* block_tables;
+  const int32_t* seq_rows;
+  const int32_t* context_lens;
+  const uint32_t* tree_mask;// [S][N]
+  uint32_t tile_bytes;
+  uint32_t stile_bytes;
+  int32_t bt_stride;
+  int32_t n_seqs, n_nodes, n_heads, n_kv_heads, n_blocks;
+  float scale_log2;
+};
+
+constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)
+struct CopyParams {
+  uint8_t* base;
+  PoolGeom g;
+  int32_t n_pairs;
+  int32_t pairs[2 * kMaxCopyPairs];
+};
+
+struct FillParams {
+  uint16_t* dst;
+  uint64_t n;
+  uint64_t seed;
+  int32_t row_len;
+  float outlier_scale;
+};
+
+}  // namespace velokv
