@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the KV-cache hot path on one MI355X.
+
+Metric: paged decode-attention achieved HBM GB/s (% of peak) and
+tokens/s at B=64 sequences x 8192 context, Llama-3-8B decode-layer shapes
+(32 query heads, 8 KV heads, head_dim 128, block size 16), INT8 KV (per-(block,
+head) fp16 scales) as the headline and fp16 KV beside it.
+
+One step = one decode token for all 64 sequences through 32 layers: per layer,
+append the new K/V token of every sequence at position 8191 (slot mapping into a
+randomly scattered 40k-block pool, on-the-fly INT8 quantization) and run paged
+decode attention over the full 8192-token context. Inputs (pool contents, new
+K/V, q) are synthetic (seeded SplitMix64 normals generated on the GPU) and are
+resident in HBM before timing starts.
+
+value        = algorithmic bytes of a step / step time (GB/s)
+tokens_per_s = 64 / step time (attention-only decode throughput, 32 layers)
+roofline     = the decode kernel (split-K partitions with the merge fused in):
+               algorithmic bytes per launch / mean launch time from HIP events
+               around every launch in the timed region, against the 8 TB/s HBM peak.
+cpu_baseline = the CPU oracle (oracle/velokv_oracle.c, a C port of the
+               reference's CPU attention math on the paged INT8 layout) timed on a
+               bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "velo-core_amd"))
+
+import velokv  # noqa: E402
+from velokv import synth  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BS, HD = 16, 128
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--kv", choices=["int8", "fp16"], default="int8", help="headline KV type")
+    ap.add_argument("--also", choices=["fp16", "int8", "none"], default="fp16", help="second KV type reported beside")
+    ap.add_argument("--seqs", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=8192)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--heads", type=int, default=32)
+    ap.add_argument("--kv-heads", type=int, default=8)
+    ap.add_argument("--pool-blocks", type=int, default=40000)
+    ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = auto)")
+    ap.add_argument("--ragged", action="store_true", help="context lengths U[1024, ctx] (configs 2/3)")
+    ap.add_argument("--decode", choices=["auto", "mfma", "valu"], default="auto",
+                    help="decode kernel family (vk_ctx_set_decode_kernel)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run one vk_copy_blocks of known size (HBM counter calibration)")
+    return ap.parse_args()
+
+
+def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride: int) -> int:
+    """Algorithmic HBM bytes of one decode call: each K/V element of every context
+    token read once, its scales, q, the output and the block-table entries used."""
+    tok = int(lens.sum())
+    blocks = int(sum(-(-int(L) // BS) for L in lens))
+    esz = {velokv.KV_F16: 2, velokv.KV_I8_BLK: 1, velokv.KV_I8_REF: 1, velokv.KV_F32: 4}[kv]
+    kvb = 2 * tok * Hkv * HD * esz
+    if kv == velokv.KV_I8_BLK:
+        kvb += 2 * blocks * Hkv * 2
+    elif kv == velokv.KV_I8_REF:
+        kvb += 2 * tok * Hkv * 4
+    return kvb + S * H * HD * 2 + S * H * HD * 4 + blocks * 4 + S * 4
+
+
+def append_bytes(kv: int, S: int, Hkv: int) -> int:
+    """New K/V read (fp16), codes written, scales written, slot mapping read."""
+    esz = {velokv.KV_F16: 2, velokv.KV_I8_BLK: 1, velokv.KV_I8_REF: 1, velokv.KV_F32: 4}[kv]
+    sc = {velokv.KV_I8_BLK: 2, velokv.KV_I8_REF: 4}.get(kv, 0)
+    return 2 * S * Hkv * HD * 2 + 2 * S * Hkv * HD * esz + 2 * S * Hkv * sc + S * 8
+
+
+def run_gpu(ctx, args, kv_name: str):
+    kv = velokv.KV_I8_BLK if kv_name == "int8" else velokv.KV_F16
+    S, H, Hkv, L, NL = args.seqs, args.heads, args.kv_heads, args.ctx, args.layers
+    if args.ragged:
+        lens = synth.rng(2024).integers(1024, L + 1, S).astype(np.int32)
+    else:
+        lens = np.full(S, L, np.int32)
+    pages = [-(-int(x) // BS) for x in lens]
+    bt = synth.scatter_block_tables(args.pool_blocks, pages, seed=11, stride=-(-L // BS))
+    pool = velokv.Pool(ctx, NL, args.pool_blocks, BS, Hkv, HD, kv)
+
+    # ---- fill the pool: prefill tokens 0 .. L-2 of every sequence, per layer ----
+    n_pre = int((lens - 1).sum())
+    rows = np.repeat(np.arange(S), lens - 1)
+    pos = np.concatenate([np.arange(int(x) - 1) for x in lens])
+    pre_slots = ctx.upload(synth.slots_for_positions(bt, pos, BS, rows))
+    kbuf = ctx.alloc(n_pre * Hkv * HD * 2)
+    vbuf = ctx.alloc(n_pre * Hkv * HD * 2)
+    outlier = 8.0 if kv == velokv.KV_I8_BLK else 1.0
+    for layer in range(NL):
+        ctx.fill_normal_f16(kbuf, n_pre * Hkv * HD, 1000 + 2 * layer, Hkv * HD, outlier)
+        ctx.fill_normal_f16(vbuf, n_pre * Hkv * HD, 1001 + 2 * layer, Hkv * HD, outlier)
+        ctx.append(pool, layer, kbuf, vbuf, velokv.DT_F16, pre_slots, n_pre)
+    ctx.sync()
+    kbuf.free()
+    vbuf.free()
+
+    # ---- per-step inputs, rotated over R sets so consecutive steps differ ----
+    R = 4
+    new_slots = ctx.upload(synth.slots_for_positions(bt, lens.astype(np.int64) - 1, BS))
+    qs, ks, vs = [], [], []
+    for r in range(R):
+        q = ctx.alloc(S * H * HD * 2)
+        ctx.fill_normal_f16(q, S * H * HD, 7000 + r, H * HD)
+        k = ctx.alloc(S * Hkv * HD * 2)
+        ctx.fill_normal_f16(k, S * Hkv * HD, 8000 + r, Hkv * HD, outlier)
+        v = ctx.alloc(S * Hkv * HD * 2)
+        ctx.fill_normal_f16(v, S * Hkv * HD, 9000 + r, Hkv * HD, outlier)
+        qs.append(q); ks.append(k); vs.append(v)
+    out = ctx.alloc(S * H * HD * 4)
+    d_lens = ctx.upload(lens)
+    d_bt = ctx.upload(bt)
+    stream = velokv.Stream(ctx)
+
+    def step(i, evs=None):
+        r = i % R
+        for layer in range(NL):
+            ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
+            if evs is not None:
+                evs[layer][0].record(stream)
+            ctx.paged_decode(pool, layer, qs[r], velokv.DT_F16, out, d_lens, S, H, int(lens.max()),
+                             block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
+                             stream=stream)
+            if evs is not None:
+                evs[layer][1].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    stream.sync()
+    ctx.sync()
+
+    start, end = velokv.Event(ctx), velokv.Event(ctx)
+    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
+    start.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    end.record(stream)
+    stream.sync()
+    ctx.sync()
+    total_ms = start.elapsed_ms(end)
+    dec_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
+
+    ms_step = total_ms / args.steps
+    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1])
+    abytes = append_bytes(kv, S, Hkv)
+    step_bytes = NL * (dbytes + abytes)
+    dec_mean_ms = float(np.mean(dec_ms))
+    achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
+    res = {
+        "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
+        "ms_per_step": round(ms_step, 4),
+        "tokens_per_s": round(S / (ms_step * 1e-3), 1),
+        "frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_bytes_per_launch": dbytes,
+        "append_bytes_per_launch": abytes,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": ("vk_decode_kv%d_g%d_q1" % (kv, H // Hkv) if args.decode == "valu" else
+                                "vk_decode_mfma_kv%d_g%d" % (kv, H // Hkv)),
+                     "launch_ms_mean": round(dec_mean_ms, 5), "launch_ms_min": round(float(np.min(dec_ms)), 5),
+                     "launches": len(dec_ms)},
+        "pool_gb": round(pool.nbytes / 1e9, 2),
+    }
+    if args.calibrate:
+        # plain copy of known size: n_pairs blocks x all layers x (K + V codes and scales)
+        used = set(bt[bt >= 0].ravel().tolist())
+        free = [b for b in range(args.pool_blocks) if b not in used]
+        n = min(2048, len(free))
+        pairs = np.stack([np.array(free[:n]), np.array(free[n:2 * n] if len(free) >= 2 * n else free[:n])], 1)
+        pairs = pairs[:len(free) // 2] if len(free) < 2 * n else pairs
+        ctx.copy_blocks(pool, pairs.astype(np.int32))
+        ctx.sync()
+        desc_tile = HD * BS * {velokv.KV_F16: 2}.get(kv, 1)
+        sc = {velokv.KV_I8_BLK: 2}.get(kv, 0)
+        res["calibration_copy_bytes_read"] = int(len(pairs) * NL * 2 * Hkv * (desc_tile + sc))
+    del pool
+    return res
+
+
+def cpu_baseline(args):
+    """The oracle's paged INT8 decode (llama_cpu.rs math on the paged layout) on a
+    bounded sample: 4 sequences x 8192 context x 32 heads, one layer."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as O
+    Ssmp, L, H, Hkv = 4, args.ctx, args.heads, args.kv_heads
+    lens = np.full(Ssmp, L, np.int32)
+    pages = [-(-L // BS)] * Ssmp
+    nb = sum(pages)
+    bt = synth.scatter_block_tables(nb, pages, seed=3)
+    layer = O.Layer(nb, Hkv, BS, HD, O.I8_BLK)
+    row = Hkv * HD
+    for s in range(Ssmp):
+        k = synth.normals_f16(L * row, 50 + 2 * s, row, 8.0).reshape(L, Hkv, HD)
+        v = synth.normals_f16(L * row, 51 + 2 * s, row, 8.0).reshape(L, Hkv, HD)
+        O.append(layer, k, v, synth.slots_for_positions(bt, np.arange(L), BS, np.full(L, s)))
+    q = synth.normals_f16(Ssmp * H * HD, 77).reshape(Ssmp, H, HD)
+    nbytes = decode_bytes(velokv.KV_I8_BLK, Ssmp, H, Hkv, lens, bt.shape[1])
+
+    def timed(threads):
+        O.set_threads(threads)
+        ts = []
+        t_end = time.time() + args.cpu_seconds / 2
+        while len(ts) < 3 or (time.time() < t_end and len(ts) < 9):
+            t0 = time.perf_counter()
+            O.paged_decode(layer, q, bt, lens)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    cores = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    t1 = timed(1)
+    tn = timed(cores)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / tn / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "tokens_per_s": round(Ssmp / (tn * args.layers), 3),
+        "sample": f"oracle paged INT8 decode, {Ssmp} seqs x {L} ctx x {H} heads, 1 layer, median of runs; "
+                  f"tokens/s scaled to {args.layers} layers",
+        "single_thread": {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                          "seconds_per_layer": round(t1, 4)},
+        "seconds_per_layer": round(tn, 4), "cpu_model": model,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(single-GPU KV hot path, see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    ctx = velokv.Context(0)
+    ctx.set_decode_kernel({"auto": velokv.DECODE_AUTO, "mfma": velokv.DECODE_MFMA,
+                           "valu": velokv.DECODE_VALU}[args.decode])
+    head = run_gpu(ctx, args, args.kv)
+    also = None
+    if args.also != "none" and args.also != args.kv:
+        also = run_gpu(ctx, args, args.also)
+    cpu = None if args.no_cpu else cpu_baseline(args)
+    workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=128, bs=16, %s KV, %d layers, append+decode per layer, pool %d blocks" %
+                (args.seqs, "U[1024,%d]" % args.ctx if args.ragged else str(args.ctx), args.heads, args.kv_heads,
+                 "INT8 per-(block,head) fp16-scale" if args.kv == "int8" else "fp16", args.layers, args.pool_blocks))
+    line = {
+        "metric": "paged decode-attn achieved HBM GB/s (% peak) + tokens/s, B=64 ctx=8k, fp16/INT8 KV",
+        "value": head["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "i8 KV codes, f16 dot2, f32 accumulate" if args.kv == "int8" else "f16 KV, f16 dot2, f32 accumulate",
+        "data": "synthetic (seeded SplitMix64 normals, 1% outlier channels x8 for INT8, random block scatter)",
+        "config": {"workload": workload, "global_batch": args.seqs, "seq_len": args.ctx, "parallelism": "single GPU"},
+        "tokens_per_s": head["tokens_per_s"], "frac_of_peak": head["frac_of_peak"],
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "detail": {args.kv: head, **({args.also: also} if also else {})},
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

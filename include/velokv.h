@@ -85,6 +85,15 @@ int vk_ctx_destroy(vk_ctx* ctx);
 /* Name of the GPU architecture the context runs on (e.g. "gfx950"). */
 int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
 
+/* Kernel family of vk_paged_decode for fp16 queries over fp16/int8 KV:
+ * VK_DECODE_MFMA (QK and PV on v_mfma_f32_16x16x{32,16}_f16), VK_DECODE_VALU
+ * (v_dot2_f32_f16 on the vector ALUs) or VK_DECODE_AUTO (= MFMA). fp32 queries
+ * and fp32 KV always use the fp32 VALU kernel. No reference counterpart. */
+#define VK_DECODE_AUTO 0
+#define VK_DECODE_VALU 1
+#define VK_DECODE_MFMA 2
+int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
+
 /* ---- pools ---------------------------------------------------------------- */
 
 typedef struct vk_pool_desc {
@@ -170,7 +179,9 @@ typedef struct vk_decode_args {
   int32_t max_context_len;    /* host upper bound of context_lens              */
   float scale;                /* softmax scale; 0 = 1/sqrt(head_dim)           */
   int32_t partition_tokens;   /* split-K partition size in tokens; 0 = auto    */
-  void* workspace;            /* dev scratch for split-K partials; NULL = owned by ctx */
+  void* workspace;            /* dev scratch for split-K partials; NULL = owned by
+                                 ctx (calls on one ctx that overlap in time must
+                                 then pass their own). Needs no initialisation. */
   uint64_t workspace_bytes;
 } vk_decode_args;
 
@@ -178,7 +189,8 @@ typedef struct vk_decode_args {
 int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes);
 
 /* Single-query paged decode attention for S sequences, with split-K over
- * context partitions and an online-softmax merge.
+ * context partitions and an online-softmax merge (a second launch, skipped
+ * when every sequence fits one partition).
  * paged_attention_flash (kernels.metal:440-501), paged_attention_flash_int8
  * (kernels.metal:672-732); GQA map kv_head = h / (H / Hkv) (kernels.metal:456);
  * math of llama_cpu.rs:251-284. */

@@ -35,7 +35,7 @@ def test_code_object_is_built_for_gfx950():
     data = open(_capi.CODE_OBJECT_PATH, "rb").read()
     assert data[:4] == b"\x7fELF"
     assert b"gfx950" in data
-    for kernel in (b"vk_decode_kv3_g4_q1", b"vk_append_kv3", b"vk_copy_blocks", b"vk_decode_merge"):
+    for kernel in (b"vk_decode_kv3_g4_q1", b"vk_decode_mfma_kv3_g4", b"vk_decode_merge", b"vk_append_kv3", b"vk_copy_blocks"):
         assert kernel in data
 
 

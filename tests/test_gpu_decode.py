@@ -12,6 +12,14 @@ from test_gpu_append_copy import gpu_pool
 pytestmark = pytest.mark.gpu
 
 KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
+IMPLS = [velokv.DECODE_MFMA, velokv.DECODE_VALU]
+
+
+@pytest.fixture(params=IMPLS, ids=["mfma", "valu"])
+def impl(request, ctx):
+    ctx.set_decode_kernel(request.param)
+    yield request.param
+    ctx.set_decode_kernel(velokv.DECODE_AUTO)
 
 
 def run_decode(ctx, pool, case, q=None, q_dtype=np.float16, partition_tokens=0, layer=0, seq_rows=None,
@@ -38,8 +46,8 @@ def check(got, ref, what):
 
 @pytest.mark.parametrize("kv", KV_ALL)
 @pytest.mark.parametrize("qd", [np.float16, np.float32])
-def test_decode_config1(ctx, kv, qd):
-    print(f"decode config1 kv={kv} q={np.dtype(qd).name}", flush=True)
+def test_decode_config1(ctx, impl, kv, qd):
+    print(f"decode config1 impl={impl} kv={kv} q={np.dtype(qd).name}", flush=True)
     case = make_case(kv, [512], n_blocks=64, seed=201)
     ref_layer = oracle_layer(case)
     pool = gpu_pool(ctx, case)
@@ -50,8 +58,8 @@ def test_decode_config1(ctx, kv, qd):
 
 @pytest.mark.parametrize("kv", KV_ALL)
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
-def test_decode_gqa_groups_ragged(ctx, kv, G):
-    print(f"decode gqa kv={kv} G={G}", flush=True)
+def test_decode_gqa_groups_ragged(ctx, impl, kv, G):
+    print(f"decode gqa impl={impl} kv={kv} G={G}", flush=True)
     Hkv = 2 if G == 8 else 4
     lens = [1, 16, 17, 100, 255, 256, 257, 600]
     case = make_case(kv, lens, n_kv_heads=Hkv, n_heads=Hkv * G, seed=202 + G, outlier_scale=8.0)
@@ -68,9 +76,9 @@ def test_decode_gqa_groups_ragged(ctx, kv, G):
 
 
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
-@pytest.mark.parametrize("P", [16, 256, 512, 1024, 4096, 0])
-def test_decode_split_k_partitions(ctx, kv, P):
-    print(f"decode split kv={kv} P={P}", flush=True)
+@pytest.mark.parametrize("P", [16, 256, 512, 1024, 0])
+def test_decode_split_k_partitions(ctx, impl, kv, P):
+    print(f"decode split impl={impl} kv={kv} P={P}", flush=True)
     lens = [3000, 1024, 2049, 777]
     case = make_case(kv, lens, seed=210, outlier_scale=8.0)
     ref_layer = oracle_layer(case)
@@ -81,9 +89,9 @@ def test_decode_split_k_partitions(ctx, kv, P):
 
 
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
-def test_decode_config2_3_shapes_reduced_batch(ctx, kv):
+def test_decode_config2_3_shapes_reduced_batch(ctx, impl, kv):
     """Configs 2 / 3: L ~ U[1024, 8192], 40k-block pool, GQA 4 (8 of the 64 sequences)."""
-    print(f"decode config2/3 kv={kv}", flush=True)
+    print(f"decode config2/3 impl={impl} kv={kv}", flush=True)
     r = np.random.default_rng(301)
     lens = r.integers(1024, 8193, 8)
     case = make_case(kv, lens, n_blocks=40000, seed=302, outlier_scale=8.0 if kv == O.I8_BLK else 1.0,
@@ -119,8 +127,8 @@ def test_decode_seq_rows_and_pool_slot_table(ctx):
     check(got, ref, "slot table")
 
 
-def test_decode_deterministic_and_block_permutation_invariant(ctx):
-    print("decode determinism", flush=True)
+def test_decode_deterministic_and_block_permutation_invariant(ctx, impl):
+    print(f"decode determinism impl={impl}", flush=True)
     case = make_case(O.I8_BLK, [700, 1500], seed=304)
     pool = gpu_pool(ctx, case)
     a = run_decode(ctx, pool, case)
@@ -135,8 +143,8 @@ def test_decode_deterministic_and_block_permutation_invariant(ctx):
     assert np.array_equal(a, c)
 
 
-def test_decode_empty_and_single_token(ctx):
-    print("decode empty / single", flush=True)
+def test_decode_empty_and_single_token(ctx, impl):
+    print(f"decode empty / single impl={impl}", flush=True)
     case = make_case(O.F16, [1, 5], seed=305)
     ref_layer = oracle_layer(case)
     pool = gpu_pool(ctx, case)
@@ -166,3 +174,24 @@ def test_decode_rejects_bad_arguments(ctx):
         ctx.paged_decode(pool, 5, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
                          ctx.upload(case.ctx_lens), 1, 32, 20, block_tables=ctx.upload(case.block_tables),
                          bt_stride=case.block_tables.shape[1])
+
+
+def test_decode_workspace_reuse_across_layouts(ctx, impl):
+    """Split-K counters stay consistent when consecutive calls change the batch
+    size and the partition layout, with the context's workspace and with a
+    caller-owned one."""
+    print(f"decode workspace reuse impl={impl}", flush=True)
+    case = make_case(O.I8_BLK, [2000, 700, 1300, 64, 999, 3100], seed=307)
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+    own = ctx.alloc(1 << 25)
+    for S, P in ((6, 16), (2, 256), (6, 1024), (3, 16), (6, 512), (1, 16), (6, 0)):
+        for ws in (None, own):
+            out = ctx.alloc(S * 32 * HD * 4)
+            ctx.paged_decode(pool, 0, ctx.upload(case.q[:S]), velokv.DT_F16, out, ctx.upload(case.ctx_lens[:S]), S, 32,
+                             int(case.ctx_lens[:S].max()), block_tables=ctx.upload(case.block_tables),
+                             bt_stride=case.block_tables.shape[1], partition_tokens=P,
+                             workspace=ws, workspace_bytes=(1 << 25) if ws is not None else 0)
+            ctx.sync()
+            check(out.download((S, 32, HD), np.float32), ref[:S], f"S={S} P={P} own_ws={ws is not None}")

@@ -48,7 +48,7 @@ int fail(int code, const char* fmt, ...) {
 
 constexpr int kBS = 16;   // block size the kernels are built for
 constexpr int kHD = 128;  // head_dim the kernels are built for
-constexpr int kChunkTokens = 256;
+constexpr int kMaxPartTokens = 1024;  // 64 blocks: one block id per lane of a wave
 
 uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
@@ -87,6 +87,7 @@ struct vk_ctx {
   std::mutex ws_mu;
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
+  int decode_kind = VK_DECODE_AUTO;
 
   hipFunction_t fn(const std::string& name) const {
     auto it = fns.find(name);
@@ -113,6 +114,9 @@ const char* const kKernelNames[] = {
 
 std::string decode_name(int kv, int g, int qt) {
   return "vk_decode_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
+}
+std::string decode_mfma_name(int kv, int g) {
+  return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g);
 }
 
 int set_device(const vk_ctx* ctx) {
@@ -175,8 +179,10 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
   }
   std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
   for (int kv = 0; kv < 4; ++kv)
-    for (int g : {1, 2, 4, 8})
+    for (int g : {1, 2, 4, 8}) {
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
+      if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
+    }
   for (const auto& nm : names) {
     hipFunction_t f = nullptr;
     e = hipModuleGetFunction(&f, ctx->module, nm.c_str());
@@ -200,6 +206,14 @@ extern "C" int vk_ctx_destroy(vk_ctx* ctx) {
   }
   if (ctx->module) hipModuleUnload(ctx->module);
   delete ctx;
+  return VK_OK;
+}
+
+extern "C" int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind) {
+  if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
+  if (kind != VK_DECODE_AUTO && kind != VK_DECODE_VALU && kind != VK_DECODE_MFMA)
+    return fail(VK_ERR_BAD_ARG, "unknown decode kernel kind %d", kind);
+  ctx->decode_kind = kind;
   return VK_OK;
 }
 
@@ -413,16 +427,15 @@ int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl) {
   if ((int64_t)a->max_context_len > (int64_t)pl->bt_stride * d.block_size)
     return fail(VK_ERR_BAD_ARG, "max_context_len %d exceeds the block-table row (%d pages)", a->max_context_len, pl->bt_stride);
   int P = a->partition_tokens;
-  if (P < 0 || P % d.block_size) return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size");
+  if (P < 0 || P % d.block_size || P > kMaxPartTokens)
+    return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
   if (P == 0) {
-    // Enough units to fill the chip several times over; long partitions keep the
-    // split-K partial traffic small.
+    // Largest partition that still leaves two rounds of resident waves on the chip;
+    // longer partitions keep the split-K partial traffic small.
     const int64_t ctx = std::max(1, a->max_context_len);
     const int64_t pairs = std::max<int64_t>(1, (int64_t)a->n_seqs * d.n_kv_heads);
-    const int64_t target_units = 8192;
-    int64_t want = (ctx * pairs + target_units - 1) / target_units;
-    P = kChunkTokens;
-    while (P < want && P < 8192) P *= 2;
+    P = kMaxPartTokens;
+    while (P > 256 && pairs * ((ctx + P - 1) / P) < 6144) P /= 2;
   }
   pl->part_tokens = P;
   pl->max_parts = std::max(1, (a->max_context_len + P - 1) / P);
@@ -501,8 +514,11 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.scale_log2 = scale * 1.4426950408889634f;
   const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
-  const std::string name = decode_name(d.kv_type, G, a->q_dtype);
+  const bool fast = a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32;
+  const std::string name = (fast && ctx->decode_kind != VK_DECODE_VALU) ? decode_mfma_name(d.kv_type, G)
+                                                                       : decode_name(d.kv_type, G, a->q_dtype);
   if ((rc = launch(ctx, name.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
+  if (pl.max_parts == 1) return VK_OK;  // every sequence was finished by the decode kernel
 
   MergeParams m{};
   m.part_acc = p.part_acc;

@@ -20,8 +20,6 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 constexpr int BS = 16;    // tokens per block
 constexpr int HD = 128;   // head_dim
 constexpr int WAVE = 64;
-constexpr int CHUNK_BLOCKS = 16;                 // blocks per two-phase chunk
-constexpr int CHUNK_TOKENS = CHUNK_BLOCKS * BS;  // 256
 constexpr float kNegInf = -__builtin_huge_valf();
 
 template <typename T, typename F>
@@ -137,38 +135,118 @@ DEV DW<N> load_dw(const uint8_t* p) {
 // Paged decode attention, split-K partial pass.
 //
 // One wave (= one workgroup) owns one unit (sequence s, KV head kvh, partition
-// part). The partition is walked in chunks of 16 blocks (256 tokens); each chunk
-// runs in phases so the softmax max inside a chunk is exact:
-//   phase 1  K tiles [tok][D]: lane = (token lane>>2, 32-dim slice lane&3). Dot
-//            products with the G query heads of the GQA group are summed over
-//            the quad; the lane keeps the score of (its token, head (lane&3)+4k)
-//            and stores it in LDS.
-//   phase 1b the chunk max joins the running max (online softmax across chunks;
-//            accumulators are rescaled when it grows); p = 2^(score - M) and
-//            p~ = p * v_scale go to LDS as (token pair, head) pairs.
-//   phase 2  V tiles [tok/2][D][2]: lane = (dims 2*lane, 2*lane+1), all 16
-//            tokens; acc[g][d] += p~_2j * v_2j[d] + p~_2j+1 * v_2j+1[d].
+// part of at most 64 blocks). The partition streams through a two-stage software
+// pipeline: while the K and V tiles of batch b (CH blocks) are consumed, the loads
+// of batch b+1 are already in flight.
+//   scores  K tile [tok][D]: lane = (token lane>>2, 32-dim slice lane&3). Dot
+//           products with the G query heads of the GQA group are summed over the
+//           quad; the lane keeps the score of (its token, head (lane&3)+4k).
+//   softmax running max M per head, updated lazily: only when some score of the
+//           batch exceeds M by more than 2^4 is M raised to the exact batch max
+//           and the accumulators rescaled, so p = 2^(score - M) <= 16 always.
+//           p~ = p * v_scale goes to LDS as (token pair, head) pairs.
+//   values  V tile [tok/2][D][2]: lane = (dims 2*lane, 2*lane+1), all 16 tokens;
+//           acc[g][d] += p~_2j * v_2j[d] + p~_2j+1 * v_2j+1[d].
 // FAST (q fp16 and fp16/int8 KV): v_dot2_f32_f16 on exact int8->fp16 codes and
 // fp16 p~ pairs. Otherwise fp32 FMA on dequantized values.
-// The unit writes unnormalised partials (acc, running max M in log2 units, sum l);
+// The unit writes unnormalised partials (acc, M in log2 units, l = sum p);
 // vk_decode_merge combines the partitions of a sequence.
 // Algorithm of kernels.metal:440-501 / 672-732 and llama_cpu.rs:255-284.
 // =============================================================================
+// ---- split-K: units with nparts > 1 store unnormalised partials (acc, M in log2
+// units, l = sum p); vk_decode_merge combines them in a second launch. A device-
+// scope release per unit would write back the XCD's whole L2 (buffer_wbl2), so
+// the merge is not fused into this kernel.
+// An empty context attends to nothing: the first partition unit writes zeros.
+template <int G>
+DEV void write_zero_rows(const DecodeParams& P, int s, int kvh) {
+  const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * G;
+#pragma unroll
+  for (int g = 0; g < G; ++g) reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (HD / 2) + lane_id()] = make_float2(0.f, 0.f);
+}
+
+constexpr float kRescaleThreshold = 4.0f;  // log2 units
+constexpr int kMaxPartBlocks = 64;         // blocks per partition (one block id per lane)
+
+template <int KV>
+struct Stage {
+  static constexpr int ESZ = Esz<KV>::v;
+  static constexpr int CH = (ESZ == 1) ? 2 : 1;  // blocks per pipeline stage
+  DW<8 * ESZ> k[CH];
+  DW<ESZ> v[CH][8];
+  float ks[CH];  // VK_KV_I8_REF: K scale of the lane's token
+  float vs[CH];  // VK_KV_I8_REF: V scale of the lane's token
+};
+
+// Buffer resource over one tile: base address and size in SGPRs, so the per-lane
+// offset stays a fixed VGPR and address registers never alias load results.
+// Word 3 = 0x00020000 (32-bit data format, the gfx9-family raw-buffer setting).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // the base is wave-uniform by construction; say so, so the descriptor lives in SGPRs
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  void* u = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, 0, (int)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
+}
+constexpr int kAuxNT = 2;  // non-temporal: K/V tiles are read once per decode
+template <int N>
+DEV DW<N> buf_load(rsrc_t r, uint32_t off) {
+  DW<N> out;
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16 * i), 0, kAuxNT);
+      out.d[4 * i] = v.x; out.d[4 * i + 1] = v.y; out.d[4 * i + 2] = v.z; out.d[4 * i + 3] = v.w;
+    }
+  } else if constexpr (N == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kAuxNT);
+    out.d[0] = v.x; out.d[1] = v.y;
+  } else {
+    out.d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kAuxNT);
+  }
+  return out;
+}
+
+// Issue the loads of batch `b` (blocks b*CH .. b*CH+CH-1 of the unit, clamped to
+// the last block so the tail needs no branch).
+template <int KV>
+DEV void stage_load(Stage<KV>& st, const DecodeParams& P, int blkv, int b, int nblk, int kvh, int t) {
+  constexpr int ESZ = Esz<KV>::v;
+  constexpr int CH = Stage<KV>::CH;
+  const int lane = lane_id();
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int i = min(b * CH + u, nblk - 1);
+    const int blk = readlane_i(blkv, i);
+    const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
+    const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
+    const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+    st.k[u] = buf_load<8 * ESZ>(kr, lane * (32 * ESZ));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st.v[u][j] = buf_load<ESZ>(vr, j * (HD * 2 * ESZ) + lane * (4 * ESZ));
+    if constexpr (KV == KV_I8_REF) {
+      const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
+      const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
+      st.ks[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(sr, t * 4, 0, 0));
+      st.vs[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(svr, t * 4, 0, 0));
+    }
+  }
+}
+
 template <int KV, int G, int QT>
 DEV void decode_unit(const DecodeParams& P) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr bool FAST = (QT == DT_F16) && (KV != KV_F32);
   constexpr bool BLK = (KV == KV_I8_BLK);
   constexpr bool REF = (KV == KV_I8_REF);
+  constexpr int CH = Stage<KV>::CH;
   constexpr int SPL = (G >= 4) ? G / 4 : 1;   // score slots per lane per block
-  constexpr int KDW = 8 * ESZ;                // dwords of K per lane per block
-  constexpr int VDW = ESZ;                    // dwords of V per lane per token pair
-  constexpr int CH = 4 / ESZ;                 // blocks per load batch
   constexpr int QW = FAST ? 16 : 32;          // q registers per head
   constexpr int PW = FAST ? 1 : 2;            // LDS dwords per (pair, head)
 
-  __shared__ float s_lds[CHUNK_BLOCKS * SPL * WAVE];
-  __shared__ uint32_t p_lds[CHUNK_BLOCKS * 8 * G * PW];
+  __shared__ uint32_t p_lds[CH * 8 * G * PW];
 
   const int lane = lane_id();
   const int t = lane >> 2;   // token of the K tile this lane reads
@@ -184,15 +262,34 @@ DEV void decode_unit(const DecodeParams& P) {
   const int cap = min(P.max_parts * P.part_tokens, P.bt_stride * BS);
   const int ctx = max(0, min(P.context_lens[s], cap));
   const int start = part * P.part_tokens;
-  if (start >= ctx) return;
+  if (start >= ctx) {
+    if (part == 0) write_zero_rows<G>(P, s, kvh);
+    return;
+  }
   const int end = min(start + P.part_tokens, ctx);
+  const int nparts = (ctx + P.part_tokens - 1) / P.part_tokens;
   int row = P.seq_rows ? P.seq_rows[s] : s;
   if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
   const int32_t* bt = P.block_tables + (int64_t)row * P.bt_stride;
   const int H = P.n_heads;
   const int Hkv = P.n_kv_heads;
-  const uint32_t tile = P.tile_bytes;
-  const int nb_max = P.n_blocks - 1;
+  const int nblk = (end - start + BS - 1) / BS;   // <= kMaxPartBlocks
+  const int blk0 = start / BS;
+  const int nbatch = (nblk + CH - 1) / CH;
+
+  // block ids (and per-(block, head) scales) of the unit, one block per lane
+  int blkv = 0;
+  float ksv = 1.f, vsv = 1.f;
+  if (lane < nblk) {
+    blkv = min(max(bt[blk0 + lane], 0), P.n_blocks - 1);
+    if constexpr (BLK) {
+      ksv = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)blkv * Hkv + kvh]);
+      vsv = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)blkv * Hkv + kvh]);
+    }
+  }
+
+  Stage<KV> sa, sb;
+  stage_load<KV>(sa, P, blkv, 0, nblk, kvh, t);
 
   // ---- query registers: 32 dims (slice c) of each head of the group ---------
   uint32_t qh[G][QW];
@@ -238,274 +335,219 @@ DEV void decode_unit(const DecodeParams& P) {
   auto slot_head = [&](int k) -> int { return (G >= 4) ? c + 4 * k : c % G; };
   const bool owner = (G >= 4) || (c < G);
 
-  float Mrun[G];   // running max per head (log2 units), wave-uniform
-  float lrun[SPL]; // per-lane partial softmax denominators
+  float M[G];        // running max per head (log2 units), wave-uniform
+  float Mlane[SPL];  // M of the head of each slot of this lane
+  float lrun[SPL];   // per-lane partial softmax denominators
   float acc[G][2];
 #pragma unroll
-  for (int g = 0; g < G; ++g) { Mrun[g] = kNegInf; acc[g][0] = 0.f; acc[g][1] = 0.f; }
+  for (int g = 0; g < G; ++g) { M[g] = kNegInf; acc[g][0] = 0.f; acc[g][1] = 0.f; }
 #pragma unroll
-  for (int k = 0; k < SPL; ++k) lrun[k] = 0.f;
+  for (int k = 0; k < SPL; ++k) { lrun[k] = 0.f; Mlane[k] = kNegInf; }
+  const int last_valid = (end - start) - (nblk - 1) * BS;  // valid tokens in the last block
 
-  for (int cs = start; cs < end; cs += CHUNK_TOKENS) {
-    const int ntok = min(CHUNK_TOKENS, end - cs);
-    const int nblk = (ntok + BS - 1) / BS;
-    const int blk0 = cs / BS;
-
-    // block ids (and per-(block, head) scales) of the chunk, one per lane
-    int blkv = 0;
-    float ksv = 1.f, vsv = 1.f;
-    if (lane < nblk) {
-      blkv = min(max(bt[blk0 + lane], 0), nb_max);
-      if constexpr (BLK) {
-        const uint16_t* ks = reinterpret_cast<const uint16_t*>(P.ks);
-        const uint16_t* vs = reinterpret_cast<const uint16_t*>(P.vs);
-        ksv = h2f(ks[(int64_t)blkv * Hkv + kvh]);
-        vsv = h2f(vs[(int64_t)blkv * Hkv + kvh]);
-      }
-    }
-
-    // ---------------- phase 1: scores ----------------
-    float mloc[SPL];
+  auto compute = [&](const Stage<KV>& st, int b) {
+    float sc[CH][SPL];
 #pragma unroll
-    for (int k = 0; k < SPL; ++k) mloc[k] = kNegInf;
-    float vsc_ref[CHUNK_BLOCKS];  // REF: V scale of this lane's token, per block
-    (void)vsc_ref;
-
-    for (int i0 = 0; i0 < nblk; i0 += CH) {
-      DW<KDW> kw[CH];
-      float ksr[CH];
-      float vsr[CH];
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
+      float a[G];
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int bi = min(i0 + u, nblk - 1);
-        const int blk = readlane_i(blkv, bi);
-        const uint8_t* tp = P.kc + ((uint64_t)blk * Hkv + kvh) * tile;
-        kw[u] = load_dw<KDW>(tp + lane * (KDW * 4));
-        if constexpr (REF) {
-          const float* ks = reinterpret_cast<const float*>(P.ks);
-          const float* vs = reinterpret_cast<const float*>(P.vs);
-          const int64_t si = ((int64_t)blk * Hkv + kvh) * BS + t;
-          ksr[u] = ks[si];
-          vsr[u] = vs[si];
+      for (int g = 0; g < G; ++g) a[g] = 0.f;
+      if constexpr (FAST) {
+        if constexpr (ESZ == 1) {
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            uint32_t lo, hi;
+            i8x4_to_h2x2(st.k[u].d[w], lo, hi);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              a[g] = dot2(qh[g][2 * w], lo, a[g]);
+              a[g] = dot2(qh[g][2 * w + 1], hi, a[g]);
+            }
+          }
         } else {
-          ksr[u] = 1.f; vsr[u] = 1.f;
+#pragma unroll
+          for (int w = 0; w < 16; ++w)
+#pragma unroll
+            for (int g = 0; g < G; ++g) a[g] = dot2(qh[g][w], st.k[u].d[w], a[g]);
         }
+      } else {
+        float kf[32];
+#pragma unroll
+        for (int d = 0; d < 32; ++d) {
+          if constexpr (ESZ == 1) kf[d] = byte_to_f(st.k[u].d[d >> 2], d & 3);
+          else if constexpr (ESZ == 2) kf[d] = (d & 1) ? half_hi(st.k[u].d[d >> 1]) : half_lo(st.k[u].d[d >> 1]);
+          else kf[d] = bitcast<float>(st.k[u].d[d]);
+        }
+#pragma unroll
+        for (int d = 0; d < 32; ++d)
+#pragma unroll
+          for (int g = 0; g < G; ++g) a[g] = fmaf(bitcast<float>(qh[g][d]), kf[d], a[g]);
       }
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int i = i0 + u;
-        if (i < nblk) {
-          float a[G];
+      for (int g = 0; g < G; ++g) {
+        a[g] += dpp<DPP_QUAD_XOR1>(a[g]);
+        a[g] += dpp<DPP_QUAD_XOR2>(a[g]);
+      }
+      float kscale = P.scale_log2;
+      if constexpr (BLK) kscale *= readlane_f(ksv, min(i, nblk - 1));
+      if constexpr (REF) kscale *= st.ks[u];
+      const bool valid = (i < nblk) && (start + i * BS + t < end);
 #pragma unroll
-          for (int g = 0; g < G; ++g) a[g] = 0.f;
-          if constexpr (FAST) {
-            if constexpr (ESZ == 1) {
-#pragma unroll
-              for (int w = 0; w < 8; ++w) {
-                uint32_t lo, hi;
-                i8x4_to_h2x2(kw[u].d[w], lo, hi);
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                  a[g] = dot2(qh[g][2 * w], lo, a[g]);
-                  a[g] = dot2(qh[g][2 * w + 1], hi, a[g]);
-                }
-              }
-            } else {
-#pragma unroll
-              for (int w = 0; w < 16; ++w)
-#pragma unroll
-                for (int g = 0; g < G; ++g) a[g] = dot2(qh[g][w], kw[u].d[w], a[g]);
-            }
-          } else {
-            float kf[32];
-#pragma unroll
-            for (int d = 0; d < 32; ++d) {
-              if constexpr (ESZ == 1) kf[d] = byte_to_f(kw[u].d[d >> 2], d & 3);
-              else if constexpr (ESZ == 2) kf[d] = (d & 1) ? half_hi(kw[u].d[d >> 1]) : half_lo(kw[u].d[d >> 1]);
-              else kf[d] = bitcast<float>(kw[u].d[d]);
-            }
-#pragma unroll
-            for (int d = 0; d < 32; ++d)
-#pragma unroll
-              for (int g = 0; g < G; ++g) a[g] = fmaf(bitcast<float>(qh[g][d]), kf[d], a[g]);
-          }
-          // sum over the quad (the 4 slices of one token)
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            a[g] += dpp<DPP_QUAD_XOR1>(a[g]);
-            a[g] += dpp<DPP_QUAD_XOR2>(a[g]);
-          }
-          float kscale = P.scale_log2;
-          if constexpr (BLK) kscale *= readlane_f(ksv, i);
-          if constexpr (REF) kscale *= ksr[u];
-          const bool valid = (cs + i * BS + t) < end;
-#pragma unroll
-          for (int k = 0; k < SPL; ++k) {
-            float v;
-            if constexpr (G >= 4) {
-              v = a[4 * k];
-              v = (c == 1) ? a[4 * k + 1] : v;
-              v = (c == 2) ? a[4 * k + 2] : v;
-              v = (c == 3) ? a[4 * k + 3] : v;
-            } else if constexpr (G == 2) {
-              v = (c & 1) ? a[1] : a[0];
-            } else {
-              v = a[0];
-            }
-            v = valid ? v * kscale : kNegInf;
-            mloc[k] = fmaxf(mloc[k], v);
-            s_lds[(i * SPL + k) * WAVE + lane] = v;
-          }
-          if constexpr (REF) {
-            // kept for phase 1b, indexed by the block of the chunk
-#pragma unroll
-            for (int b = 0; b < CHUNK_BLOCKS; ++b)
-              if (b == i) vsc_ref[b] = vsr[u];
-          }
+      for (int k = 0; k < SPL; ++k) {
+        float v;
+        if constexpr (G >= 4) {
+          v = a[4 * k];
+          v = (c == 1) ? a[4 * k + 1] : v;
+          v = (c == 2) ? a[4 * k + 2] : v;
+          v = (c == 3) ? a[4 * k + 3] : v;
+        } else if constexpr (G == 2) {
+          v = (c & 1) ? a[1] : a[0];
+        } else {
+          v = a[0];
         }
+        sc[u][k] = valid ? v * kscale : kNegInf;
       }
     }
 
-    // ---------------- phase 1b: running max, p, p~ ----------------
-    float Mnew[G], alpha[G];
+    // lazy running max: rescale only when a score passes M + threshold
+    bool need = false;
 #pragma unroll
-    for (int k = 0; k < SPL; ++k) mloc[k] = max_same_quadpos(mloc[k]);
+    for (int u = 0; u < CH; ++u)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mc;
-      if constexpr (G >= 4) mc = readlane_f(mloc[g / 4], g % 4);
-      else if constexpr (G == 2) mc = readlane_f(mloc[0], g);
-      else mc = readlane_f(mloc[0], 0);
-      Mnew[g] = fmaxf(Mrun[g], mc);
-      alpha[g] = __builtin_amdgcn_exp2f(Mrun[g] - Mnew[g]);  // 0 on the first chunk
-      Mrun[g] = Mnew[g];
-    }
-    bool rescale = false;
-#pragma unroll
-    for (int g = 0; g < G; ++g) rescale |= (alpha[g] != 1.f);
-    if (rescale) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) { acc[g][0] *= alpha[g]; acc[g][1] *= alpha[g]; }
+      for (int k = 0; k < SPL; ++k) need |= sc[u][k] > Mlane[k] + kRescaleThreshold;
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      float mb[SPL];
 #pragma unroll
       for (int k = 0; k < SPL; ++k) {
-        float al = alpha[0];
+        float m = sc[0][k];
 #pragma unroll
-        for (int g = 1; g < G; ++g) al = (slot_head(k) == g) ? alpha[g] : al;
+        for (int u = 1; u < CH; ++u) m = fmaxf(m, sc[u][k]);
+        mb[k] = max_same_quadpos(m);
+      }
+      float alpha[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float m;
+        if constexpr (G >= 4) m = readlane_f(mb[g / 4], g % 4);
+        else if constexpr (G == 2) m = readlane_f(mb[0], g);
+        else m = readlane_f(mb[0], 0);
+        const float Mn = fmaxf(M[g], m);
+        alpha[g] = __builtin_amdgcn_exp2f(M[g] - Mn);  // 0 while M is -inf
+        M[g] = Mn;
+        acc[g][0] *= alpha[g];
+        acc[g][1] *= alpha[g];
+      }
+#pragma unroll
+      for (int k = 0; k < SPL; ++k) {
+        float al = alpha[0], ml = M[0];
+#pragma unroll
+        for (int g = 1; g < G; ++g) {
+          al = (slot_head(k) == g) ? alpha[g] : al;
+          ml = (slot_head(k) == g) ? M[g] : ml;
+        }
         lrun[k] *= al;
+        Mlane[k] = ml;
       }
     }
-    float Mlane[SPL];
-#pragma unroll
-    for (int k = 0; k < SPL; ++k) {
-      float m = Mnew[0];
-#pragma unroll
-      for (int g = 1; g < G; ++g) m = (slot_head(k) == g) ? Mnew[g] : m;
-      Mlane[k] = m;
-    }
-    const int jp = t >> 1, e = t & 1;
-#pragma unroll 4
-    for (int i = 0; i < nblk; ++i) {
-      float vscale;
-      if constexpr (BLK) vscale = readlane_f(vsv, i);
-      else if constexpr (REF) {
-        vscale = vsc_ref[0];
-#pragma unroll
-        for (int b = 1; b < CHUNK_BLOCKS; ++b) vscale = (b == i) ? vsc_ref[b] : vscale;
-      } else vscale = 1.f;
-#pragma unroll
-      for (int k = 0; k < SPL; ++k) {
-        const float sv = s_lds[(i * SPL + k) * WAVE + lane];
-        const float p = __builtin_amdgcn_exp2f(sv - Mlane[k]);
-        if (owner) {
-          lrun[k] += p;
-          const int g = slot_head(k);
-          const float pt = p * vscale;
-          if constexpr (FAST) {
-            reinterpret_cast<uint16_t*>(p_lds)[(((i * 8 + jp) * G + g) << 1) + e] = f2h(pt);
-          } else {
-            reinterpret_cast<float*>(p_lds)[(((i * 8 + jp) * G + g) << 1) + e] = pt;
-          }
-        }
-      }
-    }
-    __syncthreads();
 
-    // ---------------- phase 2: V ----------------
-    const int last_tok_in_blk = (end - cs) - (nblk - 1) * BS;  // valid tokens of the last block
-    for (int i0 = 0; i0 < nblk; i0 += CH) {
-      DW<VDW> vw[CH][8];
+    // p and p~ = p * v_scale into LDS as (token pair, head) pairs
+    const int jp = t >> 1, e = t & 1;
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int bi = min(i0 + u, nblk - 1);
-        const int blk = readlane_i(blkv, bi);
-        const uint8_t* tp = P.vc + ((uint64_t)blk * Hkv + kvh) * tile;
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
+      if (i < nblk) {
+        float vscale = 1.f;
+        if constexpr (BLK) vscale = readlane_f(vsv, i);
+        if constexpr (REF) vscale = st.vs[u];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) vw[u][j] = load_dw<VDW>(tp + j * (HD * 2 * ESZ) + lane * (VDW * 4));
+        for (int k = 0; k < SPL; ++k) {
+          const float p = __builtin_amdgcn_exp2f(sc[u][k] - Mlane[k]);
+          if (owner) {
+            lrun[k] += p;
+            const int g = slot_head(k);
+            if constexpr (FAST)
+              reinterpret_cast<uint16_t*>(p_lds)[(((u * 8 + jp) * G + g) << 1) + e] = f2h(p * vscale);
+            else
+              reinterpret_cast<float*>(p_lds)[(((u * 8 + jp) * G + g) << 1) + e] = p * vscale;
+          }
+        }
       }
+    }
+    __asm__ volatile("" ::: "memory");
+
+    // values
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int i = i0 + u;
-        if (i < nblk) {
-          const bool partial = (i == nblk - 1) && (last_tok_in_blk < BS);
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
+      if (i < nblk) {
+        const bool partial = (i == nblk - 1) && (last_valid < BS);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            uint32_t pp[G * PW];
-            const uint32_t* src = p_lds + (i * 8 + j) * G * PW;
-            if constexpr (G * PW >= 4) {
+        for (int j = 0; j < 8; ++j) {
+          uint32_t pp[G * PW];
+          const uint32_t* src = p_lds + (u * 8 + j) * G * PW;
+          if constexpr (G * PW >= 4) {
 #pragma unroll
-              for (int q4 = 0; q4 < G * PW / 4; ++q4) {
-                const uint4 v = reinterpret_cast<const uint4*>(src)[q4];
-                pp[4 * q4] = v.x; pp[4 * q4 + 1] = v.y; pp[4 * q4 + 2] = v.z; pp[4 * q4 + 3] = v.w;
-              }
-            } else if constexpr (G * PW == 2) {
-              const uint2 v = reinterpret_cast<const uint2*>(src)[0];
-              pp[0] = v.x; pp[1] = v.y;
-            } else {
-              pp[0] = src[0];
+            for (int q4 = 0; q4 < G * PW / 4; ++q4) {
+              const uint4 v = reinterpret_cast<const uint4*>(src)[q4];
+              pp[4 * q4] = v.x; pp[4 * q4 + 1] = v.y; pp[4 * q4 + 2] = v.z; pp[4 * q4 + 3] = v.w;
             }
-            // element order in the lane's V words: [d0: t0, t1][d1: t0, t1]
-            const bool z0 = partial && (2 * j >= last_tok_in_blk);
-            const bool z1 = partial && (2 * j + 1 >= last_tok_in_blk);
-            if constexpr (FAST) {
-              uint32_t v0, v1;
-              if constexpr (ESZ == 1) i8x4_to_h2x2(vw[u][j].d[0], v0, v1);
-              else { v0 = vw[u][j].d[0]; v1 = vw[u][j].d[1]; }
-              if (partial) {
-                const uint32_t m = (z0 ? 0u : 0xFFFFu) | (z1 ? 0u : 0xFFFF0000u);
-                v0 &= m; v1 &= m;
-              }
+          } else if constexpr (G * PW == 2) {
+            const uint2 v = reinterpret_cast<const uint2*>(src)[0];
+            pp[0] = v.x; pp[1] = v.y;
+          } else {
+            pp[0] = src[0];
+          }
+          const bool z0 = partial && (2 * j >= last_valid);
+          const bool z1 = partial && (2 * j + 1 >= last_valid);
+          if constexpr (FAST) {
+            uint32_t v0, v1;
+            if constexpr (ESZ == 1) i8x4_to_h2x2(st.v[u][j].d[0], v0, v1);
+            else { v0 = st.v[u][j].d[0]; v1 = st.v[u][j].d[1]; }
+            if (partial) {
+              const uint32_t m = (z0 ? 0u : 0xFFFFu) | (z1 ? 0u : 0xFFFF0000u);
+              v0 &= m; v1 &= m;
+            }
 #pragma unroll
-              for (int g = 0; g < G; ++g) {
-                acc[g][0] = dot2(pp[g], v0, acc[g][0]);
-                acc[g][1] = dot2(pp[g], v1, acc[g][1]);
-              }
+            for (int g = 0; g < G; ++g) {
+              acc[g][0] = dot2(pp[g], v0, acc[g][0]);
+              acc[g][1] = dot2(pp[g], v1, acc[g][1]);
+            }
+          } else {
+            float v00, v01, v10, v11;  // v[d][tok]
+            if constexpr (ESZ == 1) {
+              const uint32_t w = st.v[u][j].d[0];
+              v00 = byte_to_f(w, 0); v01 = byte_to_f(w, 1); v10 = byte_to_f(w, 2); v11 = byte_to_f(w, 3);
+            } else if constexpr (ESZ == 2) {
+              v00 = half_lo(st.v[u][j].d[0]); v01 = half_hi(st.v[u][j].d[0]);
+              v10 = half_lo(st.v[u][j].d[1]); v11 = half_hi(st.v[u][j].d[1]);
             } else {
-              float v00, v01, v10, v11;  // v[d][tok]
-              if constexpr (ESZ == 1) {
-                const uint32_t w = vw[u][j].d[0];
-                v00 = byte_to_f(w, 0); v01 = byte_to_f(w, 1); v10 = byte_to_f(w, 2); v11 = byte_to_f(w, 3);
-              } else if constexpr (ESZ == 2) {
-                v00 = half_lo(vw[u][j].d[0]); v01 = half_hi(vw[u][j].d[0]);
-                v10 = half_lo(vw[u][j].d[1]); v11 = half_hi(vw[u][j].d[1]);
-              } else {
-                v00 = bitcast<float>(vw[u][j].d[0]); v01 = bitcast<float>(vw[u][j].d[1]);
-                v10 = bitcast<float>(vw[u][j].d[2]); v11 = bitcast<float>(vw[u][j].d[3]);
-              }
-              if (z0) { v00 = 0.f; v10 = 0.f; }
-              if (z1) { v01 = 0.f; v11 = 0.f; }
+              v00 = bitcast<float>(st.v[u][j].d[0]); v01 = bitcast<float>(st.v[u][j].d[1]);
+              v10 = bitcast<float>(st.v[u][j].d[2]); v11 = bitcast<float>(st.v[u][j].d[3]);
+            }
+            if (z0) { v00 = 0.f; v10 = 0.f; }
+            if (z1) { v01 = 0.f; v11 = 0.f; }
 #pragma unroll
-              for (int g = 0; g < G; ++g) {
-                const float pe = bitcast<float>(pp[2 * g]);
-                const float po = bitcast<float>(pp[2 * g + 1]);
-                acc[g][0] = fmaf(po, v01, fmaf(pe, v00, acc[g][0]));
-                acc[g][1] = fmaf(po, v11, fmaf(pe, v10, acc[g][1]));
-              }
+            for (int g = 0; g < G; ++g) {
+              const float pe = bitcast<float>(pp[2 * g]);
+              const float po = bitcast<float>(pp[2 * g + 1]);
+              acc[g][0] = fmaf(po, v01, fmaf(pe, v00, acc[g][0]));
+              acc[g][1] = fmaf(po, v11, fmaf(pe, v10, acc[g][1]));
             }
           }
         }
       }
     }
-    __syncthreads();
+    __asm__ volatile("" ::: "memory");
+  };
+
+  // two-stage pipeline over the batches of the unit
+  for (int b = 0; b < nbatch; b += 2) {
+    stage_load<KV>(sb, P, blkv, b + 1, nblk, kvh, t);
+    compute(sa, b);
+    if (b + 1 >= nbatch) break;
+    stage_load<KV>(sa, P, blkv, b + 2, nblk, kvh, t);
+    compute(sb, b + 1);
   }
 
   // ---- partials of this unit ----
@@ -518,16 +560,321 @@ DEV void decode_unit(const DecodeParams& P) {
     else lsum[g] = readlane_f(lrun[0], g);
   }
   const int64_t hrow0 = (int64_t)s * H + (int64_t)kvh * G;
+  if (nparts == 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float inv = 1.f / lsum[g];
+      reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (HD / 2) + lane] = make_float2(acc[g][0] * inv, acc[g][1] * inv);
+    }
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t pr = (hrow0 + g) * P.max_parts + part;
     reinterpret_cast<float2*>(P.part_acc + pr * HD)[lane] = make_float2(acc[g][0], acc[g][1]);
-    if (lane == g) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(Mrun[g], lsum[g]);
+    if (lane == g) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(M[g], lsum[g]);
   }
 }
 
-// Combine the partitions of one (sequence, head): out = sum_p w_p acc_p / sum_p w_p l_p,
-// w_p = 2^(M_p - max_p M_p). One wave per (sequence, head).
+// =============================================================================
+// Paged decode attention on the matrix cores (same unit, partials and pool layout
+// as decode_unit; fp16 q with fp16 or int8 KV).
+//
+// Scores: S[h][t] = v_mfma_f32_16x16x32_f16 over 4 chunks of 32 dims, rows = the G
+//   heads of the GQA group (zero-padded to 16), columns = the 16 tokens of a block.
+//   Lane l (n = l&15, g = l>>4) feeds q[head n][dims 32g..32g+31] and
+//   K[token n][dims 32g..32g+31]: both operands see the same dim permutation, so
+//   each lane reads 32 contiguous bytes of one token row. Lane l gets S for
+//   heads 4g..4g+3 of token n.
+// Values: out[h][d] += v_mfma_f32_16x16x16f16 per block and per 16-dim tile; the
+//   A operand is p~[head n][tokens 4g..4g+3] read back from a 16x16 fp16 tile in
+//   LDS, the B operand is V[tokens 4g..4g+3][dim 8n + tile] taken from the token
+//   pairs 2g and 2g+1 of the block (16 contiguous bytes each). Lane l gets
+//   out[heads 4g..4g+3][dims 8n..8n+7].
+// int8 codes enter the matrix cores as fp16 (1152 + c) without the subtraction;
+//   sum_d q_d (1152 + c_d) - 1152 sum_d q_d and sum_t p~_t (1152 + c_t) -
+//   1152 sum_t p~_t remove the bias exactly up to fp32 rounding.
+// The softmax bookkeeping (lazy running max, p, l) is that of decode_unit.
+// =============================================================================
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+template <int KV>
+struct MStage {
+  static constexpr int ESZ = Esz<KV>::v;
+  static constexpr int CH = (ESZ == 1) ? 2 : 1;  // blocks per pipeline stage
+  DW<8 * ESZ> k[CH];     // token n, dims 32g..32g+31
+  DW<4 * ESZ> v[CH][2];  // token pairs 2g, 2g+1; dims 8n..8n+7
+  float ks[CH];          // VK_KV_I8_REF: scales of token n
+  float vs[CH];
+};
+
+template <int KV>
+DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, int blkv, int b, int nblk, int kvh, int n, int g) {
+  constexpr int ESZ = Esz<KV>::v;
+  constexpr int CH = MStage<KV>::CH;
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int i = min(b * CH + u, nblk - 1);
+    const int blk = readlane_i(blkv, i);
+    const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
+    const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
+    const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+    st.k[u] = buf_load<8 * ESZ>(kr, (n * HD + 32 * g) * ESZ);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * HD * 2 + 16 * n) * ESZ);
+    if constexpr (KV == KV_I8_REF) {
+      const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
+      const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
+      st.ks[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(sr, n * 4, 0, 0));
+      st.vs[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(svr, n * 4, 0, 0));
+    }
+  }
+}
+
+// Four int8 codes -> two fp16 pairs holding 1152 + c exactly (no subtraction).
+DEV void i8x4_to_h2x2_biased(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+}
+
+template <int KV, int G>
+DEV void decode_unit_mfma(const DecodeParams& P) {
+  constexpr int ESZ = Esz<KV>::v;
+  constexpr bool I8 = (ESZ == 1);
+  constexpr bool BLK = (KV == KV_I8_BLK);
+  constexpr bool REF = (KV == KV_I8_REF);
+  constexpr int CH = MStage<KV>::CH;
+  constexpr float kBias = 1152.0f;
+
+  __shared__ uint16_t p_lds[16 * 16];  // p~[head][token] of one block
+
+  const int lane = lane_id();
+  const int n = lane & 15;   // token (scores) / dim group (values) / head (A operands)
+  const int g = lane >> 4;   // dim slice (scores) / row group (results) / token group (values)
+
+  const int unit = blockIdx.x;
+  const int kvh = unit % P.n_kv_heads;
+  const int rest = unit / P.n_kv_heads;
+  const int part = rest % P.max_parts;
+  const int s = rest / P.max_parts;
+  if (s >= P.n_seqs) return;
+
+  const int cap = min(P.max_parts * P.part_tokens, P.bt_stride * BS);
+  const int ctx = max(0, min(P.context_lens[s], cap));
+  const int start = part * P.part_tokens;
+  if (start >= ctx) {
+    if (part == 0) write_zero_rows<G>(P, s, kvh);
+    return;
+  }
+  const int end = min(start + P.part_tokens, ctx);
+  const int nparts = (ctx + P.part_tokens - 1) / P.part_tokens;
+  int row = P.seq_rows ? P.seq_rows[s] : s;
+  if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
+  const int32_t* bt = P.block_tables + (int64_t)row * P.bt_stride;
+  const int H = P.n_heads;
+  const int Hkv = P.n_kv_heads;
+  const int nblk = (end - start + BS - 1) / BS;
+  const int blk0 = start / BS;
+  const int nbatch = (nblk + CH - 1) / CH;
+
+  int blkv = 0;
+  float ksv = 1.f, vsv = 1.f;
+  if (lane < nblk) {
+    blkv = min(max(bt[blk0 + lane], 0), P.n_blocks - 1);
+    if constexpr (BLK) {
+      ksv = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)blkv * Hkv + kvh]);
+      vsv = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)blkv * Hkv + kvh]);
+    }
+  }
+
+  MStage<KV> sa, sb;
+  mstage_load<KV>(sa, P, blkv, 0, nblk, kvh, n, g);
+
+  // q as the A operand: head n (rows >= G are zero), dims 32g..32g+31 in 4 chunks
+  half8 qa[4];
+  float qsum_part = 0.f;
+  {
+    const uint16_t* q16 = reinterpret_cast<const uint16_t*>(P.q) + ((int64_t)s * H + (int64_t)kvh * G + n) * HD + 32 * g;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (n < G) v = reinterpret_cast<const uint4*>(q16)[kc];
+      qa[kc] = bitcast<half8>(v);
+      if constexpr (I8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qsum_part += (float)qa[kc][j];
+      }
+    }
+  }
+  // sum over the 4 slices of each head, then the 4 heads of this lane's row group
+  float qsum[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (I8) {
+    qsum_part += shfl_xor(qsum_part, 16);
+    qsum_part += shfl_xor(qsum_part, 32);   // every lane: full sum of head n
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qsum[r] = __shfl(qsum_part, 4 * g + r, WAVE);
+  }
+  // zero the p~ tile once so rows >= G stay zero
+  reinterpret_cast<uint2*>(p_lds)[lane] = make_uint2(0, 0);
+
+  const bool row_ok[4] = {4 * g + 0 < G, 4 * g + 1 < G, 4 * g + 2 < G, 4 * g + 3 < G};
+  float M[4], lrun[4], psum[4];
+  float4v acc[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) { M[r] = kNegInf; lrun[r] = 0.f; psum[r] = 0.f; }
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) acc[nt] = float4v{0.f, 0.f, 0.f, 0.f};
+  const int last_valid = (end - start) - (nblk - 1) * BS;
+
+  auto compute = [&](const MStage<KV>& st, int b) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
+      if (i >= nblk) break;
+      // ---- scores ----
+      float4v sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        uint32_t kb[4];
+        if constexpr (I8) {
+          i8x4_to_h2x2_biased(st.k[u].d[2 * kc], kb[0], kb[1]);
+          i8x4_to_h2x2_biased(st.k[u].d[2 * kc + 1], kb[2], kb[3]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) kb[w] = st.k[u].d[4 * kc + w];
+        }
+        const u32x4 kbv = {kb[0], kb[1], kb[2], kb[3]};
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kc], bitcast<half8>(kbv), sc, 0, 0, 0);
+      }
+      float kscale = P.scale_log2;
+      if constexpr (BLK) kscale *= readlane_f(ksv, i);
+      if constexpr (REF) kscale *= st.ks[u];
+      const bool tok_ok = (start + i * BS + n) < end;
+      float sv[4];
+      bool need = false;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = sc[r];
+        if constexpr (I8) x = fmaf(-kBias, qsum[r], x);
+        sv[r] = (tok_ok && row_ok[r]) ? x * kscale : kNegInf;
+        need |= sv[r] > M[r] + kRescaleThreshold;
+      }
+      // ---- lazy running max per row ----
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float m = sv[r];
+          m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
+          m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
+          m = fmaxf(m, dpp<DPP_ROW_HALF_MIRROR>(m));
+          m = fmaxf(m, dpp<DPP_ROW_MIRROR>(m));  // max over the 16 tokens of the block
+          const float Mn = fmaxf(M[r], m);
+          const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[r] - Mn);
+          M[r] = Mn;
+          lrun[r] *= alpha;
+          psum[r] *= alpha;
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt) acc[nt][r] *= alpha;
+        }
+      }
+      // ---- p, p~ -> LDS tile [head][token] ----
+      float vscale = 1.f;
+      if constexpr (BLK) vscale = readlane_f(vsv, i);
+      if constexpr (REF) vscale = st.vs[u];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = (sv[r] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(sv[r] - M[r]);
+        lrun[r] += p;
+        const uint16_t ph = f2h(p * vscale);
+        if constexpr (I8) psum[r] += h2f(ph);
+        if (row_ok[r]) p_lds[(4 * g + r) * 16 + n] = ph;
+      }
+      __asm__ volatile("" ::: "memory");
+      const uint2 pa2 = reinterpret_cast<const uint2*>(p_lds)[n * 4 + g];  // p~[head n][tokens 4g..4g+3]
+      const half4 pa = bitcast<half4>(pa2);
+      // ---- values ----
+      const bool partial = (i == nblk - 1) && (last_valid < BS);
+#pragma unroll
+      for (int w = 0; w < 4 * ESZ; w += ESZ) {
+        // tiles nt: I8 -> dword w of each pair row gives dims 2w, 2w+1; F16 -> dwords w, w+1
+        uint32_t b0[2], b1[2];   // [pair row] for tile nt0, nt1
+        int nt0, nt1;
+        if constexpr (I8) {
+          i8x4_to_h2x2_biased(st.v[u][0].d[w], b0[0], b1[0]);
+          i8x4_to_h2x2_biased(st.v[u][1].d[w], b0[1], b1[1]);
+          nt0 = 2 * w; nt1 = 2 * w + 1;
+        } else {
+          b0[0] = st.v[u][0].d[w]; b1[0] = st.v[u][0].d[w + 1];
+          b0[1] = st.v[u][1].d[w]; b1[1] = st.v[u][1].d[w + 1];
+          nt0 = w; nt1 = w + 1;
+          if (partial) {
+            // tokens 4g..4g+3 of this lane's pairs; zero the ones past the end
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int t0 = 4 * g + 2 * r;
+              const uint32_t m = (t0 < last_valid ? 0xFFFFu : 0u) | (t0 + 1 < last_valid ? 0xFFFF0000u : 0u);
+              b0[r] &= m; b1[r] &= m;
+            }
+          }
+        }
+        const uint2 v0 = make_uint2(b0[0], b0[1]), v1 = make_uint2(b1[0], b1[1]);
+        acc[nt0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bitcast<half4>(v0), acc[nt0], 0, 0, 0);
+        acc[nt1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bitcast<half4>(v1), acc[nt1], 0, 0, 0);
+      }
+      __asm__ volatile("" ::: "memory");
+    }
+  };
+
+  for (int b = 0; b < nbatch; b += 2) {
+    mstage_load<KV>(sb, P, blkv, b + 1, nblk, kvh, n, g);
+    compute(sa, b);
+    if (b + 1 >= nbatch) break;
+    mstage_load<KV>(sa, P, blkv, b + 2, nblk, kvh, n, g);
+    compute(sb, b + 1);
+  }
+
+  // ---- partials: row (head) 4g+r, dims 8n..8n+7 ----
+  const int64_t hrow0 = (int64_t)s * H + (int64_t)kvh * G;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float l = lrun[r], ps = psum[r];
+#pragma unroll
+    for (int k = 0; k < 1; ++k) {
+      l += dpp<DPP_QUAD_XOR1>(l); l += dpp<DPP_QUAD_XOR2>(l);
+      l += dpp<DPP_ROW_HALF_MIRROR>(l); l += dpp<DPP_ROW_MIRROR>(l);
+      if constexpr (I8) {
+        ps += dpp<DPP_QUAD_XOR1>(ps); ps += dpp<DPP_QUAD_XOR2>(ps);
+        ps += dpp<DPP_ROW_HALF_MIRROR>(ps); ps += dpp<DPP_ROW_MIRROR>(ps);
+      }
+    }
+    if (row_ok[r]) {
+      float o[8];
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, ps, acc[nt][r]) : acc[nt][r];
+      if (nparts == 1) {
+        const float inv = 1.f / l;
+        float4* dst = reinterpret_cast<float4*>(P.out + (hrow0 + 4 * g + r) * HD + 8 * n);
+        dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+        dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+      } else {
+        const int64_t pr = (hrow0 + 4 * g + r) * P.max_parts + part;
+        float4* dst = reinterpret_cast<float4*>(P.part_acc + pr * HD + 8 * n);
+        dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+        if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(M[r], l);
+      }
+    }
+  }
+}
+
+// Combine the partitions of one (sequence, head):
+//   out = sum_p 2^(M_p - M) acc_p / sum_p 2^(M_p - M) l_p,  M = max_p M_p.
+// One wave per (sequence, head); sequences with a single partition were
+// finished by the decode kernel itself. Partial rows are loaded 8 at a time so
+// the loads overlap.
 __device__ void decode_merge(const MergeParams& P) {
   const int lane = lane_id();
   const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
@@ -535,26 +882,38 @@ __device__ void decode_merge(const MergeParams& P) {
   const int s = r / P.n_heads;
   const int ctx = max(0, min(P.context_lens[s], P.max_parts * P.part_tokens));
   const int np = (ctx + P.part_tokens - 1) / P.part_tokens;
+  if (np <= 1) return;
   const float2* ml = reinterpret_cast<const float2*>(P.part_ml) + (int64_t)r * P.max_parts;
+  const float2* pa = reinterpret_cast<const float2*>(P.part_acc) + (int64_t)r * P.max_parts * (HD / 2);
   float M = kNegInf;
   for (int p = lane; p < np; p += WAVE) M = fmaxf(M, ml[p].x);
   M = wave_max(M);
-  float L = 0.f;
-  for (int p = lane; p < np; p += WAVE) L += __builtin_amdgcn_exp2f(ml[p].x - M) * ml[p].y;
-  L = wave_sum(L);
-  float o0 = 0.f, o1 = 0.f;
-  const float2* pa = reinterpret_cast<const float2*>(P.part_acc) + (int64_t)r * P.max_parts * (HD / 2);
+  float L = 0.f, o0 = 0.f, o1 = 0.f;
   for (int p0 = 0; p0 < np; p0 += WAVE) {
-    const float w = (p0 + lane < np) ? __builtin_amdgcn_exp2f(ml[p0 + lane].x - M) : 0.f;
-    const int n = min(WAVE, np - p0);
-    for (int k = 0; k < n; ++k) {
-      const float wk = readlane_f(w, k);
-      const float2 a = pa[(int64_t)(p0 + k) * (HD / 2) + lane];
-      o0 = fmaf(wk, a.x, o0);
-      o1 = fmaf(wk, a.y, o1);
+    float w = 0.f;
+    if (p0 + lane < np) {
+      const float2 m = ml[p0 + lane];
+      w = __builtin_amdgcn_exp2f(m.x - M);
+      L = fmaf(w, m.y, L);
+    }
+    const int cnt = min(WAVE, np - p0);
+    for (int k0 = 0; k0 < cnt; k0 += 8) {
+      float2 a[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        a[k] = (k0 + k < cnt) ? pa[(int64_t)(p0 + k0 + k) * (HD / 2) + lane] : make_float2(0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float wk = readlane_f(w, min(k0 + k, cnt - 1));
+        if (k0 + k < cnt) {
+          o0 = fmaf(wk, a[k].x, o0);
+          o1 = fmaf(wk, a[k].y, o1);
+        }
+      }
     }
   }
-  const float inv = (np > 0 && L > 0.f) ? 1.f / L : 0.f;
+  L = wave_sum(L);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
   reinterpret_cast<float2*>(P.out)[(int64_t)r * (HD / 2) + lane] = make_float2(o0 * inv, o1 * inv);
 }
 
@@ -809,7 +1168,14 @@ VK_DECODE_G(1, 0) VK_DECODE_G(1, 1)
 VK_DECODE_G(2, 0) VK_DECODE_G(2, 1)
 VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
 
-extern "C" __global__ void __launch_bounds__(256) vk_decode_merge(const MergeParams P) { decode_merge(P); }
+#define VK_DECODE_MFMA(KV, G)                                                       \
+  extern "C" __global__ void __launch_bounds__(64)                                  \
+      vk_decode_mfma_kv##KV##_g##G(const DecodeParams P) {                          \
+    decode_unit_mfma<KV, G>(P);                                                     \
+  }
+#define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
+VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
+
 
 #define VK_APPEND(KV) \
   extern "C" __global__ void __launch_bounds__(128) vk_append_kv##KV(const AppendParams P) { append_kernel<KV>(P); }
@@ -818,3 +1184,5 @@ VK_APPEND(0) VK_APPEND(1) VK_APPEND(2) VK_APPEND(3)
 extern "C" __global__ void __launch_bounds__(256) vk_slot_mapping(const SlotMapParams P) { slot_mapping_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_copy_blocks(const CopyParams P) { copy_blocks_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_fill_normal_f16(const FillParams P) { fill_normal_kernel(P); }
+extern "C" __global__ void __launch_bounds__(256) vk_decode_merge(const MergeParams P) { decode_merge(P); }
+

@@ -60,13 +60,6 @@ struct DecodeParams {
   float scale_log2;         // softmax scale * log2(e)
 };
 
-struct MergeParams {
-  const float* part_acc;
-  const float* part_ml;
-  const int32_t* context_lens;
-  float* out;
-  int32_t n_seqs, n_heads, max_parts, part_tokens;
-};
 
 struct TreeParams {
   const uint8_t* kc;
@@ -92,6 +85,14 @@ struct CopyParams {
   PoolGeom g;
   int32_t n_pairs;
   int32_t pairs[2 * kMaxCopyPairs];
+};
+
+struct MergeParams {
+  const float* part_acc;
+  const float* part_ml;
+  const int32_t* context_lens;
+  float* out;
+  int32_t n_seqs, n_heads, max_parts, part_tokens;
 };
 
 struct FillParams {

@@ -35,6 +35,7 @@ STATUS_NAMES = {
 
 # KV storage types and caller dtypes
 KV_F32, KV_F16, KV_I8_REF, KV_I8_BLK = 0, 1, 2, 3
+DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
 DT_F32, DT_F16 = 0, 1
 
 
@@ -88,6 +89,7 @@ PROTOTYPES = {
     "vk_ctx_create": [C.c_int, C.c_char_p, PP],
     "vk_ctx_destroy": [P],
     "vk_ctx_arch": [P, C.c_char_p, C.c_size_t],
+    "vk_ctx_set_decode_kernel": [P, C.c_int],
     "vk_pool_create": [P, C.POINTER(PoolDesc), PP],
     "vk_pool_destroy": [P],
     "vk_pool_get_desc": [P, C.POINTER(PoolDesc)],

@@ -73,6 +73,10 @@ class Context:
         except Exception:
             pass
 
+    def set_decode_kernel(self, kind: int):
+        """_capi.DECODE_AUTO / DECODE_VALU / DECODE_MFMA (vk_ctx_set_decode_kernel)."""
+        check(lib().vk_ctx_set_decode_kernel(self.h, kind))
+
     @property
     def arch(self) -> str:
         buf = C.create_string_buffer(64)
