@@ -76,7 +76,7 @@ def test_decode_gqa_groups_ragged(ctx, impl, kv, G):
 
 
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
-@pytest.mark.parametrize("P", [16, 256, 512, 1024, 0])
+@pytest.mark.parametrize("P", [16, 256, 1024, 2048, 4096, 0])
 def test_decode_split_k_partitions(ctx, impl, kv, P):
     print(f"decode split impl={impl} kv={kv} P={P}", flush=True)
     lens = [3000, 1024, 2049, 777]

@@ -48,7 +48,7 @@ int fail(int code, const char* fmt, ...) {
 
 constexpr int kBS = 16;   // block size the kernels are built for
 constexpr int kHD = 128;  // head_dim the kernels are built for
-constexpr int kMaxPartTokens = 1024;  // 64 blocks: one block id per lane of a wave
+constexpr int kMaxPartTokens = 4096;  // 256 blocks: four block-id windows of one wave
 
 uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
@@ -88,6 +88,8 @@ struct vk_ctx {
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
   int decode_kind = VK_DECODE_AUTO;
+  int n_cu = 256;
+  std::unordered_map<std::string, int64_t> resident;  // kernel -> resident waves
 
   hipFunction_t fn(const std::string& name) const {
     auto it = fns.find(name);
@@ -134,6 +136,19 @@ int launch(const vk_ctx* ctx, const char* name, dim3 grid, dim3 block, const P& 
   return VK_OK;
 }
 
+// Waves of a one-wave-per-workgroup kernel that fit on the device at once.
+int64_t resident_waves(vk_ctx* ctx, const std::string& name) {
+  auto it = ctx->resident.find(name);
+  if (it != ctx->resident.end()) return it->second;
+  int64_t waves = 2048;
+  hipFunction_t f = ctx->fn(name);
+  int per_cu = 0;
+  if (f && hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64, 0) == hipSuccess && per_cu > 0)
+    waves = (int64_t)per_cu * ctx->n_cu;
+  ctx->resident[name] = waves;
+  return waves;
+}
+
 int check_pool(const vk_ctx* ctx, const vk_pool* pool) {
   if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
   if (!pool) return fail(VK_ERR_NOT_WIRED, "pool is null");
@@ -172,6 +187,7 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
   auto* ctx = new vk_ctx();
   ctx->device = device;
   ctx->arch = arch;
+  ctx->n_cu = prop.multiProcessorCount;
   e = hipModuleLoad(&ctx->module, path.c_str());
   if (e != hipSuccess) {
     delete ctx;
@@ -405,7 +421,27 @@ struct DecodePlan {
   uint64_t acc_bytes, ml_bytes;
 };
 
-int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl) {
+// Decode kernel for these arguments: matrix cores for fp16 queries over fp16 / int8
+// KV unless the context asks for the VALU kernel; fp32 math otherwise.
+std::string decode_kernel_name(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a) {
+  const vk_pool_desc& d = pool->desc;
+  const int G = d.n_kv_heads > 0 ? a->n_heads / d.n_kv_heads : 0;
+  const bool fast = a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32;
+  return (fast && ctx->decode_kind != VK_DECODE_VALU) ? decode_mfma_name(d.kv_type, G)
+                                                      : decode_name(d.kv_type, G, a->q_dtype);
+}
+
+// Smallest partition (256..4096 tokens) whose units fit in one round of resident
+// waves; longer contexts get 4096-token partitions.
+int auto_partition(const vk_decode_args* a, const vk_pool_desc& d, int64_t resident_waves) {
+  const int64_t ctx = std::max(1, a->max_context_len);
+  const int64_t pairs = std::max<int64_t>(1, (int64_t)a->n_seqs * d.n_kv_heads);
+  for (int P = 256; P < kMaxPartTokens; P *= 2)
+    if (pairs * ((ctx + P - 1) / P) <= resident_waves) return P;
+  return kMaxPartTokens;
+}
+
+int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl, int64_t resident_waves = 2048) {
   if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
   const vk_pool_desc& d = pool->desc;
   if (a->layer < 0 || a->layer >= d.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", a->layer);
@@ -429,14 +465,7 @@ int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl) {
   int P = a->partition_tokens;
   if (P < 0 || P % d.block_size || P > kMaxPartTokens)
     return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
-  if (P == 0) {
-    // Largest partition that still leaves two rounds of resident waves on the chip;
-    // longer partitions keep the split-K partial traffic small.
-    const int64_t ctx = std::max(1, a->max_context_len);
-    const int64_t pairs = std::max<int64_t>(1, (int64_t)a->n_seqs * d.n_kv_heads);
-    P = kMaxPartTokens;
-    while (P > 256 && pairs * ((ctx + P - 1) / P) < 6144) P /= 2;
-  }
+  if (P == 0) P = auto_partition(a, d, resident_waves);
   pl->part_tokens = P;
   pl->max_parts = std::max(1, (a->max_context_len + P - 1) / P);
   pl->acc_bytes = align_up((uint64_t)a->n_seqs * a->n_heads * pl->max_parts * kHD * sizeof(float), 256);
@@ -447,9 +476,9 @@ int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl) {
 }  // namespace
 
 extern "C" int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes) {
-  if (!pool || !bytes) return fail(VK_ERR_BAD_ARG, "null argument");
+  if (!pool || !bytes || !a) return fail(VK_ERR_BAD_ARG, "null argument");
   DecodePlan pl;
-  int rc = plan_decode(pool, a, &pl);
+  int rc = plan_decode(pool, a, &pl, resident_waves(pool->ctx, decode_kernel_name(pool->ctx, pool, a)));
   if (rc) return rc;
   *bytes = pl.acc_bytes + pl.ml_bytes;
   return VK_OK;
@@ -458,8 +487,11 @@ extern "C" int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_ar
 extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
+  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
+  const std::string name = decode_kernel_name(ctx, pool, a);
+  const int64_t resident = resident_waves(ctx, name);
   DecodePlan pl;
-  if ((rc = plan_decode(pool, a, &pl))) return rc;
+  if ((rc = plan_decode(pool, a, &pl, resident))) return rc;
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
@@ -486,7 +518,6 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   const vk_pool_desc& d = pool->desc;
   const PoolGeom& g = pool->geom;
   const uint8_t* L = pool->base + g.layer_stride * (uint64_t)a->layer;
-  const int G = a->n_heads / d.n_kv_heads;
   const float scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)d.head_dim);
 
   DecodeParams p{};
@@ -514,9 +545,6 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.scale_log2 = scale * 1.4426950408889634f;
   const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
-  const bool fast = a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32;
-  const std::string name = (fast && ctx->decode_kind != VK_DECODE_VALU) ? decode_mfma_name(d.kv_type, G)
-                                                                       : decode_name(d.kv_type, G, a->q_dtype);
   if ((rc = launch(ctx, name.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
   if (pl.max_parts == 1) return VK_OK;  // every sequence was finished by the decode kernel
 

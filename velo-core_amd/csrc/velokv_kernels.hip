@@ -135,7 +135,7 @@ DEV DW<N> load_dw(const uint8_t* p) {
 // Paged decode attention, split-K partial pass.
 //
 // One wave (= one workgroup) owns one unit (sequence s, KV head kvh, partition
-// part of at most 64 blocks). The partition streams through a two-stage software
+// part of at most 256 blocks). The partition streams through a two-stage software
 // pipeline: while the K and V tiles of batch b (CH blocks) are consumed, the loads
 // of batch b+1 are already in flight.
 //   scores  K tile [tok][D]: lane = (token lane>>2, 32-dim slice lane&3). Dot
@@ -166,7 +166,42 @@ DEV void write_zero_rows(const DecodeParams& P, int s, int kvh) {
 }
 
 constexpr float kRescaleThreshold = 4.0f;  // log2 units
-constexpr int kMaxPartBlocks = 64;         // blocks per partition (one block id per lane)
+// Block ids (and per-(block, head) scales) of a unit, held one per lane in up to
+// kWin windows of 64 blocks: partitions of up to 256 blocks (4096 tokens).
+constexpr int kWin = 4;
+struct BlockIds {
+  int b[kWin];
+  float ks[kWin];
+  float vs[kWin];
+};
+template <bool BLK>
+DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, int blk0, int nblk, int kvh) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 0; k < kWin; ++k) {
+    w.b[k] = 0;
+    w.ks[k] = 1.f;
+    w.vs[k] = 1.f;
+    const int idx = 64 * k + lane;
+    if (idx < nblk) {
+      w.b[k] = min(max(bt[blk0 + idx], 0), P.n_blocks - 1);
+      if constexpr (BLK) {
+        w.ks[k] = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
+        w.vs[k] = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
+      }
+    }
+  }
+}
+// Value of block i (wave-uniform) from a per-lane window array.
+template <typename T>
+DEV T window_at(const T (&a)[kWin], int i) {
+  const int k = i >> 6;
+  T v = a[0];
+#pragma unroll
+  for (int j = 1; j < kWin; ++j) v = (k == j) ? a[j] : v;
+  if constexpr (sizeof(T) == 4 && __is_same(T, float)) return readlane_f(v, i & 63);
+  else return readlane_i(v, i & 63);
+}
 
 template <int KV>
 struct Stage {
@@ -190,21 +225,27 @@ DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   void* u = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
   return __builtin_amdgcn_make_buffer_rsrc(u, 0, (int)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
 }
-constexpr int kAuxNT = 2;  // non-temporal: K/V tiles are read once per decode
-template <int N>
+// Cache policy of tile loads: V is streamed non-temporally. K rows are split
+// over several load instructions (each covers a half (int8) or a quarter (fp16)
+// of every 128-byte line of the tile), so K stays in the normal L2 policy unless
+// its elements are bytes, where non-temporal measured faster.
+constexpr int kAuxNT = 2;
+template <int ESZ>
+constexpr int k_aux() { return ESZ == 1 ? kAuxNT : 0; }
+template <int N, int AUX = kAuxNT>
 DEV DW<N> buf_load(rsrc_t r, uint32_t off) {
   DW<N> out;
   if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16 * i), 0, kAuxNT);
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16 * i), 0, AUX);
       out.d[4 * i] = v.x; out.d[4 * i + 1] = v.y; out.d[4 * i + 2] = v.z; out.d[4 * i + 3] = v.w;
     }
   } else if constexpr (N == 2) {
-    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kAuxNT);
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX);
     out.d[0] = v.x; out.d[1] = v.y;
   } else {
-    out.d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kAuxNT);
+    out.d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX);
   }
   return out;
 }
@@ -212,18 +253,18 @@ DEV DW<N> buf_load(rsrc_t r, uint32_t off) {
 // Issue the loads of batch `b` (blocks b*CH .. b*CH+CH-1 of the unit, clamped to
 // the last block so the tail needs no branch).
 template <int KV>
-DEV void stage_load(Stage<KV>& st, const DecodeParams& P, int blkv, int b, int nblk, int kvh, int t) {
+DEV void stage_load(Stage<KV>& st, const DecodeParams& P, const BlockIds& bw, int b, int nblk, int kvh, int t) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr int CH = Stage<KV>::CH;
   const int lane = lane_id();
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
     const int i = min(b * CH + u, nblk - 1);
-    const int blk = readlane_i(blkv, i);
+    const int blk = window_at(bw.b, i);
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
     const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
     const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
-    st.k[u] = buf_load<8 * ESZ>(kr, lane * (32 * ESZ));
+    st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, lane * (32 * ESZ));
 #pragma unroll
     for (int j = 0; j < 8; ++j) st.v[u][j] = buf_load<ESZ>(vr, j * (HD * 2 * ESZ) + lane * (4 * ESZ));
     if constexpr (KV == KV_I8_REF) {
@@ -273,23 +314,16 @@ DEV void decode_unit(const DecodeParams& P) {
   const int32_t* bt = P.block_tables + (int64_t)row * P.bt_stride;
   const int H = P.n_heads;
   const int Hkv = P.n_kv_heads;
-  const int nblk = (end - start + BS - 1) / BS;   // <= kMaxPartBlocks
+  const int nblk = (end - start + BS - 1) / BS;   // <= 64 * kWin
   const int blk0 = start / BS;
   const int nbatch = (nblk + CH - 1) / CH;
 
   // block ids (and per-(block, head) scales) of the unit, one block per lane
-  int blkv = 0;
-  float ksv = 1.f, vsv = 1.f;
-  if (lane < nblk) {
-    blkv = min(max(bt[blk0 + lane], 0), P.n_blocks - 1);
-    if constexpr (BLK) {
-      ksv = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)blkv * Hkv + kvh]);
-      vsv = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)blkv * Hkv + kvh]);
-    }
-  }
+  BlockIds bw;
+  load_block_ids<BLK>(bw, P, bt, blk0, nblk, kvh);
 
   Stage<KV> sa, sb;
-  stage_load<KV>(sa, P, blkv, 0, nblk, kvh, t);
+  stage_load<KV>(sa, P, bw, 0, nblk, kvh, t);
 
   // ---- query registers: 32 dims (slice c) of each head of the group ---------
   uint32_t qh[G][QW];
@@ -390,7 +424,7 @@ DEV void decode_unit(const DecodeParams& P) {
         a[g] += dpp<DPP_QUAD_XOR2>(a[g]);
       }
       float kscale = P.scale_log2;
-      if constexpr (BLK) kscale *= readlane_f(ksv, min(i, nblk - 1));
+      if constexpr (BLK) kscale *= window_at(bw.ks, min(i, nblk - 1));
       if constexpr (REF) kscale *= st.ks[u];
       const bool valid = (i < nblk) && (start + i * BS + t < end);
 #pragma unroll
@@ -458,7 +492,7 @@ DEV void decode_unit(const DecodeParams& P) {
       const int i = b * CH + u;
       if (i < nblk) {
         float vscale = 1.f;
-        if constexpr (BLK) vscale = readlane_f(vsv, i);
+        if constexpr (BLK) vscale = window_at(bw.vs, i);
         if constexpr (REF) vscale = st.vs[u];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
@@ -543,10 +577,10 @@ DEV void decode_unit(const DecodeParams& P) {
 
   // two-stage pipeline over the batches of the unit
   for (int b = 0; b < nbatch; b += 2) {
-    stage_load<KV>(sb, P, blkv, b + 1, nblk, kvh, t);
+    stage_load<KV>(sb, P, bw, b + 1, nblk, kvh, t);
     compute(sa, b);
     if (b + 1 >= nbatch) break;
-    stage_load<KV>(sa, P, blkv, b + 2, nblk, kvh, t);
+    stage_load<KV>(sa, P, bw, b + 2, nblk, kvh, t);
     compute(sb, b + 1);
   }
 
@@ -603,7 +637,7 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 template <int KV>
 struct MStage {
   static constexpr int ESZ = Esz<KV>::v;
-  static constexpr int CH = (ESZ == 1) ? 2 : 1;  // blocks per pipeline stage
+  static constexpr int CH = 2;  // blocks per pipeline stage
   DW<8 * ESZ> k[CH];     // token n, dims 32g..32g+31
   DW<4 * ESZ> v[CH][2];  // token pairs 2g, 2g+1; dims 8n..8n+7
   float ks[CH];          // VK_KV_I8_REF: scales of token n
@@ -611,17 +645,17 @@ struct MStage {
 };
 
 template <int KV>
-DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, int blkv, int b, int nblk, int kvh, int n, int g) {
+DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, int b, int nblk, int kvh, int n, int g) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr int CH = MStage<KV>::CH;
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
     const int i = min(b * CH + u, nblk - 1);
-    const int blk = readlane_i(blkv, i);
+    const int blk = window_at(bw.b, i);
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
     const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
     const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
-    st.k[u] = buf_load<8 * ESZ>(kr, (n * HD + 32 * g) * ESZ);
+    st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * HD + 32 * g) * ESZ);
 #pragma unroll
     for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * HD * 2 + 16 * n) * ESZ);
     if constexpr (KV == KV_I8_REF) {
@@ -649,7 +683,7 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
   constexpr int CH = MStage<KV>::CH;
   constexpr float kBias = 1152.0f;
 
-  __shared__ uint16_t p_lds[16 * 16];  // p~[head][token] of one block
+  __shared__ uint16_t p_lds[CH * 16 * 16];  // p~[block][head][token] of one stage
 
   const int lane = lane_id();
   const int n = lane & 15;   // token (scores) / dim group (values) / head (A operands)
@@ -680,18 +714,11 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
   const int blk0 = start / BS;
   const int nbatch = (nblk + CH - 1) / CH;
 
-  int blkv = 0;
-  float ksv = 1.f, vsv = 1.f;
-  if (lane < nblk) {
-    blkv = min(max(bt[blk0 + lane], 0), P.n_blocks - 1);
-    if constexpr (BLK) {
-      ksv = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)blkv * Hkv + kvh]);
-      vsv = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)blkv * Hkv + kvh]);
-    }
-  }
+  BlockIds bw;
+  load_block_ids<BLK>(bw, P, bt, blk0, nblk, kvh);
 
   MStage<KV> sa, sb;
-  mstage_load<KV>(sa, P, blkv, 0, nblk, kvh, n, g);
+  mstage_load<KV>(sa, P, bw, 0, nblk, kvh, n, g);
 
   // q as the A operand: head n (rows >= G are zero), dims 32g..32g+31 in 4 chunks
   half8 qa[4];
@@ -717,8 +744,9 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) qsum[r] = __shfl(qsum_part, 4 * g + r, WAVE);
   }
-  // zero the p~ tile once so rows >= G stay zero
-  reinterpret_cast<uint2*>(p_lds)[lane] = make_uint2(0, 0);
+  // zero the p~ tiles once so rows >= G stay zero
+#pragma unroll
+  for (int u = 0; u < CH; ++u) reinterpret_cast<uint2*>(p_lds + u * 256)[lane] = make_uint2(0, 0);
 
   const bool row_ok[4] = {4 * g + 0 < G, 4 * g + 1 < G, 4 * g + 2 < G, 4 * g + 3 < G};
   float M[4], lrun[4], psum[4];
@@ -730,12 +758,11 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
   const int last_valid = (end - start) - (nblk - 1) * BS;
 
   auto compute = [&](const MStage<KV>& st, int b) {
+    // ---- scores of every block of the stage (independent MFMA chains) ----
+    float4v sc[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      const int i = b * CH + u;
-      if (i >= nblk) break;
-      // ---- scores ----
-      float4v sc = {0.f, 0.f, 0.f, 0.f};
+      sc[u] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         uint32_t kb[4];
@@ -747,93 +774,125 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
           for (int w = 0; w < 4; ++w) kb[w] = st.k[u].d[4 * kc + w];
         }
         const u32x4 kbv = {kb[0], kb[1], kb[2], kb[3]};
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kc], bitcast<half8>(kbv), sc, 0, 0, 0);
+        sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kc], bitcast<half8>(kbv), sc[u], 0, 0, 0);
       }
+    }
+    float sv[CH][4];
+    bool need = false;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
       float kscale = P.scale_log2;
-      if constexpr (BLK) kscale *= readlane_f(ksv, i);
+      if constexpr (BLK) kscale *= window_at(bw.ks, min(i, nblk - 1));
       if constexpr (REF) kscale *= st.ks[u];
-      const bool tok_ok = (start + i * BS + n) < end;
-      float sv[4];
-      bool need = false;
+      const bool tok_ok = (i < nblk) && (start + i * BS + n) < end;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float x = sc[r];
+        float x = sc[u][r];
         if constexpr (I8) x = fmaf(-kBias, qsum[r], x);
-        sv[r] = (tok_ok && row_ok[r]) ? x * kscale : kNegInf;
-        need |= sv[r] > M[r] + kRescaleThreshold;
+        sv[u][r] = (tok_ok && row_ok[r]) ? x * kscale : kNegInf;
+        need |= sv[u][r] > M[r] + kRescaleThreshold;
       }
-      // ---- lazy running max per row ----
-      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+    }
+    // ---- lazy running max per row ----
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float m = sv[r];
-          m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
-          m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
-          m = fmaxf(m, dpp<DPP_ROW_HALF_MIRROR>(m));
-          m = fmaxf(m, dpp<DPP_ROW_MIRROR>(m));  // max over the 16 tokens of the block
-          const float Mn = fmaxf(M[r], m);
-          const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[r] - Mn);
-          M[r] = Mn;
-          lrun[r] *= alpha;
-          psum[r] *= alpha;
+      for (int r = 0; r < 4; ++r) {
+        float m = sv[0][r];
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt) acc[nt][r] *= alpha;
-        }
+        for (int u = 1; u < CH; ++u) m = fmaxf(m, sv[u][r]);
+        m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
+        m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
+        m = fmaxf(m, dpp<DPP_ROW_HALF_MIRROR>(m));
+        m = fmaxf(m, dpp<DPP_ROW_MIRROR>(m));  // max over the 16 tokens of each block
+        const float Mn = fmaxf(M[r], m);
+        const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[r] - Mn);
+        M[r] = Mn;
+        lrun[r] *= alpha;
+        psum[r] *= alpha;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) acc[nt][r] *= alpha;
       }
-      // ---- p, p~ -> LDS tile [head][token] ----
+    }
+    // ---- p, p~ -> LDS tiles [block][head][token] ----
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
       float vscale = 1.f;
-      if constexpr (BLK) vscale = readlane_f(vsv, i);
+      if constexpr (BLK) vscale = window_at(bw.vs, min(i, nblk - 1));
       if constexpr (REF) vscale = st.vs[u];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = (sv[r] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(sv[r] - M[r]);
+        const float p = (sv[u][r] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(sv[u][r] - M[r]);
         lrun[r] += p;
         const uint16_t ph = f2h(p * vscale);
         if constexpr (I8) psum[r] += h2f(ph);
-        if (row_ok[r]) p_lds[(4 * g + r) * 16 + n] = ph;
+        if (row_ok[r]) p_lds[u * 256 + (4 * g + r) * 16 + n] = ph;
       }
-      __asm__ volatile("" ::: "memory");
-      const uint2 pa2 = reinterpret_cast<const uint2*>(p_lds)[n * 4 + g];  // p~[head n][tokens 4g..4g+3]
-      const half4 pa = bitcast<half4>(pa2);
-      // ---- values ----
-      const bool partial = (i == nblk - 1) && (last_valid < BS);
+    }
+    __asm__ volatile("" ::: "memory");
+    half4 pa[CH];
 #pragma unroll
-      for (int w = 0; w < 4 * ESZ; w += ESZ) {
-        // tiles nt: I8 -> dword w of each pair row gives dims 2w, 2w+1; F16 -> dwords w, w+1
-        uint32_t b0[2], b1[2];   // [pair row] for tile nt0, nt1
-        int nt0, nt1;
-        if constexpr (I8) {
-          i8x4_to_h2x2_biased(st.v[u][0].d[w], b0[0], b1[0]);
-          i8x4_to_h2x2_biased(st.v[u][1].d[w], b0[1], b1[1]);
-          nt0 = 2 * w; nt1 = 2 * w + 1;
-        } else {
-          b0[0] = st.v[u][0].d[w]; b1[0] = st.v[u][0].d[w + 1];
-          b0[1] = st.v[u][1].d[w]; b1[1] = st.v[u][1].d[w + 1];
-          nt0 = w; nt1 = w + 1;
-          if (partial) {
-            // tokens 4g..4g+3 of this lane's pairs; zero the ones past the end
+    for (int u = 0; u < CH; ++u)
+      pa[u] = bitcast<half4>(reinterpret_cast<const uint2*>(p_lds + u * 256)[n * 4 + g]);  // p~[head n][tokens 4g..]
+    // ---- values ----
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-              const int t0 = 4 * g + 2 * r;
-              const uint32_t m = (t0 < last_valid ? 0xFFFFu : 0u) | (t0 + 1 < last_valid ? 0xFFFF0000u : 0u);
-              b0[r] &= m; b1[r] &= m;
+    for (int u = 0; u < CH; ++u) {
+      const int i = b * CH + u;
+      if (i < nblk) {
+        const bool partial = (i == nblk - 1) && (last_valid < BS);
+#pragma unroll
+        for (int w = 0; w < 4 * ESZ; w += ESZ) {
+          uint32_t b0[2], b1[2];   // [pair row] for tiles nt0, nt1
+          int nt0, nt1;
+          if constexpr (I8) {
+            i8x4_to_h2x2_biased(st.v[u][0].d[w], b0[0], b1[0]);
+            i8x4_to_h2x2_biased(st.v[u][1].d[w], b0[1], b1[1]);
+            nt0 = 2 * w; nt1 = 2 * w + 1;
+          } else {
+            b0[0] = st.v[u][0].d[w]; b1[0] = st.v[u][0].d[w + 1];
+            b0[1] = st.v[u][1].d[w]; b1[1] = st.v[u][1].d[w + 1];
+            nt0 = w; nt1 = w + 1;
+            if (partial) {
+#pragma unroll
+              for (int r = 0; r < 2; ++r) {
+                const int t0 = 4 * g + 2 * r;
+                const uint32_t m = (t0 < last_valid ? 0xFFFFu : 0u) | (t0 + 1 < last_valid ? 0xFFFF0000u : 0u);
+                b0[r] &= m; b1[r] &= m;
+              }
             }
           }
+          const uint2 v0 = make_uint2(b0[0], b0[1]), v1 = make_uint2(b1[0], b1[1]);
+          acc[nt0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[u], bitcast<half4>(v0), acc[nt0], 0, 0, 0);
+          acc[nt1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[u], bitcast<half4>(v1), acc[nt1], 0, 0, 0);
         }
-        const uint2 v0 = make_uint2(b0[0], b0[1]), v1 = make_uint2(b1[0], b1[1]);
-        acc[nt0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bitcast<half4>(v0), acc[nt0], 0, 0, 0);
-        acc[nt1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bitcast<half4>(v1), acc[nt1], 0, 0, 0);
       }
-      __asm__ volatile("" ::: "memory");
     }
+    __asm__ volatile("" ::: "memory");
   };
 
-  for (int b = 0; b < nbatch; b += 2) {
-    mstage_load<KV>(sb, P, blkv, b + 1, nblk, kvh, n, g);
-    compute(sa, b);
-    if (b + 1 >= nbatch) break;
-    mstage_load<KV>(sa, P, blkv, b + 2, nblk, kvh, n, g);
-    compute(sb, b + 1);
+  if constexpr (I8) {
+    // three-stage pipeline: two stages in flight while one is consumed
+    MStage<KV> sc2;
+    mstage_load<KV>(sb, P, bw, 1, nblk, kvh, n, g);
+    for (int b = 0; b < nbatch; b += 3) {
+      mstage_load<KV>(sc2, P, bw, b + 2, nblk, kvh, n, g);
+      compute(sa, b);
+      if (b + 1 >= nbatch) break;
+      mstage_load<KV>(sa, P, bw, b + 3, nblk, kvh, n, g);
+      compute(sb, b + 1);
+      if (b + 2 >= nbatch) break;
+      mstage_load<KV>(sb, P, bw, b + 4, nblk, kvh, n, g);
+      compute(sc2, b + 2);
+    }
+  } else {
+    for (int b = 0; b < nbatch; b += 2) {
+      mstage_load<KV>(sb, P, bw, b + 1, nblk, kvh, n, g);
+      compute(sa, b);
+      if (b + 1 >= nbatch) break;
+      mstage_load<KV>(sa, P, bw, b + 2, nblk, kvh, n, g);
+      compute(sb, b + 1);
+    }
   }
 
   // ---- partials: row (head) 4g+r, dims 8n..8n+7 ----
