@@ -87,6 +87,23 @@ def append_bytes(kv: int, S: int, Hkv: int) -> int:
     return 2 * S * Hkv * HD * 2 + 2 * S * Hkv * HD * esz + 2 * S * Hkv * sc + S * 8
 
 
+def measured_traffic(kernel: str, S: int, L: int, H: int, Hkv: int, ragged: bool):
+    """HBM bytes per launch of `kernel` on this workload from the committed PMC
+    summary (profiles/*.md lines 'traffic <kernel> S=..,L=..,H=..,Hkv=.. <bytes>'), or None."""
+    if ragged:
+        return None
+    key = f"S={S},L={L},H={H},Hkv={Hkv}"
+    pdir = os.path.join(ROOT, "profiles")
+    for fn in sorted(os.listdir(pdir)) if os.path.isdir(pdir) else []:
+        if not fn.endswith(".md"):
+            continue
+        for line in open(os.path.join(pdir, fn)):
+            parts = line.split()
+            if len(parts) == 4 and parts[0] == "traffic" and parts[1] == kernel and parts[2] == key:
+                return int(parts[3])
+    return None
+
+
 def run_gpu(ctx, args, kv_name: str):
     kv = velokv.KV_I8_BLK if kv_name == "int8" else velokv.KV_F16
     S, H, Hkv, L, NL = args.seqs, args.heads, args.kv_heads, args.ctx, args.layers
@@ -165,6 +182,9 @@ def run_gpu(ctx, args, kv_name: str):
     step_bytes = NL * (dbytes + abytes)
     dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
+    kname = ("vk_decode_kv%d_g%d_q1" % (kv, H // Hkv)
+             if args.decode == "valu" or (args.decode == "auto" and kv == velokv.KV_F16)
+             else "vk_decode_mfma_kv%d_g%d" % (kv, H // Hkv))
     res = {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
         "ms_per_step": round(ms_step, 4),
@@ -173,9 +193,9 @@ def run_gpu(ctx, args, kv_name: str):
         "decode_bytes_per_launch": dbytes,
         "append_bytes_per_launch": abytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": ("vk_decode_kv%d_g%d_q1" % (kv, H // Hkv) if args.decode == "valu" else
-                                "vk_decode_mfma_kv%d_g%d" % (kv, H // Hkv)),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(kname, S, L, H, Hkv, args.ragged),
+                     "kernel": kname,
                      "launch_ms_mean": round(dec_mean_ms, 5), "launch_ms_min": round(float(np.min(dec_ms)), 5),
                      "launches": len(dec_ms)},
         "pool_gb": round(pool.nbytes / 1e9, 2),

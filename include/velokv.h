@@ -87,8 +87,9 @@ int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
 
 /* Kernel family of vk_paged_decode for fp16 queries over fp16/int8 KV:
  * VK_DECODE_MFMA (QK and PV on v_mfma_f32_16x16x{32,16}_f16), VK_DECODE_VALU
- * (v_dot2_f32_f16 on the vector ALUs) or VK_DECODE_AUTO (= MFMA). fp32 queries
- * and fp32 KV always use the fp32 VALU kernel. No reference counterpart. */
+ * (v_dot2_f32_f16 on the vector ALUs) or VK_DECODE_AUTO (MFMA for int8 KV,
+ * VALU for fp16 KV: the faster one on MI355X for each). fp32 queries and fp32
+ * KV always use the fp32 VALU kernel. No reference counterpart. */
 #define VK_DECODE_AUTO 0
 #define VK_DECODE_VALU 1
 #define VK_DECODE_MFMA 2

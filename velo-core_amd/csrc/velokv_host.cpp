@@ -427,8 +427,10 @@ std::string decode_kernel_name(const vk_ctx* ctx, const vk_pool* pool, const vk_
   const vk_pool_desc& d = pool->desc;
   const int G = d.n_kv_heads > 0 ? a->n_heads / d.n_kv_heads : 0;
   const bool fast = a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32;
-  return (fast && ctx->decode_kind != VK_DECODE_VALU) ? decode_mfma_name(d.kv_type, G)
-                                                      : decode_name(d.kv_type, G, a->q_dtype);
+  // AUTO: matrix cores for int8 KV; fp16 KV measured faster on the dot2 kernel
+  const bool mfma = fast && (ctx->decode_kind == VK_DECODE_MFMA ||
+                             (ctx->decode_kind == VK_DECODE_AUTO && d.kv_type != VK_KV_F16));
+  return mfma ? decode_mfma_name(d.kv_type, G) : decode_name(d.kv_type, G, a->q_dtype);
 }
 
 // Smallest partition (256..4096 tokens) whose units fit in one round of resident
