@@ -200,7 +200,7 @@ int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* s
 typedef struct vk_tree_args {
   int32_t layer;
   const void* q;              /* dev [S][n_nodes][n_heads][head_dim] of q_dtype */
-  int32_t q_dtype;
+  int32_t q_dtype;            /* VK_DT_F16, or VK_DT_F32 (rounded to fp16 for the matrix cores) */
   float* out;                 /* dev fp32 [S][n_nodes][n_heads][head_dim]       */
   const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = slot table        */
   int32_t bt_stride;
@@ -208,17 +208,35 @@ typedef struct vk_tree_args {
   const int32_t* context_lens;/* dev [S] committed tokens before the tree        */
   const uint32_t* tree_mask;  /* dev [S][n_nodes]: bit j of row i = node i sees node j */
   int32_t n_seqs;
-  int32_t n_nodes;            /* <= 32; node j's K/V sit at position context_len + j */
+  int32_t n_nodes;            /* 1..32; node j's K/V sit at position context_len + j */
   int32_t n_heads;
-  int32_t max_context_len;
-  float scale;
+  int32_t max_context_len;    /* max over context_lens (committed tokens)        */
+  float scale;                /* 0 = 1/sqrt(head_dim)                            */
+  int32_t partition_tokens;   /* split-K partition, multiple of bs, <= 4096; 0 = auto */
+  void* workspace;            /* dev split-K scratch or NULL (context-owned)     */
+  uint64_t workspace_bytes;
 } vk_tree_args;
 
-/* Multi-query tree-verify attention: node i attends to the committed context
- * and to the tree nodes its mask row selects.
+/* Bytes of split-K workspace vk_tree_verify needs for these arguments (0 when
+ * one partition covers every sequence). */
+int vk_tree_verify_workspace(const vk_pool* pool, const vk_tree_args* a, uint64_t* bytes);
+
+/* Multi-query tree-verify attention over fp16 or int8 pools: query row (node i,
+ * head h) attends to the committed context (positions 0..context_len-1) and to
+ * the tree nodes j its mask row selects (position context_len + j). Build
+ * tree_mask with vk_tree_mask (ancestors and the node itself).
  * paged_attention_tree (kernels.metal:512-599) / forward_tree
- * (metal/model.rs:574-731), with the mask semantics defined here. */
+ * (metal/model.rs:574-731). The reference places an ancestor at n_ctx + depth
+ * and skips the node itself (kernels.metal:567-575); here every node has its own
+ * position so sibling branches do not collide, and a node sees itself. */
 int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a, void* stream);
+
+/* Ancestor mask of a draft tree given as parent indices (parents[0] = -1 for
+ * the root, parents[i] < i otherwise): mask_out[i] has bit j set when node j is
+ * node i or one of its ancestors. Host only.
+ * SpeculativeTree (speculative.rs:48-95); ancestors_map of forward_tree
+ * (metal/model.rs:615-632) as a bitmask. */
+int vk_tree_mask(const int32_t* parents, int32_t n_nodes, uint32_t* mask_out);
 
 /* Copy-on-write block copy: for each (src, dst) pair in the HOST array
  * src_dst_pairs[2*n_pairs], copy the K/V codes and scales of block src to block

@@ -49,6 +49,7 @@ int fail(int code, const char* fmt, ...) {
 constexpr int kBS = 16;   // block size the kernels are built for
 constexpr int kHD = 128;  // head_dim the kernels are built for
 constexpr int kMaxPartTokens = 4096;  // 256 blocks: four block-id windows of one wave
+constexpr int kMaxTreeNodes = 32;     // one 32-bit mask row per node
 
 uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
@@ -119,6 +120,10 @@ std::string decode_name(int kv, int g, int qt) {
 }
 std::string decode_mfma_name(int kv, int g) {
   return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g);
+}
+std::string tree_name(int kv, int g, int rt, int qt) {
+  return "vk_tree_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_r" + std::to_string(rt) + "_q" +
+         std::to_string(qt);
 }
 
 int set_device(const vk_ctx* ctx) {
@@ -198,6 +203,9 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
     for (int g : {1, 2, 4, 8}) {
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
       if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
+      if (kv != VK_KV_F32)
+        for (int rt : {1, 2})
+          for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
     }
   for (const auto& nm : names) {
     hipFunction_t f = nullptr;
@@ -412,6 +420,31 @@ extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* 
 
 namespace {
 
+// Split-K workspace: the caller's buffer when given (and large enough), else the
+// context's own, grown on demand.
+int split_workspace(vk_ctx* ctx, void* given, uint64_t given_bytes, uint64_t need, uint8_t** out) {
+  if (given) {
+    if (given_bytes < need)
+      return fail(VK_ERR_BAD_ARG, "workspace of %llu bytes, need %llu", (unsigned long long)given_bytes,
+                  (unsigned long long)need);
+    *out = reinterpret_cast<uint8_t*>(given);
+    return VK_OK;
+  }
+  std::lock_guard<std::mutex> lk(ctx->ws_mu);
+  if (ctx->ws_bytes < need) {
+    if (ctx->ws) {
+      HIP_TRY(hipDeviceSynchronize());
+      HIP_TRY(hipFree(ctx->ws));
+      ctx->ws = nullptr;
+      ctx->ws_bytes = 0;
+    }
+    HIP_TRY(hipMalloc(&ctx->ws, need));
+    ctx->ws_bytes = need;
+  }
+  *out = reinterpret_cast<uint8_t*>(ctx->ws);
+  return VK_OK;
+}
+
 struct DecodePlan {
   const int32_t* bt;
   int32_t bt_stride;
@@ -497,26 +530,8 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
-  const uint64_t need = pl.acc_bytes + pl.ml_bytes;
-  uint8_t* ws = reinterpret_cast<uint8_t*>(a->workspace);
-  if (ws) {
-    if (a->workspace_bytes < need)
-      return fail(VK_ERR_BAD_ARG, "workspace of %llu bytes, need %llu", (unsigned long long)a->workspace_bytes,
-                  (unsigned long long)need);
-  } else {
-    std::lock_guard<std::mutex> lk(ctx->ws_mu);
-    if (ctx->ws_bytes < need) {
-      if (ctx->ws) {
-        HIP_TRY(hipDeviceSynchronize());
-        HIP_TRY(hipFree(ctx->ws));
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
-      }
-      HIP_TRY(hipMalloc(&ctx->ws, need));
-      ctx->ws_bytes = need;
-    }
-    ws = reinterpret_cast<uint8_t*>(ctx->ws);
-  }
+  uint8_t* ws = nullptr;
+  if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes, &ws))) return rc;
   const vk_pool_desc& d = pool->desc;
   const PoolGeom& g = pool->geom;
   const uint8_t* L = pool->base + g.layer_stride * (uint64_t)a->layer;
@@ -544,6 +559,9 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.n_blocks = d.n_blocks;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
+  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens, (int64_t)pl.bt_stride * d.block_size);
+  p.n_nodes = 1;
+  p.n_rgroups = 1;
   p.scale_log2 = scale * 1.4426950408889634f;
   const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
@@ -555,20 +573,157 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   m.part_ml = p.part_ml;
   m.context_lens = a->context_lens;
   m.out = a->out;
-  m.n_seqs = a->n_seqs;
-  m.n_heads = a->n_heads;
+  m.n_rows = a->n_seqs * a->n_heads;
+  m.rows_per_seq = a->n_heads;
+  m.extra_tokens = 0;
   m.max_parts = pl.max_parts;
   m.part_tokens = pl.part_tokens;
-  const uint64_t rows = (uint64_t)a->n_seqs * a->n_heads;
-  return launch(ctx, "vk_decode_merge", dim3((unsigned)((rows + 3) / 4)), dim3(256), m, stream);
+  m.cap_tokens = p.cap_tokens;
+  return launch(ctx, "vk_decode_merge", dim3((unsigned)((m.n_rows + 3) / 4)), dim3(256), m, stream);
+}
+
+namespace {
+
+struct TreePlan {
+  const int32_t* bt;
+  int32_t bt_stride, bt_rows, part_tokens, max_parts, rt, n_rgroups;
+  uint64_t acc_bytes, ml_bytes;
+  std::string kernel;
+};
+
+int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan* pl) {
+  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
+  const vk_pool_desc& d = pool->desc;
+  if (a->layer < 0 || a->layer >= d.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", a->layer);
+  if (a->n_seqs < 0 || a->n_heads <= 0 || a->max_context_len < 0) return fail(VK_ERR_BAD_ARG, "bad sizes");
+  if (a->n_nodes < 1 || a->n_nodes > kMaxTreeNodes)
+    return fail(VK_ERR_BAD_ARG, "n_nodes %d out of range [1, %d]", a->n_nodes, kMaxTreeNodes);
+  if (a->n_heads % d.n_kv_heads) return fail(VK_ERR_BAD_ARG, "n_heads %d not a multiple of n_kv_heads %d", a->n_heads, d.n_kv_heads);
+  const int G = a->n_heads / d.n_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (supported 1, 2, 4, 8)", G);
+  if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
+  if (d.kv_type == VK_KV_F32) return fail(VK_ERR_UNSUPPORTED, "tree verify reads fp16 or int8 KV pools, not fp32");
+  pl->bt = a->block_tables;
+  pl->bt_stride = a->bt_stride;
+  pl->bt_rows = 0;
+  if (!pl->bt) {
+    if (!pool->table) return fail(VK_ERR_BAD_ARG, "no block table given and the pool has no slot table");
+    pl->bt = pool->table;
+    pl->bt_stride = d.max_pages_per_slot;
+    pl->bt_rows = d.max_slots;
+  }
+  if (pl->bt_stride <= 0) return fail(VK_ERR_BAD_ARG, "bt_stride must be positive");
+  const int64_t tokens = (int64_t)a->max_context_len + a->n_nodes;
+  if (tokens > (int64_t)pl->bt_stride * d.block_size)
+    return fail(VK_ERR_BAD_ARG, "max_context_len %d + n_nodes %d exceeds the block-table row (%d pages)",
+                a->max_context_len, a->n_nodes, pl->bt_stride);
+  const int rows = a->n_nodes * G;
+  pl->rt = rows > 16 ? 2 : 1;
+  pl->n_rgroups = (rows + 16 * pl->rt - 1) / (16 * pl->rt);
+  pl->kernel = tree_name(d.kv_type, G, pl->rt, a->q_dtype);
+  int P = a->partition_tokens;
+  if (P < 0 || P % d.block_size || P > kMaxPartTokens)
+    return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
+  if (P == 0) {
+    const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
+    const int64_t pairs = std::max<int64_t>(1, (int64_t)a->n_seqs * d.n_kv_heads * pl->n_rgroups);
+    P = kMaxPartTokens;
+    for (int c = 256; c < kMaxPartTokens; c *= 2)
+      if (pairs * ((tokens + c - 1) / c) <= waves) { P = c; break; }
+  }
+  pl->part_tokens = P;
+  pl->max_parts = (int32_t)std::max<int64_t>(1, (tokens + P - 1) / P);
+  const uint64_t rows_total = (uint64_t)a->n_seqs * a->n_nodes * a->n_heads * pl->max_parts;
+  pl->acc_bytes = align_up(rows_total * kHD * sizeof(float), 256);
+  pl->ml_bytes = align_up(rows_total * 2 * sizeof(float), 256);
+  return VK_OK;
+}
+
+}  // namespace
+
+extern "C" int vk_tree_verify_workspace(const vk_pool* pool, const vk_tree_args* a, uint64_t* bytes) {
+  if (!pool || !bytes || !a) return fail(VK_ERR_BAD_ARG, "null argument");
+  TreePlan pl;
+  int rc = plan_tree(pool->ctx, pool, a, &pl);
+  if (rc) return rc;
+  *bytes = pl.max_parts > 1 ? pl.acc_bytes + pl.ml_bytes : 0;
+  return VK_OK;
 }
 
 extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a, void* stream) {
-  (void)stream;
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
-  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
-  return fail(VK_ERR_UNSUPPORTED, "tree verify kernel is not built yet");
+  TreePlan pl;
+  if ((rc = plan_tree(ctx, pool, a, &pl))) return rc;
+  if (a->n_seqs == 0) return VK_OK;
+  if (!a->q || !a->out || !a->context_lens || !a->tree_mask) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  if ((rc = set_device(ctx))) return rc;
+  uint8_t* ws = nullptr;
+  if (pl.max_parts > 1 &&
+      (rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes, &ws)))
+    return rc;
+  const vk_pool_desc& d = pool->desc;
+  const PoolGeom& g = pool->geom;
+  const uint8_t* L = pool->base + g.layer_stride * (uint64_t)a->layer;
+  const float scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)d.head_dim);
+
+  DecodeParams p{};
+  p.kc = L + g.k_off;
+  p.vc = L + g.v_off;
+  p.ks = g.stile_bytes ? L + g.ks_off : nullptr;
+  p.vs = g.stile_bytes ? L + g.vs_off : nullptr;
+  p.q = a->q;
+  p.out = a->out;
+  p.part_acc = reinterpret_cast<float*>(ws);
+  p.part_ml = ws ? reinterpret_cast<float*>(ws + pl.acc_bytes) : nullptr;
+  p.block_tables = pl.bt;
+  p.seq_rows = a->seq_rows;
+  p.context_lens = a->context_lens;
+  p.tree_mask = a->tree_mask;
+  p.tile_bytes = g.tile_bytes;
+  p.stile_bytes = g.stile_bytes;
+  p.bt_stride = pl.bt_stride;
+  p.bt_rows = pl.bt_rows;
+  p.n_seqs = a->n_seqs;
+  p.n_heads = a->n_heads;
+  p.n_kv_heads = d.n_kv_heads;
+  p.n_blocks = d.n_blocks;
+  p.max_parts = pl.max_parts;
+  p.part_tokens = pl.part_tokens;
+  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens, (int64_t)pl.bt_stride * d.block_size);
+  p.n_nodes = a->n_nodes;
+  p.n_rgroups = pl.n_rgroups;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads * pl.n_rgroups;
+  if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
+  if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
+  if (pl.max_parts == 1) return VK_OK;
+
+  MergeParams m{};
+  m.part_acc = p.part_acc;
+  m.part_ml = p.part_ml;
+  m.context_lens = a->context_lens;
+  m.out = a->out;
+  m.n_rows = a->n_seqs * a->n_nodes * a->n_heads;
+  m.rows_per_seq = a->n_nodes * a->n_heads;
+  m.extra_tokens = a->n_nodes;
+  m.max_parts = pl.max_parts;
+  m.part_tokens = pl.part_tokens;
+  m.cap_tokens = p.cap_tokens;
+  return launch(ctx, "vk_decode_merge", dim3((unsigned)((m.n_rows + 3) / 4)), dim3(256), m, stream);
+}
+
+extern "C" int vk_tree_mask(const int32_t* parents, int32_t n_nodes, uint32_t* mask_out) {
+  if (!parents || !mask_out) return fail(VK_ERR_BAD_ARG, "null argument");
+  if (n_nodes < 1 || n_nodes > kMaxTreeNodes) return fail(VK_ERR_BAD_ARG, "n_nodes %d out of range [1, %d]", n_nodes, kMaxTreeNodes);
+  if (parents[0] != -1) return fail(VK_ERR_BAD_ARG, "node 0 must be the root (parent -1)");
+  mask_out[0] = 1u;
+  for (int32_t i = 1; i < n_nodes; ++i) {
+    const int32_t p = parents[i];
+    if (p < 0 || p >= i) return fail(VK_ERR_BAD_ARG, "node %d has parent %d (must be in [0, %d))", i, p, i);
+    mask_out[i] = mask_out[p] | (1u << i);
+  }
+  return VK_OK;
 }
 
 extern "C" int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* pairs, int32_t n_pairs, void* stream) {

@@ -300,8 +300,7 @@ DEV void decode_unit(const DecodeParams& P) {
   const int s = rest / P.max_parts;
   if (s >= P.n_seqs) return;
 
-  const int cap = min(P.max_parts * P.part_tokens, P.bt_stride * BS);
-  const int ctx = max(0, min(P.context_lens[s], cap));
+  const int ctx = max(0, min(P.context_lens[s], P.cap_tokens));
   const int start = part * P.part_tokens;
   if (start >= ctx) {
     if (part == 0) write_zero_rows<G>(P, s, kvh);
@@ -674,8 +673,11 @@ DEV void i8x4_to_h2x2_biased(uint32_t w, uint32_t& lo, uint32_t& hi) {
   hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
 }
 
-template <int KV, int G>
-DEV void decode_unit_mfma(const DecodeParams& P) {
+// Rows of a unit: RT tiles of 16 query rows. Row R of the (sequence, KV head)
+// pair is (node R / G, head kvh*G + R % G); decode has one node.
+// An fp32 q (QT == DT_F32) is rounded to fp16 for the matrix cores.
+template <int KV, int G, int RT, bool TREE, int QT = DT_F16>
+DEV void attn_unit_mfma(const DecodeParams& P) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr bool I8 = (ESZ == 1);
   constexpr bool BLK = (KV == KV_I8_BLK);
@@ -683,24 +685,32 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
   constexpr int CH = MStage<KV>::CH;
   constexpr float kBias = 1152.0f;
 
-  __shared__ uint16_t p_lds[CH * 16 * 16];  // p~[block][head][token] of one stage
+  __shared__ uint16_t p_lds[CH * RT * 256];  // p~[block][row tile][row][token] of one stage
 
   const int lane = lane_id();
-  const int n = lane & 15;   // token (scores) / dim group (values) / head (A operands)
+  const int n = lane & 15;   // token (scores) / dim group (values) / row (A operands)
   const int g = lane >> 4;   // dim slice (scores) / row group (results) / token group (values)
 
-  const int unit = blockIdx.x;
+  int unit = blockIdx.x;
+  int rg = 0;
+  if constexpr (TREE) {
+    rg = unit % P.n_rgroups;
+    unit /= P.n_rgroups;
+  }
   const int kvh = unit % P.n_kv_heads;
   const int rest = unit / P.n_kv_heads;
   const int part = rest % P.max_parts;
   const int s = rest / P.max_parts;
   if (s >= P.n_seqs) return;
 
-  const int cap = min(P.max_parts * P.part_tokens, P.bt_stride * BS);
-  const int ctx = max(0, min(P.context_lens[s], cap));
+  const int N = TREE ? P.n_nodes : 1;
+  const int ctx_c = max(0, min(P.context_lens[s], P.cap_tokens));  // committed tokens
+  const int ctx = TREE ? min(ctx_c + N, P.cap_tokens) : ctx_c;      // committed + tree nodes
   const int start = part * P.part_tokens;
   if (start >= ctx) {
-    if (part == 0) write_zero_rows<G>(P, s, kvh);
+    if constexpr (!TREE) {
+      if (part == 0) write_zero_rows<G>(P, s, kvh);
+    }
     return;
   }
   const int end = min(start + P.part_tokens, ctx);
@@ -709,10 +719,13 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
   if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
   const int32_t* bt = P.block_tables + (int64_t)row * P.bt_stride;
   const int H = P.n_heads;
-  const int Hkv = P.n_kv_heads;
   const int nblk = (end - start + BS - 1) / BS;
   const int blk0 = start / BS;
   const int nbatch = (nblk + CH - 1) / CH;
+  const int nrows = N * G;
+  const int row0 = rg * 16 * RT;
+  // output row of row R of this (sequence, KV head) pair
+  auto out_row = [&](int R) -> int64_t { return ((int64_t)s * N + R / G) * H + (int64_t)kvh * G + R % G; };
 
   BlockIds bw;
   load_block_ids<BLK>(bw, P, bt, blk0, nblk, kvh);
@@ -720,49 +733,77 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
   MStage<KV> sa, sb;
   mstage_load<KV>(sa, P, bw, 0, nblk, kvh, n, g);
 
-  // q as the A operand: head n (rows >= G are zero), dims 32g..32g+31 in 4 chunks
-  half8 qa[4];
-  float qsum_part = 0.f;
-  {
-    const uint16_t* q16 = reinterpret_cast<const uint16_t*>(P.q) + ((int64_t)s * H + (int64_t)kvh * G + n) * HD + 32 * g;
+  // q as the A operand: row n of each tile (rows >= nrows are zero), dims 32g..32g+31 in 4 chunks
+  half8 qa[RT][4];
+  float qsum[RT][4];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int R = row0 + 16 * rt + n;
+    float qsum_part = 0.f;
+    const int64_t qoff = out_row(R) * HD + 32 * g;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (n < G) v = reinterpret_cast<const uint4*>(q16)[kc];
-      qa[kc] = bitcast<half8>(v);
+      if (R < nrows) {
+        if constexpr (QT == DT_F32) {
+          const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff) + 2 * kc;
+          const float4 x0 = q32[0], x1 = q32[1];
+          v = make_uint4(pack_h2(x0.x, x0.y), pack_h2(x0.z, x0.w), pack_h2(x1.x, x1.y), pack_h2(x1.z, x1.w));
+        } else {
+          v = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qoff)[kc];
+        }
+      }
+      qa[rt][kc] = bitcast<half8>(v);
       if constexpr (I8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qsum_part += (float)qa[kc][j];
+        for (int j = 0; j < 8; ++j) qsum_part += (float)qa[rt][kc][j];
       }
     }
-  }
-  // sum over the 4 slices of each head, then the 4 heads of this lane's row group
-  float qsum[4] = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (I8) {
-    qsum_part += shfl_xor(qsum_part, 16);
-    qsum_part += shfl_xor(qsum_part, 32);   // every lane: full sum of head n
+    // sum over the 4 slices of each row, then fetch the 4 rows of this lane's row group
 #pragma unroll
-    for (int r = 0; r < 4; ++r) qsum[r] = __shfl(qsum_part, 4 * g + r, WAVE);
-  }
-  // zero the p~ tiles once so rows >= G stay zero
+    for (int r = 0; r < 4; ++r) qsum[rt][r] = 0.f;
+    if constexpr (I8) {
+      qsum_part += shfl_xor(qsum_part, 16);
+      qsum_part += shfl_xor(qsum_part, 32);   // every lane: full sum of row n
 #pragma unroll
-  for (int u = 0; u < CH; ++u) reinterpret_cast<uint2*>(p_lds + u * 256)[lane] = make_uint2(0, 0);
+      for (int r = 0; r < 4; ++r) qsum[rt][r] = __shfl(qsum_part, 4 * g + r, WAVE);
+    }
+  }
+  // zero the p~ tiles once so rows >= nrows stay zero
+#pragma unroll
+  for (int u = 0; u < CH * RT; ++u) reinterpret_cast<uint2*>(p_lds + u * 256)[lane] = make_uint2(0, 0);
 
-  const bool row_ok[4] = {4 * g + 0 < G, 4 * g + 1 < G, 4 * g + 2 < G, 4 * g + 3 < G};
-  float M[4], lrun[4], psum[4];
-  float4v acc[8];
+  bool row_ok[RT][4];
+  uint32_t mrow[RT][4];  // tree: mask row of the node of each result row
 #pragma unroll
-  for (int r = 0; r < 4; ++r) { M[r] = kNegInf; lrun[r] = 0.f; psum[r] = 0.f; }
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) acc[nt] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < 4; ++r) {
+      const int R = row0 + 16 * rt + 4 * g + r;
+      row_ok[rt][r] = R < nrows;
+      mrow[rt][r] = 0u;
+      if constexpr (TREE) {
+        if (row_ok[rt][r]) mrow[rt][r] = P.tree_mask[(int64_t)s * N + R / G];
+      }
+    }
+  float M[RT][4], lrun[RT][4], psum[RT][4];
+  float4v acc[RT][8];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { M[rt][r] = kNegInf; lrun[rt][r] = 0.f; psum[rt][r] = 0.f; }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
   const int last_valid = (end - start) - (nblk - 1) * BS;
 
   auto compute = [&](const MStage<KV>& st, int b) {
     // ---- scores of every block of the stage (independent MFMA chains) ----
-    float4v sc[CH];
+    float4v sc[RT][CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      sc[u] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) sc[rt][u] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         uint32_t kb[4];
@@ -774,10 +815,12 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
           for (int w = 0; w < 4; ++w) kb[w] = st.k[u].d[4 * kc + w];
         }
         const u32x4 kbv = {kb[0], kb[1], kb[2], kb[3]};
-        sc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kc], bitcast<half8>(kbv), sc[u], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          sc[rt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][kc], bitcast<half8>(kbv), sc[rt][u], 0, 0, 0);
       }
     }
-    float sv[CH][4];
+    float sv[RT][CH][4];
     bool need = false;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
@@ -785,36 +828,44 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
       float kscale = P.scale_log2;
       if constexpr (BLK) kscale *= window_at(bw.ks, min(i, nblk - 1));
       if constexpr (REF) kscale *= st.ks[u];
-      const bool tok_ok = (i < nblk) && (start + i * BS + n) < end;
+      const int tpos = start + i * BS + n;
+      const bool tok_ok = (i < nblk) && tpos < end;
+      const int j = tpos - ctx_c;  // tree node of this token when >= 0 (< N <= 32)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float x = sc[u][r];
-        if constexpr (I8) x = fmaf(-kBias, qsum[r], x);
-        sv[u][r] = (tok_ok && row_ok[r]) ? x * kscale : kNegInf;
-        need |= sv[u][r] > M[r] + kRescaleThreshold;
-      }
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = sc[rt][u][r];
+          if constexpr (I8) x = fmaf(-kBias, qsum[rt][r], x);
+          bool ok = tok_ok && row_ok[rt][r];
+          if constexpr (TREE) ok = ok && (j < 0 || ((mrow[rt][r] >> (j & 31)) & 1u));
+          sv[rt][u][r] = ok ? x * kscale : kNegInf;
+          need |= sv[rt][u][r] > M[rt][r] + kRescaleThreshold;
+        }
     }
     // ---- lazy running max per row ----
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float m = sv[0][r];
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int u = 1; u < CH; ++u) m = fmaxf(m, sv[u][r]);
-        m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
-        m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
-        m = fmaxf(m, dpp<DPP_ROW_HALF_MIRROR>(m));
-        m = fmaxf(m, dpp<DPP_ROW_MIRROR>(m));  // max over the 16 tokens of each block
-        const float Mn = fmaxf(M[r], m);
-        const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[r] - Mn);
-        M[r] = Mn;
-        lrun[r] *= alpha;
-        psum[r] *= alpha;
+        for (int r = 0; r < 4; ++r) {
+          float m = sv[rt][0][r];
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) acc[nt][r] *= alpha;
-      }
+          for (int u = 1; u < CH; ++u) m = fmaxf(m, sv[rt][u][r]);
+          m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
+          m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
+          m = fmaxf(m, dpp<DPP_ROW_HALF_MIRROR>(m));
+          m = fmaxf(m, dpp<DPP_ROW_MIRROR>(m));  // max over the 16 tokens of each block
+          const float Mn = fmaxf(M[rt][r], m);
+          const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[rt][r] - Mn);
+          M[rt][r] = Mn;
+          lrun[rt][r] *= alpha;
+          psum[rt][r] *= alpha;
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt) acc[rt][nt][r] *= alpha;
+        }
     }
-    // ---- p, p~ -> LDS tiles [block][head][token] ----
+    // ---- p, p~ -> LDS tiles [block][row tile][row][token] ----
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = b * CH + u;
@@ -822,19 +873,23 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
       if constexpr (BLK) vscale = window_at(bw.vs, min(i, nblk - 1));
       if constexpr (REF) vscale = st.vs[u];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = (sv[u][r] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(sv[u][r] - M[r]);
-        lrun[r] += p;
-        const uint16_t ph = f2h(p * vscale);
-        if constexpr (I8) psum[r] += h2f(ph);
-        if (row_ok[r]) p_lds[u * 256 + (4 * g + r) * 16 + n] = ph;
-      }
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = (sv[rt][u][r] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(sv[rt][u][r] - M[rt][r]);
+          lrun[rt][r] += p;
+          const uint16_t ph = f2h(p * vscale);
+          if constexpr (I8) psum[rt][r] += h2f(ph);
+          if (row_ok[rt][r]) p_lds[(u * RT + rt) * 256 + (4 * g + r) * 16 + n] = ph;
+        }
     }
     __asm__ volatile("" ::: "memory");
-    half4 pa[CH];
+    half4 pa[RT][CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u)
-      pa[u] = bitcast<half4>(reinterpret_cast<const uint2*>(p_lds + u * 256)[n * 4 + g]);  // p~[head n][tokens 4g..]
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)  // p~[row n][tokens 4g..4g+3]
+        pa[rt][u] = bitcast<half4>(reinterpret_cast<const uint2*>(p_lds + (u * RT + rt) * 256)[n * 4 + g]);
     // ---- values ----
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
@@ -863,8 +918,11 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
             }
           }
           const uint2 v0 = make_uint2(b0[0], b0[1]), v1 = make_uint2(b1[0], b1[1]);
-          acc[nt0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[u], bitcast<half4>(v0), acc[nt0], 0, 0, 0);
-          acc[nt1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[u], bitcast<half4>(v1), acc[nt1], 0, 0, 0);
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            acc[rt][nt0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[rt][u], bitcast<half4>(v0), acc[rt][nt0], 0, 0, 0);
+            acc[rt][nt1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[rt][u], bitcast<half4>(v1), acc[rt][nt1], 0, 0, 0);
+          }
         }
       }
     }
@@ -895,38 +953,38 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
     }
   }
 
-  // ---- partials: row (head) 4g+r, dims 8n..8n+7 ----
-  const int64_t hrow0 = (int64_t)s * H + (int64_t)kvh * G;
+  // ---- partials: row 16 rt + 4g + r, dims 8n..8n+7 ----
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float l = lrun[r], ps = psum[r];
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int k = 0; k < 1; ++k) {
+    for (int r = 0; r < 4; ++r) {
+      float l = lrun[rt][r], ps = psum[rt][r];
       l += dpp<DPP_QUAD_XOR1>(l); l += dpp<DPP_QUAD_XOR2>(l);
       l += dpp<DPP_ROW_HALF_MIRROR>(l); l += dpp<DPP_ROW_MIRROR>(l);
       if constexpr (I8) {
         ps += dpp<DPP_QUAD_XOR1>(ps); ps += dpp<DPP_QUAD_XOR2>(ps);
         ps += dpp<DPP_ROW_HALF_MIRROR>(ps); ps += dpp<DPP_ROW_MIRROR>(ps);
       }
-    }
-    if (row_ok[r]) {
-      float o[8];
+      if (row_ok[rt][r]) {
+        const int64_t orow = out_row(row0 + 16 * rt + 4 * g + r);
+        float o[8];
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, ps, acc[nt][r]) : acc[nt][r];
-      if (nparts == 1) {
-        const float inv = 1.f / l;
-        float4* dst = reinterpret_cast<float4*>(P.out + (hrow0 + 4 * g + r) * HD + 8 * n);
-        dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-        dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
-      } else {
-        const int64_t pr = (hrow0 + 4 * g + r) * P.max_parts + part;
-        float4* dst = reinterpret_cast<float4*>(P.part_acc + pr * HD + 8 * n);
-        dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_float4(o[4], o[5], o[6], o[7]);
-        if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(M[r], l);
+        for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, ps, acc[rt][nt][r]) : acc[rt][nt][r];
+        if (nparts == 1) {
+          // a tree row that sees no token attends to nothing: zeros
+          const float inv = TREE ? (l > 0.f ? 1.f / l : 0.f) : 1.f / l;
+          float4* dst = reinterpret_cast<float4*>(P.out + orow * HD + 8 * n);
+          dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+          dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+        } else {
+          const int64_t pr = orow * P.max_parts + part;
+          float4* dst = reinterpret_cast<float4*>(P.part_acc + pr * HD + 8 * n);
+          dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+          dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+          if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(M[rt][r], l);
+        }
       }
     }
-  }
 }
 
 // Combine the partitions of one (sequence, head):
@@ -937,9 +995,9 @@ DEV void decode_unit_mfma(const DecodeParams& P) {
 __device__ void decode_merge(const MergeParams& P) {
   const int lane = lane_id();
   const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
-  if (r >= P.n_seqs * P.n_heads) return;
-  const int s = r / P.n_heads;
-  const int ctx = max(0, min(P.context_lens[s], P.max_parts * P.part_tokens));
+  if (r >= P.n_rows) return;
+  const int s = r / P.rows_per_seq;
+  const int ctx = min(max(0, P.context_lens[s]) + P.extra_tokens, P.cap_tokens);
   const int np = (ctx + P.part_tokens - 1) / P.part_tokens;
   if (np <= 1) return;
   const float2* ml = reinterpret_cast<const float2*>(P.part_ml) + (int64_t)r * P.max_parts;
@@ -1230,10 +1288,20 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
 #define VK_DECODE_MFMA(KV, G)                                                       \
   extern "C" __global__ void __launch_bounds__(64)                                  \
       vk_decode_mfma_kv##KV##_g##G(const DecodeParams P) {                          \
-    decode_unit_mfma<KV, G>(P);                                                     \
+    attn_unit_mfma<KV, G, 1, false>(P);                                             \
   }
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
 VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
+
+// Tree verify: RT tiles of 16 (node, head) rows per wave.
+#define VK_TREE(KV, G, RT, QT)                                                      \
+  extern "C" __global__ void __launch_bounds__(64)                                  \
+      vk_tree_kv##KV##_g##G##_r##RT##_q##QT(const DecodeParams P) {                 \
+    attn_unit_mfma<KV, G, RT, true, QT>(P);                                         \
+  }
+#define VK_TREE_G(KV, RT, QT) VK_TREE(KV, 1, RT, QT) VK_TREE(KV, 2, RT, QT) VK_TREE(KV, 4, RT, QT) VK_TREE(KV, 8, RT, QT)
+#define VK_TREE_KV(KV) VK_TREE_G(KV, 1, 0) VK_TREE_G(KV, 1, 1) VK_TREE_G(KV, 2, 0) VK_TREE_G(KV, 2, 1)
+VK_TREE_KV(1) VK_TREE_KV(2) VK_TREE_KV(3)
 
 
 #define VK_APPEND(KV) \

@@ -38,18 +38,23 @@ struct SlotMapParams {
   int32_t bt_stride, block_size, n_tok, n_blocks;
 };
 
+// Paged attention over a block table. Decode: one query row per (sequence,
+// head). Tree verify: n_nodes query rows per (sequence, head); node j's K/V sit
+// at position context_len + j and row i sees them where bit j of tree_mask[s][i]
+// is set (every row sees positions < context_len).
 struct DecodeParams {
   const uint8_t* kc;        // K codes of the layer
   const uint8_t* vc;        // V codes of the layer
   const uint8_t* ks;        // K scales of the layer (or null)
   const uint8_t* vs;        // V scales
-  const void* q;            // [S][H][D]
-  float* out;               // [S][H][D]
-  float* part_acc;          // [S][H][max_parts][D]
-  float* part_ml;           // [S][H][max_parts][2] (running max in log2 units, sum)
+  const void* q;            // [S][N][H][D]
+  float* out;               // [S][N][H][D]
+  float* part_acc;          // [S][N][H][max_parts][D]
+  float* part_ml;           // [S][N][H][max_parts][2] (running max in log2 units, sum)
   const int32_t* block_tables;
   const int32_t* seq_rows;
   const int32_t* context_lens;
+  const uint32_t* tree_mask;// [S][N] (tree kernels only)
   uint32_t tile_bytes;
   uint32_t stile_bytes;
   int32_t bt_stride;
@@ -57,26 +62,10 @@ struct DecodeParams {
   int32_t n_seqs, n_heads, n_kv_heads, n_blocks;
   int32_t max_parts;        // partitions per sequence in the grid
   int32_t part_tokens;      // tokens per partition (multiple of the block size)
+  int32_t cap_tokens;       // tokens a table row can address: min(max_parts*part_tokens, bt_stride*bs)
+  int32_t n_nodes;          // query rows per (sequence, head): 1 for decode
+  int32_t n_rgroups;        // row groups per (sequence, KV head) in the grid (tree kernels)
   float scale_log2;         // softmax scale * log2(e)
-};
-
-
-struct TreeParams {
-  const uint8_t* kc;
-  const uint8_t* vc;
-  const uint8_t* ks;
-  const uint8_t* vs;
-  const void* q;            // [S][N][H][D]
-  float* out;               // [S][N][H][D]
-  const int32_t* block_tables;
-  const int32_t* seq_rows;
-  const int32_t* context_lens;
-  const uint32_t* tree_mask;// [S][N]
-  uint32_t tile_bytes;
-  uint32_t stile_bytes;
-  int32_t bt_stride;
-  int32_t n_seqs, n_nodes, n_heads, n_kv_heads, n_blocks;
-  float scale_log2;
 };
 
 constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)
@@ -92,7 +81,10 @@ struct MergeParams {
   const float* part_ml;
   const int32_t* context_lens;
   float* out;
-  int32_t n_seqs, n_heads, max_parts, part_tokens;
+  int32_t n_rows;           // output rows: S * rows_per_seq
+  int32_t rows_per_seq;     // n_nodes * n_heads
+  int32_t extra_tokens;     // tokens after context_len (tree nodes), 0 for decode
+  int32_t max_parts, part_tokens, cap_tokens;
 };
 
 struct FillParams {

@@ -16,3 +16,4 @@ from .runtime import (  # noqa: F401
     BlockManager, Context, DeviceBuffer, Event, HipMemoryRuntime, KvCacheType, MemoryRuntimeConfig, Pool,
     SlotPool, Stream, kv_bytes_per_token_per_head,
 )
+from .tree import SpeculativeTree, TreeNode, TreeVerifyResult, branching_tree  # noqa: F401

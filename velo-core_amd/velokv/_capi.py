@@ -72,7 +72,8 @@ class TreeArgs(C.Structure):
                 ("block_tables", C.c_void_p), ("bt_stride", C.c_int32), ("seq_rows", C.c_void_p),
                 ("context_lens", C.c_void_p), ("tree_mask", C.c_void_p), ("n_seqs", C.c_int32),
                 ("n_nodes", C.c_int32), ("n_heads", C.c_int32), ("max_context_len", C.c_int32),
-                ("scale", C.c_float)]
+                ("scale", C.c_float), ("partition_tokens", C.c_int32), ("workspace", C.c_void_p),
+                ("workspace_bytes", C.c_uint64)]
 
 
 P = C.c_void_p
@@ -101,7 +102,9 @@ PROTOTYPES = {
     "vk_append": [P, P, I32, P, P, I32, P, I32, P],
     "vk_paged_decode_workspace": [P, C.POINTER(DecodeArgs), C.POINTER(U64)],
     "vk_paged_decode": [P, P, C.POINTER(DecodeArgs), P],
+    "vk_tree_verify_workspace": [P, C.POINTER(TreeArgs), C.POINTER(U64)],
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
+    "vk_tree_mask": [PI32, I32, PU32],
     "vk_copy_blocks": [P, P, PI32, I32, P],
     "vk_bm_create": [I32, I32, PP],
     "vk_bm_destroy": [P],

@@ -128,10 +128,20 @@ class Context:
 
     def tree_verify(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, tree_mask, n_seqs: int,
                     n_nodes: int, n_heads: int, max_context_len: int, block_tables=None, bt_stride: int = 0,
-                    seq_rows=None, scale: float = 0.0, stream=None):
+                    seq_rows=None, scale: float = 0.0, partition_tokens: int = 0, workspace=None,
+                    workspace_bytes: int = 0, stream=None):
         a = _capi.TreeArgs(layer, _bptr(q), q_dtype, _bptr(out), _bptr(block_tables), bt_stride, _bptr(seq_rows),
-                           _bptr(context_lens), _bptr(tree_mask), n_seqs, n_nodes, n_heads, max_context_len, scale)
+                           _bptr(context_lens), _bptr(tree_mask), n_seqs, n_nodes, n_heads, max_context_len, scale,
+                           partition_tokens, _bptr(workspace), workspace_bytes)
         check(lib().vk_tree_verify(self.h, pool.h, C.byref(a), _sptr(stream)))
+
+    def tree_workspace_bytes(self, pool: "Pool", n_seqs, n_nodes, n_heads, max_context_len, bt_stride=0,
+                             partition_tokens=0, q_dtype=DT_F16) -> int:
+        a = _capi.TreeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None, None,
+                           n_seqs, n_nodes, n_heads, max_context_len, 0.0, partition_tokens, None, 0)
+        n = C.c_uint64()
+        check(lib().vk_tree_verify_workspace(pool.h, C.byref(a), C.byref(n)))
+        return n.value
 
     def copy_blocks(self, pool: "Pool", pairs, stream=None):
         p = np.ascontiguousarray(np.asarray(pairs, dtype=np.int32).reshape(-1))
