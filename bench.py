@@ -15,9 +15,14 @@ resident in HBM before timing starts.
 
 value        = algorithmic bytes of a step / step time (GB/s)
 tokens_per_s = 64 / step time (attention-only decode throughput, 32 layers)
-roofline     = the decode kernel (split-K partitions with the merge fused in):
-               algorithmic bytes per launch / mean launch time from HIP events
-               around every launch in the timed region, against the 8 TB/s HBM peak.
+roofline     = one vk_paged_decode call (the decode kernel and, when a sequence
+               spans several partitions, the split-K merge kernel): algorithmic
+               bytes per call / mean call time from HIP events around every call in
+               the timed region, against the 8 TB/s HBM peak.
+
+--workload tree measures configuration 4 instead: 256 sequences sharing an
+aliased 4096-token prefix, suffixes U[0, 512], copy-on-write of every partial
+last block, 8 draft tokens appended and an 8-node tree verified per layer.
 cpu_baseline = the CPU oracle (oracle/velokv_oracle.c, a C port of the
                reference's CPU attention math on the paged INT8 layout) timed on a
                bounded sample of the same workload on this host.
@@ -61,6 +66,11 @@ def parse():
                     help="decode kernel family (vk_ctx_set_decode_kernel)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--workload", choices=["decode", "tree"], default="decode",
+                    help="decode: B x ctx decode (configs 2, 3, 5 by flags); tree: configuration 4")
+    ap.add_argument("--prefix", type=int, default=4096, help="tree: shared prefix tokens")
+    ap.add_argument("--max-suffix", type=int, default=512, help="tree: suffix tokens U[0, max]")
+    ap.add_argument("--nodes", type=int, default=8, help="tree: draft-tree nodes")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one vk_copy_blocks of known size (HBM counter calibration)")
     return ap.parse_args()
@@ -216,6 +226,141 @@ def run_gpu(ctx, args, kv_name: str):
     return res
 
 
+def run_tree(ctx, args):
+    """Configuration 4. Per step: one copy-on-write launch for the partial last
+    block of every sequence (all layers), then per layer the append of the N draft
+    tokens of every sequence and one tree-verify call."""
+    S, H, Hkv, NL, N = args.seqs, args.heads, args.kv_heads, args.layers, args.nodes
+    kv = velokv.KV_I8_BLK if args.kv == "int8" else velokv.KV_F16
+    prefix = args.prefix
+    if prefix % BS:
+        raise SystemExit("--prefix must be a multiple of the block size (16): the shared pages are whole blocks")
+    suffix = synth.rng(4).integers(0, args.max_suffix + 1, S).astype(np.int32)
+    committed = prefix + suffix
+    total = committed + N
+    pblocks = -(-prefix // BS)
+    stride = int(-(-int(total.max()) // BS))
+    # pages: shared prefix, then per sequence its own pages; a partial last committed
+    # block gets a second page (the copy-on-write source, i.e. the shared original)
+    nxt = pblocks
+    tables = np.zeros((S, stride), np.int32)
+    tables[:, :pblocks] = np.arange(pblocks, dtype=np.int32)
+    pairs = []
+    fill_tables = tables.copy()
+    for s_ in range(S):
+        own = -(-int(total[s_]) // BS) - pblocks
+        tables[s_, pblocks:pblocks + own] = np.arange(nxt, nxt + own)
+        nxt += own
+        fill_tables[s_] = tables[s_]
+        c = int(committed[s_])
+        if c % BS and c > prefix:
+            src = nxt
+            nxt += 1
+            fill_tables[s_, c // BS] = src
+            pairs.append((src, int(tables[s_, c // BS])))
+    n_blocks = nxt
+    perm = synth.rng(5).permutation(n_blocks).astype(np.int32)  # scatter pages over the pool
+    tables, fill_tables = perm[tables], perm[fill_tables]
+    pairs = perm[np.array(pairs, np.int64)] if pairs else np.zeros((0, 2), np.int32)
+    pool = velokv.Pool(ctx, NL, n_blocks, BS, Hkv, HD, kv)
+
+    # ---- fill: prefix once through sequence 0's row, then every suffix ----
+    outlier = 8.0 if kv == velokv.KV_I8_BLK else 1.0
+    rows = np.concatenate([np.zeros(prefix, np.int64)] + [np.full(int(x), i) for i, x in enumerate(suffix)])
+    pos = np.concatenate([np.arange(prefix)] + [np.arange(prefix, int(c)) for c in committed])
+    fill_slots = ctx.upload(synth.slots_for_positions(fill_tables, pos, BS, rows))
+    n_fill = len(pos)
+    kbuf, vbuf = ctx.alloc(n_fill * Hkv * HD * 2), ctx.alloc(n_fill * Hkv * HD * 2)
+    for layer in range(NL):
+        ctx.fill_normal_f16(kbuf, n_fill * Hkv * HD, 3000 + 2 * layer, Hkv * HD, outlier)
+        ctx.fill_normal_f16(vbuf, n_fill * Hkv * HD, 3001 + 2 * layer, Hkv * HD, outlier)
+        ctx.append(pool, layer, kbuf, vbuf, velokv.DT_F16, fill_slots, n_fill)
+    ctx.sync()
+    kbuf.free()
+    vbuf.free()
+
+    dpos = (committed[:, None] + np.arange(N)[None, :]).reshape(-1)
+    draft_slots = ctx.upload(synth.slots_for_positions(tables, dpos, BS, np.repeat(np.arange(S), N)))
+    mask = np.tile(velokv.branching_tree([2, 2, 2, 2, 2], N).ancestor_mask(), S)
+    R = 2
+    qs, ks, vs = [], [], []
+    for r in range(R):
+        q = ctx.alloc(S * N * H * HD * 2)
+        ctx.fill_normal_f16(q, S * N * H * HD, 7100 + r, H * HD)
+        k = ctx.alloc(S * N * Hkv * HD * 2)
+        ctx.fill_normal_f16(k, S * N * Hkv * HD, 8100 + r, Hkv * HD, outlier)
+        v = ctx.alloc(S * N * Hkv * HD * 2)
+        ctx.fill_normal_f16(v, S * N * Hkv * HD, 9100 + r, Hkv * HD, outlier)
+        qs.append(q); ks.append(k); vs.append(v)
+    out = ctx.alloc(S * N * H * HD * 4)
+    d_committed, d_mask, d_bt = ctx.upload(committed), ctx.upload(mask.astype(np.uint32)), ctx.upload(tables)
+    stream = velokv.Stream(ctx)
+
+    def step(i, evs=None):
+        r = i % R
+        if len(pairs):
+            ctx.copy_blocks(pool, pairs, stream=stream)
+        for layer in range(NL):
+            ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, draft_slots, S * N, stream=stream)
+            if evs is not None:
+                evs[layer][0].record(stream)
+            ctx.tree_verify(pool, layer, qs[r], velokv.DT_F16, out, d_committed, d_mask, S, N, H,
+                            int(committed.max()), block_tables=d_bt, bt_stride=stride,
+                            partition_tokens=args.partition, stream=stream)
+            if evs is not None:
+                evs[layer][1].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    stream.sync()
+    start, end = velokv.Event(ctx), velokv.Event(ctx)
+    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
+    start.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    end.record(stream)
+    stream.sync()
+    total_ms = start.elapsed_ms(end)
+    tv_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
+
+    esz = 1 if kv == velokv.KV_I8_BLK else 2
+    sc = 2 if kv == velokv.KV_I8_BLK else 0
+    tile = BS * HD * esz
+    uniq_tok = prefix + int((total - prefix).sum())
+    uniq_blk = pblocks + int(sum(-(-int(t) // BS) - pblocks for t in total))
+    logical_tok = int(total.sum())
+    logical_blk = int(sum(-(-int(t) // BS) for t in total))
+    qo = S * N * H * HD * (2 + 4) + S * N * 4 + S * 4 + logical_blk * 4
+    uniq = 2 * uniq_tok * Hkv * HD * esz + 2 * uniq_blk * Hkv * sc + qo
+    logical = 2 * logical_tok * Hkv * HD * esz + 2 * logical_blk * Hkv * sc + qo
+    G = H // Hkv
+    rows = -(-N * G // 16) * 16
+    flops = 4 * rows * HD * logical_tok * Hkv  # QK and PV over every visible-or-not row of each unit
+    cow_bytes = 2 * len(pairs) * NL * 2 * Hkv * (tile + sc)
+    step_bytes = cow_bytes + NL * (uniq + append_bytes(kv, S * N, Hkv))
+    ms_step = total_ms / args.steps
+    tv_mean = float(np.mean(tv_ms))
+    ach = uniq / (tv_mean * 1e-3) / 1e9
+    rt = 2 if N * G > 16 else 1
+    kname = "vk_tree_kv%d_g%d_r%d_q1" % (kv, G, rt)
+    return {
+        "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
+        "ms_per_step": round(ms_step, 4),
+        "tokens_per_s": round(S / (ms_step * 1e-3), 1),
+        "draft_tokens_per_s": round(S * N / (ms_step * 1e-3), 1),
+        "unique_bytes_per_launch": uniq, "logical_bytes_per_launch": logical, "cow_pairs": int(len(pairs)),
+        "logical_gbs": round(logical / (tv_mean * 1e-3) / 1e9, 2),
+        "mfma_tflops": round(flops / (tv_mean * 1e-3) / 1e12, 2),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
+                     "launch_ms_mean": round(tv_mean, 5), "launch_ms_min": round(float(np.min(tv_ms)), 5),
+                     "launches": len(tv_ms)},
+        "pool_gb": round(pool.nbytes / 1e9, 2),
+        "workload": "S=%d, prefix %d (aliased), suffix U[0,%d], %d-node tree, H=%d/Hkv=%d, %s KV, %d layers" %
+                    (S, prefix, args.max_suffix, N, H, Hkv, args.kv, NL),
+    }
+
+
 def cpu_baseline(args):
     """The oracle's paged INT8 decode (llama_cpu.rs math on the paged layout) on a
     bounded sample: 4 sequences x 8192 context x 32 heads, one layer."""
@@ -270,12 +415,25 @@ def cpu_baseline(args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
-              "(single-GPU KV hot path, see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build is the "
+              "single-GPU KV-cache hot path (no collectives)", file=sys.stderr)
         sys.exit(2)
     ctx = velokv.Context(0)
     ctx.set_decode_kernel({"auto": velokv.DECODE_AUTO, "mfma": velokv.DECODE_MFMA,
                            "valu": velokv.DECODE_VALU}[args.decode])
+    if args.workload == "tree":
+        if args.seqs == 64 and "--seqs" not in sys.argv:
+            args.seqs = 256
+        t = run_tree(ctx, args)
+        print(json.dumps({
+            "metric": "tree-verify attention GB/s (unique bytes) + tokens/s, configuration 4",
+            "value": t["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": t["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "i8" if args.kv == "int8" else "f16", "data": "synthetic",
+            "config": {"workload": t["workload"], "global_batch": args.seqs, "seq_len": args.prefix,
+                       "parallelism": "single GPU"},
+            "tokens_per_s": t["tokens_per_s"], "roofline": t["roofline"], "cpu_baseline": None, "detail": t}))
+        return
     head = run_gpu(ctx, args, args.kv)
     also = None
     if args.also != "none" and args.also != args.kv:
@@ -288,7 +446,7 @@ def main():
         "metric": "paged decode-attn achieved HBM GB/s (% peak) + tokens/s, B=64 ctx=8k, fp16/INT8 KV",
         "value": head["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "i8 KV codes, f16 dot2, f32 accumulate" if args.kv == "int8" else "f16 KV, f16 dot2, f32 accumulate",
+        "dtype": "i8" if args.kv == "int8" else "f16",
         "data": "synthetic (seeded SplitMix64 normals, 1% outlier channels x8 for INT8, random block scatter)",
         "config": {"workload": workload, "global_batch": args.seqs, "seq_len": args.ctx, "parallelism": "single GPU"},
         "tokens_per_s": head["tokens_per_s"], "frac_of_peak": head["frac_of_peak"],

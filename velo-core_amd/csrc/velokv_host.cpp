@@ -625,11 +625,15 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
   if (P < 0 || P % d.block_size || P > kMaxPartTokens)
     return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
   if (P == 0) {
+    // Smallest partition with at most four units per resident wave: the tree
+    // kernels are bound by issue, not by HBM, and short partitions even out
+    // contexts of different lengths (a 4096-token prefix plus a short suffix
+    // would otherwise leave one long and one short unit per sequence).
     const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
     const int64_t pairs = std::max<int64_t>(1, (int64_t)a->n_seqs * d.n_kv_heads * pl->n_rgroups);
     P = kMaxPartTokens;
     for (int c = 256; c < kMaxPartTokens; c *= 2)
-      if (pairs * ((tokens + c - 1) / c) <= waves) { P = c; break; }
+      if (pairs * ((tokens + c - 1) / c) <= 4 * waves) { P = c; break; }
   }
   pl->part_tokens = P;
   pl->max_parts = (int32_t)std::max<int64_t>(1, (tokens + P - 1) / P);

@@ -192,15 +192,20 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
     }
   }
 }
-// Value of block i (wave-uniform) from a per-lane window array.
+// Value of block i (wave-uniform) from a per-lane window array: each window is
+// read at lane i % 64 and the window i / 64 is selected among the (scalar)
+// results, so the array stays in registers (a select over the array elements
+// themselves is turned into a dynamically indexed array in memory).
 template <typename T>
 DEV T window_at(const T (&a)[kWin], int i) {
-  const int k = i >> 6;
-  T v = a[0];
+  const int k = i >> 6, l = i & 63;
+  int v = readlane_i(bitcast<int>(a[0]), l);
 #pragma unroll
-  for (int j = 1; j < kWin; ++j) v = (k == j) ? a[j] : v;
-  if constexpr (sizeof(T) == 4 && __is_same(T, float)) return readlane_f(v, i & 63);
-  else return readlane_i(v, i & 63);
+  for (int j = 1; j < kWin; ++j) {
+    const int w = readlane_i(bitcast<int>(a[j]), l);
+    v = (k == j) ? w : v;
+  }
+  return bitcast<T>(v);
 }
 
 template <int KV>
@@ -610,24 +615,28 @@ DEV void decode_unit(const DecodeParams& P) {
 }
 
 // =============================================================================
-// Paged decode attention on the matrix cores (same unit, partials and pool layout
-// as decode_unit; fp16 q with fp16 or int8 KV).
+// Paged attention on the matrix cores: decode (one query row per head) and tree
+// verify (one row per (node, head)), with the unit, partials and pool layout of
+// decode_unit; fp16 (or fp32, rounded) q with fp16 or int8 KV.
 //
-// Scores: S[h][t] = v_mfma_f32_16x16x32_f16 over 4 chunks of 32 dims, rows = the G
-//   heads of the GQA group (zero-padded to 16), columns = the 16 tokens of a block.
-//   Lane l (n = l&15, g = l>>4) feeds q[head n][dims 32g..32g+31] and
-//   K[token n][dims 32g..32g+31]: both operands see the same dim permutation, so
+// Scores, transposed: S^T[t][r] = v_mfma_f32_16x16x32_f16(A = K block, B = q^T)
+//   over 4 chunks of 32 dims: rows = the 16 tokens of a block, columns = 16 query
+//   rows (heads of the GQA group, or (node, head) pairs, zero-padded). Lane l
+//   (n = l&15, g = l>>4) feeds K[token n][dims 32g..32g+31] and
+//   q[row n][dims 32g..32g+31]: both operands see the same dim permutation, so
 //   each lane reads 32 contiguous bytes of one token row. Lane l gets S for
-//   heads 4g..4g+3 of token n.
-// Values: out[h][d] += v_mfma_f32_16x16x16f16 per block and per 16-dim tile; the
-//   A operand is p~[head n][tokens 4g..4g+3] read back from a 16x16 fp16 tile in
-//   LDS, the B operand is V[tokens 4g..4g+3][dim 8n + tile] taken from the token
-//   pairs 2g and 2g+1 of the block (16 contiguous bytes each). Lane l gets
-//   out[heads 4g..4g+3][dims 8n..8n+7].
+//   tokens 4g..4g+3 of query row n -- exactly the A operand p[row n][tokens
+//   4g..4g+3] of the value product, so p never leaves the registers, and each
+//   lane keeps the softmax state (running max, sums) of one row.
+// Values: out[r][d] += v_mfma_f32_16x16x16f16 per block and per 16-dim tile; the
+//   B operand is V[tokens 4g..4g+3][dim 8n + tile] taken from the token pairs 2g
+//   and 2g+1 of the block (16 contiguous bytes each). Lane l gets
+//   out[rows 4g..4g+3][dims 8n..8n+7].
 // int8 codes enter the matrix cores as fp16 (1152 + c) without the subtraction;
 //   sum_d q_d (1152 + c_d) - 1152 sum_d q_d and sum_t p~_t (1152 + c_t) -
 //   1152 sum_t p~_t remove the bias exactly up to fp32 rounding.
-// The softmax bookkeeping (lazy running max, p, l) is that of decode_unit.
+// Softmax: lazy running max as in decode_unit (rescale only when a score exceeds
+//   the row's max by more than 2^4).
 // =============================================================================
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -639,8 +648,8 @@ struct MStage {
   static constexpr int CH = 2;  // blocks per pipeline stage
   DW<8 * ESZ> k[CH];     // token n, dims 32g..32g+31
   DW<4 * ESZ> v[CH][2];  // token pairs 2g, 2g+1; dims 8n..8n+7
-  float ks[CH];          // VK_KV_I8_REF: scales of token n
-  float vs[CH];
+  float4 ks[CH];         // VK_KV_I8_REF: scales of tokens 4g..4g+3
+  float4 vs[CH];
 };
 
 template <int KV>
@@ -660,8 +669,8 @@ DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, 
     if constexpr (KV == KV_I8_REF) {
       const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
       const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
-      st.ks[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(sr, n * 4, 0, 0));
-      st.vs[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(svr, n * 4, 0, 0));
+      st.ks[u] = bitcast<float4>(__builtin_amdgcn_raw_buffer_load_b128(sr, g * 16, 0, 0));
+      st.vs[u] = bitcast<float4>(__builtin_amdgcn_raw_buffer_load_b128(svr, g * 16, 0, 0));
     }
   }
 }
@@ -672,6 +681,8 @@ DEV void i8x4_to_h2x2_biased(uint32_t w, uint32_t& lo, uint32_t& hi) {
   lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
   hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
 }
+
+DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r == 2 ? v.z : v.w; }
 
 // Rows of a unit: RT tiles of 16 query rows. Row R of the (sequence, KV head)
 // pair is (node R / G, head kvh*G + R % G); decode has one node.
@@ -685,11 +696,9 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   constexpr int CH = MStage<KV>::CH;
   constexpr float kBias = 1152.0f;
 
-  __shared__ uint16_t p_lds[CH * RT * 256];  // p~[block][row tile][row][token] of one stage
-
   const int lane = lane_id();
-  const int n = lane & 15;   // token (scores) / dim group (values) / row (A operands)
-  const int g = lane >> 4;   // dim slice (scores) / row group (results) / token group (values)
+  const int n = lane & 15;   // K token (A operand) / query row (scores, p) / dim group (values)
+  const int g = lane >> 4;   // dim slice (operands) / token group (scores, p, values) / row group (results)
 
   int unit = blockIdx.x;
   int rg = 0;
@@ -724,6 +733,7 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   const int nbatch = (nblk + CH - 1) / CH;
   const int nrows = N * G;
   const int row0 = rg * 16 * RT;
+  const int plain_end = min(end, ctx_c);  // tokens below this need no validity or mask test
   // output row of row R of this (sequence, KV head) pair
   auto out_row = [&](int R) -> int64_t { return ((int64_t)s * N + R / G) * H + (int64_t)kvh * G + R % G; };
 
@@ -733,13 +743,15 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   MStage<KV> sa, sb;
   mstage_load<KV>(sa, P, bw, 0, nblk, kvh, n, g);
 
-  // q as the A operand: row n of each tile (rows >= nrows are zero), dims 32g..32g+31 in 4 chunks
+  // q^T as the B operand: row n of each tile (rows >= nrows are zero and their
+  // results are dropped), dims 32g..32g+31 in 4 chunks
   half8 qa[RT][4];
-  float qsum[RT][4];
+  float qb[RT];        // int8 KV: 1152 * sum_d q[row n][d]
+  uint32_t mrow[RT];   // tree: mask row of row n's node
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int R = row0 + 16 * rt + n;
-    float qsum_part = 0.f;
+    float qsum = 0.f;
     const int64_t qoff = out_row(R) * HD + 32 * g;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
@@ -756,49 +768,34 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
       qa[rt][kc] = bitcast<half8>(v);
       if constexpr (I8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qsum_part += (float)qa[rt][kc][j];
+        for (int j = 0; j < 8; ++j) qsum += (float)qa[rt][kc][j];
       }
     }
-    // sum over the 4 slices of each row, then fetch the 4 rows of this lane's row group
-#pragma unroll
-    for (int r = 0; r < 4; ++r) qsum[rt][r] = 0.f;
+    qb[rt] = 0.f;
     if constexpr (I8) {
-      qsum_part += shfl_xor(qsum_part, 16);
-      qsum_part += shfl_xor(qsum_part, 32);   // every lane: full sum of row n
-#pragma unroll
-      for (int r = 0; r < 4; ++r) qsum[rt][r] = __shfl(qsum_part, 4 * g + r, WAVE);
+      qsum += shfl_xor(qsum, 16);
+      qsum += shfl_xor(qsum, 32);   // full sum of row n
+      qb[rt] = kBias * qsum;
+    }
+    mrow[rt] = 0u;
+    if constexpr (TREE) {
+      if (R < nrows) mrow[rt] = P.tree_mask[(int64_t)s * N + R / G];
     }
   }
-  // zero the p~ tiles once so rows >= nrows stay zero
-#pragma unroll
-  for (int u = 0; u < CH * RT; ++u) reinterpret_cast<uint2*>(p_lds + u * 256)[lane] = make_uint2(0, 0);
 
-  bool row_ok[RT][4];
-  uint32_t mrow[RT][4];  // tree: mask row of the node of each result row
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int R = row0 + 16 * rt + 4 * g + r;
-      row_ok[rt][r] = R < nrows;
-      mrow[rt][r] = 0u;
-      if constexpr (TREE) {
-        if (row_ok[rt][r]) mrow[rt][r] = P.tree_mask[(int64_t)s * N + R / G];
-      }
-    }
-  float M[RT][4], lrun[RT][4], psum[RT][4];
+  float M[RT], lrun[RT], psum[RT];   // state of row n (each lane holds a quarter of the row's sums)
   float4v acc[RT][8];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) { M[rt][r] = kNegInf; lrun[rt][r] = 0.f; psum[rt][r] = 0.f; }
+    M[rt] = kNegInf; lrun[rt] = 0.f; psum[rt] = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
   const int last_valid = (end - start) - (nblk - 1) * BS;
+  const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
   auto compute = [&](const MStage<KV>& st, int b) {
-    // ---- scores of every block of the stage (independent MFMA chains) ----
+    // ---- S^T of every block of the stage (independent MFMA chains) ----
     float4v sc[RT][CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
@@ -817,79 +814,89 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
         const u32x4 kbv = {kb[0], kb[1], kb[2], kb[3]};
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
-          sc[rt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[rt][kc], bitcast<half8>(kbv), sc[rt][u], 0, 0, 0);
+          sc[rt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<half8>(kbv), qa[rt][kc], sc[rt][u], 0, 0, 0);
       }
     }
+    // ---- scaled scores (log2 units) of tokens 4g..4g+3, row n ----
     float sv[RT][CH][4];
     bool need = false;
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int i = b * CH + u;
+      const int tpos0 = start + i * BS + 4 * g;
+      // wave-uniform: every token of the block is committed context inside the partition
+      const bool plain = (i < nblk) && (start + (i + 1) * BS <= plain_end);
       float kscale = P.scale_log2;
       if constexpr (BLK) kscale *= window_at(bw.ks, min(i, nblk - 1));
-      if constexpr (REF) kscale *= st.ks[u];
-      const int tpos = start + i * BS + n;
-      const bool tok_ok = (i < nblk) && tpos < end;
-      const int j = tpos - ctx_c;  // tree node of this token when >= 0 (< N <= 32)
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float x = sc[rt][u][r];
-          if constexpr (I8) x = fmaf(-kBias, qsum[rt][r], x);
-          bool ok = tok_ok && row_ok[rt][r];
-          if constexpr (TREE) ok = ok && (j < 0 || ((mrow[rt][r] >> (j & 31)) & 1u));
-          sv[rt][u][r] = ok ? x * kscale : kNegInf;
-          need |= sv[rt][u][r] > M[rt][r] + kRescaleThreshold;
+          float ksr = kscale;
+          if constexpr (REF) ksr *= f4_at(st.ks[u], r);
+          float x = I8 ? (sc[rt][u][r] - qb[rt]) * ksr : sc[rt][u][r] * ksr;
+          if (!plain) {
+            const int tpos = tpos0 + r;
+            bool ok = (i < nblk) && tpos < end;
+            if constexpr (TREE) {
+              const int j = tpos - ctx_c;  // tree node of this token when >= 0 (< N <= 32)
+              ok = ok && (j < 0 || ((mrow[rt] >> (j & 31)) & 1u));
+            }
+            x = ok ? x : kNegInf;
+          }
+          sv[rt][u][r] = x;
+          need |= x > M[rt] + kRescaleThreshold;
         }
     }
-    // ---- lazy running max per row ----
+    // ---- lazy running max of row n ----
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
+      for (int rt = 0; rt < RT; ++rt) {
+        float m = sv[rt][0][0];
+#pragma unroll
+        for (int u = 0; u < CH; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m = fmaxf(m, sv[rt][u][r]);
+        m = fmaxf(m, shfl_xor(m, 16));
+        m = fmaxf(m, shfl_xor(m, 32));  // max over the stage's tokens of row n
+        const float Mn = fmaxf(M[rt], m);
+        const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[rt] - Mn);
+        M[rt] = Mn;
+        lrun[rt] *= alpha;
+        psum[rt] *= alpha;
+        // acc holds rows 4g..4g+3: their factors live in lanes 4g..4g+3
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float m = sv[rt][0][r];
+          const float ar = __shfl(alpha, 4 * g + r, WAVE);
 #pragma unroll
-          for (int u = 1; u < CH; ++u) m = fmaxf(m, sv[rt][u][r]);
-          m = fmaxf(m, dpp<DPP_QUAD_XOR1>(m));
-          m = fmaxf(m, dpp<DPP_QUAD_XOR2>(m));
-          m = fmaxf(m, dpp<DPP_ROW_HALF_MIRROR>(m));
-          m = fmaxf(m, dpp<DPP_ROW_MIRROR>(m));  // max over the 16 tokens of each block
-          const float Mn = fmaxf(M[rt][r], m);
-          const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[rt][r] - Mn);
-          M[rt][r] = Mn;
-          lrun[rt][r] *= alpha;
-          psum[rt][r] *= alpha;
-#pragma unroll
-          for (int nt = 0; nt < 8; ++nt) acc[rt][nt][r] *= alpha;
+          for (int nt = 0; nt < 8; ++nt) acc[rt][nt][r] *= ar;
         }
+      }
     }
-    // ---- p, p~ -> LDS tiles [block][row tile][row][token] ----
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int i = b * CH + u;
-      float vscale = 1.f;
-      if constexpr (BLK) vscale = window_at(bw.vs, min(i, nblk - 1));
-      if constexpr (REF) vscale = st.vs[u];
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = (sv[rt][u][r] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(sv[rt][u][r] - M[rt][r]);
-          lrun[rt][r] += p;
-          const uint16_t ph = f2h(p * vscale);
-          if constexpr (I8) psum[rt][r] += h2f(ph);
-          if (row_ok[rt][r]) p_lds[(u * RT + rt) * 256 + (4 * g + r) * 16 + n] = ph;
-        }
-    }
-    __asm__ volatile("" ::: "memory");
+    // ---- p = 2^(s - M), p~ = fp16(p * v_scale): the A operand of the value product ----
     half4 pa[RT][CH];
 #pragma unroll
-    for (int u = 0; u < CH; ++u)
+    for (int rt = 0; rt < RT; ++rt) {
+      const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];  // a row that has seen nothing keeps p = 0
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)  // p~[row n][tokens 4g..4g+3]
-        pa[rt][u] = bitcast<half4>(reinterpret_cast<const uint2*>(p_lds + (u * RT + rt) * 256)[n * 4 + g]);
+      for (int u = 0; u < CH; ++u) {
+        const int i = b * CH + u;
+        float vscale = 1.f;
+        if constexpr (BLK) vscale = window_at(bw.vs, min(i, nblk - 1));
+        float ph[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(sv[rt][u][r] - Ms);
+          lrun[rt] += p;
+          float vsr = vscale;
+          if constexpr (REF) vsr = f4_at(st.vs[u], r);
+          ph[r] = p * vsr;
+        }
+        const uint32_t lo = pack_h2(ph[0], ph[1]), hi = pack_h2(ph[2], ph[3]);
+        if constexpr (I8) psum[rt] = dot2(hi, bitcast<uint32_t>(ones), dot2(lo, bitcast<uint32_t>(ones), psum[rt]));
+        pa[rt][u] = bitcast<half4>(make_uint2(lo, hi));
+      }
+    }
     // ---- values ----
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
@@ -908,7 +915,7 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
             b0[0] = st.v[u][0].d[w]; b1[0] = st.v[u][0].d[w + 1];
             b0[1] = st.v[u][1].d[w]; b1[1] = st.v[u][1].d[w + 1];
             nt0 = w; nt1 = w + 1;
-            if (partial) {
+            if (partial) {  // fp16 bytes past the context may be anything, NaN included
 #pragma unroll
               for (int r = 0; r < 2; ++r) {
                 const int t0 = 4 * g + 2 * r;
@@ -926,11 +933,12 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
         }
       }
     }
-    __asm__ volatile("" ::: "memory");
   };
 
-  if constexpr (I8) {
-    // three-stage pipeline: two stages in flight while one is consumed
+  if constexpr (I8 && !TREE) {
+    // three-stage pipeline: two stages in flight while one is consumed (the tree
+    // kernels read mostly cached prefix pages and keep two stages so that two
+    // waves fit per SIMD)
     MStage<KV> sc2;
     mstage_load<KV>(sb, P, bw, 1, nblk, kvh, n, g);
     for (int b = 0; b < nbatch; b += 3) {
@@ -953,26 +961,30 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
     }
   }
 
-  // ---- partials: row 16 rt + 4g + r, dims 8n..8n+7 ----
+  // ---- partials: acc rows 16 rt + 4g + r, dims 8n..8n+7 ----
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+  for (int rt = 0; rt < RT; ++rt) {
+    float l = lrun[rt], ps = psum[rt];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);     // row n
+    if constexpr (I8) {
+      ps += shfl_xor(ps, 16);
+      ps += shfl_xor(ps, 32);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float l = lrun[rt][r], ps = psum[rt][r];
-      l += dpp<DPP_QUAD_XOR1>(l); l += dpp<DPP_QUAD_XOR2>(l);
-      l += dpp<DPP_ROW_HALF_MIRROR>(l); l += dpp<DPP_ROW_MIRROR>(l);
-      if constexpr (I8) {
-        ps += dpp<DPP_QUAD_XOR1>(ps); ps += dpp<DPP_QUAD_XOR2>(ps);
-        ps += dpp<DPP_ROW_HALF_MIRROR>(ps); ps += dpp<DPP_ROW_MIRROR>(ps);
-      }
-      if (row_ok[rt][r]) {
-        const int64_t orow = out_row(row0 + 16 * rt + 4 * g + r);
+      const int src = 4 * g + r;  // the lane that holds row 4g + r's state
+      const float lr = __shfl(l, src, WAVE);
+      const float psr = I8 ? __shfl(ps, src, WAVE) : 0.f;
+      const float Mr = __shfl(M[rt], src, WAVE);
+      const int R = row0 + 16 * rt + 4 * g + r;
+      if (R < nrows) {
+        const int64_t orow = out_row(R);
         float o[8];
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, ps, acc[rt][nt][r]) : acc[rt][nt][r];
+        for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
         if (nparts == 1) {
-          // a tree row that sees no token attends to nothing: zeros
-          const float inv = TREE ? (l > 0.f ? 1.f / l : 0.f) : 1.f / l;
+          const float inv = lr > 0.f ? 1.f / lr : 0.f;  // a tree row that sees no token attends to nothing
           float4* dst = reinterpret_cast<float4*>(P.out + orow * HD + 8 * n);
           dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
           dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
@@ -981,10 +993,11 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
           float4* dst = reinterpret_cast<float4*>(P.part_acc + pr * HD + 8 * n);
           dst[0] = make_float4(o[0], o[1], o[2], o[3]);
           dst[1] = make_float4(o[4], o[5], o[6], o[7]);
-          if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(M[rt][r], l);
+          if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(Mr, lr);
         }
       }
     }
+  }
 }
 
 // Combine the partitions of one (sequence, head):
@@ -1293,15 +1306,22 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
 VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
 
-// Tree verify: RT tiles of 16 (node, head) rows per wave.
-#define VK_TREE(KV, G, RT, QT)                                                      \
-  extern "C" __global__ void __launch_bounds__(64)                                  \
+// Tree verify: RT tiles of 16 (node, head) rows per wave. Over int8 pools the
+// kernels are held to 256 registers (two waves per SIMD) without spills; the fp16
+// ones would spill, so they keep one wave per SIMD.
+#define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
+#define VK_TREE(KV, G, RT, QT, ATTR)                                                \
+  extern "C" __global__ void __launch_bounds__(64) ATTR                             \
       vk_tree_kv##KV##_g##G##_r##RT##_q##QT(const DecodeParams P) {                 \
     attn_unit_mfma<KV, G, RT, true, QT>(P);                                         \
   }
-#define VK_TREE_G(KV, RT, QT) VK_TREE(KV, 1, RT, QT) VK_TREE(KV, 2, RT, QT) VK_TREE(KV, 4, RT, QT) VK_TREE(KV, 8, RT, QT)
-#define VK_TREE_KV(KV) VK_TREE_G(KV, 1, 0) VK_TREE_G(KV, 1, 1) VK_TREE_G(KV, 2, 0) VK_TREE_G(KV, 2, 1)
-VK_TREE_KV(1) VK_TREE_KV(2) VK_TREE_KV(3)
+#define VK_TREE_G(KV, RT, QT, ATTR) \
+  VK_TREE(KV, 1, RT, QT, ATTR) VK_TREE(KV, 2, RT, QT, ATTR) VK_TREE(KV, 4, RT, QT, ATTR) VK_TREE(KV, 8, RT, QT, ATTR)
+#define VK_TREE_KV(KV, ATTR) \
+  VK_TREE_G(KV, 1, 0, ATTR) VK_TREE_G(KV, 1, 1, ATTR) VK_TREE_G(KV, 2, 0, ATTR) VK_TREE_G(KV, 2, 1, ATTR)
+VK_TREE_KV(1, )
+VK_TREE_KV(2, VK_TWO_WAVES)
+VK_TREE_KV(3, VK_TWO_WAVES)
 
 
 #define VK_APPEND(KV) \
