@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--ragged", action="store_true", help="context lengths U[1024, ctx] (configs 2/3)")
     ap.add_argument("--decode", choices=["auto", "mfma", "valu"], default="auto",
                     help="decode kernel family (vk_ctx_set_decode_kernel)")
+    ap.add_argument("--sched", choices=["auto", "split", "stream"], default="auto",
+                    help="decode work schedule (vk_ctx_set_decode_schedule)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", choices=["decode", "tree"], default="decode",
@@ -166,7 +168,7 @@ def run_gpu(ctx, args, kv_name: str):
                 evs[layer][0].record(stream)
             ctx.paged_decode(pool, layer, qs[r], velokv.DT_F16, out, d_lens, S, H, int(lens.max()),
                              block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
-                             stream=stream)
+                             stream=stream, sum_context_len=int(lens.sum()))
             if evs is not None:
                 evs[layer][1].record(stream)
 
@@ -192,9 +194,8 @@ def run_gpu(ctx, args, kv_name: str):
     step_bytes = NL * (dbytes + abytes)
     dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
-    kname = ("vk_decode_kv%d_g%d_q1" % (kv, H // Hkv)
-             if args.decode == "valu" or (args.decode == "auto" and kv == velokv.KV_F16)
-             else "vk_decode_mfma_kv%d_g%d" % (kv, H // Hkv))
+    kname = ctx.decode_kernel_name(pool, S, H, int(lens.max()), bt_stride=bt.shape[1],
+                                   partition_tokens=args.partition, sum_context_len=int(lens.sum()))
     res = {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
         "ms_per_step": round(ms_step, 4),
@@ -421,6 +422,8 @@ def main():
     ctx = velokv.Context(0)
     ctx.set_decode_kernel({"auto": velokv.DECODE_AUTO, "mfma": velokv.DECODE_MFMA,
                            "valu": velokv.DECODE_VALU}[args.decode])
+    ctx.set_decode_schedule({"auto": velokv.SCHED_AUTO, "split": velokv.SCHED_SPLIT,
+                             "stream": velokv.SCHED_STREAM}[args.sched])
     if args.workload == "tree":
         if args.seqs == 64 and "--seqs" not in sys.argv:
             args.seqs = 256

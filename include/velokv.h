@@ -95,6 +95,20 @@ int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
 #define VK_DECODE_MFMA 2
 int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
 
+/* Work schedule of vk_paged_decode for fp16 queries over fp16 / int8 KV when
+ * partition_tokens is 0: VK_SCHED_SPLIT (units = fixed context partitions, sized
+ * to fill one round of resident waves; kernel family per
+ * vk_ctx_set_decode_kernel), VK_SCHED_STREAM (stream-K on the matrix cores: one
+ * wave per resident slot, each taking an equal share of all (sequence, KV head)
+ * blocks, so ragged batches stay balanced) or VK_SCHED_AUTO (stream-K unless
+ * vk_decode_args.sum_context_len says the batch is uniform, or the VALU family
+ * was requested). A nonzero partition_tokens always uses fixed partitions. No
+ * reference counterpart. */
+#define VK_SCHED_AUTO 0
+#define VK_SCHED_SPLIT 1
+#define VK_SCHED_STREAM 2
+int vk_ctx_set_decode_schedule(vk_ctx* ctx, int schedule);
+
 /* ---- pools ---------------------------------------------------------------- */
 
 typedef struct vk_pool_desc {
@@ -184,10 +198,18 @@ typedef struct vk_decode_args {
                                  ctx (calls on one ctx that overlap in time must
                                  then pass their own). Needs no initialisation. */
   uint64_t workspace_bytes;
+  int64_t sum_context_len;    /* host sum of context_lens if known, else 0: with
+                                 VK_SCHED_AUTO a batch whose sum is within 3 % of
+                                 n_seqs * max_context_len runs fixed partitions,
+                                 any other (or unknown) batch runs stream-K    */
 } vk_decode_args;
 
 /* Bytes of workspace vk_paged_decode needs for these arguments. */
 int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes);
+
+/* Name of the attention kernel vk_paged_decode would launch for these arguments
+ * (for profiling and reports). No reference counterpart. */
+int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args* a, char* buf, size_t cap);
 
 /* Single-query paged decode attention for S sequences, with split-K over
  * context partitions and an online-softmax merge (a second launch, skipped

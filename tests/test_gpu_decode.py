@@ -6,20 +6,25 @@ import pytest
 
 import pyoracle as O
 import velokv
+from velokv import synth
 from cases import BS, HD, make_case, oracle_layer, tol_check
 from test_gpu_append_copy import gpu_pool
 
 pytestmark = pytest.mark.gpu
 
 KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
-IMPLS = [velokv.DECODE_MFMA, velokv.DECODE_VALU]
+IMPLS = [(velokv.DECODE_MFMA, velokv.SCHED_SPLIT), (velokv.DECODE_MFMA, velokv.SCHED_STREAM),
+         (velokv.DECODE_VALU, velokv.SCHED_SPLIT)]
 
 
-@pytest.fixture(params=IMPLS, ids=["mfma", "valu"])
+@pytest.fixture(params=IMPLS, ids=["mfma", "mfma-streamk", "valu"])
 def impl(request, ctx):
-    ctx.set_decode_kernel(request.param)
+    kind, sched = request.param
+    ctx.set_decode_kernel(kind)
+    ctx.set_decode_schedule(sched)
     yield request.param
     ctx.set_decode_kernel(velokv.DECODE_AUTO)
+    ctx.set_decode_schedule(velokv.SCHED_AUTO)
 
 
 def run_decode(ctx, pool, case, q=None, q_dtype=np.float16, partition_tokens=0, layer=0, seq_rows=None,
@@ -195,3 +200,33 @@ def test_decode_workspace_reuse_across_layouts(ctx, impl):
                              workspace=ws, workspace_bytes=(1 << 25) if ws is not None else 0)
             ctx.sync()
             check(out.download((S, 32, HD), np.float32), ref[:S], f"S={S} P={P} own_ws={ws is not None}")
+
+
+@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("shape", ["mixed", "many_small", "wide"])
+def test_decode_streamk_worker_boundaries(ctx, kv, shape):
+    """Stream-K ranges that split segments at arbitrary blocks, cross several
+    sequences, skip empty contexts, and (many_small) leave fewer blocks than
+    workers; more than 64 sequences exercise the chunked prefix scan."""
+    print(f"decode stream-K kv={kv} shape={shape}", flush=True)
+    ctx.set_decode_kernel(velokv.DECODE_MFMA)
+    ctx.set_decode_schedule(velokv.SCHED_STREAM)
+    try:
+        if shape == "mixed":
+            lens = [0, 1, 0, 5, 16, 17, 4096, 3, 0, 2049, 100, 33, 0, 1500]
+        elif shape == "many_small":
+            lens = [(i * 7) % 20 for i in range(150)]
+        else:
+            lens = list(synth.rng(9).integers(0, 3000, 130))
+        # fill every sequence with at least one token, then attend over the real lengths
+        case = make_case(kv, [max(1, int(L)) for L in lens], n_kv_heads=2, n_heads=8, seed=401, outlier_scale=8.0)
+        ref_layer = oracle_layer(case)
+        pool = gpu_pool(ctx, case)
+        case.ctx_lens = np.asarray(lens, np.int32)
+        got = run_decode(ctx, pool, case)
+        ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+        check(got, ref, f"stream-K {shape}")
+        assert np.all(got[np.asarray(lens) == 0] == 0.0)
+    finally:
+        ctx.set_decode_kernel(velokv.DECODE_AUTO)
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)

@@ -89,6 +89,7 @@ struct vk_ctx {
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
   int decode_kind = VK_DECODE_AUTO;
+  int decode_sched = VK_SCHED_AUTO;
   int n_cu = 256;
   std::unordered_map<std::string, int64_t> resident;  // kernel -> resident waves
 
@@ -111,7 +112,7 @@ struct vk_pool {
 namespace {
 
 const char* const kKernelNames[] = {
-    "vk_decode_merge", "vk_append_kv0", "vk_append_kv1", "vk_append_kv2", "vk_append_kv3",
+    "vk_decode_merge", "vk_decode_merge_sk", "vk_append_kv0", "vk_append_kv1", "vk_append_kv2", "vk_append_kv3",
     "vk_slot_mapping", "vk_copy_blocks", "vk_fill_normal_f16",
 };
 
@@ -120,6 +121,9 @@ std::string decode_name(int kv, int g, int qt) {
 }
 std::string decode_mfma_name(int kv, int g) {
   return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g);
+}
+std::string decode_sk_name(int kv, int g) {
+  return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g);
 }
 std::string tree_name(int kv, int g, int rt, int qt) {
   return "vk_tree_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_r" + std::to_string(rt) + "_q" +
@@ -203,6 +207,7 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
     for (int g : {1, 2, 4, 8}) {
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
       if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
+      if (kv != VK_KV_F32) names.push_back(decode_sk_name(kv, g));
       if (kv != VK_KV_F32)
         for (int rt : {1, 2})
           for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
@@ -238,6 +243,14 @@ extern "C" int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind) {
   if (kind != VK_DECODE_AUTO && kind != VK_DECODE_VALU && kind != VK_DECODE_MFMA)
     return fail(VK_ERR_BAD_ARG, "unknown decode kernel kind %d", kind);
   ctx->decode_kind = kind;
+  return VK_OK;
+}
+
+extern "C" int vk_ctx_set_decode_schedule(vk_ctx* ctx, int schedule) {
+  if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
+  if (schedule != VK_SCHED_AUTO && schedule != VK_SCHED_SPLIT && schedule != VK_SCHED_STREAM)
+    return fail(VK_ERR_BAD_ARG, "unknown decode schedule %d", schedule);
+  ctx->decode_sched = schedule;
   return VK_OK;
 }
 
@@ -451,19 +464,27 @@ struct DecodePlan {
   int32_t bt_rows;
   int32_t part_tokens;
   int32_t max_parts;
-  uint64_t acc_bytes, ml_bytes;
+  bool stream_k;
+  int32_t n_workers;
+  std::string kernel;
+  uint64_t acc_bytes, ml_bytes, prefix_bytes;
 };
 
-// Decode kernel for these arguments: matrix cores for fp16 queries over fp16 / int8
-// KV unless the context asks for the VALU kernel; fp32 math otherwise.
-std::string decode_kernel_name(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a) {
+// Schedule and kernel family for these arguments. fp32 queries or fp32 KV take
+// the fp32 VALU kernel with fixed partitions. Otherwise stream-K (matrix cores)
+// when requested, or under AUTO unless the batch is known to be uniform or the
+// VALU family was requested; fixed partitions run the matrix cores for int8 KV
+// and the dot2 kernel for fp16 KV under AUTO (measured faster for each).
+void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, bool* stream_k, bool* mfma) {
   const vk_pool_desc& d = pool->desc;
-  const int G = d.n_kv_heads > 0 ? a->n_heads / d.n_kv_heads : 0;
   const bool fast = a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32;
-  // AUTO: matrix cores for int8 KV; fp16 KV measured faster on the dot2 kernel
-  const bool mfma = fast && (ctx->decode_kind == VK_DECODE_MFMA ||
-                             (ctx->decode_kind == VK_DECODE_AUTO && d.kv_type != VK_KV_F16));
-  return mfma ? decode_mfma_name(d.kv_type, G) : decode_name(d.kv_type, G, a->q_dtype);
+  const int kind = ctx ? ctx->decode_kind : VK_DECODE_AUTO;
+  const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
+  const bool uniform = a->sum_context_len > 0 &&
+                       (double)a->sum_context_len >= 0.97 * (double)a->n_seqs * (double)a->max_context_len;
+  *stream_k = fast && a->partition_tokens == 0 && kind != VK_DECODE_VALU &&
+              (sched == VK_SCHED_STREAM || (sched == VK_SCHED_AUTO && !uniform));
+  *mfma = *stream_k || (fast && (kind == VK_DECODE_MFMA || (kind == VK_DECODE_AUTO && d.kv_type != VK_KV_F16)));
 }
 
 // Smallest partition (256..4096 tokens) whose units fit in one round of resident
@@ -476,7 +497,7 @@ int auto_partition(const vk_decode_args* a, const vk_pool_desc& d, int64_t resid
   return kMaxPartTokens;
 }
 
-int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl, int64_t resident_waves = 2048) {
+int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl) {
   if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
   const vk_pool_desc& d = pool->desc;
   if (a->layer < 0 || a->layer >= d.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", a->layer);
@@ -500,7 +521,28 @@ int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl, in
   int P = a->partition_tokens;
   if (P < 0 || P % d.block_size || P > kMaxPartTokens)
     return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
-  if (P == 0) P = auto_partition(a, d, resident_waves);
+  bool mfma = false;
+  decode_choice(ctx, pool, a, &pl->stream_k, &mfma);
+  pl->acc_bytes = pl->ml_bytes = pl->prefix_bytes = 0;
+  pl->n_workers = 0;
+  if (pl->stream_k) {
+    pl->kernel = decode_sk_name(d.kv_type, G);
+    // one wave per resident slot, and at most 256 blocks (four id windows) per worker
+    const int64_t blocks_max = (int64_t)a->n_seqs * d.n_kv_heads * ((a->max_context_len + d.block_size - 1) / d.block_size);
+    const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
+    const int64_t nw = std::max<int64_t>(1, std::max(waves, (blocks_max + 255) / 256));
+    if (nw > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "grid too large");
+    pl->n_workers = (int32_t)nw;
+    pl->part_tokens = kMaxPartTokens;  // unused by the stream-K kernels
+    pl->max_parts = 1;
+    const uint64_t prow = (uint64_t)nw * 2 * G;
+    pl->acc_bytes = align_up(prow * kHD * sizeof(float), 256);
+    pl->ml_bytes = align_up(prow * 2 * sizeof(float), 256);
+    pl->prefix_bytes = align_up(((uint64_t)a->n_seqs + 1) * sizeof(int32_t), 256);
+    return VK_OK;
+  }
+  pl->kernel = mfma ? decode_mfma_name(d.kv_type, G) : decode_name(d.kv_type, G, a->q_dtype);
+  if (P == 0) P = auto_partition(a, d, ctx ? resident_waves(ctx, pl->kernel) : 2048);
   pl->part_tokens = P;
   pl->max_parts = std::max(1, (a->max_context_len + P - 1) / P);
   pl->acc_bytes = align_up((uint64_t)a->n_seqs * a->n_heads * pl->max_parts * kHD * sizeof(float), 256);
@@ -513,25 +555,32 @@ int plan_decode(const vk_pool* pool, const vk_decode_args* a, DecodePlan* pl, in
 extern "C" int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes) {
   if (!pool || !bytes || !a) return fail(VK_ERR_BAD_ARG, "null argument");
   DecodePlan pl;
-  int rc = plan_decode(pool, a, &pl, resident_waves(pool->ctx, decode_kernel_name(pool->ctx, pool, a)));
+  int rc = plan_decode(pool->ctx, pool, a, &pl);
   if (rc) return rc;
-  *bytes = pl.acc_bytes + pl.ml_bytes;
+  *bytes = pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes;
+  return VK_OK;
+}
+
+extern "C" int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args* a, char* buf, size_t cap) {
+  if (!pool || !a || !buf || cap == 0) return fail(VK_ERR_BAD_ARG, "null argument");
+  DecodePlan pl;
+  int rc = plan_decode(pool->ctx, pool, a, &pl);
+  if (rc) return rc;
+  snprintf(buf, cap, "%s", pl.kernel.c_str());
   return VK_OK;
 }
 
 extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
-  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
-  const std::string name = decode_kernel_name(ctx, pool, a);
-  const int64_t resident = resident_waves(ctx, name);
   DecodePlan pl;
-  if ((rc = plan_decode(pool, a, &pl, resident))) return rc;
+  if ((rc = plan_decode(ctx, pool, a, &pl))) return rc;
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
   uint8_t* ws = nullptr;
-  if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes, &ws))) return rc;
+  if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes, &ws)))
+    return rc;
   const vk_pool_desc& d = pool->desc;
   const PoolGeom& g = pool->geom;
   const uint8_t* L = pool->base + g.layer_stride * (uint64_t)a->layer;
@@ -546,6 +595,7 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.out = a->out;
   p.part_acc = reinterpret_cast<float*>(ws);
   p.part_ml = reinterpret_cast<float*>(ws + pl.acc_bytes);
+  p.sk_prefix = pl.stream_k ? reinterpret_cast<int32_t*>(ws + pl.acc_bytes + pl.ml_bytes) : nullptr;
   p.block_tables = pl.bt;
   p.seq_rows = a->seq_rows;
   p.context_lens = a->context_lens;
@@ -559,14 +609,15 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.n_blocks = d.n_blocks;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
-  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens, (int64_t)pl.bt_stride * d.block_size);
+  // stream-K: contexts are clamped to max_context_len, which bounds every worker's
+  // range to 256 blocks (the planner sized the grid for it)
+  p.cap_tokens = pl.stream_k ? a->max_context_len
+                             : (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens,
+                                                          (int64_t)pl.bt_stride * d.block_size);
   p.n_nodes = 1;
   p.n_rgroups = 1;
+  p.n_workers = pl.n_workers;
   p.scale_log2 = scale * 1.4426950408889634f;
-  const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
-  if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
-  if ((rc = launch(ctx, name.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
-  if (pl.max_parts == 1) return VK_OK;  // every sequence was finished by the decode kernel
 
   MergeParams m{};
   m.part_acc = p.part_acc;
@@ -579,7 +630,20 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   m.max_parts = pl.max_parts;
   m.part_tokens = pl.part_tokens;
   m.cap_tokens = p.cap_tokens;
-  return launch(ctx, "vk_decode_merge", dim3((unsigned)((m.n_rows + 3) / 4)), dim3(256), m, stream);
+  m.sk_prefix = p.sk_prefix;
+  m.n_workers = pl.n_workers;
+  m.n_kv_heads = d.n_kv_heads;
+  m.n_seqs = a->n_seqs;
+  const dim3 merge_grid((unsigned)((m.n_rows + 3) / 4));
+  if (pl.stream_k) {
+    if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64), p, stream))) return rc;
+    return launch(ctx, "vk_decode_merge_sk", merge_grid, dim3(256), m, stream);
+  }
+  const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
+  if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
+  if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
+  if (pl.max_parts == 1) return VK_OK;  // every sequence was finished by the decode kernel
+  return launch(ctx, "vk_decode_merge", merge_grid, dim3(256), m, stream);
 }
 
 namespace {

@@ -687,8 +687,13 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 // Rows of a unit: RT tiles of 16 query rows. Row R of the (sequence, KV head)
 // pair is (node R / G, head kvh*G + R % G); decode has one node.
 // An fp32 q (QT == DT_F32) is rounded to fp16 for the matrix cores.
-template <int KV, int G, int RT, bool TREE, int QT = DT_F16>
-DEV void attn_unit_mfma(const DecodeParams& P) {
+// One piece of work: tokens [start, end) of (sequence s, KV head kvh), row group
+// rg, committed context ctx_c. direct: the piece is the whole context and writes
+// normalised rows; otherwise it writes the unnormalised partial (acc, M, l) of
+// row R at index TREE ? out_row(R) * max_parts + pbase : pbase + R * pstride.
+template <int KV, int G, int RT, bool TREE, int QT>
+DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
+                    int64_t pbase, int pstride) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr bool I8 = (ESZ == 1);
   constexpr bool BLK = (KV == KV_I8_BLK);
@@ -699,31 +704,7 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   const int lane = lane_id();
   const int n = lane & 15;   // K token (A operand) / query row (scores, p) / dim group (values)
   const int g = lane >> 4;   // dim slice (operands) / token group (scores, p, values) / row group (results)
-
-  int unit = blockIdx.x;
-  int rg = 0;
-  if constexpr (TREE) {
-    rg = unit % P.n_rgroups;
-    unit /= P.n_rgroups;
-  }
-  const int kvh = unit % P.n_kv_heads;
-  const int rest = unit / P.n_kv_heads;
-  const int part = rest % P.max_parts;
-  const int s = rest / P.max_parts;
-  if (s >= P.n_seqs) return;
-
   const int N = TREE ? P.n_nodes : 1;
-  const int ctx_c = max(0, min(P.context_lens[s], P.cap_tokens));  // committed tokens
-  const int ctx = TREE ? min(ctx_c + N, P.cap_tokens) : ctx_c;      // committed + tree nodes
-  const int start = part * P.part_tokens;
-  if (start >= ctx) {
-    if constexpr (!TREE) {
-      if (part == 0) write_zero_rows<G>(P, s, kvh);
-    }
-    return;
-  }
-  const int end = min(start + P.part_tokens, ctx);
-  const int nparts = (ctx + P.part_tokens - 1) / P.part_tokens;
   int row = P.seq_rows ? P.seq_rows[s] : s;
   if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
   const int32_t* bt = P.block_tables + (int64_t)row * P.bt_stride;
@@ -983,13 +964,13 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
         float o[8];
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
-        if (nparts == 1) {
+        if (direct) {
           const float inv = lr > 0.f ? 1.f / lr : 0.f;  // a tree row that sees no token attends to nothing
           float4* dst = reinterpret_cast<float4*>(P.out + orow * HD + 8 * n);
           dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
           dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
         } else {
-          const int64_t pr = orow * P.max_parts + part;
+          const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
           float4* dst = reinterpret_cast<float4*>(P.part_acc + pr * HD + 8 * n);
           dst[0] = make_float4(o[0], o[1], o[2], o[3]);
           dst[1] = make_float4(o[4], o[5], o[6], o[7]);
@@ -1000,30 +981,152 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   }
 }
 
+// Split-K entry: unit = (row group, KV head, partition, sequence), kv head
+// fastest. Partitions that start past the context exit; an empty decode context
+// writes zero rows.
+template <int KV, int G, int RT, bool TREE, int QT = DT_F16>
+DEV void attn_unit_mfma(const DecodeParams& P) {
+  int unit = blockIdx.x;
+  int rg = 0;
+  if constexpr (TREE) {
+    rg = unit % P.n_rgroups;
+    unit /= P.n_rgroups;
+  }
+  const int kvh = unit % P.n_kv_heads;
+  const int rest = unit / P.n_kv_heads;
+  const int part = rest % P.max_parts;
+  const int s = rest / P.max_parts;
+  if (s >= P.n_seqs) return;
+  const int N = TREE ? P.n_nodes : 1;
+  const int ctx_c = max(0, min(P.context_lens[s], P.cap_tokens));  // committed tokens
+  const int ctx = TREE ? min(ctx_c + N, P.cap_tokens) : ctx_c;      // committed + tree nodes
+  const int start = part * P.part_tokens;
+  if (start >= ctx) {
+    if constexpr (!TREE) {
+      if (part == 0) write_zero_rows<G>(P, s, kvh);
+    }
+    return;
+  }
+  const int end = min(start + P.part_tokens, ctx);
+  const int nparts = (ctx + P.part_tokens - 1) / P.part_tokens;
+  const int64_t pbase = TREE ? part : ((int64_t)s * P.n_heads + (int64_t)kvh * G) * P.max_parts + part;
+  attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1, pbase, P.max_parts);
+}
+
+// ---- stream-K decode -------------------------------------------------------
+// The blocks of all (sequence, KV head) segments in order form one range of
+// W = sum_s Hkv * ceil(ctx_s / 16) blocks; worker w (one wave) takes
+// [w W / nw, (w + 1) W / nw), nw = min(workers, W). A segment inside one worker's range is written
+// directly; a split segment leaves one partial per worker: slot 1 for the worker
+// where it starts, slot 0 for the workers that continue it. vk_decode_merge_sk
+// combines them. Worker 0 also stores the per-sequence block prefix and W for
+// the merge.
+DEV int wave_sum_i(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_HALF_MIRROR, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, DPP_ROW_MIRROR, 0xF, 0xF, false);
+  x += __shfl_xor(x, 16, WAVE);
+  x += __shfl_xor(x, 32, WAVE);
+  return x;
+}
+DEV int wave_incl_scan_i(int x) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < WAVE; d <<= 1) {
+    const int y = __shfl_up(x, d, WAVE);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+DEV int seq_blocks(const DecodeParams& P, int s) {
+  return (max(0, min(P.context_lens[s], P.cap_tokens)) + BS - 1) / BS;
+}
+// first worker whose range holds global block x: b(w) <= x < b(w + 1), b(w) = w W / nw
+DEV int sk_worker_of(int64_t x, int64_t W, int nw) { return (int)(((x + 1) * nw + W - 1) / W) - 1; }
+
+template <int KV, int G>
+DEV void attn_streamk_mfma(const DecodeParams& P) {
+  const int lane = lane_id();
+  const int w = blockIdx.x;
+  const int nw = P.n_workers;
+  const int S = P.n_seqs, Hkv = P.n_kv_heads;
+  int W = 0;
+  for (int b = 0; b < S; b += WAVE) {
+    const int s = b + lane;
+    W += wave_sum_i(s < S ? Hkv * seq_blocks(P, s) : 0);
+  }
+  if (w == 0) {  // block prefix per sequence for the merge
+    int off = 0;
+    for (int b = 0; b < S; b += WAVE) {
+      const int s = b + lane;
+      const int nb = s < S ? Hkv * seq_blocks(P, s) : 0;
+      const int incl = wave_incl_scan_i(nb);
+      if (s < S) P.sk_prefix[s] = off + incl - nb;
+      off += readlane_i(incl, WAVE - 1);
+    }
+    if (lane == 0) P.sk_prefix[S] = W;
+  }
+  const int nwe = min(nw, W);  // workers with work: every range holds at least one block
+  if (w >= nwe) return;
+  const int64_t b0 = (int64_t)w * W / nwe, b1 = (int64_t)(w + 1) * W / nwe;
+  // the sequence holding block b0 and its first global block
+  int s = -1, pre = 0;
+  {
+    int off = 0;
+    for (int b = 0; b < S && s < 0; b += WAVE) {
+      const int sl = b + lane;
+      const int nb = sl < S ? Hkv * seq_blocks(P, sl) : 0;
+      const int incl = wave_incl_scan_i(nb);
+      const uint64_t m = __builtin_amdgcn_ballot_w64(off + incl > b0);
+      if (m != 0) {
+        const int l = __builtin_ctzll(m);
+        s = b + l;
+        pre = off + readlane_i(incl - nb, l);
+      }
+      off += readlane_i(incl, WAVE - 1);
+    }
+  }
+  int64_t x = b0;
+  while (x < b1 && s < S) {
+    const int ctx_s = max(0, min(P.context_lens[s], P.cap_tokens));
+    const int nb = (ctx_s + BS - 1) / BS;
+    if (nb == 0) { ++s; continue; }
+    const int rel = (int)(x - pre);
+    const int kvh = rel / nb;
+    const int o0 = rel - kvh * nb;
+    const int o1 = (int)min((int64_t)nb, (int64_t)o0 + (b1 - x));
+    const int slot = o0 > 0 ? 0 : 1;
+    attn_piece<KV, G, 1, false, DT_F16>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
+                                        ((int64_t)w * 2 + slot) * G, 1);
+    x += o1 - o0;
+    if (o1 == nb && kvh == Hkv - 1) {
+      pre += Hkv * nb;
+      ++s;
+    }
+  }
+}
+
 // Combine the partitions of one (sequence, head):
 //   out = sum_p 2^(M_p - M) acc_p / sum_p 2^(M_p - M) l_p,  M = max_p M_p.
 // One wave per (sequence, head); sequences with a single partition were
 // finished by the decode kernel itself. Partial rows are loaded 8 at a time so
 // the loads overlap.
-__device__ void decode_merge(const MergeParams& P) {
+// Combine np partials (index pr(k), k = 0..np-1) into one output row.
+template <typename PR>
+DEV void merge_row(const MergeParams& P, int64_t out_row, int np, PR pr) {
   const int lane = lane_id();
-  const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
-  if (r >= P.n_rows) return;
-  const int s = r / P.rows_per_seq;
-  const int ctx = min(max(0, P.context_lens[s]) + P.extra_tokens, P.cap_tokens);
-  const int np = (ctx + P.part_tokens - 1) / P.part_tokens;
-  if (np <= 1) return;
-  const float2* ml = reinterpret_cast<const float2*>(P.part_ml) + (int64_t)r * P.max_parts;
-  const float2* pa = reinterpret_cast<const float2*>(P.part_acc) + (int64_t)r * P.max_parts * (HD / 2);
+  const float2* ml = reinterpret_cast<const float2*>(P.part_ml);
+  const float2* pa = reinterpret_cast<const float2*>(P.part_acc);
   float M = kNegInf;
-  for (int p = lane; p < np; p += WAVE) M = fmaxf(M, ml[p].x);
+  for (int p = lane; p < np; p += WAVE) M = fmaxf(M, ml[pr(p)].x);
   M = wave_max(M);
   float L = 0.f, o0 = 0.f, o1 = 0.f;
   for (int p0 = 0; p0 < np; p0 += WAVE) {
     float w = 0.f;
     if (p0 + lane < np) {
-      const float2 m = ml[p0 + lane];
-      w = __builtin_amdgcn_exp2f(m.x - M);
+      const float2 m = ml[pr(p0 + lane)];
+      w = (m.x == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m.x - M);
       L = fmaf(w, m.y, L);
     }
     const int cnt = min(WAVE, np - p0);
@@ -1031,7 +1134,7 @@ __device__ void decode_merge(const MergeParams& P) {
       float2 a[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        a[k] = (k0 + k < cnt) ? pa[(int64_t)(p0 + k0 + k) * (HD / 2) + lane] : make_float2(0.f, 0.f);
+        a[k] = (k0 + k < cnt) ? pa[pr(p0 + k0 + k) * (HD / 2) + lane] : make_float2(0.f, 0.f);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const float wk = readlane_f(w, min(k0 + k, cnt - 1));
@@ -1044,7 +1147,49 @@ __device__ void decode_merge(const MergeParams& P) {
   }
   L = wave_sum(L);
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  reinterpret_cast<float2*>(P.out)[(int64_t)r * (HD / 2) + lane] = make_float2(o0 * inv, o1 * inv);
+  reinterpret_cast<float2*>(P.out)[out_row * (HD / 2) + lane] = make_float2(o0 * inv, o1 * inv);
+}
+
+// Split-K merge: one wave per (sequence, row) with partials [row][max_parts]:
+//   out = sum_p 2^(M_p - M) acc_p / sum_p 2^(M_p - M) l_p,  M = max_p M_p.
+// Rows whose context fits one partition were finished by the attention kernel.
+__device__ void decode_merge(const MergeParams& P) {
+  const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
+  if (r >= P.n_rows) return;
+  const int s = r / P.rows_per_seq;
+  const int ctx = min(max(0, P.context_lens[s]) + P.extra_tokens, P.cap_tokens);
+  const int np = (ctx + P.part_tokens - 1) / P.part_tokens;
+  if (np <= 1) return;
+  const int64_t base = (int64_t)r * P.max_parts;
+  merge_row(P, r, np, [&](int k) -> int64_t { return base + k; });
+}
+
+// Stream-K merge: one wave per (sequence, head). The segment (s, kvh) covers
+// global blocks [S0, S1); workers w_lo..w_hi touched it: w_lo left slot 1, the
+// others slot 0. Unsplit segments were written by their worker; empty contexts
+// get zeros.
+__device__ void decode_merge_sk(const MergeParams& P) {
+  const int lane = lane_id();
+  const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
+  if (r >= P.n_rows) return;
+  const int H = P.rows_per_seq;
+  const int s = r / H, h = r - s * H;
+  const int G = H / P.n_kv_heads;
+  const int kvh = h / G, gi = h - kvh * G;
+  const int nb = (max(0, min(P.context_lens[s], P.cap_tokens)) + BS - 1) / BS;
+  if (nb == 0) {
+    reinterpret_cast<float2*>(P.out)[(int64_t)r * (HD / 2) + lane] = make_float2(0.f, 0.f);
+    return;
+  }
+  const int64_t W = P.sk_prefix[P.n_seqs];
+  const int nwe = (int)min((int64_t)P.n_workers, W);
+  const int64_t S0 = (int64_t)P.sk_prefix[s] + (int64_t)kvh * nb;
+  const int w_lo = sk_worker_of(S0, W, nwe);
+  const int w_hi = sk_worker_of(S0 + nb - 1, W, nwe);
+  if (w_lo == w_hi) return;
+  merge_row(P, r, w_hi - w_lo + 1, [&](int k) -> int64_t {
+    return ((int64_t)(w_lo + k) * 2 + (k == 0 ? 1 : 0)) * G + gi;
+  });
 }
 
 // =============================================================================
@@ -1306,10 +1451,19 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
 VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
 
+// Two waves per SIMD (at most 256 registers).
+#define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
+#define VK_DECODE_SK(KV, G)                                                         \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
+      vk_decode_sk_kv##KV##_g##G(const DecodeParams P) {                            \
+    attn_streamk_mfma<KV, G>(P);                                                    \
+  }
+#define VK_DECODE_SK_G(KV) VK_DECODE_SK(KV, 1) VK_DECODE_SK(KV, 2) VK_DECODE_SK(KV, 4) VK_DECODE_SK(KV, 8)
+VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
+
 // Tree verify: RT tiles of 16 (node, head) rows per wave. Over int8 pools the
 // kernels are held to 256 registers (two waves per SIMD) without spills; the fp16
 // ones would spill, so they keep one wave per SIMD.
-#define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
 #define VK_TREE(KV, G, RT, QT, ATTR)                                                \
   extern "C" __global__ void __launch_bounds__(64) ATTR                             \
       vk_tree_kv##KV##_g##G##_r##RT##_q##QT(const DecodeParams P) {                 \
@@ -1332,4 +1486,5 @@ extern "C" __global__ void __launch_bounds__(256) vk_slot_mapping(const SlotMapP
 extern "C" __global__ void __launch_bounds__(256) vk_copy_blocks(const CopyParams P) { copy_blocks_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_fill_normal_f16(const FillParams P) { fill_normal_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_decode_merge(const MergeParams P) { decode_merge(P); }
+extern "C" __global__ void __launch_bounds__(256) vk_decode_merge_sk(const MergeParams P) { decode_merge_sk(P); }
 

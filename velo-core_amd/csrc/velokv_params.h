@@ -65,6 +65,8 @@ struct DecodeParams {
   int32_t cap_tokens;       // tokens a table row can address: min(max_parts*part_tokens, bt_stride*bs)
   int32_t n_nodes;          // query rows per (sequence, head): 1 for decode
   int32_t n_rgroups;        // row groups per (sequence, KV head) in the grid (tree kernels)
+  int32_t n_workers;        // stream-K: workers in the grid
+  int32_t* sk_prefix;       // stream-K: [S + 1] first global block of each sequence, then W
   float scale_log2;         // softmax scale * log2(e)
 };
 
@@ -85,6 +87,9 @@ struct MergeParams {
   int32_t rows_per_seq;     // n_nodes * n_heads
   int32_t extra_tokens;     // tokens after context_len (tree nodes), 0 for decode
   int32_t max_parts, part_tokens, cap_tokens;
+  // stream-K merge (vk_decode_merge_sk): partials indexed by (worker, slot, row of the group)
+  const int32_t* sk_prefix;
+  int32_t n_workers, n_kv_heads, n_seqs;
 };
 
 struct FillParams {

@@ -8,7 +8,7 @@ block copy) plus tree-verify attention. Every compute call goes to the gfx950
 code object through libvelokv.so.
 """
 from ._capi import (  # noqa: F401
-    DT_F16, DT_F32, DECODE_AUTO, DECODE_MFMA, DECODE_VALU, KV_F16, KV_F32, KV_I8_BLK, KV_I8_REF, VkError,
+    DT_F16, DT_F32, DECODE_AUTO, DECODE_MFMA, DECODE_VALU, SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM, KV_F16, KV_F32, KV_I8_BLK, KV_I8_REF, VkError,
     ERR_BAD_ARG, ERR_INVALID_BLOCK_SIZE, ERR_OUT_OF_PAGES, ERR_TOO_MANY_PAGES, ERR_NO_FREE_SLOTS,
     ERR_NOT_WIRED, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_UNKNOWN_HANDLE,
 )

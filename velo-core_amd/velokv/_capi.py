@@ -36,6 +36,7 @@ STATUS_NAMES = {
 # KV storage types and caller dtypes
 KV_F32, KV_F16, KV_I8_REF, KV_I8_BLK = 0, 1, 2, 3
 DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
+SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM = 0, 1, 2
 DT_F32, DT_F16 = 0, 1
 
 
@@ -64,7 +65,7 @@ class DecodeArgs(C.Structure):
                 ("block_tables", C.c_void_p), ("bt_stride", C.c_int32), ("seq_rows", C.c_void_p),
                 ("context_lens", C.c_void_p), ("n_seqs", C.c_int32), ("n_heads", C.c_int32),
                 ("max_context_len", C.c_int32), ("scale", C.c_float), ("partition_tokens", C.c_int32),
-                ("workspace", C.c_void_p), ("workspace_bytes", C.c_uint64)]
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_uint64), ("sum_context_len", C.c_int64)]
 
 
 class TreeArgs(C.Structure):
@@ -91,6 +92,7 @@ PROTOTYPES = {
     "vk_ctx_destroy": [P],
     "vk_ctx_arch": [P, C.c_char_p, C.c_size_t],
     "vk_ctx_set_decode_kernel": [P, C.c_int],
+    "vk_ctx_set_decode_schedule": [P, C.c_int],
     "vk_pool_create": [P, C.POINTER(PoolDesc), PP],
     "vk_pool_destroy": [P],
     "vk_pool_get_desc": [P, C.POINTER(PoolDesc)],
@@ -102,6 +104,7 @@ PROTOTYPES = {
     "vk_append": [P, P, I32, P, P, I32, P, I32, P],
     "vk_paged_decode_workspace": [P, C.POINTER(DecodeArgs), C.POINTER(U64)],
     "vk_paged_decode": [P, P, C.POINTER(DecodeArgs), P],
+    "vk_paged_decode_kernel": [P, C.POINTER(DecodeArgs), C.c_char_p, C.c_size_t],
     "vk_tree_verify_workspace": [P, C.POINTER(TreeArgs), C.POINTER(U64)],
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
     "vk_tree_mask": [PI32, I32, PU32],

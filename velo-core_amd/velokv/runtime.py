@@ -77,6 +77,10 @@ class Context:
         """_capi.DECODE_AUTO / DECODE_VALU / DECODE_MFMA (vk_ctx_set_decode_kernel)."""
         check(lib().vk_ctx_set_decode_kernel(self.h, kind))
 
+    def set_decode_schedule(self, schedule: int):
+        """_capi.SCHED_AUTO / SCHED_SPLIT / SCHED_STREAM (vk_ctx_set_decode_schedule)."""
+        check(lib().vk_ctx_set_decode_schedule(self.h, schedule))
+
     @property
     def arch(self) -> str:
         buf = C.create_string_buffer(64)
@@ -112,19 +116,29 @@ class Context:
 
     def paged_decode(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, n_seqs: int, n_heads: int,
                      max_context_len: int, block_tables=None, bt_stride: int = 0, seq_rows=None, scale: float = 0.0,
-                     partition_tokens: int = 0, workspace=None, workspace_bytes: int = 0, stream=None):
+                     partition_tokens: int = 0, workspace=None, workspace_bytes: int = 0, stream=None,
+                     sum_context_len: int = 0):
         a = _capi.DecodeArgs(layer, _bptr(q), q_dtype, _bptr(out), _bptr(block_tables), bt_stride, _bptr(seq_rows),
                              _bptr(context_lens), n_seqs, n_heads, max_context_len, scale, partition_tokens,
-                             _bptr(workspace), workspace_bytes)
+                             _bptr(workspace), workspace_bytes, sum_context_len)
         check(lib().vk_paged_decode(self.h, pool.h, C.byref(a), _sptr(stream)))
 
     def decode_workspace_bytes(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0,
-                               partition_tokens=0, q_dtype=DT_F16) -> int:
+                               partition_tokens=0, q_dtype=DT_F16, sum_context_len=0) -> int:
         a = _capi.DecodeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None,
-                             n_seqs, n_heads, max_context_len, 0.0, partition_tokens, None, 0)
+                             n_seqs, n_heads, max_context_len, 0.0, partition_tokens, None, 0, sum_context_len)
         n = C.c_uint64()
         check(lib().vk_paged_decode_workspace(pool.h, C.byref(a), C.byref(n)))
         return n.value
+
+    def decode_kernel_name(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0, partition_tokens=0,
+                           q_dtype=DT_F16, sum_context_len=0) -> str:
+        """The attention kernel vk_paged_decode would launch (vk_paged_decode_kernel)."""
+        a = _capi.DecodeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None,
+                             n_seqs, n_heads, max_context_len, 0.0, partition_tokens, None, 0, sum_context_len)
+        buf = C.create_string_buffer(128)
+        check(lib().vk_paged_decode_kernel(pool.h, C.byref(a), buf, 128))
+        return buf.value.decode()
 
     def tree_verify(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, tree_mask, n_seqs: int,
                     n_nodes: int, n_heads: int, max_context_len: int, block_tables=None, bt_stride: int = 0,
