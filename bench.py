@@ -22,7 +22,11 @@ roofline     = one vk_paged_decode call (the decode kernel and, when a sequence
 
 --workload tree measures configuration 4 instead: 256 sequences sharing an
 aliased 4096-token prefix, suffixes U[0, 512], copy-on-write of every partial
-last block, 8 draft tokens appended and an 8-node tree verified per layer.
+last block, 8 draft tokens appended and an 8-node tree verified per layer, then
+the accepted path of every sequence committed in all layers (vk_tree_commit).
+--workload nixl measures the NIXL handoff of KV pages: every sequence of the
+decode workload packed into wire records (vk_nixl_pack) and unpacked into
+other pages (vk_nixl_unpack), all layers.
 cpu_baseline = the CPU oracle (oracle/velokv_oracle.c, a C port of the
                reference's CPU attention math on the paged INT8 layout) timed on a
                bounded sample of the same workload on this host.
@@ -68,8 +72,9 @@ def parse():
                     help="decode work schedule (vk_ctx_set_decode_schedule)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--workload", choices=["decode", "tree"], default="decode",
-                    help="decode: B x ctx decode (configs 2, 3, 5 by flags); tree: configuration 4")
+    ap.add_argument("--workload", choices=["decode", "tree", "nixl"], default="decode",
+                    help="decode: B x ctx decode (configs 2, 3, 5 by flags); tree: configuration 4; "
+                         "nixl: pack + unpack of every sequence's KV pages in the NIXL wire format")
     ap.add_argument("--prefix", type=int, default=4096, help="tree: shared prefix tokens")
     ap.add_argument("--max-suffix", type=int, default=512, help="tree: suffix tokens U[0, max]")
     ap.add_argument("--nodes", type=int, default=8, help="tree: draft-tree nodes")
@@ -295,6 +300,16 @@ def run_tree(ctx, args):
         qs.append(q); ks.append(k); vs.append(v)
     out = ctx.alloc(S * N * H * HD * 4)
     d_committed, d_mask, d_bt = ctx.upload(committed), ctx.upload(mask.astype(np.uint32)), ctx.upload(tables)
+    # accepted path per sequence: root to node s % N (what find_best_path returns
+    # when the target agrees along that branch)
+    tree = velokv.branching_tree([2, 2, 2, 2, 2], N)
+    acc_rows = [tree.path_nodes(s_ % N) for s_ in range(S)]
+    acc = np.full((S, 32), -1, np.int32)
+    n_acc = np.array([len(a) for a in acc_rows], np.int32)
+    for s_, a in enumerate(acc_rows):
+        acc[s_, :len(a)] = a
+    d_acc, d_nacc = ctx.upload(acc), ctx.upload(n_acc)
+    moved_tok = sum(len(a) - next((d for d, x in enumerate(a) if x != d), len(a)) for a in acc_rows)
     stream = velokv.Stream(ctx)
 
     def step(i, evs=None):
@@ -310,12 +325,18 @@ def run_tree(ctx, args):
                             partition_tokens=args.partition, stream=stream)
             if evs is not None:
                 evs[layer][1].record(stream)
+        # the accepted paths move to committed + 0, 1, ... in every layer
+        if evs is not None:
+            evs[NL][0].record(stream)
+        ctx.tree_commit(pool, d_bt, stride, d_committed, d_acc, 32, d_nacc, S, stream=stream)
+        if evs is not None:
+            evs[NL][1].record(stream)
 
     for i in range(args.warmup):
         step(i)
     stream.sync()
     start, end = velokv.Event(ctx), velokv.Event(ctx)
-    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
+    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL + 1)] for _ in range(args.steps)]
     start.record(stream)
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
@@ -323,6 +344,7 @@ def run_tree(ctx, args):
     stream.sync()
     total_ms = start.elapsed_ms(end)
     tv_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
+    commit_ms = float(np.mean([evs[i][NL][0].elapsed_ms(evs[i][NL][1]) for i in range(args.steps)]))
 
     esz = 1 if kv == velokv.KV_I8_BLK else 2
     sc = 2 if kv == velokv.KV_I8_BLK else 0
@@ -338,7 +360,9 @@ def run_tree(ctx, args):
     rows = -(-N * G // 16) * 16
     flops = 4 * rows * HD * logical_tok * Hkv  # QK and PV over every visible-or-not row of each unit
     cow_bytes = 2 * len(pairs) * NL * 2 * Hkv * (tile + sc)
-    step_bytes = cow_bytes + NL * (uniq + append_bytes(kv, S * N, Hkv))
+    # commit: each moved token's K and V rows read and written once per layer
+    commit_bytes = NL * moved_tok * 2 * 2 * Hkv * (HD * esz + sc)
+    step_bytes = cow_bytes + commit_bytes + NL * (uniq + append_bytes(kv, S * N, Hkv))
     ms_step = total_ms / args.steps
     tv_mean = float(np.mean(tv_ms))
     ach = uniq / (tv_mean * 1e-3) / 1e9
@@ -350,6 +374,8 @@ def run_tree(ctx, args):
         "tokens_per_s": round(S / (ms_step * 1e-3), 1),
         "draft_tokens_per_s": round(S * N / (ms_step * 1e-3), 1),
         "unique_bytes_per_launch": uniq, "logical_bytes_per_launch": logical, "cow_pairs": int(len(pairs)),
+        "commit": {"kernel": "vk_tree_commit_kv%d" % kv, "ms_mean": round(commit_ms, 5), "layers": NL,
+                   "accepted_tokens": int(n_acc.sum()), "moved_tokens": int(moved_tok)},
         "logical_gbs": round(logical / (tv_mean * 1e-3) / 1e9, 2),
         "mfma_tflops": round(flops / (tv_mean * 1e-3) / 1e12, 2),
         "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -359,6 +385,101 @@ def run_tree(ctx, args):
         "pool_gb": round(pool.nbytes / 1e9, 2),
         "workload": "S=%d, prefix %d (aliased), suffix U[0,%d], %d-node tree, H=%d/Hkv=%d, %s KV, %d layers" %
                     (S, prefix, args.max_suffix, N, H, Hkv, args.kv, NL),
+    }
+
+
+def run_nixl(ctx, args):
+    """NIXL handoff of the decode workload's KV: one record per sequence (all
+    layers, ceil(L/16) pages) packed from the pool into a wire buffer in HBM, then
+    unpacked into a second set of pages of the same pool. Bytes per call = payload
+    read + payload written + headers."""
+    kv = velokv.KV_I8_BLK if args.kv == "int8" else velokv.KV_F16
+    S, Hkv, L, NL = args.seqs, args.kv_heads, args.ctx, args.layers
+    if args.ragged:
+        lens = synth.rng(2024).integers(1024, L + 1, S).astype(np.int32)
+    else:
+        lens = np.full(S, L, np.int32)
+    pages = [-(-int(x) // BS) for x in lens]
+    need = 2 * sum(pages)
+    if "--pool-blocks" not in sys.argv:
+        args.pool_blocks = max(args.pool_blocks, need)
+    if need > args.pool_blocks:
+        raise SystemExit(f"--pool-blocks {args.pool_blocks} < {need} pages (source and destination)")
+    perm = synth.rng(12).permutation(args.pool_blocks).astype(np.int32)
+    src_pages, dst_pages = perm[:need // 2], perm[need // 2:need]
+    pool = velokv.Pool(ctx, NL, args.pool_blocks, BS, Hkv, HD, kv)
+    # fill the source pages of every layer with synthetic K/V through the append path
+    n_tok = int(lens.sum())
+    firsts = np.concatenate([[0], np.cumsum(pages)[:-1]]).astype(np.int64)
+    bt = np.zeros((S, max(pages)), np.int32)
+    for s_ in range(S):
+        bt[s_, :pages[s_]] = src_pages[firsts[s_]:firsts[s_] + pages[s_]]
+    rows = np.repeat(np.arange(S), lens)
+    pos = np.concatenate([np.arange(int(x)) for x in lens])
+    slots = ctx.upload(synth.slots_for_positions(bt, pos, BS, rows))
+    kbuf, vbuf = ctx.alloc(n_tok * Hkv * HD * 2), ctx.alloc(n_tok * Hkv * HD * 2)
+    outlier = 8.0 if kv == velokv.KV_I8_BLK else 1.0
+    for layer in range(NL):
+        ctx.fill_normal_f16(kbuf, n_tok * Hkv * HD, 5000 + 2 * layer, Hkv * HD, outlier)
+        ctx.fill_normal_f16(vbuf, n_tok * Hkv * HD, 5001 + 2 * layer, Hkv * HD, outlier)
+        ctx.append(pool, layer, kbuf, vbuf, velokv.DT_F16, slots, n_tok)
+    ctx.sync()
+    kbuf.free()
+    vbuf.free()
+    items, off = [], 0
+    for s_ in range(S):
+        items.append((s_, int(lens[s_]), int(firsts[s_]), off))
+        off += 16 + pool.nixl_payload_bytes(int(lens[s_]))
+        off = (off + 255) // 256 * 256
+    wire_bytes = off
+    payload = sum(pool.nixl_payload_bytes(int(x)) for x in lens)
+    wire = ctx.alloc(wire_bytes)
+    d_src, d_dst = ctx.upload(src_pages), ctx.upload(dst_pages)
+    st = ctx.alloc(4 * S)
+    stream = velokv.Stream(ctx)
+
+    def step(evs=None):
+        if evs is not None:
+            evs[0].record(stream)
+        ctx.nixl_pack(pool, items, d_src, len(src_pages), wire, wire_bytes, st, stream=stream)
+        if evs is not None:
+            evs[1].record(stream)
+        ctx.nixl_unpack(pool, items, d_dst, len(dst_pages), wire, wire_bytes, st, stream=stream)
+        if evs is not None:
+            evs[2].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    stream.sync()
+    status = st.download((S,), np.int32)
+    if np.any(status != velokv.NIXL_OK):
+        raise SystemExit(f"nixl statuses not OK: {np.unique(status)}")
+    evs = [[velokv.Event(ctx) for _ in range(3)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(evs[i])
+    stream.sync()
+    pack_ms = [e[0].elapsed_ms(e[1]) for e in evs]
+    unpack_ms = [e[1].elapsed_ms(e[2]) for e in evs]
+    call_bytes = 2 * payload + 16 * S
+    pk, up = float(np.mean(pack_ms)), float(np.mean(unpack_ms))
+    ms_step = pk + up
+    ach = call_bytes / (pk * 1e-3) / 1e9
+    return {
+        "value": round(2 * call_bytes / (ms_step * 1e-3) / 1e9, 2),
+        "ms_per_step": round(ms_step, 4),
+        "payload_bytes": int(payload), "records": S,
+        "pack": {"ms_mean": round(pk, 4), "gbs": round(call_bytes / (pk * 1e-3) / 1e9, 2)},
+        "unpack": {"ms_mean": round(up, 4), "gbs": round(call_bytes / (up * 1e-3) / 1e9, 2)},
+        "handles_per_s": round(S / (ms_step * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("vk_nixl_copy", S, L, args.heads, Hkv, args.ragged),
+                     "kernel": "vk_nixl_copy",
+                     "launch_ms_mean": round(pk, 5), "launch_ms_min": round(float(np.min(pack_ms)), 5),
+                     "launches": len(pack_ms)},
+        "pool_gb": round(pool.nbytes / 1e9, 2), "wire_gb": round(wire_bytes / 1e9, 2),
+        "workload": "%d records, L=%s, Hkv=%d, D=128, bs=16, %s KV, %d layers, pack then unpack into other pages" %
+                    (S, "U[1024,%d]" % L if args.ragged else str(L), Hkv, args.kv, NL),
     }
 
 
@@ -436,6 +557,17 @@ def main():
             "config": {"workload": t["workload"], "global_batch": args.seqs, "seq_len": args.prefix,
                        "parallelism": "single GPU"},
             "tokens_per_s": t["tokens_per_s"], "roofline": t["roofline"], "cpu_baseline": None, "detail": t}))
+        return
+    if args.workload == "nixl":
+        t = run_nixl(ctx, args)
+        print(json.dumps({
+            "metric": "NIXL KV-page pack + unpack GB/s (bytes read + written)",
+            "value": t["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": t["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "u8", "data": "synthetic",
+            "config": {"workload": t["workload"], "global_batch": args.seqs, "seq_len": args.ctx,
+                       "parallelism": "single GPU"},
+            "roofline": t["roofline"], "cpu_baseline": None, "detail": t}))
         return
     head = run_gpu(ctx, args, args.kv)
     also = None

@@ -268,6 +268,90 @@ int vk_tree_mask(const int32_t* parents, int32_t n_nodes, uint32_t* mask_out);
 int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* src_dst_pairs,
                    int32_t n_pairs, void* stream);
 
+/* Commit the accepted path of a verified draft tree in layers
+ * [layer0, layer0 + n_layers): for sequence s with committed length
+ * context_lens[s], the K/V of tree node accept[s][d] (position
+ * context_lens[s] + accept[s][d]) move to position context_lens[s] + d, for
+ * d < n_accept[s]. All pointers are device pointers; accept is
+ * [n_seqs][accept_stride], each row strictly increasing with accept[s][d] >= d
+ * and < 32. A row that breaks this, or whose positions fall outside its block
+ * table row or the pool, is left untouched. Leading nodes already in place
+ * (accept[s][d] == d) are not rewritten. The blocks written must belong to one
+ * sequence only (copy-on-write before appending the tree makes them private).
+ * F32 / F16 / I8_REF: the token rows (with their per-token scales) move
+ * unchanged. I8_BLK: every moved token is first dequantized (code x block
+ * scale, exact in fp32) from the pre-commit pool; the moved tokens are then
+ * appended in order by vk_append's rule, so a destination at block offset 0
+ * starts a fresh scale and a token that needs a larger scale re-quantizes the
+ * codes before it.
+ * Completes the tree-verify step: verify_tree (speculative.rs:217-242) accepts
+ * a root-to-node path of SpeculativeTree (speculative.rs:48-130) whose K/V
+ * were appended at context_len + node by the draft pass. */
+int vk_tree_commit(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
+                   const int32_t* block_tables, int32_t bt_stride,
+                   const int32_t* context_lens, const int32_t* accept,
+                   int32_t accept_stride, const int32_t* n_accept,
+                   int32_t n_seqs, void* stream);
+
+/* ---- NIXL wire records of KV pages ------------------------------------------
+ * Wire format of nixl.rs:24-61 (serialize_block / deserialize_block): a record
+ * is [block_id u64 LE][token_len u32 LE][byte_len u32 LE][payload byte_len B].
+ * The reference leaves the payload opaque (nixl.rs:365-367); here it is the
+ * KV pages of one KvCacheHandle (radix_cache.rs:6-9) over a layer range
+ * [layer0, layer0 + n_layers), n_pages = ceil(token_len / block_size):
+ *    tiles   for page i, for layer l: K codes of the page's n_kv_heads tiles,
+ *            then V codes (2 * n_kv_heads * tile bytes, in pool layout)
+ *    scales  for page i, for layer l: K scales of the page, then V scales
+ *            (I8 pools only; fp16 per head for I8_BLK, fp32 per token for I8_REF)
+ * Whole pages travel, including the slots past token_len in the last page. */
+#define VK_NIXL_HEADER_BYTES 16
+
+typedef struct vk_nixl_item {
+  uint64_t block_id;     /* KvCacheHandle.block_id                              */
+  uint32_t token_len;    /* KvCacheHandle.token_len                             */
+  int32_t first_page;    /* index into the pages array of this handle's first page */
+  uint64_t wire_offset;  /* byte offset of the record in the wire buffer (16-aligned) */
+} vk_nixl_item;
+
+/* Per-record status written by pack / unpack (dev int32 [n_items]). The first
+ * two are the cases where deserialize_block returns None (nixl.rs:50-58). */
+#define VK_NIXL_OK               0
+#define VK_NIXL_SHORT_HEADER     1  /* fewer than 16 bytes left in the wire      */
+#define VK_NIXL_TRUNCATED        2  /* header + byte_len runs past the wire      */
+#define VK_NIXL_HANDLE_MISMATCH  3  /* header block_id / token_len != the item   */
+#define VK_NIXL_LENGTH_MISMATCH  4  /* byte_len != the payload for this pool     */
+#define VK_NIXL_BAD_PAGE         5  /* a page id outside the pool                */
+
+/* Payload bytes of one record (without the 16-byte header). */
+int vk_nixl_payload_bytes(const vk_pool* pool, int32_t n_layers, uint32_t token_len,
+                          uint64_t* bytes);
+
+/* Serialise n_items handles into the wire buffer (dev, wire_bytes long).
+ * items is a HOST array; pages is a dev int32 array of n_pages page ids (item i
+ * uses pages[first_page .. first_page + ceil(token_len/bs))); status is dev
+ * int32 [n_items]. A record whose pages are all in range gets its header and
+ * payload and status VK_NIXL_OK; otherwise VK_NIXL_BAD_PAGE and its bytes are
+ * not written. Records must fit in the wire buffer and not overlap
+ * (VK_ERR_BAD_ARG otherwise); byte_len must fit in u32.
+ * DmaBlockManager::write_and_serialize (nixl.rs:129-144) / serialize_block
+ * (nixl.rs:36-43), done as one gather of pool pages in HBM. */
+int vk_nixl_pack(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
+                 const vk_nixl_item* items, int32_t n_items, const int32_t* pages,
+                 int32_t n_pages, void* wire, uint64_t wire_bytes, int32_t* status,
+                 void* stream);
+
+/* Deserialise records from the wire buffer into pool pages: item i's record is
+ * read at wire_offset and checked (status codes above, in that order); a
+ * record that passes writes its payload into pages[first_page ..] of this pool
+ * (which need not be the pages it was packed from), a record that fails writes
+ * nothing. Destination pages must be distinct across items.
+ * DmaBlockManager::receive_into (nixl.rs:147-155) / deserialize_block
+ * (nixl.rs:49-61), done as one scatter into pool pages in HBM. */
+int vk_nixl_unpack(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
+                   const vk_nixl_item* items, int32_t n_items, const int32_t* pages,
+                   int32_t n_pages, const void* wire, uint64_t wire_bytes,
+                   int32_t* status, void* stream);
+
 /* ---- host block manager ----------------------------------------------------
  * PagedAttentionBlockManager (paged_attention.rs:92-212): FIFO free list,
  * pages_for_tokens = ceil(len / bs), plus per-page reference counts for

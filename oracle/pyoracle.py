@@ -215,3 +215,115 @@ def set_threads(n):
 
 def get_threads():
     return lib().vko_get_threads()
+
+
+# ---- accepted-path commit of a draft tree ------------------------------------
+
+def tree_commit(layer: Layer, block_table_row, ctx_len, accept):
+    """vko_tree_commit on one sequence of one layer; returns 0, or 1 when the row
+    is rejected and the layer left untouched."""
+    bt = np.ascontiguousarray(block_table_row, dtype=np.int32)
+    a = np.ascontiguousarray(accept, dtype=np.int32)
+    s = layer.struct()
+    return lib().vko_tree_commit(C.byref(s), _ptr(bt), C.c_int(len(bt)), C.c_int(int(ctx_len)), _ptr(a),
+                                 C.c_int(len(a)))
+
+
+# ---- NIXL wire records (nixl.rs:24-61) -----------------------------------------
+
+NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH, NIXL_BAD_PAGE = range(6)
+
+
+def nixl_serialize(block_id, token_len, payload):
+    """serialize_block (nixl.rs:36-43) -> bytes."""
+    payload = np.ascontiguousarray(payload, dtype=np.uint8)
+    out = np.zeros(16 + payload.size, np.uint8)
+    n = lib().vko_nixl_serialize(C.c_uint64(block_id), C.c_uint32(token_len), _ptr(payload),
+                                 C.c_uint32(payload.size), _ptr(out))
+    assert n == out.size
+    return out
+
+
+def nixl_deserialize(buf):
+    """deserialize_block (nixl.rs:49-61): None, or (block_id, token_len, payload)."""
+    buf = np.ascontiguousarray(buf, dtype=np.uint8)
+    bid, tl, bl = C.c_uint64(), C.c_uint32(), C.c_uint32()
+    ok = lib().vko_nixl_deserialize(_ptr(buf) if buf.size else None, C.c_uint64(buf.size), C.byref(bid),
+                                    C.byref(tl), C.byref(bl))
+    if not ok:
+        return None
+    return bid.value, tl.value, buf[16:16 + bl.value]
+
+
+def _layers_array(layers):
+    arr = (VkoLayer * len(layers))()
+    for i, L in enumerate(layers):
+        arr[i] = L.struct()
+    return arr
+
+
+def nixl_payload_bytes(layer: Layer, n_layers, token_len):
+    lib().vko_nixl_payload_bytes.restype = C.c_uint64
+    s = layer.struct()
+    return lib().vko_nixl_payload_bytes(C.byref(s), C.c_int(n_layers), C.c_uint32(token_len))
+
+
+def nixl_gather(layers, pages):
+    pages = np.ascontiguousarray(pages, dtype=np.int32)
+    n = nixl_payload_bytes(layers[0], len(layers), len(pages) * layers[0].block_size)
+    out = np.zeros(n, np.uint8)
+    arr = _layers_array(layers)
+    lib().vko_nixl_move(arr, C.c_int(len(layers)), _ptr(pages), C.c_int(len(pages)), _ptr(out), C.c_int(0))
+    return out
+
+
+def nixl_scatter(layers, pages, payload):
+    pages = np.ascontiguousarray(pages, dtype=np.int32)
+    payload = np.ascontiguousarray(payload, dtype=np.uint8)
+    arr = _layers_array(layers)
+    lib().vko_nixl_move(arr, C.c_int(len(layers)), _ptr(pages), C.c_int(len(pages)), _ptr(payload), C.c_int(1))
+
+
+def nixl_pack(layers, items, pages, wire):
+    """Multi-record pack into `wire` (uint8 array, modified in place); items are
+    (block_id, token_len, first_page, wire_offset). Returns the status list."""
+    bs, nb = layers[0].block_size, layers[0].n_blocks
+    status = []
+    for bid, tl, fp, off in items:
+        pg = np.asarray(pages[fp:fp + (tl + bs - 1) // bs], np.int64)
+        if np.any((pg < 0) | (pg >= nb)):
+            status.append(NIXL_BAD_PAGE)
+            continue
+        rec = nixl_serialize(bid, tl, nixl_gather(layers, pg))
+        wire[off:off + rec.size] = rec
+        status.append(NIXL_OK)
+    return status
+
+
+def nixl_unpack(layers, items, pages, wire):
+    """Multi-record unpack from `wire` into `layers` (modified in place); returns
+    the status list (header checks in deserialize_block's order, then ours)."""
+    bs, nb = layers[0].block_size, layers[0].n_blocks
+    status = []
+    for bid, tl, fp, off in items:
+        if off > wire.size or wire.size - off < 16:
+            status.append(NIXL_SHORT_HEADER)
+            continue
+        r = nixl_deserialize(wire[off:])
+        if r is None:
+            status.append(NIXL_TRUNCATED)
+            continue
+        rbid, rtl, payload = r
+        if rbid != bid or rtl != tl:
+            status.append(NIXL_HANDLE_MISMATCH)
+            continue
+        if payload.size != nixl_payload_bytes(layers[0], len(layers), tl):
+            status.append(NIXL_LENGTH_MISMATCH)
+            continue
+        pg = np.asarray(pages[fp:fp + (tl + bs - 1) // bs], np.int64)
+        if np.any((pg < 0) | (pg >= nb)):
+            status.append(NIXL_BAD_PAGE)
+            continue
+        nixl_scatter(layers, pg, payload)
+        status.append(NIXL_OK)
+    return status

@@ -494,6 +494,144 @@ void vko_copy_blocks(vko_layer* L, const int32_t* pairs, int n_pairs) {
   }
 }
 
+/* Accepted-path commit of a draft tree, one sequence and one layer (defined
+ * here; the reference appends no tree KV). Node accept[d] sits at position
+ * ctx + accept[d] and moves to ctx + d. Returns 1 (pool untouched) for a row
+ * that is not strictly increasing with d <= accept[d] < 32, n_accept > 32, or
+ * positions outside the table row / pool; 0 otherwise. Every moved token is
+ * read before anything is written. F32 / F16 / I8_REF rows (with per-token
+ * scales) move unchanged; I8_BLK tokens are dequantized (code x block scale)
+ * and appended in order with vko_append's rule. */
+int vko_tree_commit(vko_layer* L, const int32_t* bt, int bt_stride, int ctx, const int32_t* accept, int n_accept) {
+  const int D = L->head_dim, Hkv = L->n_kv_heads, bs = L->block_size;
+  if (ctx < 0 || n_accept <= 0) return n_accept == 0 ? 0 : 1;
+  if (n_accept > 32) return 1;
+  for (int d = 0; d < n_accept; ++d)
+    if (accept[d] < d || accept[d] >= 32 || (d > 0 && accept[d] <= accept[d - 1])) return 1;
+  int d0 = 0;
+  while (d0 < n_accept && accept[d0] == d0) ++d0;
+  if (d0 == n_accept) return 0;
+  const int last = ctx + accept[n_accept - 1];
+  if ((int64_t)last >= (int64_t)bt_stride * bs) return 1;
+  for (int b = (ctx + d0) / bs; b <= last / bs; ++b)
+    if (bt[b] < 0 || bt[b] >= L->n_blocks) return 1;
+  const int n = n_accept - d0;
+  if (L->kv_type == VKO_I8_BLK) {
+    float* kx = (float*)malloc(sizeof(float) * (size_t)n * Hkv * D);
+    float* vx = (float*)malloc(sizeof(float) * (size_t)n * Hkv * D);
+    int64_t* slots = (int64_t*)malloc(sizeof(int64_t) * (size_t)n);
+    for (int i = 0; i < n; ++i) {
+      const int q = ctx + accept[d0 + i], p = ctx + d0 + i;
+      for (int h = 0; h < Hkv; ++h)
+        for (int d = 0; d < D; ++d) {
+          kx[((size_t)i * Hkv + h) * D + d] = load_elem(L, 0, bt[q / bs], h, q % bs, d);
+          vx[((size_t)i * Hkv + h) * D + d] = load_elem(L, 1, bt[q / bs], h, q % bs, d);
+        }
+      slots[i] = (int64_t)bt[p / bs] * bs + p % bs;
+    }
+    vko_append(L, kx, vx, VKO_F32, slots, n);
+    free(kx);
+    free(vx);
+    free(slots);
+    return 0;
+  }
+  const int esz = esz_of(L->kv_type);
+  const int ref = L->kv_type == VKO_I8_REF;
+  uint8_t* row = (uint8_t*)malloc((size_t)n * 2 * Hkv * D * esz);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)n * 2 * Hkv);
+  for (int pass = 0; pass < 2; ++pass) /* 0: read every source, 1: write every destination */
+    for (int i = 0; i < n; ++i) {
+      const int pos = ctx + (pass == 0 ? accept[d0 + i] : d0 + i);
+      const int64_t blk = bt[pos / bs];
+      const int o = pos % bs;
+      for (int is_v = 0; is_v < 2; ++is_v) {
+        uint8_t* codes = is_v ? L->v : L->k;
+        for (int h = 0; h < Hkv; ++h) {
+          uint8_t* r = row + (((size_t)i * 2 + is_v) * Hkv + h) * D * esz;
+          for (int d = 0; d < D; ++d) {
+            uint8_t* e = codes + elem_off(L, is_v, blk, h, o, d);
+            if (pass == 0) memcpy(r + (size_t)d * esz, e, esz); else memcpy(e, r + (size_t)d * esz, esz);
+          }
+          if (ref) {
+            uint8_t* s = (is_v ? L->vs : L->ks) + (((uint64_t)blk * Hkv + h) * bs + o) * 4;
+            float* t = &sc[((size_t)i * 2 + is_v) * Hkv + h];
+            if (pass == 0) memcpy(t, s, 4); else memcpy(s, t, 4);
+          }
+        }
+      }
+    }
+  free(row);
+  free(sc);
+  return 0;
+}
+
+/* ---- NIXL wire format (nixl.rs:24-61) ------------------------------------ */
+
+/* serialize_block (nixl.rs:36-43): block_id.to_le_bytes(), (token_len as
+ * u32).to_le_bytes(), (payload.len() as u32).to_le_bytes(), payload. Returns
+ * the record length 16 + byte_len. */
+uint64_t vko_nixl_serialize(uint64_t block_id, uint32_t token_len, const uint8_t* payload, uint32_t byte_len,
+                            uint8_t* out) {
+  for (int i = 0; i < 8; ++i) out[i] = (uint8_t)(block_id >> (8 * i));
+  for (int i = 0; i < 4; ++i) out[8 + i] = (uint8_t)(token_len >> (8 * i));
+  for (int i = 0; i < 4; ++i) out[12 + i] = (uint8_t)(byte_len >> (8 * i));
+  if (byte_len) memcpy(out + 16, payload, byte_len);
+  return 16u + (uint64_t)byte_len;
+}
+
+/* deserialize_block (nixl.rs:49-61): None (0) when the buffer is shorter than
+ * the 16-byte header or than header + byte_len; else 1 with the handle and the
+ * payload's length (the payload starts at buf + 16). */
+int vko_nixl_deserialize(const uint8_t* buf, uint64_t len, uint64_t* block_id, uint32_t* token_len,
+                         uint32_t* byte_len) {
+  if (len < 16) return 0;
+  uint64_t id = 0;
+  uint32_t tl = 0, bl = 0;
+  for (int i = 0; i < 8; ++i) id |= (uint64_t)buf[i] << (8 * i);
+  for (int i = 0; i < 4; ++i) tl |= (uint32_t)buf[8 + i] << (8 * i);
+  for (int i = 0; i < 4; ++i) bl |= (uint32_t)buf[12 + i] << (8 * i);
+  if (len < 16u + (uint64_t)bl) return 0;
+  *block_id = id;
+  *token_len = tl;
+  *byte_len = bl;
+  return 1;
+}
+
+static uint64_t scale_bytes_per_head(const vko_layer* L) {
+  return L->kv_type == VKO_I8_BLK ? 2u : L->kv_type == VKO_I8_REF ? 4u * (uint64_t)L->block_size : 0u;
+}
+
+/* Payload of one KV-cache handle over n_layers layers (velokv.h): tiles of
+ * every (page, layer) -- K codes of the page's heads, then V codes -- then the
+ * scales of every (page, layer), K then V. */
+uint64_t vko_nixl_payload_bytes(const vko_layer* L, int n_layers, uint32_t token_len) {
+  const uint64_t pages = ((uint64_t)token_len + L->block_size - 1) / L->block_size;
+  const uint64_t cb = (uint64_t)L->n_kv_heads * L->block_size * L->head_dim * esz_of(L->kv_type);
+  const uint64_t sb = (uint64_t)L->n_kv_heads * scale_bytes_per_head(L);
+  return pages * (uint64_t)n_layers * 2 * (cb + sb);
+}
+
+/* pool pages -> payload (dir 0) or payload -> pool pages (dir 1) */
+void vko_nixl_move(vko_layer* Ls, int n_layers, const int32_t* pages, int n_pages, uint8_t* payload, int dir) {
+  const vko_layer* L0 = &Ls[0];
+  const uint64_t cb = (uint64_t)L0->n_kv_heads * L0->block_size * L0->head_dim * esz_of(L0->kv_type);
+  const uint64_t sb = (uint64_t)L0->n_kv_heads * scale_bytes_per_head(L0);
+  uint8_t* scales = payload + (uint64_t)n_pages * n_layers * 2 * cb;
+  for (int i = 0; i < n_pages; ++i)
+    for (int l = 0; l < n_layers; ++l) {
+      vko_layer* L = &Ls[l];
+      const uint64_t r = (uint64_t)i * n_layers + l;
+      const uint64_t pg = (uint64_t)pages[i];
+      uint8_t* parts[4] = {L->k + pg * cb, L->v + pg * cb, sb ? L->ks + pg * sb : 0, sb ? L->vs + pg * sb : 0};
+      uint8_t* wire[4] = {payload + r * 2 * cb, payload + r * 2 * cb + cb, scales + r * 2 * sb, scales + r * 2 * sb + sb};
+      const uint64_t len[4] = {cb, cb, sb, sb};
+      for (int k = 0; k < 4; ++k) {
+        if (!len[k]) continue;
+        if (dir == 0) memcpy(wire[k], parts[k], len[k]); else memcpy(parts[k], wire[k], len[k]);
+      }
+    }
+}
+
 /* Layout translation: build layout -> reference layout for the I8_REF and F32
  * types ([blk][tok][head][D] fp32; [blk][tok][head][D codes + fp32 scale]). */
 void vko_to_reference_layout(const vko_layer* L, int is_v, uint8_t* dst) {

@@ -89,6 +89,35 @@ def test_append_blk_token_by_token_equals_one_call(ctx):
         assert np.array_equal(a[key], b[key])
 
 
+@pytest.mark.parametrize("gap", [0, 5, 70, 130])
+def test_append_blk_runs_with_padding_windows(ctx, gap):
+    """Runs whose tokens are separated by `gap` padding slots (more than one
+    64-slot window when gap >= 64), a run of a whole block (16 tokens in a row),
+    and a run that restarts its block at offset 0 (positions 16..19 then 16..23,
+    adjacent in the call: more than one 16-token chunk). Tokens of one block stay
+    adjacent in the call, as vk_append requires."""
+    print(f"append blk padding gap={gap}", flush=True)
+    case = make_case(O.I8_BLK, [64], n_kv_heads=2, n_heads=8, seed=106, outlier_scale=8.0)
+    bt = case.block_tables
+    pos = list(range(0, 20)) + list(range(16, 24)) + list(range(32, 40)) + list(range(48, 64))
+    rows = np.zeros(len(pos), np.int64)
+    slots = synth.slots_for_positions(bt, np.array(pos), BS, rows)
+    k = np.stack([case.k[0][p] for p in pos])
+    v = np.stack([case.v[0][p] for p in pos])
+    # interleave `gap` padding slots after every token
+    n = len(pos) * (gap + 1)
+    sl = np.full(n, -1, np.int64)
+    kk = np.zeros((n, 2, HD), np.float16)
+    vv = np.zeros((n, 2, HD), np.float16)
+    sl[::gap + 1], kk[::gap + 1], vv[::gap + 1] = slots, k, v
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, 2, HD, O.I8_BLK)
+    ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), n)
+    ctx.sync()
+    ref = O.Layer(case.n_blocks, 2, BS, HD, O.I8_BLK)
+    O.append(ref, kk, vv, sl)
+    assert_layer_equal(pool, 0, ref)
+
+
 def test_append_skips_negative_slots_and_layers_are_separate(ctx):
     print("append negative slots / layers", flush=True)
     case = make_case(O.I8_BLK, [20], seed=105)

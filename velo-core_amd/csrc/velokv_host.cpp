@@ -113,7 +113,8 @@ namespace {
 
 const char* const kKernelNames[] = {
     "vk_decode_merge", "vk_decode_merge_sk", "vk_append_kv0", "vk_append_kv1", "vk_append_kv2", "vk_append_kv3",
-    "vk_slot_mapping", "vk_copy_blocks", "vk_fill_normal_f16",
+    "vk_slot_mapping", "vk_copy_blocks", "vk_fill_normal_f16", "vk_nixl_check", "vk_nixl_copy",
+    "vk_tree_commit_kv0", "vk_tree_commit_kv1", "vk_tree_commit_kv2", "vk_tree_commit_kv3",
 };
 
 std::string decode_name(int kv, int g, int qt) {
@@ -822,6 +823,149 @@ extern "C" int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* pairs, 
       return rc;
   }
   return VK_OK;
+}
+
+extern "C" int vk_tree_commit(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
+                              const int32_t* block_tables, int32_t bt_stride, const int32_t* context_lens,
+                              const int32_t* accept, int32_t accept_stride, const int32_t* n_accept, int32_t n_seqs,
+                              void* stream) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  const vk_pool_desc& d = pool->desc;
+  if (layer0 < 0 || n_layers < 0 || layer0 + n_layers > d.n_layer)
+    return fail(VK_ERR_BAD_ARG, "layer range [%d, %d) outside [0, %d)", layer0, layer0 + n_layers, d.n_layer);
+  if (n_seqs < 0) return fail(VK_ERR_BAD_ARG, "n_seqs < 0");
+  if (bt_stride <= 0 || accept_stride <= 0) return fail(VK_ERR_BAD_ARG, "strides must be positive");
+  if (n_seqs == 0 || n_layers == 0) return VK_OK;
+  if (!block_tables || !context_lens || !accept || !n_accept) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  CommitParams p{};
+  p.base = pool->base;
+  p.g = pool->geom;
+  p.block_tables = block_tables;
+  p.context_lens = context_lens;
+  p.accept = accept;
+  p.n_accept = n_accept;
+  p.bt_stride = bt_stride;
+  p.accept_stride = accept_stride;
+  p.n_seqs = n_seqs;
+  p.layer0 = layer0;
+  p.n_layers = n_layers;
+  const std::string name = "vk_tree_commit_kv" + std::to_string(d.kv_type);
+  if ((rc = set_device(ctx))) return rc;
+  constexpr int kCommitLayers = 8;  // layers per workgroup (velokv_kernels.hip)
+  return launch(ctx, name.c_str(),
+                dim3((unsigned)n_seqs, (unsigned)d.n_kv_heads, (unsigned)((n_layers + kCommitLayers - 1) / kCommitLayers)),
+                dim3(128), p, stream);
+}
+
+// ---- NIXL wire records ------------------------------------------------------
+namespace {
+
+uint64_t nixl_payload(const vk_pool* pool, int32_t n_layers, uint32_t token_len) {
+  const vk_pool_desc& d = pool->desc;
+  const uint64_t pages = ((uint64_t)token_len + d.block_size - 1) / d.block_size;
+  return pages * (uint64_t)n_layers * 2 * (uint64_t)d.n_kv_heads * (pool->geom.tile_bytes + pool->geom.stile_bytes);
+}
+
+int nixl_run(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers, const vk_nixl_item* items,
+             int32_t n_items, const int32_t* pages, int32_t n_pages, const void* wire, uint64_t wire_bytes,
+             int32_t* status, void* stream, bool unpack) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  const vk_pool_desc& d = pool->desc;
+  if (layer0 < 0 || n_layers <= 0 || layer0 + n_layers > d.n_layer)
+    return fail(VK_ERR_BAD_ARG, "layer range [%d, %d) outside [0, %d)", layer0, layer0 + n_layers, d.n_layer);
+  if (n_items < 0 || n_pages < 0) return fail(VK_ERR_BAD_ARG, "negative count");
+  if (n_items == 0) return VK_OK;
+  if (!items || !wire || !status) return fail(VK_ERR_BAD_ARG, "null argument");
+  std::vector<NixlItemArg> args((size_t)n_items);
+  std::vector<std::pair<uint64_t, uint64_t>> spans;  // pack: [offset, end) of each record
+  for (int32_t i = 0; i < n_items; ++i) {
+    const vk_nixl_item& it = items[i];
+    if (it.wire_offset % 16) return fail(VK_ERR_BAD_ARG, "record %d: wire_offset %llu is not 16-aligned", i,
+                                         (unsigned long long)it.wire_offset);
+    const uint64_t np = ((uint64_t)it.token_len + d.block_size - 1) / d.block_size;
+    if (it.first_page < 0 || (uint64_t)it.first_page + np > (uint64_t)n_pages)
+      return fail(VK_ERR_BAD_ARG, "record %d: pages [%d, %llu) outside the %d page ids given", i, it.first_page,
+                  (unsigned long long)(it.first_page + np), n_pages);
+    if (np > 0 && !pages) return fail(VK_ERR_BAD_ARG, "pages is null");
+    const uint64_t payload = nixl_payload(pool, n_layers, it.token_len);
+    if (payload > 0xFFFFFFFFull)
+      return fail(VK_ERR_BAD_ARG, "record %d: payload of %llu bytes exceeds the wire format's u32 byte_len", i,
+                  (unsigned long long)payload);
+    if (!unpack) {
+      if (it.wire_offset > wire_bytes || wire_bytes - it.wire_offset < VK_NIXL_HEADER_BYTES + payload)
+        return fail(VK_ERR_BAD_ARG, "record %d (%llu bytes at %llu) runs past the %llu-byte wire buffer", i,
+                    (unsigned long long)(VK_NIXL_HEADER_BYTES + payload), (unsigned long long)it.wire_offset,
+                    (unsigned long long)wire_bytes);
+      spans.emplace_back(it.wire_offset, it.wire_offset + VK_NIXL_HEADER_BYTES + payload);
+    }
+    NixlItemArg& a = args[(size_t)i];
+    a.block_id = it.block_id;
+    a.wire_offset = it.wire_offset;
+    a.token_len = it.token_len;
+    a.first_page = it.first_page;
+    a.n_pages = (uint32_t)np;
+    a.byte_len = (uint32_t)payload;
+  }
+  if (!unpack) {
+    std::sort(spans.begin(), spans.end());
+    for (size_t i = 1; i < spans.size(); ++i)
+      if (spans[i].first < spans[i - 1].second) return fail(VK_ERR_BAD_ARG, "wire records overlap");
+  }
+  if ((rc = set_device(ctx))) return rc;
+  const uint64_t page_codes = 2ull * (uint64_t)d.n_kv_heads * pool->geom.tile_bytes;  // K + V of one page
+  const int32_t n_slices = (int32_t)((page_codes / 16 + kNixlSliceVecs - 1) / kNixlSliceVecs);
+  for (int32_t i0 = 0; i0 < n_items;) {
+    NixlParams p{};
+    p.base = pool->base;
+    p.g = pool->geom;
+    p.pages = pages;
+    p.wire = reinterpret_cast<uint8_t*>(const_cast<void*>(wire));
+    p.wire_bytes = wire_bytes;
+    p.status = status + i0;
+    p.layer0 = layer0;
+    p.n_layers = n_layers;
+    p.unpack = unpack ? 1 : 0;
+    p.n_slices = n_slices;
+    uint64_t units = 0;  // slices of this launch
+    int n = 0;
+    while (i0 + n < n_items && n < kMaxNixlItems) {
+      const uint64_t u = (uint64_t)args[(size_t)(i0 + n)].n_pages * (uint64_t)n_layers * (uint64_t)n_slices;
+      if (n > 0 && units + u > 0x7FFFFFFFull) break;
+      if (u > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "record %d has too many pages x layers", i0 + n);
+      p.items[n] = args[(size_t)(i0 + n)];
+      p.items[n].unit_begin = (uint32_t)units;
+      units += u;
+      ++n;
+    }
+    p.n_items = n;
+    if ((rc = launch(ctx, "vk_nixl_check", dim3((unsigned)n), dim3(256), p, stream))) return rc;
+    if (units > 0 && (rc = launch(ctx, "vk_nixl_copy", dim3((unsigned)units), dim3(256), p, stream))) return rc;
+    i0 += n;
+  }
+  return VK_OK;
+}
+
+}  // namespace
+
+extern "C" int vk_nixl_payload_bytes(const vk_pool* pool, int32_t n_layers, uint32_t token_len, uint64_t* bytes) {
+  if (!pool || !bytes) return fail(VK_ERR_BAD_ARG, "null argument");
+  if (n_layers <= 0 || n_layers > pool->desc.n_layer) return fail(VK_ERR_BAD_ARG, "n_layers %d out of range", n_layers);
+  *bytes = nixl_payload(pool, n_layers, token_len);
+  return VK_OK;
+}
+
+extern "C" int vk_nixl_pack(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers, const vk_nixl_item* items,
+                            int32_t n_items, const int32_t* pages, int32_t n_pages, void* wire, uint64_t wire_bytes,
+                            int32_t* status, void* stream) {
+  return nixl_run(ctx, pool, layer0, n_layers, items, n_items, pages, n_pages, wire, wire_bytes, status, stream, false);
+}
+
+extern "C" int vk_nixl_unpack(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers, const vk_nixl_item* items,
+                              int32_t n_items, const int32_t* pages, int32_t n_pages, const void* wire,
+                              uint64_t wire_bytes, int32_t* status, void* stream) {
+  return nixl_run(ctx, pool, layer0, n_layers, items, n_items, pages, n_pages, wire, wire_bytes, status, stream, true);
 }
 
 // ============================================================================

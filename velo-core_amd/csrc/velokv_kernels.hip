@@ -1216,6 +1216,36 @@ DEV uint32_t tile_elem(int tok, int d, int esz) {
 
 DEV int clamp127(float r) { return (int)fminf(fmaxf(r, -127.f), 127.f); }
 
+// One token (dims 2*lane, 2*lane + 1 of x) into offset o of a block whose codes
+// are in registers (cd) and whose scale is s_old (bits s_bits); the I8_BLK rule:
+//   s_new = max(s_old, fp16(amax / 127))
+//   if s_new > s_old: c' = clamp(rne((c * s_old) / s_new)) for tokens before o
+//   c = s_new > 0 ? clamp(rne(x / s_new)) : 0
+DEV void blk_put(int (&cd)[BS][2], int o, float& s_old, uint16_t& s_bits, float x0, float x1) {
+  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+  const uint16_t cand = f2h(amax / 127.0f);
+  float s_new = s_old;
+  if (h2f(cand) > s_old) { s_new = h2f(cand); s_bits = cand; }
+  if (s_new > s_old && o > 0) {
+#pragma unroll
+    for (int u = 0; u < BS; ++u) {
+      if (u < o) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const float r = ((float)cd[u][k] * s_old) / s_new;
+          cd[u][k] = clamp127(__builtin_rintf(r));
+        }
+      }
+    }
+  }
+  const int c0 = (s_new > 0.f) ? clamp127(__builtin_rintf(x0 / s_new)) : 0;
+  const int c1 = (s_new > 0.f) ? clamp127(__builtin_rintf(x1 / s_new)) : 0;
+#pragma unroll
+  for (int u = 0; u < BS; ++u)
+    if (u == o) { cd[u][0] = c0; cd[u][1] = c1; }
+  s_old = s_new;
+}
+
 // VK_KV_I8_BLK: per-(block, head) fp16 scale, round-half-even codes clamped to +-127.
 // A run = consecutive tokens of the call that fall in one block; the run's first
 // token does the work for all of them, in order, keeping the block's codes in
@@ -1259,29 +1289,8 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
   for (int m = n; m < P.n_tok;) {
     float x0, x1;
     load_x2(src, P.in_dtype, ((int64_t)m * Hkv + h) * HD + d0, x0, x1);
-    const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-    const uint16_t cand = f2h(amax / 127.0f);
-    float s_new = s_old;
-    if (h2f(cand) > s_old) { s_new = h2f(cand); s_bits = cand; }
-    if (s_new > s_old && o > 0) {
-#pragma unroll
-      for (int u = 0; u < BS; ++u) {
-        if (u < o) {
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const float r = ((float)cd[u][k] * s_old) / s_new;
-            cd[u][k] = clamp127(__builtin_rintf(r));
-          }
-        }
-      }
-    }
-    const int c0 = (s_new > 0.f) ? clamp127(__builtin_rintf(x0 / s_new)) : 0;
-    const int c1 = (s_new > 0.f) ? clamp127(__builtin_rintf(x1 / s_new)) : 0;
-#pragma unroll
-    for (int u = 0; u < BS; ++u)
-      if (u == o) { cd[u][0] = c0; cd[u][1] = c1; }
+    blk_put(cd, o, s_old, s_bits, x0, x1);
     hi_written = max(hi_written, o);
-    s_old = s_new;
     // next token of the run (padding slots in between are skipped)
     ++m;
     while (m < P.n_tok && P.slot_mapping[m] < 0) ++m;
@@ -1406,6 +1415,232 @@ __device__ void copy_blocks_kernel(const CopyParams& P) {
   }
 }
 
+// ---- NIXL wire records (nixl.rs:24-61) ------------------------------------
+// Status codes of include/velokv.h.
+constexpr int kNixlOk = 0, kNixlShortHeader = 1, kNixlTruncated = 2, kNixlHandleMismatch = 3,
+              kNixlLengthMismatch = 4, kNixlBadPage = 5;
+
+// grid = records of the launch, 256 threads. Decides each record's status
+// before any payload moves: unpack checks the header as deserialize_block does
+// (nixl.rs:50-58: header present, payload within the buffer) and then that it
+// names this item and this pool's payload size; both directions check that
+// every page id is inside the pool. Pack writes the header of a good record.
+__device__ void nixl_check_kernel(const NixlParams& P) {
+  __shared__ int bad_page;
+  const int it = blockIdx.x;
+  const NixlItemArg& I = P.items[it];
+  if (threadIdx.x == 0) bad_page = 0;
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < I.n_pages; i += blockDim.x) {
+    const int32_t pg = P.pages[I.first_page + (int64_t)i];
+    if (pg < 0 || pg >= P.g.n_blocks) bad_page = 1;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  int st = kNixlOk;
+  if (P.unpack) {
+    if (I.wire_offset > P.wire_bytes || P.wire_bytes - I.wire_offset < 16) {
+      st = kNixlShortHeader;
+    } else {
+      const uint4 h = *reinterpret_cast<const uint4*>(P.wire + I.wire_offset);
+      const uint64_t block_id = (uint64_t)h.x | ((uint64_t)h.y << 32);
+      const uint32_t token_len = h.z, byte_len = h.w;
+      if ((uint64_t)byte_len > P.wire_bytes - I.wire_offset - 16) st = kNixlTruncated;
+      else if (block_id != I.block_id || token_len != I.token_len) st = kNixlHandleMismatch;
+      else if (byte_len != I.byte_len) st = kNixlLengthMismatch;
+    }
+  }
+  if (st == kNixlOk && bad_page) st = kNixlBadPage;
+  P.status[it] = st;
+  if (!P.unpack && st == kNixlOk) {
+    // little-endian header: block_id, token_len, byte_len
+    *reinterpret_cast<uint4*>(P.wire + I.wire_offset) =
+        make_uint4((uint32_t)I.block_id, (uint32_t)(I.block_id >> 32), I.token_len, I.byte_len);
+  }
+}
+
+// grid = work units of the launch x slices, 256 threads: unit = (record, page i,
+// layer l), whose K and V codes of every KV head (two contiguous runs in the
+// pool, one run in the record) are cut into 4 KB slices, one per workgroup and
+// one 16-byte load per lane (many small workgroups copy fastest on MI355X);
+// slice 0 also moves the unit's scales.
+__device__ void nixl_copy_kernel(const NixlParams& P) {
+  const uint32_t gid = blockIdx.x;
+  int lo = 0, hi = P.n_items - 1;  // last record whose slices start at or before gid
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (P.items[mid].unit_begin <= gid) lo = mid; else hi = mid - 1;
+  }
+  const NixlItemArg& I = P.items[lo];
+  if (P.status[lo] != kNixlOk) return;
+  const uint32_t rs = gid - I.unit_begin;
+  const uint32_t r = rs / (uint32_t)P.n_slices;          // i * n_layers + l
+  const uint32_t slice = rs - r * (uint32_t)P.n_slices;
+  const uint32_t i = r / (uint32_t)P.n_layers, l = r - i * (uint32_t)P.n_layers;
+  const int64_t page = P.pages[I.first_page + (int64_t)i];
+  uint8_t* L = P.base + (uint64_t)(P.layer0 + (int)l) * P.g.layer_stride;
+  const uint64_t cb = (uint64_t)P.g.n_kv_heads * P.g.tile_bytes;   // codes of one page, K or V
+  const uint64_t sb = (uint64_t)P.g.n_kv_heads * P.g.stile_bytes;  // scales of one page, K or V
+  uint8_t* payload = P.wire + I.wire_offset + 16;
+  const uint32_t nv = (uint32_t)(cb / 16);  // 16-byte vectors per K (or V) run
+  const uint32_t j = slice * kNixlSliceVecs + threadIdx.x;
+  if (j < 2 * nv) {
+    uint8_t* wt = payload + (uint64_t)r * 2 * cb + (uint64_t)j * 16;
+    uint8_t* pt = L + (j < nv ? P.g.k_off + (uint64_t)page * cb + (uint64_t)j * 16
+                              : P.g.v_off + (uint64_t)page * cb + (uint64_t)(j - nv) * 16);
+    const u32x4* src = reinterpret_cast<const u32x4*>(P.unpack ? wt : pt);
+    u32x4* dst = reinterpret_cast<u32x4*>(P.unpack ? pt : wt);
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src), dst);
+  }
+  if (sb && slice == 0) {
+    uint16_t* ws = reinterpret_cast<uint16_t*>(payload + (uint64_t)I.n_pages * P.n_layers * 2 * cb + (uint64_t)r * 2 * sb);
+    uint16_t* sk = reinterpret_cast<uint16_t*>(L + P.g.ks_off + (uint64_t)page * sb);
+    uint16_t* sv = reinterpret_cast<uint16_t*>(L + P.g.vs_off + (uint64_t)page * sb);
+    const uint32_t ne = (uint32_t)(sb / 2);
+    for (uint32_t e = threadIdx.x; e < 2 * ne; e += blockDim.x) {
+      uint16_t* pe = e < ne ? sk + e : sv + (e - ne);
+      if (P.unpack) *pe = ws[e]; else ws[e] = *pe;
+    }
+  }
+}
+
+// ---- accepted-path commit of a draft tree -----------------------------------
+// grid (sequence, KV head, group of kCommitLayers layers), wave 0 = K, wave 1 =
+// V, lane = dims 2l, 2l+1. The row is validated once; then per layer every moved
+// token is read (raw element bytes and its scale, 8 tokens' loads in flight at a
+// time) into LDS before any write, so a write never changes a source still to
+// be read; then the tokens are written in order: rows and per-token scales as
+// they were, or for I8_BLK dequantized (code x block scale, exact in fp32) and
+// put through the append rule (blk_put), one destination block at a time.
+constexpr int kMaxCommit = 32;
+constexpr int kCommitLayers = 8;
+template <int KV>
+DEV void tree_commit(const CommitParams& P) {
+  constexpr int ESZ = Esz<KV>::v;
+  __shared__ uint8_t raw[2][kMaxCommit][2 * WAVE * ESZ];  // [wave][token][lane's 2 elements]
+  __shared__ float xsc[2][kMaxCommit];
+  const int s = blockIdx.x, h = blockIdx.y;
+  const int l0 = P.layer0 + (int)blockIdx.z * kCommitLayers;
+  const int l1 = min(l0 + kCommitLayers, P.layer0 + P.n_layers);
+  const int w = threadIdx.x / WAVE;
+  const bool is_v = w != 0;
+  const int lane = lane_id();
+  const int ctx = P.context_lens[s];
+  const int na = P.n_accept[s];
+  if (ctx < 0 || na <= 0 || na > min(P.accept_stride, kMaxCommit)) return;
+  const int32_t* acc = P.accept + (int64_t)s * P.accept_stride;
+  const int a = lane < na ? acc[lane] : 0;
+  const int prev = __shfl_up(a, 1, WAVE);
+  const bool bad = lane < na && (a < lane || a >= kMaxCommit || (lane > 0 && a <= prev));
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) return;
+  const uint64_t moved = __builtin_amdgcn_ballot_w64(lane < na && a != lane);
+  if (moved == 0) return;  // every accepted node is already in place
+  const int d0 = __builtin_ctzll(moved);
+  const int last = ctx + readlane_i(a, na - 1);
+  if ((int64_t)last >= (int64_t)P.bt_stride * BS) return;
+  const int32_t* bt = P.block_tables + (int64_t)s * P.bt_stride;
+  const int b_first = (ctx + d0) / BS, nb = last / BS - b_first + 1;  // at most 3 blocks
+  const int blk_l = lane < nb ? bt[b_first + lane] : 0;
+  if (__builtin_amdgcn_ballot_w64(lane < nb && (blk_l < 0 || blk_l >= P.g.n_blocks)) != 0) return;
+  const int Hkv = P.g.n_kv_heads;
+  const int c0 = 2 * lane;
+  auto blk_of = [&](int pos) -> int64_t { return readlane_i(blk_l, pos / BS - b_first); };
+  for (int layer = l0; layer < l1; ++layer) {
+    uint8_t* L = P.base + (uint64_t)layer * P.g.layer_stride;
+    uint8_t* codes = L + (is_v ? P.g.v_off : P.g.k_off);
+    uint8_t* scales = L + (is_v ? P.g.vs_off : P.g.ks_off);
+    // ---- read every moved token ----
+    constexpr int RC = 8;
+    for (int d = d0; d < na; d += RC) {
+      uint32_t e[RC][2];
+      float sv[RC];
+#pragma unroll
+      for (int k = 0; k < RC; ++k) {
+        const int q = ctx + readlane_i(a, min(d + k, na - 1));  // past na: a valid token, result dropped
+        const int64_t blk = blk_of(q);
+        const uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
+        const int o = q % BS;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const uint32_t off = is_v ? tile_elem<true>(o, c0 + c, ESZ) : tile_elem<false>(o, c0 + c, ESZ);
+          if constexpr (ESZ == 4) e[k][c] = *reinterpret_cast<const uint32_t*>(t + off);
+          else if constexpr (ESZ == 2) e[k][c] = *reinterpret_cast<const uint16_t*>(t + off);
+          else e[k][c] = t[off];
+        }
+        sv[k] = 0.f;
+        if constexpr (KV == KV_I8_BLK) sv[k] = h2f(reinterpret_cast<const uint16_t*>(scales)[(uint64_t)blk * Hkv + h]);
+        if constexpr (KV == KV_I8_REF) sv[k] = reinterpret_cast<const float*>(scales)[((uint64_t)blk * Hkv + h) * BS + o];
+      }
+#pragma unroll
+      for (int k = 0; k < RC; ++k) {
+        if (d + k < na) {
+          uint8_t* r = &raw[w][d + k][2 * lane * ESZ];
+          if constexpr (ESZ == 4) *reinterpret_cast<uint2*>(r) = make_uint2(e[k][0], e[k][1]);
+          else if constexpr (ESZ == 2) *reinterpret_cast<uint32_t*>(r) = e[k][0] | (e[k][1] << 16);
+          else *reinterpret_cast<uint16_t*>(r) = (uint16_t)(e[k][0] | (e[k][1] << 8));
+          if (ESZ == 1 && lane == 0) xsc[w][d + k] = sv[k];
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // ---- write them at context_len + d ----
+    if constexpr (KV != KV_I8_BLK) {
+      for (int d = d0; d < na; ++d) {
+        const int p = ctx + d;
+        const int64_t blk = blk_of(p);
+        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
+        const int o = p % BS;
+        const uint8_t* r = &raw[w][d][2 * lane * ESZ];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const uint32_t off = is_v ? tile_elem<true>(o, c0 + c, ESZ) : tile_elem<false>(o, c0 + c, ESZ);
+          if constexpr (ESZ == 4) *reinterpret_cast<uint32_t*>(t + off) = reinterpret_cast<const uint32_t*>(r)[c];
+          else if constexpr (ESZ == 2) *reinterpret_cast<uint16_t*>(t + off) = reinterpret_cast<const uint16_t*>(r)[c];
+          else t[off] = r[c];
+        }
+        if constexpr (KV == KV_I8_REF) {
+          if (lane == 0) reinterpret_cast<float*>(scales)[((uint64_t)blk * Hkv + h) * BS + o] = xsc[w][d];
+        }
+      }
+    } else {
+      // one run per destination block: [ctx + d, ctx + dend)
+      int d = d0;
+      while (d < na) {
+        const int p = ctx + d;
+        const int dend = min(na, (p / BS + 1) * BS - ctx);
+        const int64_t blk = blk_of(p);
+        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
+        uint16_t* sp = reinterpret_cast<uint16_t*>(scales) + (uint64_t)blk * Hkv + h;
+        int cd[BS][2];
+#pragma unroll
+        for (int u = 0; u < BS; ++u) {
+          cd[u][0] = (int8_t)t[is_v ? tile_elem<true>(u, c0, 1) : tile_elem<false>(u, c0, 1)];
+          cd[u][1] = (int8_t)t[is_v ? tile_elem<true>(u, c0 + 1, 1) : tile_elem<false>(u, c0 + 1, 1)];
+        }
+        const int o0 = p % BS;
+        float s_old = (o0 == 0) ? 0.f : h2f(*sp);
+        uint16_t s_bits = (o0 == 0) ? (uint16_t)0 : *sp;
+        for (int e = d; e < dend; ++e) {
+          const uint8_t* r = &raw[w][e][2 * lane];
+          const float sc = xsc[w][e];
+          blk_put(cd, (ctx + e) % BS, s_old, s_bits, (float)(int8_t)r[0] * sc, (float)(int8_t)r[1] * sc);
+        }
+        const int hi_written = (ctx + dend - 1) % BS;
+#pragma unroll
+        for (int u = 0; u < BS; ++u) {
+          if (u <= hi_written) {
+            t[is_v ? tile_elem<true>(u, c0, 1) : tile_elem<false>(u, c0, 1)] = (uint8_t)(int8_t)cd[u][0];
+            t[is_v ? tile_elem<true>(u, c0 + 1, 1) : tile_elem<false>(u, c0 + 1, 1)] = (uint8_t)(int8_t)cd[u][1];
+          }
+        }
+        if (lane == 0) *sp = s_bits;
+        d = dend;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  }
+}
+
 DEV uint64_t splitmix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
   x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1487,4 +1722,9 @@ extern "C" __global__ void __launch_bounds__(256) vk_copy_blocks(const CopyParam
 extern "C" __global__ void __launch_bounds__(256) vk_fill_normal_f16(const FillParams P) { fill_normal_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_decode_merge(const MergeParams P) { decode_merge(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_decode_merge_sk(const MergeParams P) { decode_merge_sk(P); }
+extern "C" __global__ void __launch_bounds__(256) vk_nixl_check(const NixlParams P) { nixl_check_kernel(P); }
+extern "C" __global__ void __launch_bounds__(256) vk_nixl_copy(const NixlParams P) { nixl_copy_kernel(P); }
+#define VK_COMMIT(KV) \
+  extern "C" __global__ void __launch_bounds__(128) vk_tree_commit_kv##KV(const CommitParams P) { tree_commit<KV>(P); }
+VK_COMMIT(0) VK_COMMIT(1) VK_COMMIT(2) VK_COMMIT(3)
 

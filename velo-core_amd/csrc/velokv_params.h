@@ -78,6 +78,49 @@ struct CopyParams {
   int32_t pairs[2 * kMaxCopyPairs];
 };
 
+// NIXL wire records (include/velokv.h): one launch covers up to kMaxNixlItems
+// records. Work unit = (record, page i, layer l), numbered r = i * n_layers + l
+// inside a record and cut into n_slices slices of kNixlSliceVecs 16-byte
+// vectors (one workgroup each); unit_begin is the record's first slice in the
+// launch.
+constexpr int kMaxNixlItems = 80;  // kernarg limit
+constexpr int kNixlSliceVecs = 256;  // 4 KB per workgroup of 256 lanes
+struct NixlItemArg {
+  uint64_t block_id;
+  uint64_t wire_offset;  // record start (16-aligned)
+  uint32_t token_len;
+  int32_t first_page;    // index into pages[]
+  uint32_t n_pages;      // ceil(token_len / bs)
+  uint32_t unit_begin;
+  uint32_t byte_len;     // payload bytes for this pool and layer range
+  uint32_t pad;
+};
+struct NixlParams {
+  uint8_t* base;         // pool base (all layers)
+  PoolGeom g;
+  const int32_t* pages;
+  uint8_t* wire;         // written by pack, read by unpack
+  uint64_t wire_bytes;
+  int32_t* status;       // status of this launch's first record
+  int32_t layer0, n_layers;
+  int32_t unpack;        // 0: pool -> wire, 1: wire -> pool
+  int32_t n_items;
+  int32_t n_slices;      // slices per unit: ceil(2 * codes bytes of a page / 4 KB)
+  NixlItemArg items[kMaxNixlItems];
+};
+
+// Accepted-path commit of a draft tree: grid (sequence, KV head, group of 8
+// layers), two waves (K, V).
+struct CommitParams {
+  uint8_t* base;
+  PoolGeom g;
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  const int32_t* accept;
+  const int32_t* n_accept;
+  int32_t bt_stride, accept_stride, n_seqs, layer0, n_layers;
+};
+
 struct MergeParams {
   const float* part_acc;
   const float* part_ml;

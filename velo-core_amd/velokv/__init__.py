@@ -4,13 +4,16 @@ Python host mirror of the reference's memory boundary (runtime.rs:8-42,
 paged_attention.rs:92-212, metal/runtime.rs:274-324): a HIP context, K/V pools
 in HBM with a slot block table, the block manager, and the three hot-path
 operations (append with INT8 quantization, paged decode attention, copy-on-write
-block copy) plus tree-verify attention. Every compute call goes to the gfx950
+block copy) plus tree-verify attention, the accepted-path commit of a verified
+tree, and NIXL wire-record pack/unpack of KV pages. Every compute call goes to the gfx950
 code object through libvelokv.so.
 """
 from ._capi import (  # noqa: F401
     DT_F16, DT_F32, DECODE_AUTO, DECODE_MFMA, DECODE_VALU, SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM, KV_F16, KV_F32, KV_I8_BLK, KV_I8_REF, VkError,
     ERR_BAD_ARG, ERR_INVALID_BLOCK_SIZE, ERR_OUT_OF_PAGES, ERR_TOO_MANY_PAGES, ERR_NO_FREE_SLOTS,
     ERR_NOT_WIRED, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_UNKNOWN_HANDLE,
+    NIXL_HEADER_BYTES, NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH,
+    NIXL_BAD_PAGE,
 )
 from .runtime import (  # noqa: F401
     BlockManager, Context, DeviceBuffer, Event, HipMemoryRuntime, KvCacheType, MemoryRuntimeConfig, Pool,

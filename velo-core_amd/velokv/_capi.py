@@ -38,6 +38,8 @@ KV_F32, KV_F16, KV_I8_REF, KV_I8_BLK = 0, 1, 2, 3
 DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
 SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM = 0, 1, 2
 DT_F32, DT_F16 = 0, 1
+NIXL_HEADER_BYTES = 16
+NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH, NIXL_BAD_PAGE = range(6)
 
 
 class VkError(RuntimeError):
@@ -77,6 +79,11 @@ class TreeArgs(C.Structure):
                 ("workspace_bytes", C.c_uint64)]
 
 
+class NixlItem(C.Structure):
+    _fields_ = [("block_id", C.c_uint64), ("token_len", C.c_uint32), ("first_page", C.c_int32),
+                ("wire_offset", C.c_uint64)]
+
+
 P = C.c_void_p
 I32 = C.c_int32
 U32 = C.c_uint32
@@ -109,6 +116,10 @@ PROTOTYPES = {
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
     "vk_tree_mask": [PI32, I32, PU32],
     "vk_copy_blocks": [P, P, PI32, I32, P],
+    "vk_tree_commit": [P, P, I32, I32, P, I32, P, P, I32, P, I32, P],
+    "vk_nixl_payload_bytes": [P, I32, U32, C.POINTER(U64)],
+    "vk_nixl_pack": [P, P, I32, I32, C.POINTER(NixlItem), I32, P, I32, P, U64, P, P],
+    "vk_nixl_unpack": [P, P, I32, I32, C.POINTER(NixlItem), I32, P, I32, P, U64, P, P],
     "vk_bm_create": [I32, I32, PP],
     "vk_bm_destroy": [P],
     "vk_bm_free_pages": [P, PI32],

@@ -162,6 +162,36 @@ class Context:
         check(lib().vk_copy_blocks(self.h, pool.h, p.ctypes.data_as(C.POINTER(C.c_int32)), len(p) // 2,
                                    _sptr(stream)))
 
+    def tree_commit(self, pool: "Pool", block_tables, bt_stride: int, context_lens, accept, accept_stride: int,
+                    n_accept, n_seqs: int, layer0: int = 0, n_layers: int | None = None, stream=None):
+        """vk_tree_commit: move the accepted path's K/V to context_len + d (device arrays)."""
+        n_layers = pool.n_layer - layer0 if n_layers is None else n_layers
+        check(lib().vk_tree_commit(self.h, pool.h, layer0, n_layers, _bptr(block_tables), bt_stride,
+                                   _bptr(context_lens), _bptr(accept), accept_stride, _bptr(n_accept), n_seqs,
+                                   _sptr(stream)))
+
+    @staticmethod
+    def _nixl_items(items):
+        arr = (_capi.NixlItem * max(1, len(items)))()
+        for i, (bid, tl, fp, off) in enumerate(items):
+            arr[i] = _capi.NixlItem(bid, tl, fp, off)
+        return arr
+
+    def nixl_pack(self, pool: "Pool", items, pages, n_pages: int, wire, wire_bytes: int, status, layer0: int = 0,
+                  n_layers: int | None = None, stream=None):
+        """vk_nixl_pack: items are (block_id, token_len, first_page, wire_offset) on the host;
+        pages, wire and status are device buffers."""
+        n_layers = pool.n_layer - layer0 if n_layers is None else n_layers
+        check(lib().vk_nixl_pack(self.h, pool.h, layer0, n_layers, self._nixl_items(items), len(items),
+                                 _bptr(pages), n_pages, _bptr(wire), wire_bytes, _bptr(status), _sptr(stream)))
+
+    def nixl_unpack(self, pool: "Pool", items, pages, n_pages: int, wire, wire_bytes: int, status, layer0: int = 0,
+                    n_layers: int | None = None, stream=None):
+        """vk_nixl_unpack: the inverse of nixl_pack, with per-record status."""
+        n_layers = pool.n_layer - layer0 if n_layers is None else n_layers
+        check(lib().vk_nixl_unpack(self.h, pool.h, layer0, n_layers, self._nixl_items(items), len(items),
+                                   _bptr(pages), n_pages, _bptr(wire), wire_bytes, _bptr(status), _sptr(stream)))
+
     def fill_normal_f16(self, buf: "DeviceBuffer", n: int, seed: int, row_len: int, outlier_scale: float = 1.0,
                         stream=None):
         check(lib().vk_fill_normal_f16(self.h, _bptr(buf), n, seed & 0xFFFFFFFFFFFFFFFF, row_len, outlier_scale,
@@ -302,6 +332,13 @@ class Pool:
     def nbytes(self) -> int:
         n = C.c_uint64()
         check(lib().vk_pool_bytes(self.h, C.byref(n)))
+        return n.value
+
+    def nixl_payload_bytes(self, token_len: int, n_layers: int | None = None) -> int:
+        """Payload bytes of one NIXL record of token_len tokens (vk_nixl_payload_bytes)."""
+        n = C.c_uint64()
+        check(lib().vk_nixl_payload_bytes(self.h, self.n_layer if n_layers is None else n_layers, token_len,
+                                          C.byref(n)))
         return n.value
 
     def layer_view(self, layer: int) -> _capi.LayerView:

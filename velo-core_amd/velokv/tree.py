@@ -70,6 +70,33 @@ class SpeculativeTree:
                     rejected = verified.expected[i] if i < len(verified.expected) else None
         return best, rejected
 
+    def path_nodes(self, node_idx: int) -> list[int]:
+        """Node indices from the root to node_idx (get_path, speculative.rs:81-94, as node indices)."""
+        path = []
+        cur: int | None = node_idx
+        while cur is not None:
+            path.append(cur)
+            cur = self.nodes[cur].parent
+        return path[::-1]
+
+    def best_path_nodes(self, verified: TreeVerifyResult) -> list[int]:
+        """Node indices of find_best_path's path (speculative.rs:97-128): the rows vk_tree_commit moves to
+        context_len + 0, 1, ... (root first)."""
+        n = len(self.nodes)
+        valid = [False] * n
+        valid[0] = True
+        for i in range(1, n):
+            p = self.nodes[i].parent
+            if p is not None and valid[p] and self.nodes[i].token == verified.expected[p]:
+                valid[i] = True
+        best: list[int] = []
+        for i in range(n):
+            if valid[i]:
+                path = self.path_nodes(i)
+                if len(path) >= len(best):
+                    best = path
+        return best
+
     def parents(self) -> np.ndarray:
         return np.array([-1 if nd.parent is None else nd.parent for nd in self.nodes], dtype=np.int32)
 
