@@ -70,6 +70,9 @@ def parse():
                     help="decode kernel family (vk_ctx_set_decode_kernel)")
     ap.add_argument("--sched", choices=["auto", "split", "stream"], default="auto",
                     help="decode work schedule (vk_ctx_set_decode_schedule)")
+    ap.add_argument("--rope", choices=["none", "interleaved", "half"], default="none",
+                    help="decode step: fused RoPE + append (vk_append_rope: K rotated before quantization, "
+                         "q rotated in place in the same launch) instead of the plain append")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", choices=["decode", "tree", "nixl"], default="decode",
@@ -164,11 +167,22 @@ def run_gpu(ctx, args, kv_name: str):
     d_lens = ctx.upload(lens)
     d_bt = ctx.upload(bt)
     stream = velokv.Stream(ctx)
+    rope = {"none": 0, "interleaved": velokv.ROPE_INTERLEAVED, "half": velokv.ROPE_HALF}[args.rope]
+    if rope:
+        n_pos = int(lens.max())
+        d_table = ctx.upload(velokv.rope_table(n_pos, HD, 500000.0))
+        d_pos = ctx.upload(lens.astype(np.int32) - 1)
 
     def step(i, evs=None):
         r = i % R
         for layer in range(NL):
-            ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
+            if evs is not None:
+                evs[layer][2].record(stream)
+            if rope:
+                ctx.append_rope(pool, layer, ks[r], vs[r], velokv.DT_F16, d_pos, new_slots, S, d_table, n_pos, rope,
+                                q=qs[r], q_dtype=velokv.DT_F16, n_heads=H, stream=stream)
+            else:
+                ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
             if evs is not None:
                 evs[layer][0].record(stream)
             ctx.paged_decode(pool, layer, qs[r], velokv.DT_F16, out, d_lens, S, H, int(lens.max()),
@@ -183,7 +197,7 @@ def run_gpu(ctx, args, kv_name: str):
     ctx.sync()
 
     start, end = velokv.Event(ctx), velokv.Event(ctx)
-    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
+    evs = [[[velokv.Event(ctx), velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
     start.record(stream)
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
@@ -192,10 +206,13 @@ def run_gpu(ctx, args, kv_name: str):
     ctx.sync()
     total_ms = start.elapsed_ms(end)
     dec_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
+    app_ms = [evs[i][l][2].elapsed_ms(evs[i][l][0]) for i in range(args.steps) for l in range(NL)]
 
     ms_step = total_ms / args.steps
     dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1])
     abytes = append_bytes(kv, S, Hkv)
+    if rope:  # q read and written (fp16), positions, one table row (D/2 cos, sin pairs) per token
+        abytes += 2 * S * H * HD * 2 + S * 4 + S * HD * 4
     step_bytes = NL * (dbytes + abytes)
     dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
@@ -208,6 +225,8 @@ def run_gpu(ctx, args, kv_name: str):
         "frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "decode_bytes_per_launch": dbytes,
         "append_bytes_per_launch": abytes,
+        "append": {"kernel": "vk_append_kv%d" % kv, "rope": args.rope, "ms_mean": round(float(np.mean(app_ms)), 5),
+                   "q_rotated_heads": S * H if rope else 0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(kname, S, L, H, Hkv, args.ragged),
@@ -574,9 +593,10 @@ def main():
     if args.also != "none" and args.also != args.kv:
         also = run_gpu(ctx, args, args.also)
     cpu = None if args.no_cpu else cpu_baseline(args)
-    workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=128, bs=16, %s KV, %d layers, append+decode per layer, pool %d blocks" %
+    workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=128, bs=16, %s KV, %d layers, %sappend+decode per layer, pool %d blocks" %
                 (args.seqs, "U[1024,%d]" % args.ctx if args.ragged else str(args.ctx), args.heads, args.kv_heads,
-                 "INT8 per-(block,head) fp16-scale" if args.kv == "int8" else "fp16", args.layers, args.pool_blocks))
+                 "INT8 per-(block,head) fp16-scale" if args.kv == "int8" else "fp16", args.layers,
+                 "" if args.rope == "none" else "RoPE(%s)+" % args.rope, args.pool_blocks))
     line = {
         "metric": "paged decode-attn achieved HBM GB/s (% peak) + tokens/s, B=64 ctx=8k, fp16/INT8 KV",
         "value": head["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

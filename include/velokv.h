@@ -180,6 +180,37 @@ int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* k,
               const void* v, int32_t in_dtype, const int64_t* slot_mapping,
               int32_t n_tok, void* stream);
 
+/* ---- RoPE fused into the append -------------------------------------------
+ * The reference rotates q and k in two ways that disagree: the Metal kernel
+ * pairs dims (2i, 2i+1) (kernels.metal:103-131, the GPU path) and the CPU model
+ * pairs (i, i + head_dim/2) (llama_cpu.rs:113-131). Both use the angle
+ * pos * freq_base^(-2i/head_dim) for pair i; the caller picks the style its
+ * weights were exported for. */
+#define VK_ROPE_INTERLEAVED 1  /* pairs (2i, 2i+1): kernels.metal:103-131    */
+#define VK_ROPE_HALF        2  /* pairs (i, i+D/2): llama_cpu.rs:113-131     */
+
+/* Host: fill out[n_pos][head_dim/2][2] (fp32) with cos and sin of the angle
+ * p * freq_base^(-2i/head_dim) of pair i at position p, evaluated in double
+ * precision and rounded to fp32 once. Upload it once; vk_append_rope reads it
+ * (the reference evaluates the angle in fp32 per call, llama_cpu.rs:124-125). */
+int vk_rope_table(float* out, int32_t n_pos, int32_t head_dim, float freq_base);
+
+/* vk_append with rotary position embedding fused in: each token's K row is
+ * rotated by its position (positions: dev int32 [n_tok]) before it is stored
+ * (and quantized for the I8 types); V is stored as is. When q is not NULL the
+ * same launch rotates q in place (dev [n_tok][n_heads][head_dim] of q_dtype;
+ * fp16 q is rounded to fp16 after the fp32 rotation). cos_sin is the dev table
+ * of vk_rope_table with n_pos positions; a token whose position is outside
+ * [0, n_pos) is skipped like a negative slot (not appended, q not rotated).
+ * Rotation: y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32, every product and sum
+ * rounded separately, the reference's expression order (llama_cpu.rs:128-129).
+ * Replaces the separate rope dispatch before kv_update (metal/model.rs:380-396)
+ * and rope() of the CPU model (llama_cpu.rs:99-111, called at 249). */
+int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q, int32_t q_dtype,
+                   int32_t n_heads, const void* k, const void* v, int32_t in_dtype,
+                   const int32_t* positions, const int64_t* slot_mapping, int32_t n_tok,
+                   const float* cos_sin, int32_t n_pos, int32_t rope_style, void* stream);
+
 typedef struct vk_decode_args {
   int32_t layer;
   const void* q;              /* dev [S][n_heads][head_dim] of q_dtype         */

@@ -327,3 +327,59 @@ def nixl_unpack(layers, items, pages, wire):
         nixl_scatter(layers, pg, payload)
         status.append(NIXL_OK)
     return status
+
+
+# ---- RoPE ------------------------------------------------------------------------
+
+ROPE_INTERLEAVED, ROPE_HALF = 1, 2
+
+
+def rope_table(n_pos, head_dim, freq_base):
+    out = np.zeros((n_pos, head_dim // 2, 2), np.float32)
+    lib().vko_rope_table(_ptr(out), C.c_int(n_pos), C.c_int(head_dim), C.c_float(freq_base))
+    return out
+
+
+def rope_apply(x, positions, style, table):
+    """Rotate rows x[..., n, head, D] (fp32) of token n by positions[n] (copy)."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    n_tok = x.shape[0]
+    D = x.shape[-1]
+    rows = x.reshape(n_tok, -1, D)
+    tb = np.ascontiguousarray(table, dtype=np.float32)
+    for n in range(n_tok):
+        for h in range(rows.shape[1]):
+            r = np.ascontiguousarray(rows[n, h])
+            lib().vko_rope_apply(_ptr(r), C.c_int(D), C.c_int(int(positions[n])), C.c_int(style), _ptr(tb))
+            rows[n, h] = r
+    return rows.reshape(x.shape)
+
+
+def ref_rope_cpu(x, pos, freq_base):
+    """llama_cpu.rs:113-131 on one head row (fp32)."""
+    r = np.array(x, dtype=np.float32, copy=True)
+    lib().vko_ref_rope_cpu(_ptr(r), C.c_int(r.size), C.c_int(pos), C.c_float(freq_base))
+    return r
+
+
+def ref_rope_metal(x, pos, freq_base):
+    """kernels.metal:103-131 on one head row (fp32)."""
+    r = np.array(x, dtype=np.float32, copy=True)
+    lib().vko_ref_rope_metal(_ptr(r), C.c_int(r.size), C.c_int(pos), C.c_float(freq_base))
+    return r
+
+
+def append_rope(layer: Layer, k, v, slot_mapping, positions, style, table, q=None):
+    """The fused RoPE + append: K rows rotated in fp32 then appended (V as is);
+    tokens with positions outside the table are skipped. Returns the rotated q
+    (in q's dtype) or None."""
+    n_pos = table.shape[0]
+    pos = np.asarray(positions, np.int64)
+    ok = (pos >= 0) & (pos < n_pos)
+    sm = np.where(ok, np.asarray(slot_mapping, np.int64), -1)
+    kr = rope_apply(np.asarray(k, np.float32), np.where(ok, pos, 0), style, table)
+    append(layer, np.ascontiguousarray(kr), np.ascontiguousarray(np.asarray(v, np.float32)), sm)
+    if q is None:
+        return None
+    qr = rope_apply(np.asarray(q, np.float32), np.where(ok, pos, 0), style, table).astype(q.dtype)
+    return np.where(ok.reshape((-1,) + (1,) * (q.ndim - 1)), qr, q)

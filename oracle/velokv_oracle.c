@@ -565,6 +565,64 @@ int vko_tree_commit(vko_layer* L, const int32_t* bt, int bt_stride, int ctx, con
   return 0;
 }
 
+/* ---- RoPE -------------------------------------------------------------- */
+
+/* apply_rope of the CPU model (llama_cpu.rs:113-131) on one head row:
+ * half-split pairs (i, i + D/2), angle pos / freq_base^(2i/D) in fp32. */
+void vko_ref_rope_cpu(float* x, int head_dim, int pos, float freq_base) {
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    const float theta = (float)pos / powf(freq_base, 2.0f * (float)i / (float)head_dim);
+    const float s = sinf(theta), c = cosf(theta);
+    const float x0 = x[i], x1 = x[i + half];
+    x[i] = x0 * c - x1 * s;
+    x[i + half] = x0 * s + x1 * c;
+  }
+}
+
+/* The Metal rope kernel (kernels.metal:103-131) on one head row: interleaved
+ * pairs (2j, 2j+1), angle pos * freq_base^(-(2j)/D) in fp32. */
+void vko_ref_rope_metal(float* x, int head_dim, int pos, float freq_base) {
+  for (int i = 0; i < head_dim; i += 2) {
+    const float theta = powf(freq_base, -(float)i / (float)head_dim);
+    const float m = (float)pos * theta;
+    const float c = cosf(m), s = sinf(m);
+    const float x0 = x[i], x1 = x[i + 1];
+    x[i] = x0 * c - x1 * s;
+    x[i + 1] = x0 * s + x1 * c;
+  }
+}
+
+/* cos / sin table [n_pos][D/2][2] of the angle p * freq_base^(-2i/D), in double
+ * precision, rounded to fp32 once (what vk_rope_table computes). */
+void vko_rope_table(float* out, int n_pos, int head_dim, float freq_base) {
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    const double inv = pow((double)freq_base, -2.0 * (double)i / (double)head_dim);
+    for (int p = 0; p < n_pos; ++p) {
+      const double a = (double)p * inv;
+      out[((int64_t)p * half + i) * 2] = (float)cos(a);
+      out[((int64_t)p * half + i) * 2 + 1] = (float)sin(a);
+    }
+  }
+}
+
+/* Rotate one head row in place with the table: style 1 = interleaved pairs
+ * (2i, 2i+1), style 2 = half-split pairs (i, i + D/2); y0 = x0 c - x1 s,
+ * y1 = x0 s + x1 c in fp32, no contraction (this file builds with
+ * -ffp-contract=off). */
+void vko_rope_apply(float* x, int head_dim, int pos, int style, const float* table) {
+  const int half = head_dim / 2;
+  const float* row = table + (int64_t)pos * head_dim;
+  for (int i = 0; i < half; ++i) {
+    const float c = row[2 * i], s = row[2 * i + 1];
+    const int a = style == 1 ? 2 * i : i, b = style == 1 ? 2 * i + 1 : i + half;
+    const float x0 = x[a], x1 = x[b];
+    x[a] = x0 * c - x1 * s;
+    x[b] = x0 * s + x1 * c;
+  }
+}
+
 /* ---- NIXL wire format (nixl.rs:24-61) ------------------------------------ */
 
 /* serialize_block (nixl.rs:36-43): block_id.to_le_bytes(), (token_len as

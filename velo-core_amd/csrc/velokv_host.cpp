@@ -432,6 +432,59 @@ extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* 
   return launch(ctx, name.c_str(), dim3((unsigned)n_tok, (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
 }
 
+extern "C" int vk_rope_table(float* out, int32_t n_pos, int32_t head_dim, float freq_base) {
+  if (!out || n_pos < 0 || head_dim <= 0 || head_dim % 2) return fail(VK_ERR_BAD_ARG, "bad rope table arguments");
+  if (!(freq_base > 0.f)) return fail(VK_ERR_BAD_ARG, "freq_base must be positive");
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    const double inv = std::pow((double)freq_base, -2.0 * (double)i / (double)head_dim);
+    for (int32_t p = 0; p < n_pos; ++p) {
+      const double a = (double)p * inv;
+      out[((int64_t)p * half + i) * 2] = (float)std::cos(a);
+      out[((int64_t)p * half + i) * 2 + 1] = (float)std::sin(a);
+    }
+  }
+  return VK_OK;
+}
+
+extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q, int32_t q_dtype, int32_t n_heads,
+                              const void* k, const void* v, int32_t in_dtype, const int32_t* positions,
+                              const int64_t* slot_mapping, int32_t n_tok, const float* cos_sin, int32_t n_pos,
+                              int32_t rope_style, void* stream) {
+  int rc = check_pool(ctx, pool);
+  if (rc) return rc;
+  if (layer < 0 || layer >= pool->desc.n_layer) return fail(VK_ERR_BAD_ARG, "layer %d out of range", layer);
+  if (in_dtype != VK_DT_F32 && in_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "in_dtype %d", in_dtype);
+  if (rope_style != VK_ROPE_INTERLEAVED && rope_style != VK_ROPE_HALF)
+    return fail(VK_ERR_BAD_ARG, "rope_style %d (VK_ROPE_INTERLEAVED or VK_ROPE_HALF)", rope_style);
+  if (pool->desc.head_dim != kHD) return fail(VK_ERR_UNSUPPORTED, "head_dim %d", pool->desc.head_dim);
+  if (n_tok < 0 || n_pos <= 0) return fail(VK_ERR_BAD_ARG, "n_tok < 0 or n_pos <= 0");
+  if (q && (n_heads <= 0 || (q_dtype != VK_DT_F32 && q_dtype != VK_DT_F16)))
+    return fail(VK_ERR_BAD_ARG, "q needs n_heads > 0 and q_dtype VK_DT_F32 / VK_DT_F16");
+  if (n_tok == 0) return VK_OK;
+  if (!k || !v || !slot_mapping || !positions || !cos_sin) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  AppendParams p{};
+  p.base = pool->base;
+  p.g = pool->geom;
+  p.layer = layer;
+  p.in_dtype = in_dtype;
+  p.k = k;
+  p.v = v;
+  p.slot_mapping = slot_mapping;
+  p.n_tok = n_tok;
+  p.rope = rope_style;
+  p.positions = positions;
+  p.cos_sin = cos_sin;
+  p.n_pos = n_pos;
+  p.n_heads = q ? n_heads : 0;
+  p.q = q;
+  p.q_dtype = q_dtype;
+  const unsigned rows = (unsigned)pool->desc.n_kv_heads + (q ? (unsigned)((n_heads + 1) / 2) : 0u);
+  const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
+  if ((rc = set_device(ctx))) return rc;
+  return launch(ctx, name.c_str(), dim3((unsigned)n_tok, rows), dim3(128), p, stream);
+}
+
 namespace {
 
 // Split-K workspace: the caller's buffer when given (and large enough), else the

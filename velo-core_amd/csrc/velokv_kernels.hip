@@ -1207,6 +1207,58 @@ DEV void load_x2(const void* src, int in_dtype, int64_t off, float& x0, float& x
   }
 }
 
+// ---- RoPE (fused into the append) --------------------------------------------
+// Pair i of a head row at position p is rotated by the table's (cos, sin) of
+// angle p * base^(-2i/D): ROPE_INTERLEAVED pairs dims (2i, 2i+1)
+// (kernels.metal:103-131), ROPE_HALF pairs dims (i, i + D/2)
+// (llama_cpu.rs:113-131). y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32 with
+// every product and sum rounded separately (no fused multiply-add), the
+// reference's expression order. Lane l holds dims 2l, 2l+1 of the row.
+DEV void rope_rotate(int style, const float* cos_sin, int pos, float& x0, float& x1) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const float* row = cos_sin + (int64_t)pos * HD;  // D/2 pairs of (cos, sin)
+  if (style == ROPE_INTERLEAVED) {
+    const float2 cs = reinterpret_cast<const float2*>(row)[lane];
+    const float y0 = x0 * cs.x - x1 * cs.y;
+    const float y1 = x0 * cs.y + x1 * cs.x;
+    x0 = y0;
+    x1 = y1;
+  } else {
+    const float p0 = __shfl_xor(x0, 32, WAVE), p1 = __shfl_xor(x1, 32, WAVE);  // dims d ^ 64
+    const float4 cs = reinterpret_cast<const float4*>(row)[lane & 31];  // pairs 2(l%32), 2(l%32)+1
+    if (lane < 32) {  // first half: y = x c - partner s
+      const float y0 = x0 * cs.x - p0 * cs.y;
+      const float y1 = x1 * cs.z - p1 * cs.w;
+      x0 = y0;
+      x1 = y1;
+    } else {          // second half: y = partner s + x c
+      const float y0 = p0 * cs.y + x0 * cs.x;
+      const float y1 = p1 * cs.w + x1 * cs.z;
+      x0 = y0;
+      x1 = y1;
+    }
+  }
+}
+
+// Flat slot of token m, or -1 when it is padding (negative slot) or, with RoPE,
+// its position is outside the table.
+DEV int64_t token_slot(const AppendParams& P, int m) {
+  const int64_t slot = P.slot_mapping[m];
+  if (slot < 0) return -1;
+  if (P.rope != ROPE_NONE) {
+    const int pos = P.positions[m];
+    if (pos < 0 || pos >= P.n_pos) return -1;
+  }
+  return slot;
+}
+
+// K/V row elements (dims 2l, 2l+1) of token m, head h, rotated for K when RoPE is on.
+DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h, float& x0, float& x1) {
+  load_x2(src, P.in_dtype, ((int64_t)m * P.g.n_kv_heads + h) * HD + 2 * lane_id(), x0, x1);
+  if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, P.positions[m], x0, x1);
+}
+
 // Byte offset inside a (block, head) tile of element (token, dim).
 template <bool IS_V>
 DEV uint32_t tile_elem(int tok, int d, int esz) {
@@ -1258,14 +1310,14 @@ template <bool IS_V>
 DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales) {
   const int lane = lane_id();
   const int n = blockIdx.x, h = blockIdx.y;
-  const int64_t slot = P.slot_mapping[n];
+  const int64_t slot = token_slot(P, n);
   if (slot < 0) return;
   const int bs = BS;
   const int64_t b = slot / bs;
   // Not the first token of its run when the previous non-padding token of the
   // call is in the same block (padding slots are negative).
   for (int m = n - 1; m >= 0; --m) {
-    const int64_t prev = P.slot_mapping[m];
+    const int64_t prev = token_slot(P, m);
     if (prev < 0) continue;
     if (prev / bs == b) return;
     break;
@@ -1288,14 +1340,14 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
   int hi_written = -1;
   for (int m = n; m < P.n_tok;) {
     float x0, x1;
-    load_x2(src, P.in_dtype, ((int64_t)m * Hkv + h) * HD + d0, x0, x1);
+    load_kv(P, src, IS_V, m, h, x0, x1);
     blk_put(cd, o, s_old, s_bits, x0, x1);
     hi_written = max(hi_written, o);
     // next token of the run (padding slots in between are skipped)
     ++m;
-    while (m < P.n_tok && P.slot_mapping[m] < 0) ++m;
+    while (m < P.n_tok && token_slot(P, m) < 0) ++m;
     if (m >= P.n_tok) break;
-    const int64_t ns = P.slot_mapping[m];
+    const int64_t ns = token_slot(P, m);
     if (ns / bs != b) break;
     o = (int)(ns % bs);
     if (o == 0) { s_old = 0.f; s_bits = 0; }
@@ -1315,7 +1367,7 @@ template <bool IS_V>
 DEV void append_ref(const AppendParams& P, const void* src, uint8_t* codes, float* scales) {
   const int lane = lane_id();
   const int n = blockIdx.x, h = blockIdx.y;
-  const int64_t slot = P.slot_mapping[n];
+  const int64_t slot = token_slot(P, n);
   if (slot < 0) return;
   const int64_t b = slot / BS;
   const int o = (int)(slot % BS);
@@ -1323,7 +1375,7 @@ DEV void append_ref(const AppendParams& P, const void* src, uint8_t* codes, floa
   const int Hkv = P.g.n_kv_heads;
   const int d0 = 2 * lane;
   float x0, x1;
-  load_x2(src, P.in_dtype, ((int64_t)n * Hkv + h) * HD + d0, x0, x1);
+  load_kv(P, src, IS_V, n, h, x0, x1);
   const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
   const float scale = amax / 127.0f;
   const float inv = amax > 0.f ? 127.0f / amax : 0.f;
@@ -1338,7 +1390,7 @@ template <bool IS_V, int ESZ>
 DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes) {
   const int lane = lane_id();
   const int n = blockIdx.x, h = blockIdx.y;
-  const int64_t slot = P.slot_mapping[n];
+  const int64_t slot = token_slot(P, n);
   if (slot < 0) return;
   const int64_t b = slot / BS;
   const int o = (int)(slot % BS);
@@ -1346,14 +1398,14 @@ DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes) {
   const int Hkv = P.g.n_kv_heads;
   const int d0 = 2 * lane;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
-  if (ESZ == 2 && P.in_dtype == DT_F16) {
+  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE)) {
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src) + ((int64_t)n * Hkv + h) * HD + d0;
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2)) = s16[0];
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2)) = s16[1];
     return;
   }
   float x0, x1;
-  load_x2(src, P.in_dtype, ((int64_t)n * Hkv + h) * HD + d0, x0, x1);
+  load_kv(P, src, IS_V, n, h, x0, x1);
   if constexpr (ESZ == 2) {
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2)) = f2h(x0);
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2)) = f2h(x1);
@@ -1365,6 +1417,23 @@ DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes) {
 
 template <int KV>
 DEV void append_kernel(const AppendParams& P) {
+  if ((int)blockIdx.y >= P.g.n_kv_heads) {  // RoPE of two query heads of token blockIdx.x
+    const int n = blockIdx.x;
+    const int head = 2 * ((int)blockIdx.y - P.g.n_kv_heads) + (int)(threadIdx.x / WAVE);
+    const int pos = P.positions[n];
+    if (head >= P.n_heads || pos < 0 || pos >= P.n_pos) return;
+    const int64_t off = ((int64_t)n * P.n_heads + head) * HD + 2 * lane_id();
+    float x0, x1;
+    load_x2(P.q, P.q_dtype, off, x0, x1);
+    rope_rotate(P.rope, P.cos_sin, pos, x0, x1);
+    if (P.q_dtype == DT_F16) {
+      reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(P.q) + off)[0] =
+          (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+    } else {
+      reinterpret_cast<float2*>(reinterpret_cast<float*>(P.q) + off)[0] = make_float2(x0, x1);
+    }
+    return;
+  }
   const bool is_v = (threadIdx.x >= WAVE);
   uint8_t* L = P.base + (uint64_t)P.layer * P.g.layer_stride;
   const void* src = is_v ? P.v : P.k;

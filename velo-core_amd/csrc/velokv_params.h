@@ -19,6 +19,11 @@ struct PoolGeom {
   int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
 };
 
+enum RopeStyle : int32_t { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
+
+// Append of n_tok tokens; grid (n_tok, Hkv + ceil(n_heads / 2)): rows y < Hkv
+// write K (wave 0) and V (wave 1) of KV head y; with RoPE, rows y >= Hkv rotate
+// query heads 2(y - Hkv) and 2(y - Hkv) + 1 in place.
 struct AppendParams {
   uint8_t* base;            // pool base (all layers)
   PoolGeom g;
@@ -28,6 +33,13 @@ struct AppendParams {
   const void* v;
   const int64_t* slot_mapping;
   int32_t n_tok;
+  int32_t rope;             // RopeStyle; ROPE_NONE = plain append
+  const int32_t* positions; // [n_tok] RoPE positions (rope only)
+  const float* cos_sin;     // [n_pos][D/2][2] cos, sin of pair i at each position
+  int32_t n_pos;
+  int32_t n_heads;          // query heads rotated in place (0 = none)
+  void* q;                  // [n_tok][n_heads][D] of q_dtype
+  int32_t q_dtype;
 };
 
 struct SlotMapParams {

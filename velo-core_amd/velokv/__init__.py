@@ -13,10 +13,10 @@ from ._capi import (  # noqa: F401
     ERR_BAD_ARG, ERR_INVALID_BLOCK_SIZE, ERR_OUT_OF_PAGES, ERR_TOO_MANY_PAGES, ERR_NO_FREE_SLOTS,
     ERR_NOT_WIRED, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_UNKNOWN_HANDLE,
     NIXL_HEADER_BYTES, NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH,
-    NIXL_BAD_PAGE,
+    NIXL_BAD_PAGE, ROPE_HALF, ROPE_INTERLEAVED,
 )
 from .runtime import (  # noqa: F401
     BlockManager, Context, DeviceBuffer, Event, HipMemoryRuntime, KvCacheType, MemoryRuntimeConfig, Pool,
-    SlotPool, Stream, kv_bytes_per_token_per_head,
+    SlotPool, Stream, kv_bytes_per_token_per_head, rope_table,
 )
 from .tree import SpeculativeTree, TreeNode, TreeVerifyResult, branching_tree  # noqa: F401

@@ -39,6 +39,7 @@ DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
 SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM = 0, 1, 2
 DT_F32, DT_F16 = 0, 1
 NIXL_HEADER_BYTES = 16
+ROPE_INTERLEAVED, ROPE_HALF = 1, 2
 NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH, NIXL_BAD_PAGE = range(6)
 
 
@@ -109,6 +110,8 @@ PROTOTYPES = {
     "vk_bind_slot": [P, U32, PU32, I32],
     "vk_slot_mapping": [P, P, P, I32, P, P, I32, P, P],
     "vk_append": [P, P, I32, P, P, I32, P, I32, P],
+    "vk_rope_table": [C.POINTER(C.c_float), I32, I32, C.c_float],
+    "vk_append_rope": [P, P, I32, P, I32, I32, P, P, I32, P, P, I32, P, I32, I32, P],
     "vk_paged_decode_workspace": [P, C.POINTER(DecodeArgs), C.POINTER(U64)],
     "vk_paged_decode": [P, P, C.POINTER(DecodeArgs), P],
     "vk_paged_decode_kernel": [P, C.POINTER(DecodeArgs), C.c_char_p, C.c_size_t],

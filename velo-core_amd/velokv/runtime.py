@@ -114,6 +114,13 @@ class Context:
         check(lib().vk_append(self.h, pool.h, layer, _bptr(k), _bptr(v), in_dtype, _bptr(slot_mapping), n_tok,
                               _sptr(stream)))
 
+    def append_rope(self, pool: "Pool", layer: int, k, v, in_dtype: int, positions, slot_mapping, n_tok: int,
+                    cos_sin, n_pos: int, style: int, q=None, q_dtype: int = DT_F16, n_heads: int = 0, stream=None):
+        """vk_append_rope: K rotated by position and appended, q (optional) rotated in place."""
+        check(lib().vk_append_rope(self.h, pool.h, layer, _bptr(q), q_dtype, n_heads, _bptr(k), _bptr(v), in_dtype,
+                                   _bptr(positions), _bptr(slot_mapping), n_tok, _bptr(cos_sin), n_pos, style,
+                                   _sptr(stream)))
+
     def paged_decode(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, n_seqs: int, n_heads: int,
                      max_context_len: int, block_tables=None, bt_stride: int = 0, seq_rows=None, scale: float = 0.0,
                      partition_tokens: int = 0, workspace=None, workspace_bytes: int = 0, stream=None,
@@ -196,6 +203,13 @@ class Context:
                         stream=None):
         check(lib().vk_fill_normal_f16(self.h, _bptr(buf), n, seed & 0xFFFFFFFFFFFFFFFF, row_len, outlier_scale,
                                        _sptr(stream)))
+
+
+def rope_table(n_pos: int, head_dim: int, freq_base: float) -> np.ndarray:
+    """vk_rope_table: float32 [n_pos][head_dim/2][2] cos, sin (host)."""
+    out = np.zeros((n_pos, head_dim // 2, 2), np.float32)
+    check(lib().vk_rope_table(out.ctypes.data_as(C.POINTER(C.c_float)), n_pos, head_dim, freq_base))
+    return out
 
 
 def _bptr(b):
