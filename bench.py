@@ -263,27 +263,40 @@ def run_tree(ctx, args):
     suffix = synth.rng(4).integers(0, args.max_suffix + 1, S).astype(np.int32)
     committed = prefix + suffix
     total = committed + N
-    pblocks = -(-prefix // BS)
     stride = int(-(-int(total.max()) // BS))
-    # pages: shared prefix, then per sequence its own pages; a partial last committed
-    # block gets a second page (the copy-on-write source, i.e. the shared original)
-    nxt = pblocks
+    # Pages from the radix prefix cache (vk_radix_cache_sequence): the prefix is
+    # cached once; every prompt (prefix + its own suffix) aliases the prefix's
+    # pages and gets fresh pages for its suffix, then grows by the N draft slots.
+    # The cache keeps a second handle on every prompt's pages, so a partially
+    # filled last prompt page is shared and is copied on write (vk_bm_cow) before
+    # the drafts are appended: that copy is the step's vk_copy_blocks.
+    budget = -(-prefix // BS) + int(sum(-(-int(t) // BS) + 1 for t in total))
+    bm = velokv.BlockManager(BS, budget)
+    rc = velokv.RadixCache(bm)
+    prefix_tokens = list(range(prefix))
+    t0 = time.perf_counter()
+    rc.cache_sequence(prefix_tokens, seq_handle=1 << 40, cache_handle=(1 << 40) + 1)
+    bm.release(1 << 40)
     tables = np.zeros((S, stride), np.int32)
-    tables[:, :pblocks] = np.arange(pblocks, dtype=np.int32)
+    fill_tables = np.zeros((S, stride), np.int32)
     pairs = []
-    fill_tables = tables.copy()
     for s_ in range(S):
-        own = -(-int(total[s_]) // BS) - pblocks
-        tables[s_, pblocks:pblocks + own] = np.arange(nxt, nxt + own)
-        nxt += own
-        fill_tables[s_] = tables[s_]
+        toks = prefix_tokens + [10 ** 6 + s_ * 1000 + t for t in range(int(suffix[s_]))]
+        r = rc.cache_sequence(toks, seq_handle=2 * s_, cache_handle=2 * s_ + 1)
+        pages = bm.extend(2 * s_, int(total[s_]))
+        fill_tables[s_, :len(pages)] = pages
         c = int(committed[s_])
-        if c % BS and c > prefix:
-            src = nxt
-            nxt += 1
-            fill_tables[s_, c // BS] = src
-            pairs.append((src, int(tables[s_, c // BS])))
-    n_blocks = nxt
+        if c % BS:
+            cw = bm.cow(2 * s_, c // BS)
+            if cw is not None:
+                pairs.append(cw)
+            pages = bm.materialize_span(2 * s_)
+        tables[s_, :len(pages)] = pages
+    host_ms = (time.perf_counter() - t0) * 1e3
+    used_pages = budget - bm.free_pages()
+    reference_pages = -(-prefix // BS) + int(sum(-(-int(t) // BS) for t in total))  # a fresh page list per prompt
+    n_blocks = int(max(tables.max(), fill_tables.max(), max((max(p_) for p_ in pairs), default=0))) + 1
+    pblocks = -(-prefix // BS)
     perm = synth.rng(5).permutation(n_blocks).astype(np.int32)  # scatter pages over the pool
     tables, fill_tables = perm[tables], perm[fill_tables]
     pairs = perm[np.array(pairs, np.int64)] if pairs else np.zeros((0, 2), np.int32)
@@ -393,6 +406,9 @@ def run_tree(ctx, args):
         "tokens_per_s": round(S / (ms_step * 1e-3), 1),
         "draft_tokens_per_s": round(S * N / (ms_step * 1e-3), 1),
         "unique_bytes_per_launch": uniq, "logical_bytes_per_launch": logical, "cow_pairs": int(len(pairs)),
+        "radix": {"host_ms": round(host_ms, 3), "pages": int(used_pages), "pages_without_aliasing": int(reference_pages),
+                  "pool_gb": round(pool.nbytes / 1e9, 3),
+                  "pool_gb_without_aliasing": round(pool.nbytes / 1e9 * reference_pages / used_pages, 3)},
         "commit": {"kernel": "vk_tree_commit_kv%d" % kv, "ms_mean": round(commit_ms, 5), "layers": NL,
                    "accepted_tokens": int(n_acc.sum()), "moved_tokens": int(moved_tok)},
         "logical_gbs": round(logical / (tv_mean * 1e-3) / 1e9, 2),

@@ -390,6 +390,7 @@ int vk_nixl_unpack(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
 int vk_bm_create(int32_t block_size, int32_t total_pages, vk_block_manager** out);
 int vk_bm_destroy(vk_block_manager* bm);
 int vk_bm_free_pages(const vk_block_manager* bm, int32_t* out);
+int vk_bm_block_size(const vk_block_manager* bm, int32_t* out);
 /* allocate(handle, token_len): pops ceil(token_len/bs) pages; pages_out gets them. */
 int vk_bm_allocate(vk_block_manager* bm, uint64_t handle, int64_t token_len,
                    uint32_t* pages_out, int32_t cap, int32_t* n_out);
@@ -404,12 +405,61 @@ int vk_bm_pages(const vk_block_manager* bm, uint64_t handle, uint32_t* pages_out
 int vk_bm_fork(vk_block_manager* bm, uint64_t parent, uint64_t child,
                int64_t shared_tokens, int64_t token_len, uint32_t* pages_out,
                int32_t cap, int32_t* n_out);
+/* Grow `handle` to cover token_len tokens: fresh pages are appended (FIFO);
+ * a handle that already covers them is unchanged. For a sequence that outgrows
+ * the pages its prompt was given (decode tokens, draft-tree slots); the
+ * reference binds a slot's pages once at prefill (engine.rs:266-268). */
+int vk_bm_extend(vk_block_manager* bm, uint64_t handle, int64_t token_len,
+                 uint32_t* pages_out, int32_t cap, int32_t* n_out);
 /* Before writing into page index `page_idx` of `handle`: if that page is
  * shared, replace it by a fresh page and report the (src, dst) copy to issue
  * through vk_copy_blocks; *copied = 0 when the page was already private. */
 int vk_bm_cow(vk_block_manager* bm, uint64_t handle, int32_t page_idx,
               int32_t* src, int32_t* dst, int32_t* copied);
 int vk_bm_refcount(const vk_block_manager* bm, uint32_t page, int32_t* out);
+
+/* ---- prefix cache over page handles ------------------------------------------
+ * RadixCache (radix_cache.rs:28-264): a radix tree of token edges whose nodes
+ * hold KV handles, with the reference's insert / lookup / edge split, logical
+ * clock and coldest-first eviction (same results as the reference on the same
+ * calls). Handles are block-manager handles (vk_bm_*), token_len = the tokens
+ * inserted. Created with a block manager, the cache owns the handles inserted
+ * into it and releases replaced and evicted ones there (pages return to the
+ * free list once no other handle references them); with bm = NULL handles are
+ * opaque ids and nothing is released, as in the reference. Host only. */
+typedef struct vk_radix vk_radix;
+/* RadixCache::new / with_capacity_tokens (capacity_tokens < 0: no limit). */
+int vk_radix_create(vk_block_manager* bm, int64_t capacity_tokens, vk_radix** out);
+/* Releases every handle the cache holds (bound caches). */
+int vk_radix_destroy(vk_radix* rc);
+/* RadixCache::insert (radix_cache.rs:73-99): *has_replaced / *replaced report
+ * the handle this prefix held before (released when bound). */
+int vk_radix_insert(vk_radix* rc, const uint32_t* tokens, int32_t n_tokens, uint64_t handle,
+                    uint64_t* replaced, int32_t* has_replaced);
+/* RadixCache::lookup (radix_cache.rs:101-140): longest cached prefix. */
+int vk_radix_lookup(vk_radix* rc, const uint32_t* tokens, int32_t n_tokens, int32_t* matched,
+                    uint64_t* handle, int32_t* has_handle);
+int vk_radix_len(const vk_radix* rc, int32_t* out);
+int vk_radix_resident_tokens(const vk_radix* rc, int64_t* out);
+int vk_radix_capacity_tokens(const vk_radix* rc, int64_t* out);   /* -1 = no limit */
+int vk_radix_set_capacity(vk_radix* rc, int64_t capacity_tokens);
+/* RadixCache::evict_coldest (radix_cache.rs:163-187); evicted handles in order. */
+int vk_radix_evict_coldest(vk_radix* rc, int64_t tokens, uint64_t* evicted, int32_t cap,
+                           int32_t* n_out);
+/* The engine's prefill + cache_sequence (engine.rs:435-494) with the cached
+ * prefix's pages aliased instead of allocated again: looks up the longest
+ * cached prefix (matched tokens m), gives seq_handle the prefix's pages
+ * (reference count + 1) and fresh pages for the rest of the prompt, and, when
+ * the prompt continues inside a partially filled shared page, makes that page
+ * private (*has_cow = 1: copy *cow_src to *cow_dst with vk_copy_blocks before
+ * writing). When m < n_tokens the whole prompt is then cached under
+ * cache_handle, a second handle on the same pages owned by the cache (the
+ * reference caches the prompt only on a miss, engine.rs:437-441). pages_out
+ * receives seq_handle's pages. Needs a bound cache. */
+int vk_radix_cache_sequence(vk_radix* rc, const uint32_t* tokens, int32_t n_tokens,
+                            uint64_t seq_handle, uint64_t cache_handle, int32_t* matched_tokens,
+                            uint32_t* pages_out, int32_t cap, int32_t* n_pages, int32_t* cow_src,
+                            int32_t* cow_dst, int32_t* has_cow);
 
 /* ---- device memory and stream helpers for hosts without their own HIP ----- */
 int vk_dev_alloc(vk_ctx* ctx, uint64_t bytes, void** out);

@@ -48,7 +48,7 @@ def build_host_library():
     tmp = out + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{INCLUDE}", f"-I{CSRC}",
-          os.path.join(CSRC, "velokv_host.cpp"), "-o", tmp,
+          os.path.join(CSRC, "velokv_host.cpp"), os.path.join(CSRC, "velokv_radix.cpp"), "-o", tmp,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, out)
     return out

@@ -80,6 +80,13 @@ std::string default_code_object_path() {
 
 }  // namespace
 
+// Error channel shared with the other translation units of the library
+// (velokv_radix.cpp): sets the calling thread's vk_last_error() message.
+int vk_internal_set_error(int code, const char* msg) {
+  g_last_error = msg ? msg : "";
+  return code;
+}
+
 struct vk_ctx {
   int device = 0;
   std::string arch;
@@ -1076,6 +1083,12 @@ extern "C" int vk_bm_destroy(vk_block_manager* bm) {
   return VK_OK;
 }
 
+extern "C" int vk_bm_block_size(const vk_block_manager* bm, int32_t* out) {
+  if (!bm || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  *out = bm->block_size;
+  return VK_OK;
+}
+
 extern "C" int vk_bm_free_pages(const vk_block_manager* bm, int32_t* out) {
   if (!bm || !out) return fail(VK_ERR_BAD_ARG, "null argument");
   *out = (int32_t)bm->free_pages.size();
@@ -1130,6 +1143,22 @@ extern "C" int vk_bm_fork(vk_block_manager* bm, uint64_t parent, uint64_t child,
   pages.insert(pages.end(), fresh.begin(), fresh.end());
   bm->mappings[child] = pages;
   return copy_pages(pages, pages_out, cap, n_out);
+}
+
+extern "C" int vk_bm_extend(vk_block_manager* bm, uint64_t handle, int64_t token_len, uint32_t* pages_out,
+                            int32_t cap, int32_t* n_out) {
+  if (!bm) return fail(VK_ERR_BAD_ARG, "null manager");
+  auto it = bm->mappings.find(handle);
+  if (it == bm->mappings.end()) return fail(VK_ERR_UNKNOWN_HANDLE, "unknown KV handle %llu", (unsigned long long)handle);
+  if (token_len < 0) return fail(VK_ERR_BAD_ARG, "token_len < 0");
+  const int64_t need = bm->pages_for(token_len) - (int64_t)it->second.size();
+  if (need > 0) {
+    std::vector<uint32_t> fresh;
+    int rc = take_pages(bm, need, &fresh);
+    if (rc) return rc;
+    it->second.insert(it->second.end(), fresh.begin(), fresh.end());
+  }
+  return copy_pages(it->second, pages_out, cap, n_out);
 }
 
 extern "C" int vk_bm_cow(vk_block_manager* bm, uint64_t handle, int32_t page_idx, int32_t* src, int32_t* dst,

@@ -16,7 +16,8 @@ from ._capi import (  # noqa: F401
     NIXL_BAD_PAGE, ROPE_HALF, ROPE_INTERLEAVED,
 )
 from .runtime import (  # noqa: F401
-    BlockManager, Context, DeviceBuffer, Event, HipMemoryRuntime, KvCacheType, MemoryRuntimeConfig, Pool,
+    BlockManager, CacheLookup, CachedSequence, Context, DeviceBuffer, Event, HipMemoryRuntime, KvCacheType,
+    MemoryRuntimeConfig, Pool, RadixCache,
     SlotPool, Stream, kv_bytes_per_token_per_head, rope_table,
 )
 from .tree import SpeculativeTree, TreeNode, TreeVerifyResult, branching_tree  # noqa: F401

@@ -132,6 +132,18 @@ PROTOTYPES = {
     "vk_bm_fork": [P, U64, U64, I64, I64, PU32, I32, PI32],
     "vk_bm_cow": [P, U64, I32, PI32, PI32, PI32],
     "vk_bm_refcount": [P, U32, PI32],
+    "vk_bm_block_size": [P, PI32],
+    "vk_bm_extend": [P, U64, I64, PU32, I32, PI32],
+    "vk_radix_create": [P, I64, PP],
+    "vk_radix_destroy": [P],
+    "vk_radix_insert": [P, PU32, I32, U64, C.POINTER(U64), PI32],
+    "vk_radix_lookup": [P, PU32, I32, PI32, C.POINTER(U64), PI32],
+    "vk_radix_len": [P, PI32],
+    "vk_radix_resident_tokens": [P, C.POINTER(I64)],
+    "vk_radix_capacity_tokens": [P, C.POINTER(I64)],
+    "vk_radix_set_capacity": [P, I64],
+    "vk_radix_evict_coldest": [P, I64, C.POINTER(U64), I32, PI32],
+    "vk_radix_cache_sequence": [P, PU32, I32, U64, U64, PI32, PU32, I32, PI32, PI32, PI32, PI32],
     "vk_dev_alloc": [P, U64, PP],
     "vk_dev_free": [P, P],
     "vk_memcpy_h2d": [P, P, P, U64],

@@ -435,6 +435,10 @@ class BlockManager:
     def fork(self, parent: int, child: int, shared_tokens: int, token_len: int) -> list[int]:
         return self._pages_call(lib().vk_bm_fork, parent, child, shared_tokens, token_len)
 
+    def extend(self, handle: int, token_len: int) -> list[int]:
+        """Grow the handle's pages to cover token_len tokens (vk_bm_extend)."""
+        return self._pages_call(lib().vk_bm_extend, C.c_uint64(handle), C.c_int64(token_len))
+
     def cow(self, handle: int, page_idx: int):
         s, d, c = C.c_int32(), C.c_int32(), C.c_int32()
         check(lib().vk_bm_cow(self.h, handle, page_idx, C.byref(s), C.byref(d), C.byref(c)))
@@ -444,6 +448,108 @@ class BlockManager:
         n = C.c_int32()
         check(lib().vk_bm_refcount(self.h, page, C.byref(n)))
         return n.value
+
+
+@dataclass
+class CacheLookup:
+    """radix_cache.rs:11-15: matched tokens and the handle of the longest cached prefix."""
+    matched_tokens: int
+    handle: int | None
+
+
+@dataclass
+class CachedSequence:
+    """Result of RadixCache.cache_sequence: the sequence's pages and the copy to
+    issue (vk_copy_blocks) before it writes into its shared partial page."""
+    matched_tokens: int
+    pages: list
+    cow: tuple | None
+
+
+def _tokens(tokens):
+    a = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+    return a, a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+class RadixCache:
+    """RadixCache (radix_cache.rs:28-264) over block-manager handles
+    (vk_radix_*). With a BlockManager the cache owns the handles inserted into
+    it and releases replaced and evicted ones; without one handles are opaque
+    ids, as in the reference."""
+
+    def __init__(self, block_manager: "BlockManager | None" = None, capacity_tokens: int | None = None):
+        h = C.c_void_p()
+        self.bm = block_manager
+        check(lib().vk_radix_create(block_manager.h if block_manager else None,
+                                    -1 if capacity_tokens is None else capacity_tokens, C.byref(h)))
+        self.h = h
+
+    @classmethod
+    def with_capacity_tokens(cls, capacity_tokens: int, block_manager=None) -> "RadixCache":
+        return cls(block_manager, capacity_tokens)
+
+    def close(self):
+        if self.h:
+            lib().vk_radix_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def insert(self, tokens, handle: int) -> int | None:
+        """Insert tokens -> handle; returns the replaced handle (CacheInsert.replaced)."""
+        a, p = _tokens(tokens)
+        old, has = C.c_uint64(), C.c_int32()
+        check(lib().vk_radix_insert(self.h, p, len(a), handle, C.byref(old), C.byref(has)))
+        return old.value if has.value else None
+
+    def lookup(self, tokens) -> CacheLookup:
+        a, p = _tokens(tokens)
+        m, hd, has = C.c_int32(), C.c_uint64(), C.c_int32()
+        check(lib().vk_radix_lookup(self.h, p, len(a), C.byref(m), C.byref(hd), C.byref(has)))
+        return CacheLookup(m.value, hd.value if has.value else None)
+
+    def __len__(self) -> int:
+        n = C.c_int32()
+        check(lib().vk_radix_len(self.h, C.byref(n)))
+        return n.value
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def resident_tokens(self) -> int:
+        n = C.c_int64()
+        check(lib().vk_radix_resident_tokens(self.h, C.byref(n)))
+        return n.value
+
+    def capacity_tokens(self) -> int | None:
+        n = C.c_int64()
+        check(lib().vk_radix_capacity_tokens(self.h, C.byref(n)))
+        return None if n.value < 0 else n.value
+
+    def set_capacity_tokens(self, capacity_tokens: int | None):
+        check(lib().vk_radix_set_capacity(self.h, -1 if capacity_tokens is None else capacity_tokens))
+
+    def evict_coldest(self, tokens_to_evict: int) -> list[int]:
+        n = C.c_int32()
+        cap = max(1, len(self))
+        out = (C.c_uint64 * cap)()
+        check(lib().vk_radix_evict_coldest(self.h, tokens_to_evict, out, cap, C.byref(n)))
+        return [out[i] for i in range(n.value)]
+
+    def cache_sequence(self, tokens, seq_handle: int, cache_handle: int) -> CachedSequence:
+        """Prefill with the cached prefix's pages aliased (vk_radix_cache_sequence)."""
+        a, p = _tokens(tokens)
+        cap = max(1, (len(a) + self.bm.block_size - 1) // self.bm.block_size)
+        pages = (C.c_uint32 * cap)()
+        m, n, src, dst, has = C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32(), C.c_int32()
+        check(lib().vk_radix_cache_sequence(self.h, p, len(a), seq_handle, cache_handle, C.byref(m), pages, cap,
+                                            C.byref(n), C.byref(src), C.byref(dst), C.byref(has)))
+        return CachedSequence(m.value, [pages[i] for i in range(n.value)],
+                              (src.value, dst.value) if has.value else None)
 
 
 class SlotPool:
