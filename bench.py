@@ -173,16 +173,18 @@ def run_gpu(ctx, args, kv_name: str):
         d_table = ctx.upload(velokv.rope_table(n_pos, HD, 500000.0))
         d_pos = ctx.upload(lens.astype(np.int32) - 1)
 
-    def step(i, evs=None):
+    def step(i, evs=None, app_evs=None):
         r = i % R
         for layer in range(NL):
-            if evs is not None:
-                evs[layer][2].record(stream)
+            if app_evs is not None:
+                app_evs[layer][0].record(stream)
             if rope:
                 ctx.append_rope(pool, layer, ks[r], vs[r], velokv.DT_F16, d_pos, new_slots, S, d_table, n_pos, rope,
                                 q=qs[r], q_dtype=velokv.DT_F16, n_heads=H, stream=stream)
             else:
                 ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
+            if app_evs is not None:
+                app_evs[layer][1].record(stream)
             if evs is not None:
                 evs[layer][0].record(stream)
             ctx.paged_decode(pool, layer, qs[r], velokv.DT_F16, out, d_lens, S, H, int(lens.max()),
@@ -197,7 +199,7 @@ def run_gpu(ctx, args, kv_name: str):
     ctx.sync()
 
     start, end = velokv.Event(ctx), velokv.Event(ctx)
-    evs = [[[velokv.Event(ctx), velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
+    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
     start.record(stream)
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
@@ -206,7 +208,12 @@ def run_gpu(ctx, args, kv_name: str):
     ctx.sync()
     total_ms = start.elapsed_ms(end)
     dec_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
-    app_ms = [evs[i][l][2].elapsed_ms(evs[i][l][0]) for i in range(args.steps) for l in range(NL)]
+    # append time per layer, from two more (untimed) steps with events around the appends only
+    app_evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(2)]
+    for i in range(2):
+        step(i, None, app_evs[i])
+    stream.sync()
+    app_ms = [app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]
 
     ms_step = total_ms / args.steps
     dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1])

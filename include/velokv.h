@@ -98,7 +98,10 @@ int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
 /* Work schedule of vk_paged_decode for fp16 queries over fp16 / int8 KV when
  * partition_tokens is 0: VK_SCHED_SPLIT (units = fixed context partitions, sized
  * to fill one round of resident waves; kernel family per
- * vk_ctx_set_decode_kernel), VK_SCHED_STREAM (stream-K on the matrix cores: one
+ * vk_ctx_set_decode_kernel; over int8 KV with the matrix cores, a batch whose
+ * (sequence, KV head) pairs fill the GPU with at most 8 waves each runs one
+ * workgroup per pair instead, its waves splitting the context and combining in
+ * LDS, with no merge launch and no workspace), VK_SCHED_STREAM (stream-K on the matrix cores: one
  * wave per resident slot, each taking an equal share of all (sequence, KV head)
  * blocks, so ragged batches stay balanced) or VK_SCHED_AUTO (stream-K unless
  * vk_decode_args.sum_context_len says the batch is uniform, or the VALU family

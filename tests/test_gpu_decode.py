@@ -230,3 +230,35 @@ def test_decode_streamk_worker_boundaries(ctx, kv, shape):
     finally:
         ctx.set_decode_kernel(velokv.DECODE_AUTO)
         ctx.set_decode_schedule(velokv.SCHED_AUTO)
+
+
+@pytest.mark.parametrize("kv", [O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("S,G,nw", [(256, 4, 1), (128, 4, 2), (64, 4, 4), (32, 8, 8)])
+def test_decode_workgroup_split(ctx, kv, S, G, nw):
+    """The workgroup-split kernel (one workgroup of nw waves per (sequence, KV
+    head), partials combined in LDS) on ragged contexts, including empty and
+    one-token ones and waves whose share is empty."""
+    print(f"decode workgroup split kv={kv} S={S} G={G} nw={nw}", flush=True)
+    Hkv = 8
+    rng = synth.rng(300 + S)
+    lens = rng.integers(0, 700, S)
+    lens[:6] = [0, 1, 15, 16, 17, 33]
+    case = make_case(kv, [max(1, int(L)) for L in lens], n_kv_heads=Hkv, n_heads=Hkv * G, seed=311 + S,
+                     outlier_scale=8.0)
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    case.ctx_lens = np.asarray(lens, np.int32)
+    ctx.set_decode_kernel(velokv.DECODE_MFMA)
+    ctx.set_decode_schedule(velokv.SCHED_SPLIT)
+    try:
+        name = ctx.decode_kernel_name(pool, S, Hkv * G, int(lens.max()), bt_stride=case.block_tables.shape[1])
+        assert name == f"vk_decode_wg_kv{kv}_g{G}", name
+        assert ctx.decode_workspace_bytes(pool, S, Hkv * G, int(lens.max()),
+                                          bt_stride=case.block_tables.shape[1]) == 0
+        got = run_decode(ctx, pool, case)
+        ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
+        check(got, ref, f"workgroup split S={S} G={G}")
+        assert np.all(got[lens == 0] == 0.0)
+    finally:
+        ctx.set_decode_kernel(velokv.DECODE_AUTO)
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)

@@ -130,6 +130,9 @@ std::string decode_name(int kv, int g, int qt) {
 std::string decode_mfma_name(int kv, int g) {
   return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g);
 }
+std::string decode_wg_name(int kv, int g) {
+  return "vk_decode_wg_kv" + std::to_string(kv) + "_g" + std::to_string(g);
+}
 std::string decode_sk_name(int kv, int g) {
   return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g);
 }
@@ -216,6 +219,7 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
       if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
       if (kv != VK_KV_F32) names.push_back(decode_sk_name(kv, g));
+      if (kv == VK_KV_I8_REF || kv == VK_KV_I8_BLK) names.push_back(decode_wg_name(kv, g));
       if (kv != VK_KV_F32)
         for (int rt : {1, 2})
           for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
@@ -527,6 +531,7 @@ struct DecodePlan {
   int32_t max_parts;
   bool stream_k;
   int32_t n_workers;
+  int32_t wg_waves;  // > 0: workgroup-split kernel with this many waves per (sequence, KV head)
   std::string kernel;
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
 };
@@ -586,6 +591,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   decode_choice(ctx, pool, a, &pl->stream_k, &mfma);
   pl->acc_bytes = pl->ml_bytes = pl->prefix_bytes = 0;
   pl->n_workers = 0;
+  pl->wg_waves = 0;
   if (pl->stream_k) {
     pl->kernel = decode_sk_name(d.kv_type, G);
     // one wave per resident slot, and at most 256 blocks (four id windows) per worker
@@ -601,6 +607,25 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     pl->ml_bytes = align_up(prow * 2 * sizeof(float), 256);
     pl->prefix_bytes = align_up(((uint64_t)a->n_seqs + 1) * sizeof(int32_t), 256);
     return VK_OK;
+  }
+  pl->wg_waves = 0;
+  if (mfma && P == 0 && (d.kv_type == VK_KV_I8_REF || d.kv_type == VK_KV_I8_BLK)) {
+    // Workgroup split: NW waves per (sequence, KV head), the smallest power of two
+    // whose workgroups fill one round of resident waves, when each wave's share
+    // fits its four block-id windows (256 blocks).
+    const int64_t pairs = (int64_t)a->n_seqs * d.n_kv_heads;
+    const int64_t waves = ctx ? resident_waves(ctx, decode_mfma_name(d.kv_type, G)) : 2048;
+    int nw = 1;
+    while (nw < 8 && pairs * nw < waves) nw *= 2;
+    const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
+    if (pairs > 0 && pairs * nw >= waves && (nb + nw - 1) / nw <= kMaxPartTokens / d.block_size &&
+        pairs <= 0x7FFFFFFF) {
+      pl->wg_waves = nw;
+      pl->kernel = decode_wg_name(d.kv_type, G);
+      pl->part_tokens = kMaxPartTokens;
+      pl->max_parts = 1;
+      return VK_OK;
+    }
   }
   pl->kernel = mfma ? decode_mfma_name(d.kv_type, G) : decode_name(d.kv_type, G, a->q_dtype);
   if (P == 0) P = auto_partition(a, d, ctx ? resident_waves(ctx, pl->kernel) : 2048);
@@ -673,8 +698,9 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   // stream-K: contexts are clamped to max_context_len, which bounds every worker's
   // range to 256 blocks (the planner sized the grid for it)
   p.cap_tokens = pl.stream_k ? a->max_context_len
-                             : (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens,
-                                                          (int64_t)pl.bt_stride * d.block_size);
+                : pl.wg_waves ? a->max_context_len  // bounds every wave's share to 256 blocks (planner)
+                              : (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens,
+                                                           (int64_t)pl.bt_stride * d.block_size);
   p.n_nodes = 1;
   p.n_rgroups = 1;
   p.n_workers = pl.n_workers;
@@ -700,6 +726,9 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
     if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64), p, stream))) return rc;
     return launch(ctx, "vk_decode_merge_sk", merge_grid, dim3(256), m, stream);
   }
+  if (pl.wg_waves)
+    return launch(ctx, pl.kernel.c_str(), dim3((unsigned)(a->n_seqs * d.n_kv_heads)), dim3(64 * (unsigned)pl.wg_waves),
+                  p, stream);
   const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
   if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;

@@ -690,10 +690,11 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 // One piece of work: tokens [start, end) of (sequence s, KV head kvh), row group
 // rg, committed context ctx_c. direct: the piece is the whole context and writes
 // normalised rows; otherwise it writes the unnormalised partial (acc, M, l) of
-// row R at index TREE ? out_row(R) * max_parts + pbase : pbase + R * pstride.
+// row R at index TREE ? out_row(R) * max_parts + pbase : pbase + R * pstride of
+// pacc ([.][HD] fp32) and pml ([.][2] fp32), in HBM or in LDS.
 template <int KV, int G, int RT, bool TREE, int QT>
 DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
-                    int64_t pbase, int pstride) {
+                    int64_t pbase, int pstride, float* pacc, float* pml) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr bool I8 = (ESZ == 1);
   constexpr bool BLK = (KV == KV_I8_BLK);
@@ -971,10 +972,10 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
           dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
         } else {
           const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
-          float4* dst = reinterpret_cast<float4*>(P.part_acc + pr * HD + 8 * n);
+          float4* dst = reinterpret_cast<float4*>(pacc + pr * HD + 8 * n);
           dst[0] = make_float4(o[0], o[1], o[2], o[3]);
           dst[1] = make_float4(o[4], o[5], o[6], o[7]);
-          if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(Mr, lr);
+          if (n == 0) reinterpret_cast<float2*>(pml)[pr] = make_float2(Mr, lr);
         }
       }
     }
@@ -1010,7 +1011,8 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   const int end = min(start + P.part_tokens, ctx);
   const int nparts = (ctx + P.part_tokens - 1) / P.part_tokens;
   const int64_t pbase = TREE ? part : ((int64_t)s * P.n_heads + (int64_t)kvh * G) * P.max_parts + part;
-  attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1, pbase, P.max_parts);
+  attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1, pbase, P.max_parts, P.part_acc,
+                                  P.part_ml);
 }
 
 // ---- stream-K decode -------------------------------------------------------
@@ -1098,12 +1100,63 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     const int o1 = (int)min((int64_t)nb, (int64_t)o0 + (b1 - x));
     const int slot = o0 > 0 ? 0 : 1;
     attn_piece<KV, G, 1, false, DT_F16>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                        ((int64_t)w * 2 + slot) * G, 1);
+                                        ((int64_t)w * 2 + slot) * G, 1, P.part_acc, P.part_ml);
     x += o1 - o0;
     if (o1 == nb && kvh == Hkv - 1) {
       pre += Hkv * nb;
       ++s;
     }
+  }
+}
+
+// ---- workgroup-split decode ------------------------------------------------
+// One workgroup of NW = blockDim.x / 64 waves per (sequence, KV head), KV head
+// fastest: wave w takes the w-th of NW equal block ranges of the context,
+// leaves its unnormalised partial (acc, M, l) in LDS, and after one barrier the
+// workgroup combines them into the output rows,
+//   out = sum_w 2^(M_w - M) acc_w / sum_w 2^(M_w - M) l_w,  M = max_w M_w,
+// so a uniform batch needs no partials in HBM and no merge launch.
+constexpr int kWgMaxWaves = 8;
+template <int KV, int G>
+DEV void attn_wg_mfma(const DecodeParams& P) {
+  __shared__ float wacc[kWgMaxWaves][G][HD];
+  __shared__ float wml[kWgMaxWaves][G][2];
+  const int nw = (int)blockDim.x / WAVE;
+  const int w = (int)threadIdx.x / WAVE;
+  const int lane = lane_id();
+  const int kvh = (int)blockIdx.x % P.n_kv_heads;
+  const int s = (int)blockIdx.x / P.n_kv_heads;
+  if (s >= P.n_seqs) return;  // the whole workgroup
+  const int ctx = max(0, min(P.context_lens[s], P.cap_tokens));
+  if (ctx == 0) {
+    if (w == 0) write_zero_rows<G>(P, s, kvh);
+    return;
+  }
+  const int nb = (ctx + BS - 1) / BS;
+  const int per = (nb + nw - 1) / nw;
+  const int b0 = min(nb, w * per), b1 = min(nb, b0 + per);
+  if (b0 < b1) {
+    attn_piece<KV, G, 1, false, DT_F16>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
+                                        &wml[w][0][0]);
+  } else if (lane < G) {
+    wml[w][lane][0] = kNegInf;
+    wml[w][lane][1] = 0.f;
+  }
+  __syncthreads();
+  const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * G;
+  for (int i = (int)threadIdx.x; i < G * HD; i += (int)blockDim.x) {
+    const int r = i / HD, d = i - r * HD;
+    float M = kNegInf;
+    for (int v = 0; v < nw; ++v) M = fmaxf(M, wml[v][r][0]);
+    float L = 0.f, o = 0.f;
+    for (int v = 0; v < nw; ++v) {
+      const float mv = wml[v][r][0];
+      if (mv == kNegInf) continue;  // a wave with no tokens (its acc row is not written)
+      const float e = __builtin_amdgcn_exp2f(mv - M);
+      L = fmaf(e, wml[v][r][1], L);
+      o = fmaf(e, wacc[v][r][d], o);
+    }
+    P.out[(hrow0 + r) * HD + d] = L > 0.f ? o / L : 0.f;
   }
 }
 
@@ -1754,6 +1807,15 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
   }
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
 VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
+
+// Workgroup-split decode: up to kWgMaxWaves waves of 64 per workgroup.
+#define VK_DECODE_WG(KV, G)                                                         \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves)                    \
+      vk_decode_wg_kv##KV##_g##G(const DecodeParams P) {                            \
+    attn_wg_mfma<KV, G>(P);                                                         \
+  }
+#define VK_DECODE_WG_G(KV) VK_DECODE_WG(KV, 1) VK_DECODE_WG(KV, 2) VK_DECODE_WG(KV, 4) VK_DECODE_WG(KV, 8)
+VK_DECODE_WG_G(2) VK_DECODE_WG_G(3)
 
 // Two waves per SIMD (at most 256 registers).
 #define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
