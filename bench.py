@@ -351,12 +351,16 @@ def run_tree(ctx, args):
     moved_tok = sum(len(a) - next((d for d, x in enumerate(a) if x != d), len(a)) for a in acc_rows)
     stream = velokv.Stream(ctx)
 
-    def step(i, evs=None):
+    def step(i, evs=None, app_evs=None):
         r = i % R
         if len(pairs):
             ctx.copy_blocks(pool, pairs, stream=stream)
         for layer in range(NL):
+            if app_evs is not None:
+                app_evs[layer][0].record(stream)
             ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, draft_slots, S * N, stream=stream)
+            if app_evs is not None:
+                app_evs[layer][1].record(stream)
             if evs is not None:
                 evs[layer][0].record(stream)
             ctx.tree_verify(pool, layer, qs[r], velokv.DT_F16, out, d_committed, d_mask, S, N, H,
@@ -384,6 +388,12 @@ def run_tree(ctx, args):
     total_ms = start.elapsed_ms(end)
     tv_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
     commit_ms = float(np.mean([evs[i][NL][0].elapsed_ms(evs[i][NL][1]) for i in range(args.steps)]))
+    # draft-append time per layer, from two more (untimed) steps with events around the appends only
+    app_evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(2)]
+    for i in range(2):
+        step(i, None, app_evs[i])
+    stream.sync()
+    append_ms = float(np.mean([app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]))
 
     esz = 1 if kv == velokv.KV_I8_BLK else 2
     sc = 2 if kv == velokv.KV_I8_BLK else 0
@@ -416,6 +426,7 @@ def run_tree(ctx, args):
         "radix": {"host_ms": round(host_ms, 3), "pages": int(used_pages), "pages_without_aliasing": int(reference_pages),
                   "pool_gb": round(pool.nbytes / 1e9, 3),
                   "pool_gb_without_aliasing": round(pool.nbytes / 1e9 * reference_pages / used_pages, 3)},
+        "draft_append": {"kernel": "vk_append_kv%d" % kv, "ms_mean": round(append_ms, 5), "tokens": S * N},
         "commit": {"kernel": "vk_tree_commit_kv%d" % kv, "ms_mean": round(commit_ms, 5), "layers": NL,
                    "accepted_tokens": int(n_acc.sum()), "moved_tokens": int(moved_tok)},
         "logical_gbs": round(logical / (tv_mean * 1e-3) / 1e9, 2),

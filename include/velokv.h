@@ -23,7 +23,10 @@
  *
  * Layout of one layer of a pool in HBM ("build layout"; the reference layout
  * is [blk][tok][head][D(+4)], kernels.metal:474,700):
- *    K codes   [n_blocks][n_kv_heads][block_size][head_dim]
+ *    K codes   [n_blocks][n_kv_heads][block_size][head_dim] for F32 / F16;
+ *              I8_*: [n_blocks][n_kv_heads][2][block_size][head_dim/32][16] (dims
+ *              32c..32c+15 of token t at byte (4t + c)*16 of the tile, dims
+ *              32c+16..32c+31 at 1024 + (4t + c)*16)
  *    V codes   [n_blocks][n_kv_heads][block_size/2][head_dim][2]   (token pairs interleaved)
  *    K scales  I8_BLK: fp16 [n_blocks][n_kv_heads]; I8_REF: fp32 [n_blocks][n_kv_heads][block_size]
  *    V scales  same as K scales

@@ -84,9 +84,38 @@ class Layer:
             o.vs[:] = self.vs
         return o
 
+    def tile_codes(self, is_v, blk, h):
+        """Codes of one (block, head) tile as [block_size][head_dim] elements
+        (int8 / uint16 fp16 bits / float32), gathered through the build layout."""
+        idx = _tile_index(self, is_v)
+        esz = ESZ[self.kv_type]
+        raw = self.v if is_v else self.k
+        tile = self.block_size * self.head_dim * esz
+        base = (blk * self.n_kv_heads + h) * tile
+        b = raw[base:base + tile]
+        if esz == 1:
+            return b.view(np.int8)[idx]
+        dt = np.uint16 if esz == 2 else np.float32
+        return b.view(dt)[idx // esz]
+
     def elem(self, is_v, blk, h, tok, d):
         s = self.struct()
         return lib().vko_load_elem(C.byref(s), int(is_v), C.c_int64(blk), h, tok, d)
+
+
+_TILE_INDEX = {}
+
+
+def _tile_index(layer, is_v):
+    """[block_size][head_dim] byte offsets of a tile's elements (vko_elem_offset)."""
+    key = (layer.kv_type, layer.block_size, layer.head_dim, int(is_v))
+    if key not in _TILE_INDEX:
+        lib().vko_elem_offset.restype = C.c_uint64
+        one = Layer(1, 1, layer.block_size, layer.head_dim, layer.kv_type)
+        s = one.struct()
+        _TILE_INDEX[key] = np.array([[lib().vko_elem_offset(C.byref(s), int(is_v), C.c_int64(0), 0, t, d)
+                                      for d in range(layer.head_dim)] for t in range(layer.block_size)], np.int64)
+    return _TILE_INDEX[key]
 
 
 def f16_to_f32(bits):

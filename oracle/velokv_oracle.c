@@ -13,7 +13,8 @@
  *      ([blk][tok][head][D] fp32, [blk][tok][head][D codes + 4-byte fp32 scale]
  *      int8) with the reference's operation order.
  *  (2) vko_*: the same semantics on the BUILD layout the GPU pool uses
- *      (K [blk][head][tok][D], V [blk][head][tok/2][D][2], scales separate),
+ *      (K [blk][head][tok][D] for fp32 / fp16 and [blk][head][D/16 % 2][tok][D/32][16]
+ *      for int8, V [blk][head][tok/2][D][2], scales separate; elem_off),
  *      plus what the reference lacks (fp16 KV, per-block INT8 scales,
  *      tree verify, copy-on-write), so outputs compare byte for byte.
  *
@@ -240,6 +241,8 @@ static uint64_t elem_off(const vko_layer* L, int is_v, int64_t blk, int h, int t
   const int esz = esz_of(L->kv_type);
   const uint64_t tile = (uint64_t)L->block_size * L->head_dim * esz;
   const uint64_t base = ((uint64_t)blk * L->n_kv_heads + h) * tile;
+  /* int8 K: [h][tok][D/32][16], h = (d/16) % 2 (two 16-byte pieces per 32 dims) */
+  if (!is_v && esz == 1) return base + (uint64_t)(((d >> 4) & 1) * (tile / 2) + (4 * tok + (d >> 5)) * 16 + (d & 15));
   if (!is_v) return base + ((uint64_t)tok * L->head_dim + d) * esz;
   return base + ((uint64_t)((tok >> 1) * L->head_dim + d) * 2 + (tok & 1)) * esz;
 }
@@ -262,6 +265,11 @@ static float load_elem(const vko_layer* L, int is_v, int64_t blk, int h, int tok
       return (float)(int8_t)base[off] * vko_f16_to_f32(sb);
     }
   }
+}
+
+/* byte offset of element (blk, head, tok, d) in the K (is_v = 0) or V codes */
+uint64_t vko_elem_offset(const vko_layer* L, int is_v, int64_t blk, int h, int tok, int d) {
+  return elem_off(L, is_v, blk, h, tok, d);
 }
 
 float vko_load_elem(const vko_layer* L, int is_v, int64_t blk, int h, int tok, int d) {

@@ -158,7 +158,7 @@ def _blk_block(tokens):
     L = O.Layer(1, 1, BS, HD, O.I8_BLK)
     for o, x in enumerate(tokens):
         O.append(L, np.asarray(x, np.float32)[None, None], np.asarray(x, np.float32)[None, None], [o])
-    codes = L.k.view(np.int8).reshape(BS, HD)
+    codes = L.tile_codes(0, 0, 0)
     scale = L.ks.view(np.float16)[0]
     return codes, scale, L
 
@@ -414,3 +414,24 @@ def test_copy_blocks_invariants(kv):
     cb = 2 * BS * HD * esz
     changed = np.nonzero(layer.k.reshape(12, cb) != before.k.reshape(12, cb))[0]
     assert set(changed.tolist()) <= set(dst)
+
+
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
+def test_tile_layout_is_a_permutation_with_line_friendly_int8_k(kv):
+    """Every (token, dim) of a tile has its own offset (a permutation of the
+    tile); int8 K puts the 32 codes of dims 32c..32c+31 of token t in two
+    16-byte pieces at (4t + c)*16 and 1024 + (4t + c)*16."""
+    L = O.Layer(1, 1, BS, HD, kv)
+    esz = O.ESZ[kv]
+    for is_v in (0, 1):
+        idx = O._tile_index(L, is_v)
+        assert np.array_equal(np.sort(idx.ravel() // esz), np.arange(BS * HD))
+    idx = O._tile_index(L, 0)
+    if esz == 1:
+        for t in (0, 7, 15):
+            for c in range(4):
+                assert list(idx[t, 32 * c:32 * c + 16]) == list(range((4 * t + c) * 16, (4 * t + c) * 16 + 16))
+                assert list(idx[t, 32 * c + 16:32 * c + 32]) == list(range(1024 + (4 * t + c) * 16,
+                                                                          1024 + (4 * t + c) * 16 + 16))
+    else:
+        assert np.array_equal(idx, (np.arange(BS)[:, None] * HD + np.arange(HD)[None, :]) * esz)

@@ -269,7 +269,14 @@ DEV void stage_load(Stage<KV>& st, const DecodeParams& P, const BlockIds& bw, in
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
     const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
     const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
-    st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, lane * (32 * ESZ));
+    if constexpr (ESZ == 1) {  // lane 4t + c: pieces at 16 lane and 1024 + 16 lane (int8 K layout)
+      const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, lane * 16);
+      const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 1024 + lane * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) { st.k[u].d[w] = lo.d[w]; st.k[u].d[4 + w] = hi.d[w]; }
+    } else {
+      st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, lane * (32 * ESZ));
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) st.v[u][j] = buf_load<ESZ>(vr, j * (HD * 2 * ESZ) + lane * (4 * ESZ));
     if constexpr (KV == KV_I8_REF) {
@@ -663,7 +670,14 @@ DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, 
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
     const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
     const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
-    st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * HD + 32 * g) * ESZ);
+    if constexpr (ESZ == 1) {  // pieces (4n + g) of the two 1 KB halves (int8 K layout)
+      const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, (4 * n + g) * 16);
+      const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 1024 + (4 * n + g) * 16);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) { st.k[u].d[w] = lo.d[w]; st.k[u].d[4 + w] = hi.d[w]; }
+    } else {
+      st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * HD + 32 * g) * ESZ);
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * HD * 2 + 16 * n) * ESZ);
     if constexpr (KV == KV_I8_REF) {
@@ -1313,10 +1327,16 @@ DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h
 }
 
 // Byte offset inside a (block, head) tile of element (token, dim).
+//   V: [tok/2][D][2] (token pairs interleaved)
+//   K, fp16 / fp32: [tok][D]
+//   K, int8: [h][tok][D/32][16] with h = (d/16) % 2: the 32 codes of dims
+//     32c..32c+31 of token t are two 16-byte pieces at (4t + c)*16 and
+//     1024 + (4t + c)*16, so one 16-byte load per lane covers whole cache lines
 template <bool IS_V>
 DEV uint32_t tile_elem(int tok, int d, int esz) {
-  return IS_V ? (uint32_t)(((tok >> 1) * HD + d) * 2 + (tok & 1)) * esz
-              : (uint32_t)(tok * HD + d) * esz;
+  if (IS_V) return (uint32_t)(((tok >> 1) * HD + d) * 2 + (tok & 1)) * esz;
+  if (esz == 1) return (uint32_t)(((d >> 4) & 1) * 1024 + (4 * tok + (d >> 5)) * 16 + (d & 15));
+  return (uint32_t)(tok * HD + d) * esz;
 }
 
 DEV int clamp127(float r) { return (int)fminf(fmaxf(r, -127.f), 127.f); }
