@@ -48,6 +48,7 @@ import velokv  # noqa: E402
 from velokv import synth  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 / bf16 matrix-core peak
 BS, HD = 16, 128
 
 
@@ -81,6 +82,8 @@ def parse():
     ap.add_argument("--prefix", type=int, default=4096, help="tree: shared prefix tokens")
     ap.add_argument("--max-suffix", type=int, default=512, help="tree: suffix tokens U[0, max]")
     ap.add_argument("--nodes", type=int, default=8, help="tree: draft-tree nodes")
+    ap.add_argument("--no-shared-prefix", action="store_true",
+                    help="tree: do not pass the radix cache's shared prefix to vk_tree_verify (shared_blocks = 0)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one vk_copy_blocks of known size (HBM counter calibration)")
     return ap.parse_args()
@@ -324,6 +327,9 @@ def run_tree(ctx, args):
     kbuf.free()
     vbuf.free()
 
+    # every table row starts with the prefix's pages (the radix cache aliases them)
+    shared_blocks = 0 if args.no_shared_prefix else prefix // BS
+    assert np.all(tables[:, :prefix // BS] == tables[0, :prefix // BS])
     dpos = (committed[:, None] + np.arange(N)[None, :]).reshape(-1)
     draft_slots = ctx.upload(synth.slots_for_positions(tables, dpos, BS, np.repeat(np.arange(S), N)))
     mask = np.tile(velokv.branching_tree([2, 2, 2, 2, 2], N).ancestor_mask(), S)
@@ -365,7 +371,7 @@ def run_tree(ctx, args):
                 evs[layer][0].record(stream)
             ctx.tree_verify(pool, layer, qs[r], velokv.DT_F16, out, d_committed, d_mask, S, N, H,
                             int(committed.max()), block_tables=d_bt, bt_stride=stride,
-                            partition_tokens=args.partition, stream=stream)
+                            partition_tokens=args.partition, stream=stream, shared_blocks=shared_blocks)
             if evs is not None:
                 evs[layer][1].record(stream)
         # the accepted paths move to committed + 0, 1, ... in every layer
@@ -417,6 +423,11 @@ def run_tree(ctx, args):
     ach = uniq / (tv_mean * 1e-3) / 1e9
     rt = 2 if N * G > 16 else 1
     kname = "vk_tree_kv%d_g%d_r%d_q1" % (kv, G, rt)
+    call_kernels = [kname, "vk_decode_merge"]
+    if shared_blocks and kv in (velokv.KV_I8_BLK, velokv.KV_F16):
+        kname = "vk_tree_pfx_kv%d_g%d_q1" % (kv, G)
+        call_kernels = [kname] + call_kernels
+    tflops = flops / (tv_mean * 1e-3) / 1e12
     return {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
         "ms_per_step": round(ms_step, 4),
@@ -430,14 +441,22 @@ def run_tree(ctx, args):
         "commit": {"kernel": "vk_tree_commit_kv%d" % kv, "ms_mean": round(commit_ms, 5), "layers": NL,
                    "accepted_tokens": int(n_acc.sum()), "moved_tokens": int(moved_tok)},
         "logical_gbs": round(logical / (tv_mean * 1e-3) / 1e9, 2),
-        "mfma_tflops": round(flops / (tv_mean * 1e-3) / 1e12, 2),
+        "mfma_tflops": round(tflops, 2),
+        "shared_blocks": shared_blocks,
+        "call_kernels": call_kernels,
+        # the same call against the matrix cores' dense fp16 peak (QK and PV of
+        # every row over its committed context and the tree nodes)
+        "roofline_mfma": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                          "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                          "flops_per_launch": int(flops)},
         "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kname,
                      "launch_ms_mean": round(tv_mean, 5), "launch_ms_min": round(float(np.min(tv_ms)), 5),
                      "launches": len(tv_ms)},
         "pool_gb": round(pool.nbytes / 1e9, 2),
-        "workload": "S=%d, prefix %d (aliased), suffix U[0,%d], %d-node tree, H=%d/Hkv=%d, %s KV, %d layers" %
-                    (S, prefix, args.max_suffix, N, H, Hkv, args.kv, NL),
+        "workload": "S=%d, prefix %d (aliased%s), suffix U[0,%d], %d-node tree, H=%d/Hkv=%d, %s KV, %d layers" %
+                    (S, prefix, ", shared_blocks %d" % shared_blocks if shared_blocks else "", args.max_suffix, N, H,
+                     Hkv, args.kv, NL),
     }
 
 

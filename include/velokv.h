@@ -274,6 +274,14 @@ typedef struct vk_tree_args {
   int32_t partition_tokens;   /* split-K partition, multiple of bs, <= 4096; 0 = auto */
   void* workspace;            /* dev split-K scratch or NULL (context-owned)     */
   uint64_t workspace_bytes;
+  int32_t shared_blocks;      /* the first shared_blocks pages of every table row
+                                 used by the call are the same fully written pages
+                                 (a prefix shared through the radix cache), 0 if
+                                 unknown; shared_blocks * block_size <=
+                                 max_context_len. Over F16 and I8_BLK pools the
+                                 prefix is attended once per KV head for all rows
+                                 (the results are those of shared_blocks = 0 up to
+                                 fp32 rounding); other pools ignore it. */
 } vk_tree_args;
 
 /* Bytes of split-K workspace vk_tree_verify needs for these arguments (0 when

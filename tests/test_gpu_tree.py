@@ -18,7 +18,7 @@ KV_TREE = [O.F16, O.I8_REF, O.I8_BLK]
 
 
 def run_tree(ctx, pool, case, q, committed, mask, q_dtype=np.float16, partition_tokens=0, block_tables=None,
-             seq_rows=None, layer=0):
+             seq_rows=None, layer=0, shared_blocks=0):
     S, N = q.shape[0], q.shape[1]
     qd = q.astype(q_dtype)
     out = ctx.alloc(S * N * case.n_heads * HD * 4)
@@ -28,7 +28,7 @@ def run_tree(ctx, pool, case, q, committed, mask, q_dtype=np.float16, partition_
                     ctx.upload(np.asarray(committed, np.int32)), ctx.upload(mk), S, N, case.n_heads,
                     int(np.max(committed)) if S else 0, block_tables=ctx.upload(bt), bt_stride=bt.shape[1],
                     seq_rows=ctx.upload(seq_rows) if seq_rows is not None else None,
-                    partition_tokens=partition_tokens)
+                    partition_tokens=partition_tokens, shared_blocks=shared_blocks)
     ctx.sync()
     return out.download((S, N, case.n_heads, HD), np.float32)
 
@@ -226,3 +226,92 @@ def test_config4_flow_reduced(ctx, kv, prefix_len):
     # sequences share the prefix pages (all but the copied partial one)
     shared = prefix_len // BS
     assert np.all(tables[:, :shared] == np.array(parent[:shared], np.int32))
+
+
+# ---- shared-prefix pass (vk_tree_args.shared_blocks) --------------------------
+
+@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16, O.I8_REF])
+@pytest.mark.parametrize("prefix_len,S", [(4096, 64), (4100, 16)])
+def test_tree_shared_prefix_flow(ctx, kv, prefix_len, S):
+    """Config-4 flow with the shared prefix declared: the prefix pass over the
+    aliased pages plus the rest of each context must match the oracle and the
+    call without the hint (I8_REF pools ignore it). 16 sequences leave few row
+    tiles, so the prefix is cut into chunks."""
+    print(f"tree shared prefix kv={kv} prefix={prefix_len} S={S}", flush=True)
+    N = 8
+    pool, ref, tables, committed, parent, H = config4_flow(ctx, kv, S, prefix_len, 512, N, seed=307)
+    q = tree_q(S, N, H, 3071)
+    mask = np.tile(mask_222(N), (S, 1))
+
+    class C:
+        n_heads = H
+        block_tables = tables
+    shared = prefix_len // BS
+    assert np.all(tables[:, :shared] == tables[0, :shared])
+    got = run_tree(ctx, pool, C, q, committed, mask, shared_blocks=shared)
+    plain = run_tree(ctx, pool, C, q, committed, mask)
+    expect = O.tree_verify(ref, q, tables, committed, mask)
+    check(got, expect, "shared prefix vs oracle")
+    check(got, plain, "shared prefix vs no hint")
+
+
+@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16])
+@pytest.mark.parametrize("qd", [np.float16, np.float32])
+@pytest.mark.parametrize("G,N", [(4, 5), (1, 3), (8, 8)])
+def test_tree_shared_prefix_short_contexts(ctx, kv, qd, G, N):
+    """Contexts shorter than the shared prefix (0, 5, 16, 639 tokens), equal to
+    it and longer, with 40 shared pages cut into two chunks: each row sees only
+    its own committed tokens of the shared pages."""
+    print(f"tree shared prefix short kv={kv} q={np.dtype(qd).name} G={G} N={N}", flush=True)
+    P = 40
+    committed = np.array([P * BS + 37, 5, 16, P * BS - 1, P * BS, P * BS + 100, 0, 33], np.int32)
+    case = tree_case(kv, committed, N, G=G, Hkv=2, seed=311, outlier_scale=8.0 if kv != O.F16 else 1.0)
+    # every row shares row 0's first P pages (row 0 holds the longest context, so they are fully written)
+    bt = case.block_tables.copy()
+    bt[:, :P] = bt[0, :P]
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    q = tree_q(case.S, N, case.n_heads, 3111)
+    rng = np.random.default_rng(5 + G * N)
+    full = (1 << N) - 1
+    mask = rng.integers(0, 1 << 32, size=(case.S, N), dtype=np.uint64).astype(np.uint32) & np.uint32(full)
+    got = run_tree(ctx, pool, case, q, committed, mask, q_dtype=qd, block_tables=bt, shared_blocks=P)
+    ref = O.tree_verify(ref_layer, q.astype(qd), bt, committed, mask)
+    check(got, ref, "shared prefix, short contexts")
+
+
+@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16])
+@pytest.mark.parametrize("P", [16, 64, 0])
+def test_tree_shared_prefix_partitions(ctx, kv, P):
+    """Shared prefix with the rest of each context cut into partitions of P
+    tokens (merged by vk_decode_merge after the prefix slots) or, for P = 0, in
+    one partition whose kernel folds the prefix partials into the output."""
+    print(f"tree shared prefix partitions kv={kv} P={P}", flush=True)
+    pb = 24
+    committed = np.array([pb * BS + 300, pb * BS, pb * BS + 1, pb * BS + 77, 3 * BS + 5], np.int32)
+    N = 8
+    case = tree_case(kv, committed, N, Hkv=2, seed=313, outlier_scale=8.0 if kv != O.F16 else 1.0)
+    bt = case.block_tables.copy()
+    bt[:, :pb] = bt[0, :pb]
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    q = tree_q(case.S, N, case.n_heads, 3131)
+    mask = np.tile(mask_222(N), (case.S, 1))
+    got = run_tree(ctx, pool, case, q, committed, mask, block_tables=bt, shared_blocks=pb, partition_tokens=P)
+    ref = O.tree_verify(ref_layer, q, bt, committed, mask)
+    check(got, ref, "shared prefix partitions")
+
+
+def test_tree_shared_prefix_bad_arguments(ctx):
+    case = tree_case(O.I8_BLK, [64, 80], 4, Hkv=2)
+    pool = gpu_pool(ctx, case)
+    q = ctx.upload(tree_q(case.S, 4, case.n_heads, 1))
+    out = ctx.alloc(case.S * 4 * case.n_heads * HD * 4)
+    cl = ctx.upload(np.array([64, 80], np.int32))
+    mk = ctx.upload(np.tile(mask_222(4), (case.S, 1)).astype(np.uint32))
+    bt = ctx.upload(case.block_tables)
+    for shared in (-1, 6):  # 6 pages = 96 tokens > max_context_len 80
+        with pytest.raises(velokv.VkError) as e:
+            ctx.tree_verify(pool, 0, q, velokv.DT_F16, out, cl, mk, case.S, 4, case.n_heads, 80, block_tables=bt,
+                            bt_stride=case.block_tables.shape[1], shared_blocks=shared)
+        assert e.value.code == velokv.ERR_BAD_ARG

@@ -136,6 +136,9 @@ std::string decode_wg_name(int kv, int g) {
 std::string decode_sk_name(int kv, int g) {
   return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g);
 }
+std::string tree_pfx_name(int kv, int g, int qt) {
+  return "vk_tree_pfx_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
+}
 std::string tree_name(int kv, int g, int rt, int qt) {
   return "vk_tree_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_r" + std::to_string(rt) + "_q" +
          std::to_string(qt);
@@ -223,6 +226,8 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       if (kv != VK_KV_F32)
         for (int rt : {1, 2})
           for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
+      if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK)
+        for (int qt = 0; qt < 2; ++qt) names.push_back(tree_pfx_name(kv, g, qt));
     }
   for (const auto& nm : names) {
     hipFunction_t f = nullptr;
@@ -531,6 +536,7 @@ struct DecodePlan {
   int32_t max_parts;
   bool stream_k;
   int32_t n_workers;
+  int32_t sk_fast, sk_wf, sk_ws;  // weighted stream-K split (velokv_params.h sk_split)
   int32_t wg_waves;  // > 0: workgroup-split kernel with this many waves per (sequence, KV head)
   std::string kernel;
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
@@ -552,6 +558,12 @@ void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args*
               (sched == VK_SCHED_STREAM || (sched == VK_SCHED_AUTO && !uniform));
   *mfma = *stream_k || (fast && (kind == VK_DECODE_MFMA || (kind == VK_DECODE_AUTO && d.kv_type != VK_KV_F16)));
 }
+
+// Stream-K weights at two waves per SIMD: the first-dispatched wave of a SIMD
+// streamed its range in 0.85 of the time the second one took (INT8 decode,
+// uniform and ragged batches, MI355X), so it is given proportionally more blocks.
+constexpr int32_t kSkWeightFast = 117;
+constexpr int32_t kSkWeightSlow = 100;
 
 // Smallest partition (256..4096 tokens) whose units fit in one round of resident
 // waves; longer contexts get 4096-token partitions.
@@ -591,6 +603,8 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   decode_choice(ctx, pool, a, &pl->stream_k, &mfma);
   pl->acc_bytes = pl->ml_bytes = pl->prefix_bytes = 0;
   pl->n_workers = 0;
+  pl->sk_fast = 0;
+  pl->sk_wf = pl->sk_ws = 1;
   pl->wg_waves = 0;
   if (pl->stream_k) {
     pl->kernel = decode_sk_name(d.kv_type, G);
@@ -600,6 +614,11 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     const int64_t nw = std::max<int64_t>(1, std::max(waves, (blocks_max + 255) / 256));
     if (nw > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "grid too large");
     pl->n_workers = (int32_t)nw;
+    // one round of two waves per SIMD: the first half of the grid is the faster half
+    const bool two_per_simd = ctx && ctx->n_cu > 0 && waves == 8LL * ctx->n_cu && nw == waves;
+    pl->sk_fast = two_per_simd ? (int32_t)(nw / 2) : 0;
+    pl->sk_wf = kSkWeightFast;
+    pl->sk_ws = kSkWeightSlow;
     pl->part_tokens = kMaxPartTokens;  // unused by the stream-K kernels
     pl->max_parts = 1;
     const uint64_t prow = (uint64_t)nw * 2 * G;
@@ -704,6 +723,9 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.n_nodes = 1;
   p.n_rgroups = 1;
   p.n_workers = pl.n_workers;
+  p.sk_fast = pl.sk_fast;
+  p.sk_wf = pl.sk_wf;
+  p.sk_ws = pl.sk_ws;
   p.scale_log2 = scale * 1.4426950408889634f;
 
   MergeParams m{};
@@ -719,6 +741,9 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   m.cap_tokens = p.cap_tokens;
   m.sk_prefix = p.sk_prefix;
   m.n_workers = pl.n_workers;
+  m.sk_fast = pl.sk_fast;
+  m.sk_wf = pl.sk_wf;
+  m.sk_ws = pl.sk_ws;
   m.n_kv_heads = d.n_kv_heads;
   m.n_seqs = a->n_seqs;
   const dim3 merge_grid((unsigned)((m.n_rows + 3) / 4));
@@ -738,11 +763,17 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
 
 namespace {
 
+constexpr int kPfxRowsPerGroup = 256;  // query rows per workgroup of the shared-prefix pass (8 waves of 32)
+constexpr int kPfxThreads = 512;
+
 struct TreePlan {
   const int32_t* bt;
   int32_t bt_stride, bt_rows, part_tokens, max_parts, rt, n_rgroups;
+  // shared-prefix pass: prefix pages, chunks (partial slots 0..prefix_chunks-1),
+  // row tiles of kPfxRows query rows per KV head; 0 chunks = no prefix pass
+  int32_t prefix_blocks, prefix_chunks, pfx_row_tiles;
   uint64_t acc_bytes, ml_bytes;
-  std::string kernel;
+  std::string kernel, pfx_kernel;
 };
 
 int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan* pl) {
@@ -767,18 +798,44 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
     pl->bt_rows = d.max_slots;
   }
   if (pl->bt_stride <= 0) return fail(VK_ERR_BAD_ARG, "bt_stride must be positive");
-  const int64_t tokens = (int64_t)a->max_context_len + a->n_nodes;
-  if (tokens > (int64_t)pl->bt_stride * d.block_size)
+  if ((int64_t)a->max_context_len + a->n_nodes > (int64_t)pl->bt_stride * d.block_size)
     return fail(VK_ERR_BAD_ARG, "max_context_len %d + n_nodes %d exceeds the block-table row (%d pages)",
                 a->max_context_len, a->n_nodes, pl->bt_stride);
   const int rows = a->n_nodes * G;
   pl->rt = rows > 16 ? 2 : 1;
   pl->n_rgroups = (rows + 16 * pl->rt - 1) / (16 * pl->rt);
   pl->kernel = tree_name(d.kv_type, G, pl->rt, a->q_dtype);
+  if (a->shared_blocks < 0 || a->shared_blocks > pl->bt_stride ||
+      (int64_t)a->shared_blocks * d.block_size > a->max_context_len)
+    return fail(VK_ERR_BAD_ARG, "shared_blocks %d: must be within the table row (%d pages) and max_context_len %d",
+                a->shared_blocks, pl->bt_stride, a->max_context_len);
+  pl->prefix_blocks = pl->prefix_chunks = pl->pfx_row_tiles = 0;
+  int64_t tokens = (int64_t)a->max_context_len + a->n_nodes;
+  if (a->shared_blocks > 0 && (d.kv_type == VK_KV_F16 || d.kv_type == VK_KV_I8_BLK)) {
+    // One workgroup per (256 query rows, KV head, prefix chunk); the prefix is cut
+    // into chunks of at least 16 pages until the workgroups cover the CUs.
+    const int64_t qrows = (int64_t)a->n_seqs * rows;
+    pl->pfx_row_tiles = (int32_t)((qrows + kPfxRowsPerGroup - 1) / kPfxRowsPerGroup);
+    const int64_t groups = std::max<int64_t>(1, (int64_t)pl->pfx_row_tiles * d.n_kv_heads);
+    const int64_t n_cu = ctx ? ctx->n_cu : 256;
+    const int64_t max_chunks = std::max(1, a->shared_blocks / 16);
+    pl->prefix_chunks = (int32_t)std::min(max_chunks, std::max<int64_t>(1, (n_cu + groups - 1) / groups));
+    pl->prefix_blocks = a->shared_blocks;
+    pl->pfx_kernel = tree_pfx_name(d.kv_type, G, a->q_dtype);
+    // the rest of a context: past the prefix, or the last partial page of a
+    // context shorter than the prefix, then the tree nodes
+    tokens = std::max<int64_t>((int64_t)a->max_context_len - (int64_t)a->shared_blocks * d.block_size,
+                               d.block_size - 1) + a->n_nodes;
+  }
   int P = a->partition_tokens;
   if (P < 0 || P % d.block_size || P > kMaxPartTokens)
     return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
-  if (P == 0) {
+  if (P == 0 && pl->prefix_chunks > 0 && tokens <= kMaxPartTokens) {
+    // after a shared prefix, the rest of each context in one partition: the
+    // tree kernel then folds the prefix partials into the output itself and no
+    // merge launch follows
+    P = (int)((tokens + d.block_size - 1) / d.block_size * d.block_size);
+  } else if (P == 0) {
     // Smallest partition with at most four units per resident wave: the tree
     // kernels are bound by issue, not by HBM, and short partitions even out
     // contexts of different lengths (a 4096-token prefix plus a short suffix
@@ -790,7 +847,7 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
       if (pairs * ((tokens + c - 1) / c) <= 4 * waves) { P = c; break; }
   }
   pl->part_tokens = P;
-  pl->max_parts = (int32_t)std::max<int64_t>(1, (tokens + P - 1) / P);
+  pl->max_parts = pl->prefix_chunks + (int32_t)std::max<int64_t>(1, (tokens + P - 1) / P);
   const uint64_t rows_total = (uint64_t)a->n_seqs * a->n_nodes * a->n_heads * pl->max_parts;
   pl->acc_bytes = align_up(rows_total * kHD * sizeof(float), 256);
   pl->ml_bytes = align_up(rows_total * 2 * sizeof(float), 256);
@@ -848,14 +905,24 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   p.n_blocks = d.n_blocks;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
-  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens, (int64_t)pl.bt_stride * d.block_size);
+  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.prefix_blocks * d.block_size +
+                                                (int64_t)(pl.max_parts - pl.prefix_chunks) * pl.part_tokens,
+                                            (int64_t)pl.bt_stride * d.block_size);
   p.n_nodes = a->n_nodes;
   p.n_rgroups = pl.n_rgroups;
   p.scale_log2 = scale * 1.4426950408889634f;
-  const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads * pl.n_rgroups;
+  p.prefix_blocks = pl.prefix_blocks;
+  p.prefix_chunks = pl.prefix_chunks;
+  const uint64_t units = (uint64_t)a->n_seqs * (pl.max_parts - pl.prefix_chunks) * d.n_kv_heads * pl.n_rgroups;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
+  if (pl.prefix_chunks > 0 &&
+      (rc = launch(ctx, pl.pfx_kernel.c_str(), dim3((unsigned)pl.pfx_row_tiles, (unsigned)d.n_kv_heads,
+                                                    (unsigned)pl.prefix_chunks),
+                   dim3(kPfxThreads), p, stream)))
+    return rc;
   if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
-  if (pl.max_parts == 1) return VK_OK;
+  // one partition (after any prefix chunks): the tree kernel wrote the output
+  if (pl.max_parts == pl.prefix_chunks + 1) return VK_OK;
 
   MergeParams m{};
   m.part_acc = p.part_acc;
@@ -868,6 +935,8 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   m.max_parts = pl.max_parts;
   m.part_tokens = pl.part_tokens;
   m.cap_tokens = p.cap_tokens;
+  m.prefix_blocks = pl.prefix_blocks;
+  m.prefix_chunks = pl.prefix_chunks;
   return launch(ctx, "vk_decode_merge", dim3((unsigned)((m.n_rows + 3) / 4)), dim3(256), m, stream);
 }
 

@@ -8,6 +8,7 @@
 // append kernels; the host rejects other shapes with VK_ERR_UNSUPPORTED.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #include "velokv_params.h"
 
@@ -689,6 +690,11 @@ DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, 
   }
 }
 
+// Tokens of a sequence with ctx committed tokens that a shared prefix of pb
+// pages covers: whole pages only, so that the rest of the context starts on a
+// page boundary.
+DEV int prefix_tokens_of(int ctx, int pb) { return min(ctx / BS, pb) * BS; }
+
 // Four int8 codes -> two fp16 pairs holding 1152 + c exactly (no subtraction).
 DEV void i8x4_to_h2x2_biased(uint32_t w, uint32_t& lo, uint32_t& hi) {
   const uint32_t u = w ^ 0x80808080u;
@@ -708,7 +714,7 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 // pacc ([.][HD] fp32) and pml ([.][2] fp32), in HBM or in LDS.
 template <int KV, int G, int RT, bool TREE, int QT>
 DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
-                    int64_t pbase, int pstride, float* pacc, float* pml) {
+                    int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr bool I8 = (ESZ == 1);
   constexpr bool BLK = (KV == KV_I8_BLK);
@@ -980,7 +986,29 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
         if (direct) {
-          const float inv = lr > 0.f ? 1.f / lr : 0.f;  // a tree row that sees no token attends to nothing
+          float L = lr;
+          if (npre > 0) {
+            // fold in the shared-prefix partials of the row (slots 0..npre-1):
+            //   out = (2^(Mr-M) o + sum_k 2^(M_k-M) acc_k) / (2^(Mr-M) lr + sum_k 2^(M_k-M) l_k)
+            const float2* pm = reinterpret_cast<const float2*>(P.part_ml) + orow * P.max_parts;
+            float Mt = Mr;
+            for (int k = 0; k < npre; ++k) Mt = fmaxf(Mt, pm[k].x);
+            const float es = (Mr == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(Mr - Mt);
+            L = lr * es;
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) o[nt] *= es;
+            for (int k = 0; k < npre; ++k) {
+              const float2 mk = pm[k];
+              if (mk.x == kNegInf) continue;
+              const float e = __builtin_amdgcn_exp2f(mk.x - Mt);
+              L = fmaf(e, mk.y, L);
+              const float4* src = reinterpret_cast<const float4*>(P.part_acc + (orow * P.max_parts + k) * HD + 8 * n);
+              const float4 a0 = src[0], a1 = src[1];
+              o[0] = fmaf(e, a0.x, o[0]); o[1] = fmaf(e, a0.y, o[1]); o[2] = fmaf(e, a0.z, o[2]); o[3] = fmaf(e, a0.w, o[3]);
+              o[4] = fmaf(e, a1.x, o[4]); o[5] = fmaf(e, a1.y, o[5]); o[6] = fmaf(e, a1.z, o[6]); o[7] = fmaf(e, a1.w, o[7]);
+            }
+          }
+          const float inv = L > 0.f ? 1.f / L : 0.f;  // a tree row that sees no token attends to nothing
           float4* dst = reinterpret_cast<float4*>(P.out + orow * HD + 8 * n);
           dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
           dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
@@ -1009,13 +1037,18 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   }
   const int kvh = unit % P.n_kv_heads;
   const int rest = unit / P.n_kv_heads;
-  const int part = rest % P.max_parts;
-  const int s = rest / P.max_parts;
+  const int gparts = P.max_parts - (TREE ? P.prefix_chunks : 0);  // partitions in the grid
+  const int part = rest % gparts;
+  const int s = rest / gparts;
   if (s >= P.n_seqs) return;
   const int N = TREE ? P.n_nodes : 1;
   const int ctx_c = max(0, min(P.context_lens[s], P.cap_tokens));  // committed tokens
   const int ctx = TREE ? min(ctx_c + N, P.cap_tokens) : ctx_c;      // committed + tree nodes
-  const int start = part * P.part_tokens;
+  // tree verify with a shared prefix: tokens below pre were covered by the
+  // prefix pass (partial slots 0..C0-1); the partitions start at pre
+  const int C0 = TREE ? P.prefix_chunks : 0;
+  const int pre = C0 > 0 ? prefix_tokens_of(ctx_c, P.prefix_blocks) : 0;
+  const int start = pre + part * P.part_tokens;
   if (start >= ctx) {
     if constexpr (!TREE) {
       if (part == 0) write_zero_rows<G>(P, s, kvh);
@@ -1023,20 +1056,23 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
     return;
   }
   const int end = min(start + P.part_tokens, ctx);
-  const int nparts = (ctx + P.part_tokens - 1) / P.part_tokens;
-  const int64_t pbase = TREE ? part : ((int64_t)s * P.n_heads + (int64_t)kvh * G) * P.max_parts + part;
-  attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1, pbase, P.max_parts, P.part_acc,
-                                  P.part_ml);
+  const int nparts = C0 + (ctx - pre + P.part_tokens - 1) / P.part_tokens;
+  const int64_t pbase = TREE ? C0 + part : ((int64_t)s * P.n_heads + (int64_t)kvh * G) * P.max_parts + part;
+  // the rest of a context in one partition after a shared prefix writes the
+  // output itself, folding in the prefix partials
+  const bool fold = C0 > 0 && nparts == C0 + 1;
+  attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1 || fold, pbase, P.max_parts, P.part_acc,
+                                  P.part_ml, fold ? C0 : 0);
 }
 
 // ---- stream-K decode -------------------------------------------------------
 // The blocks of all (sequence, KV head) segments in order form one range of
-// W = sum_s Hkv * ceil(ctx_s / 16) blocks; worker w (one wave) takes
-// [w W / nw, (w + 1) W / nw), nw = min(workers, W). A segment inside one worker's range is written
-// directly; a split segment leaves one partial per worker: slot 1 for the worker
-// where it starts, slot 0 for the workers that continue it. vk_decode_merge_sk
-// combines them. Worker 0 also stores the per-sequence block prefix and W for
-// the merge.
+// W = sum_s Hkv * ceil(ctx_s / 16) blocks; worker w (one wave) takes the w-th
+// range of the (weighted) stream-K split, sk_split in velokv_params.h. A
+// segment inside one worker's range is written directly; a split segment leaves
+// one partial per worker: slot 1 for the worker where it starts, slot 0 for the
+// workers that continue it. vk_decode_merge_sk combines them. Worker 0 also
+// stores the per-sequence block prefix and W for the merge.
 DEV int wave_sum_i(int x) {
   x += __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, false);
   x += __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, false);
@@ -1058,8 +1094,6 @@ DEV int wave_incl_scan_i(int x) {
 DEV int seq_blocks(const DecodeParams& P, int s) {
   return (max(0, min(P.context_lens[s], P.cap_tokens)) + BS - 1) / BS;
 }
-// first worker whose range holds global block x: b(w) <= x < b(w + 1), b(w) = w W / nw
-DEV int sk_worker_of(int64_t x, int64_t W, int nw) { return (int)(((x + 1) * nw + W - 1) / W) - 1; }
 
 template <int KV, int G>
 DEV void attn_streamk_mfma(const DecodeParams& P) {
@@ -1083,9 +1117,10 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     }
     if (lane == 0) P.sk_prefix[S] = W;
   }
-  const int nwe = min(nw, W);  // workers with work: every range holds at least one block
-  if (w >= nwe) return;
-  const int64_t b0 = (int64_t)w * W / nwe, b1 = (int64_t)(w + 1) * W / nwe;
+  if (W == 0) return;
+  const SkSplit sp = sk_split(W, nw, P.sk_fast, P.sk_wf, P.sk_ws);
+  if (w >= sp.nw) return;  // workers past the split have no blocks
+  const int64_t b0 = sk_begin(sp, w), b1 = sk_begin(sp, w + 1);
   // the sequence holding block b0 and its first global block
   int s = -1, pre = 0;
   {
@@ -1174,6 +1209,381 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   }
 }
 
+// ---- tree verify: shared-prefix pass ----------------------------------------
+// When every sequence of a tree-verify call starts with the same pb pages (a
+// prefix shared through the radix cache), attention over those pages is one
+// dense product per KV head: all S * n_nodes * G query rows against the same
+// keys. The prefix tiles are then read and converted once per workgroup of 256
+// rows instead of once per (sequence, KV head). Workgroup (row tile, KV head,
+// prefix chunk): 8 waves of 32 rows (two 16-row tiles). Each stage of 4 blocks
+// is loaded by all 512 threads, converted to fp16 (int8 codes become 1152 + c
+// exactly, as in attn_piece) and written to LDS; each wave then runs its score
+// and value products on the matrix cores against the staged tiles, two blocks
+// at a time, with the lazy running max of attn_piece. Row r of sequence s sees
+// prefix positions below prefix_tokens_of(ctx_s, pb). The chunk's unnormalised
+// partial (acc, M, l) goes to partial slot `chunk` of the row; the tree kernel
+// writes the rest of the context to the slots that follow and vk_decode_merge
+// combines them.
+//   scores  16x16x32: A = staged K (token n, dims 32kc + 8g .. +7), B = q^T (row
+//           n, the same dims); lane (n, g) gets row n, tokens 4g..4g+3.
+//   values  16x16x32 over a block pair (u0, u1): the 32 token slots of lane group
+//           g are tokens 4g..4g+3 of u0 then of u1, in A = p~ (row n) and in
+//           B = staged V (dim 16 nt + n); lane (n, g) accumulates rows 4g..4g+3,
+//           dims 16 nt + n.
+//   softmax y = S a + c with a = scale_log2 * k_scale and c = -(1152 sum q) a - M
+//           folded per block, p = 2^y; l and the int8 bias term sum over the
+//           fp16 p pairs with v_dot2 (p~ = p * v_scale in fp16).
+// LDS (two stage buffers, one barrier per stage, global loads two stages
+// ahead), each layout written and read without bank conflicts:
+//   K [tok][D + 8] fp16: 16-byte operand reads of 8 lanes (tokens n..n+7) land
+//     on distinct banks at the 272-byte pitch; the loader writes 8 bytes per
+//     lane along a token row.
+//   V per block pair [D][2 x 16 + 8] fp16: a dim row holds, for g = 0..3,
+//     tokens 4g..4g+3 of u0 then of u1, so that a lane's 8 token slots are one
+//     16-byte read; at the 80-byte pitch the reads of 8 lanes (dims n..n+7) land
+//     on distinct banks. The loader writes 8 bytes (one dim, four tokens of one
+//     block) per lane, gathered from two token-pair rows of the pool tile.
+constexpr int kPfxWaves = 8;
+constexpr int kPfxRows = 32 * kPfxWaves;  // query rows per workgroup
+constexpr int kPfxCH = 4;                 // blocks per stage (two pairs)
+constexpr int kPfxKPitch = HD + 8;        // fp16 per staged K row
+constexpr int kPfxVPitch = 2 * BS + 8;    // fp16 per staged V dim row of a block pair
+
+template <int KV>
+struct PfxRaw {  // this thread's share of one stage
+  uint32_t k[kPfxCH][Esz<KV>::v];  // 4 dims of one K token row (int8: 4 bytes, fp16: 8 bytes)
+  uint32_t v[kPfxCH][2];           // tokens 4t..4t+1 and 4t+2..4t+3 of one V dim (int8: 2 bytes each, fp16: 4)
+  float sc;                        // a block scale (threads 0 .. 2 kPfxCH - 1, int8 only)
+};
+
+template <int KV, int G, int QT>
+DEV void tree_prefix_mfma(const DecodeParams& P) {
+  constexpr bool I8 = (KV == KV_I8_BLK);
+  constexpr int ESZ = Esz<KV>::v;
+  constexpr float kBias = 1152.0f;
+  __shared__ __attribute__((aligned(16))) _Float16 kl[2][kPfxCH][BS * kPfxKPitch];
+  __shared__ __attribute__((aligned(16))) _Float16 vl[2][kPfxCH / 2][HD * kPfxVPitch];
+  __shared__ float sl[2][kPfxCH][2];
+
+  const int tid = (int)threadIdx.x;
+  const int wave = tid / WAVE;
+  const int lane = lane_id();
+  const int n = lane & 15, g = lane >> 4;
+  const int kvh = (int)blockIdx.y;
+  const int chunk = (int)blockIdx.z, nchunks = (int)gridDim.z;
+  const int N = P.n_nodes, H = P.n_heads;
+  const int RS = N * G;  // rows of one sequence for this KV head
+  const int R = P.n_seqs * RS;
+  const int wrow0 = (int)blockIdx.x * kPfxRows + wave * 32;
+  const int PB = P.prefix_blocks;
+  const int per = (PB + nchunks - 1) / nchunks;
+  const int cb0 = min(PB, chunk * per), cb1 = min(PB, cb0 + per);
+  const int nst = (cb1 - cb0 + kPfxCH - 1) / kPfxCH;
+  int prow = P.seq_rows ? P.seq_rows[0] : 0;
+  if (P.bt_rows > 0) prow = min(max(prow, 0), P.bt_rows - 1);
+  const int32_t* bt = P.block_tables + (int64_t)prow * P.bt_stride;
+  auto out_row = [&](int r) -> int64_t {
+    const int s = r / RS, rem = r - s * RS;
+    return ((int64_t)s * N + rem / G) * H + (int64_t)kvh * G + rem % G;
+  };
+
+  // ---- q^T operands of rows wrow0 + 16 rt + n, and the prefix each row sees ----
+  half8 qa[2][4];
+  float qb[2];
+  int lim[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = wrow0 + 16 * rt + n;
+    const bool valid = r < R;
+    const int64_t qoff = (valid ? out_row(r) : 0) * HD + 8 * g;
+    float qsum = 0.f;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (valid) {
+        if constexpr (QT == DT_F32) {
+          const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 32 * kc);
+          const float4 x0 = q32[0], x1 = q32[1];
+          v = make_uint4(pack_h2(x0.x, x0.y), pack_h2(x0.z, x0.w), pack_h2(x1.x, x1.y), pack_h2(x1.z, x1.w));
+        } else {
+          v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qoff + 32 * kc);
+        }
+      }
+      qa[rt][kc] = bitcast<half8>(v);
+      if constexpr (I8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qsum += (float)qa[rt][kc][j];
+      }
+    }
+    qb[rt] = 0.f;
+    if constexpr (I8) {
+      qsum += shfl_xor(qsum, 16);
+      qsum += shfl_xor(qsum, 32);
+      qb[rt] = kBias * qsum;
+    }
+    // rows past the end see the whole chunk (their results are dropped)
+    lim[rt] = valid ? prefix_tokens_of(max(0, min(P.context_lens[r / RS], P.cap_tokens)), PB) : PB * BS;
+  }
+  // blocks below every row's limit need no mask (wave-uniform)
+  const int minlim = __builtin_amdgcn_readfirstlane((int)(-wave_max(-(float)min(lim[0], lim[1]))));
+
+  float M[2], lrun[2], psum[2];
+  float4v acc[2][8];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    M[rt] = kNegInf; lrun[rt] = 0.f; psum[rt] = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- stage loader: every thread reads 4 dims of K token kt and 4 tokens of V
+  // dim vd (token group vq) of each block ----
+  const int kt = tid >> 5, kd = (tid & 31) * 4;
+  const int vd = tid & (HD - 1), vq = tid >> 7;
+  // byte offset of K dims kd..kd+3 of token kt: int8 tiles hold dims 32c + 16h + j
+  // of token t at byte 1024 h + (4t + c) 16 + j
+  const uint32_t koff = (ESZ == 1) ? (uint32_t)(((kd >> 4) & 1) * 1024 + (4 * kt + (kd >> 5)) * 16 + (kd & 15))
+                                   : (uint32_t)((kt * HD + kd) * 2);
+  // V token pairs 2 vq and 2 vq + 1 of dim vd ([pair][D][2] tile)
+  const uint32_t voff0 = (uint32_t)(((2 * vq) * HD + vd) * 2 * ESZ), voff1 = voff0 + HD * 2 * ESZ;
+  auto gload = [&](PfxRaw<KV>& rw, int st) {
+#pragma unroll
+    for (int u = 0; u < kPfxCH; ++u) {
+      const int b = cb0 + st * kPfxCH + u;
+#pragma unroll
+      for (int j = 0; j < ESZ; ++j) rw.k[u][j] = 0u;
+      rw.v[u][0] = rw.v[u][1] = 0u;
+      if (st < nst && b < cb1) {
+        const int blk = min(max(bt[b], 0), P.n_blocks - 1);
+        const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
+        const uint8_t* kt_ = P.kc + tix * P.tile_bytes;
+        const uint8_t* vt_ = P.vc + tix * P.tile_bytes;
+        if constexpr (ESZ == 1) {
+          rw.k[u][0] = *reinterpret_cast<const uint32_t*>(kt_ + koff);
+          rw.v[u][0] = *reinterpret_cast<const uint16_t*>(vt_ + voff0);
+          rw.v[u][1] = *reinterpret_cast<const uint16_t*>(vt_ + voff1);
+        } else {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(kt_ + koff);
+          rw.k[u][0] = x.x; rw.k[u][1] = x.y;
+          rw.v[u][0] = *reinterpret_cast<const uint32_t*>(vt_ + voff0);
+          rw.v[u][1] = *reinterpret_cast<const uint32_t*>(vt_ + voff1);
+        }
+      }
+    }
+    rw.sc = 1.f;
+    if constexpr (I8) {
+      if (tid < 2 * kPfxCH) {
+        const int u = tid % kPfxCH;
+        const int b = cb0 + st * kPfxCH + u;
+        if (st < nst && b < cb1) {
+          const int blk = min(max(bt[b], 0), P.n_blocks - 1);
+          const uint8_t* sp = (tid < kPfxCH) ? P.ks : P.vs;
+          rw.sc = h2f(reinterpret_cast<const uint16_t*>(sp)[(int64_t)blk * P.n_kv_heads + kvh]);
+        }
+      }
+    }
+  };
+  auto lwrite = [&](int buf, const PfxRaw<KV>& rw) {
+#pragma unroll
+    for (int u = 0; u < kPfxCH; ++u) {
+      uint32_t kw0, kw1, vw0, vw1;
+      if constexpr (ESZ == 1) {
+        i8x4_to_h2x2_biased(rw.k[u][0], kw0, kw1);
+        i8x4_to_h2x2_biased(rw.v[u][0] | (rw.v[u][1] << 16), vw0, vw1);
+      } else {
+        kw0 = rw.k[u][0]; kw1 = rw.k[u][1];
+        vw0 = rw.v[u][0]; vw1 = rw.v[u][1];
+      }
+      *reinterpret_cast<u32x2*>(&kl[buf][u][kt * kPfxKPitch + kd]) = u32x2{kw0, kw1};
+      *reinterpret_cast<u32x2*>(&vl[buf][u >> 1][vd * kPfxVPitch + 8 * vq + 4 * (u & 1)]) = u32x2{vw0, vw1};
+    }
+    if constexpr (I8) {
+      if (tid < 2 * kPfxCH) sl[buf][tid % kPfxCH][tid / kPfxCH] = rw.sc;
+    }
+  };
+
+  const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+  // one block pair (u0 = up, u1 = up + 1) of stage buffer buf. Masks: row n sees
+  // tokens 4g + r of block b0 + j for r < vis; a lane whose four tokens are all
+  // hidden gets -inf in the score offset, and the per-token mask runs only when
+  // some lane sees part of its four tokens (one block per row at most).
+  auto pair_body = [&](int buf, int up, int b0, bool has1, bool plain) {
+    half8 kop[2][4];
+    float a[2], vs[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const _Float16* kb = &kl[buf][up + j][n * kPfxKPitch + 8 * g];
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) kop[j][kc] = *reinterpret_cast<const half8*>(kb + 32 * kc);
+      a[j] = P.scale_log2 * (I8 ? sl[buf][up + j][0] : 1.f);
+      vs[j] = I8 ? sl[buf][up + j][1] : 1.f;
+    }
+    int vis[2][2];
+    float hide[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    bool partial = false;
+    if (!plain) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          vis[rt][j] = (j == 0 || has1) ? lim[rt] - (b0 + j) * BS - 4 * g : 0;
+          hide[rt][j] = vis[rt][j] > 0 ? 0.f : kNegInf;
+          partial |= vis[rt][j] > 0 && vis[rt][j] < 4;
+        }
+    }
+    // scores relative to the running max: y = S a + c - M (log2 units)
+    float y[2][2][4];
+    bool need = false;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
+      const float thr = (M[rt] == kNegInf) ? kNegInf : kRescaleThreshold;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float4v sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[j][kc], qa[rt][kc], sc, 0, 0, 0);
+        const float c = (I8 ? fmaf(-qb[rt], a[j], -Ms) : -Ms) + hide[rt][j];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[rt][j][r] = fmaf(sc[r], a[j], c);
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(partial) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[rt][j][r] = (r < vis[rt][j]) ? y[rt][j][r] : kNegInf;
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float thr = (M[rt] == kNegInf) ? kNegInf : kRescaleThreshold;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) need |= y[rt][j][r] > thr;
+    }
+    // lazy running max of row n (rare after the first blocks)
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
+        float m = y[rt][0][0];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m = fmaxf(m, y[rt][j][r]);
+        m = fmaxf(m, shfl_xor(m, 16));
+        m = fmaxf(m, shfl_xor(m, 32));  // max over the pair's tokens of row n, relative to Ms
+        const float Mn = fmaxf(M[rt], m + Ms);
+        const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[rt] - Mn);
+        const float shift = (Mn == kNegInf) ? 0.f : Mn - Ms;
+        M[rt] = Mn;
+        lrun[rt] *= alpha;
+        psum[rt] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[rt][j][r] -= shift;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * g + r, WAVE);
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt) acc[rt][nt][r] *= ar;
+        }
+      }
+    }
+    // p = 2^y in fp16 pairs; l += sum p; p~ = p * v_scale is the A operand
+    half8 pa[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      uint32_t pw[4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t lo = pack_h2(__builtin_amdgcn_exp2f(y[rt][j][0]), __builtin_amdgcn_exp2f(y[rt][j][1]));
+        const uint32_t hi = pack_h2(__builtin_amdgcn_exp2f(y[rt][j][2]), __builtin_amdgcn_exp2f(y[rt][j][3]));
+        lrun[rt] = dot2(hi, bitcast<uint32_t>(ones), dot2(lo, bitcast<uint32_t>(ones), lrun[rt]));
+        if constexpr (I8) {
+          const half2v v2 = {(_Float16)vs[j], (_Float16)vs[j]};
+          const uint32_t plo = bitcast<uint32_t>(bitcast<half2v>(lo) * v2);
+          const uint32_t phi = bitcast<uint32_t>(bitcast<half2v>(hi) * v2);
+          psum[rt] = dot2(phi, bitcast<uint32_t>(ones), dot2(plo, bitcast<uint32_t>(ones), psum[rt]));
+          pw[2 * j] = plo; pw[2 * j + 1] = phi;
+        } else {
+          pw[2 * j] = lo; pw[2 * j + 1] = hi;
+        }
+      }
+      pa[rt] = bitcast<half8>(u32x4{pw[0], pw[1], pw[2], pw[3]});
+    }
+    // values: B = V of dim 16 nt + n, tokens 4g..4g+3 of u0 then of u1
+    const _Float16* vb = &vl[buf][up >> 1][n * kPfxVPitch + 8 * g];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const half8 vop = *reinterpret_cast<const half8*>(vb + 16 * nt * kPfxVPitch);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vop, acc[rt][nt], 0, 0, 0);
+    }
+  };
+  auto compute = [&](int buf, int st) {
+#pragma unroll
+    for (int up = 0; up < kPfxCH; up += 2) {
+      const int b0 = cb0 + st * kPfxCH + up;  // first block of the pair (wave-uniform)
+      if (b0 < cb1) {
+        const bool has1 = b0 + 1 < cb1;
+        pair_body(buf, up, b0, has1, has1 && (b0 + 2) * BS <= minlim);
+      }
+    }
+  };
+
+  // ---- pipeline: LDS buffers alternate, raw stages ra / rb two ahead ----
+  PfxRaw<KV> ra, rb;
+  gload(ra, 0);
+  gload(rb, 1);
+  lwrite(0, ra);
+  gload(ra, 2);
+  __syncthreads();
+  for (int st = 0; st < nst; st += 2) {
+    compute(0, st);
+    lwrite(1, rb);       // stage st + 1
+    gload(rb, st + 3);
+    __syncthreads();
+    if (st + 1 >= nst) break;
+    compute(1, st + 1);
+    lwrite(0, ra);       // stage st + 2
+    gload(ra, st + 4);
+    __syncthreads();
+  }
+
+  // ---- partials: rows 16 rt + 4g + r, dims 16 nt + n ----
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float l = lrun[rt], ps = psum[rt];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    if constexpr (I8) {
+      ps += shfl_xor(ps, 16);
+      ps += shfl_xor(ps, 32);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int src = 4 * g + r;
+      const float lr = __shfl(l, src, WAVE);
+      const float psr = I8 ? __shfl(ps, src, WAVE) : 0.f;
+      const float Mr = __shfl(M[rt], src, WAVE);
+      const int row = wrow0 + 16 * rt + 4 * g + r;
+      if (row < R) {
+        const int64_t pr = out_row(row) * P.max_parts + chunk;
+        float* dst = P.part_acc + pr * HD + n;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) dst[16 * nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
+        if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(Mr, lr);
+      }
+    }
+  }
+}
+
 // Combine the partitions of one (sequence, head):
 //   out = sum_p 2^(M_p - M) acc_p / sum_p 2^(M_p - M) l_p,  M = max_p M_p.
 // One wave per (sequence, head); sequences with a single partition were
@@ -1220,13 +1630,19 @@ DEV void merge_row(const MergeParams& P, int64_t out_row, int np, PR pr) {
 // Split-K merge: one wave per (sequence, row) with partials [row][max_parts]:
 //   out = sum_p 2^(M_p - M) acc_p / sum_p 2^(M_p - M) l_p,  M = max_p M_p.
 // Rows whose context fits one partition were finished by the attention kernel.
+// With a shared prefix (tree verify), slots 0..prefix_chunks-1 hold the prefix
+// pass and the partitions of the rest follow; a row whose rest fits one
+// partition was finished by the tree kernel (it folds the prefix slots in).
 __device__ void decode_merge(const MergeParams& P) {
   const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
   if (r >= P.n_rows) return;
   const int s = r / P.rows_per_seq;
-  const int ctx = min(max(0, P.context_lens[s]) + P.extra_tokens, P.cap_tokens);
-  const int np = (ctx + P.part_tokens - 1) / P.part_tokens;
-  if (np <= 1) return;
+  const int ctx_c = max(0, min(P.context_lens[s], P.cap_tokens));
+  const int ctx = min(ctx_c + P.extra_tokens, P.cap_tokens);
+  const int pre = P.prefix_chunks > 0 ? prefix_tokens_of(ctx_c, P.prefix_blocks) : 0;
+  const int np = P.prefix_chunks + (ctx - pre + P.part_tokens - 1) / P.part_tokens;
+  // one partition, or one after the prefix chunks: the attention kernel wrote the row
+  if (np == P.prefix_chunks + 1) return;
   const int64_t base = (int64_t)r * P.max_parts;
   merge_row(P, r, np, [&](int k) -> int64_t { return base + k; });
 }
@@ -1249,10 +1665,10 @@ __device__ void decode_merge_sk(const MergeParams& P) {
     return;
   }
   const int64_t W = P.sk_prefix[P.n_seqs];
-  const int nwe = (int)min((int64_t)P.n_workers, W);
+  const SkSplit sp = sk_split(W, P.n_workers, P.sk_fast, P.sk_wf, P.sk_ws);
   const int64_t S0 = (int64_t)P.sk_prefix[s] + (int64_t)kvh * nb;
-  const int w_lo = sk_worker_of(S0, W, nwe);
-  const int w_hi = sk_worker_of(S0 + nb - 1, W, nwe);
+  const int w_lo = sk_worker_of(sp, S0);
+  const int w_hi = sk_worker_of(sp, S0 + nb - 1);
   if (w_lo == w_hi) return;
   merge_row(P, r, w_hi - w_lo + 1, [&](int k) -> int64_t {
     return ((int64_t)(w_lo + k) * 2 + (k == 0 ? 1 : 0)) * G + gi;
@@ -1862,6 +2278,16 @@ VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
 VK_TREE_KV(1, )
 VK_TREE_KV(2, VK_TWO_WAVES)
 VK_TREE_KV(3, VK_TWO_WAVES)
+
+// Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
+#define VK_TREE_PFX(KV, G, QT)                                                      \
+  extern "C" __global__ void __launch_bounds__(64 * kPfxWaves) VK_TWO_WAVES         \
+      vk_tree_pfx_kv##KV##_g##G##_q##QT(const DecodeParams P) {                     \
+    tree_prefix_mfma<KV, G, QT>(P);                                                 \
+  }
+#define VK_TREE_PFX_G(KV, QT) \
+  VK_TREE_PFX(KV, 1, QT) VK_TREE_PFX(KV, 2, QT) VK_TREE_PFX(KV, 4, QT) VK_TREE_PFX(KV, 8, QT)
+VK_TREE_PFX_G(1, 0) VK_TREE_PFX_G(1, 1) VK_TREE_PFX_G(3, 0) VK_TREE_PFX_G(3, 1)
 
 
 #define VK_APPEND(KV) \

@@ -77,7 +77,7 @@ class TreeArgs(C.Structure):
                 ("context_lens", C.c_void_p), ("tree_mask", C.c_void_p), ("n_seqs", C.c_int32),
                 ("n_nodes", C.c_int32), ("n_heads", C.c_int32), ("max_context_len", C.c_int32),
                 ("scale", C.c_float), ("partition_tokens", C.c_int32), ("workspace", C.c_void_p),
-                ("workspace_bytes", C.c_uint64)]
+                ("workspace_bytes", C.c_uint64), ("shared_blocks", C.c_int32)]
 
 
 class NixlItem(C.Structure):

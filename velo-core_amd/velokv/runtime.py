@@ -150,16 +150,17 @@ class Context:
     def tree_verify(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, tree_mask, n_seqs: int,
                     n_nodes: int, n_heads: int, max_context_len: int, block_tables=None, bt_stride: int = 0,
                     seq_rows=None, scale: float = 0.0, partition_tokens: int = 0, workspace=None,
-                    workspace_bytes: int = 0, stream=None):
+                    workspace_bytes: int = 0, stream=None, shared_blocks: int = 0):
+        """vk_tree_verify; shared_blocks = leading table pages every row shares (radix-cache prefix)."""
         a = _capi.TreeArgs(layer, _bptr(q), q_dtype, _bptr(out), _bptr(block_tables), bt_stride, _bptr(seq_rows),
                            _bptr(context_lens), _bptr(tree_mask), n_seqs, n_nodes, n_heads, max_context_len, scale,
-                           partition_tokens, _bptr(workspace), workspace_bytes)
+                           partition_tokens, _bptr(workspace), workspace_bytes, shared_blocks)
         check(lib().vk_tree_verify(self.h, pool.h, C.byref(a), _sptr(stream)))
 
     def tree_workspace_bytes(self, pool: "Pool", n_seqs, n_nodes, n_heads, max_context_len, bt_stride=0,
-                             partition_tokens=0, q_dtype=DT_F16) -> int:
+                             partition_tokens=0, q_dtype=DT_F16, shared_blocks: int = 0) -> int:
         a = _capi.TreeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None, None,
-                           n_seqs, n_nodes, n_heads, max_context_len, 0.0, partition_tokens, None, 0)
+                           n_seqs, n_nodes, n_heads, max_context_len, 0.0, partition_tokens, None, 0, shared_blocks)
         n = C.c_uint64()
         check(lib().vk_tree_verify_workspace(pool.h, C.byref(a), C.byref(n)))
         return n.value
