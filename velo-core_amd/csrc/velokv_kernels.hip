@@ -1234,26 +1234,28 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
 //           folded per block, p = 2^y; l and the int8 bias term sum over the
 //           fp16 p pairs with v_dot2 (p~ = p * v_scale in fp16).
 // LDS (two stage buffers, one barrier per stage, global loads two stages
-// ahead), each layout written and read without bank conflicts:
-//   K [tok][D + 8] fp16: 16-byte operand reads of 8 lanes (tokens n..n+7) land
-//     on distinct banks at the 272-byte pitch; the loader writes 8 bytes per
-//     lane along a token row.
-//   V per block pair [D][2 x 16 + 8] fp16: a dim row holds, for g = 0..3,
-//     tokens 4g..4g+3 of u0 then of u1, so that a lane's 8 token slots are one
-//     16-byte read; at the 80-byte pitch the reads of 8 lanes (dims n..n+7) land
-//     on distinct banks. The loader writes 8 bytes (one dim, four tokens of one
-//     block) per lane, gathered from two token-pair rows of the pool tile.
+// ahead). gfx950 serves a 16-byte read for lanes {0-7, 16-23} (then
+// {8-15, 24-31}, ...) in one pass over 64 four-byte banks: with lane (n, g)
+// reading row n at word 4g, rows must start 8 (mod 16) words apart for the
+// 16 lanes to cover the 64 banks once (measured: 72-word rows 0 conflict
+// cycles, 68- or 20-word rows 4 per read).
+//   K [tok][D + 16] fp16 (72-word rows); the loader writes 8 bytes per lane
+//     along a token row.
+//   V per block pair [D][2 x 16 + 16] fp16 (24-word rows): a dim row holds, for
+//     g = 0..3, tokens 4g..4g+3 of u0 then of u1, so that a lane's 8 token slots
+//     are one 16-byte read. The loader writes 8 bytes (one dim, four tokens of
+//     one block) per lane, gathered from two token-pair rows of the pool tile.
 constexpr int kPfxWaves = 8;
 constexpr int kPfxRows = 32 * kPfxWaves;  // query rows per workgroup
 constexpr int kPfxCH = 4;                 // blocks per stage (two pairs)
-constexpr int kPfxKPitch = HD + 8;        // fp16 per staged K row
-constexpr int kPfxVPitch = 2 * BS + 8;    // fp16 per staged V dim row of a block pair
+constexpr int kPfxKPitch = HD + 16;       // fp16 per staged K row (72 words)
+constexpr int kPfxVPitch = 2 * BS + 16;   // fp16 per staged V dim row of a block pair (24 words)
 
 template <int KV>
 struct PfxRaw {  // this thread's share of one stage
   uint32_t k[kPfxCH][Esz<KV>::v];  // 4 dims of one K token row (int8: 4 bytes, fp16: 8 bytes)
   uint32_t v[kPfxCH][2];           // tokens 4t..4t+1 and 4t+2..4t+3 of one V dim (int8: 2 bytes each, fp16: 4)
-  float sc;                        // a block scale (threads 0 .. 2 kPfxCH - 1, int8 only)
+  uint32_t sc;                     // fp16 bits of a block scale (threads 0 .. 2 kPfxCH - 1, int8 only)
 };
 
 template <int KV, int G, int QT>
@@ -1346,40 +1348,42 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
                                    : (uint32_t)((kt * HD + kd) * 2);
   // V token pairs 2 vq and 2 vq + 1 of dim vd ([pair][D][2] tile)
   const uint32_t voff0 = (uint32_t)(((2 * vq) * HD + vd) * 2 * ESZ), voff1 = voff0 + HD * 2 * ESZ;
+  // Loads are unconditional: a block past the chunk (or a stage past the last)
+  // reads the chunk's first page, a written prefix page, whose tokens the
+  // compute then skips or masks. (A zero fill on a branch let the compiler hoist
+  // the first step of the int8 conversion right behind each load, which turned
+  // the two-stage prefetch into waits.)
   auto gload = [&](PfxRaw<KV>& rw, int st) {
+    int blk[kPfxCH];  // wave-uniform page ids of the stage
 #pragma unroll
     for (int u = 0; u < kPfxCH; ++u) {
-      const int b = cb0 + st * kPfxCH + u;
-#pragma unroll
-      for (int j = 0; j < ESZ; ++j) rw.k[u][j] = 0u;
-      rw.v[u][0] = rw.v[u][1] = 0u;
-      if (st < nst && b < cb1) {
-        const int blk = min(max(bt[b], 0), P.n_blocks - 1);
-        const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
-        const uint8_t* kt_ = P.kc + tix * P.tile_bytes;
-        const uint8_t* vt_ = P.vc + tix * P.tile_bytes;
-        if constexpr (ESZ == 1) {
-          rw.k[u][0] = *reinterpret_cast<const uint32_t*>(kt_ + koff);
-          rw.v[u][0] = *reinterpret_cast<const uint16_t*>(vt_ + voff0);
-          rw.v[u][1] = *reinterpret_cast<const uint16_t*>(vt_ + voff1);
-        } else {
-          const u32x2 x = *reinterpret_cast<const u32x2*>(kt_ + koff);
-          rw.k[u][0] = x.x; rw.k[u][1] = x.y;
-          rw.v[u][0] = *reinterpret_cast<const uint32_t*>(vt_ + voff0);
-          rw.v[u][1] = *reinterpret_cast<const uint32_t*>(vt_ + voff1);
-        }
+      int b = cb0 + st * kPfxCH + u;
+      b = (st < nst && b < cb1) ? b : cb0;
+      blk[u] = min(max(bt[b], 0), P.n_blocks - 1);
+      const uint64_t tix = (uint64_t)blk[u] * P.n_kv_heads + kvh;
+      const uint8_t* kt_ = P.kc + tix * P.tile_bytes;
+      const uint8_t* vt_ = P.vc + tix * P.tile_bytes;
+      if constexpr (ESZ == 1) {
+        rw.k[u][0] = *reinterpret_cast<const uint32_t*>(kt_ + koff);
+        rw.v[u][0] = *reinterpret_cast<const uint16_t*>(vt_ + voff0);
+        rw.v[u][1] = *reinterpret_cast<const uint16_t*>(vt_ + voff1);
+      } else {
+        const u32x2 x = *reinterpret_cast<const u32x2*>(kt_ + koff);
+        rw.k[u][0] = x.x; rw.k[u][1] = x.y;
+        rw.v[u][0] = *reinterpret_cast<const uint32_t*>(vt_ + voff0);
+        rw.v[u][1] = *reinterpret_cast<const uint32_t*>(vt_ + voff1);
       }
     }
-    rw.sc = 1.f;
+    rw.sc = 0u;
     if constexpr (I8) {
+      // threads 0..3: K scales, 4..7: V scales of the stage's blocks, as raw bits
+      // (converting here would wait for the load); the page ids are the
+      // uniform ones above, so no per-lane id load precedes them
+      const int u = tid % kPfxCH;
+      const int bsel = u == 0 ? blk[0] : u == 1 ? blk[1] : u == 2 ? blk[2] : blk[3];
       if (tid < 2 * kPfxCH) {
-        const int u = tid % kPfxCH;
-        const int b = cb0 + st * kPfxCH + u;
-        if (st < nst && b < cb1) {
-          const int blk = min(max(bt[b], 0), P.n_blocks - 1);
-          const uint8_t* sp = (tid < kPfxCH) ? P.ks : P.vs;
-          rw.sc = h2f(reinterpret_cast<const uint16_t*>(sp)[(int64_t)blk * P.n_kv_heads + kvh]);
-        }
+        const uint8_t* sp = (tid < kPfxCH) ? P.ks : P.vs;
+        rw.sc = reinterpret_cast<const uint16_t*>(sp)[(int64_t)bsel * P.n_kv_heads + kvh];
       }
     }
   };
@@ -1398,7 +1402,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       *reinterpret_cast<u32x2*>(&vl[buf][u >> 1][vd * kPfxVPitch + 8 * vq + 4 * (u & 1)]) = u32x2{vw0, vw1};
     }
     if constexpr (I8) {
-      if (tid < 2 * kPfxCH) sl[buf][tid % kPfxCH][tid / kPfxCH] = rw.sc;
+      if (tid < 2 * kPfxCH) sl[buf][tid % kPfxCH][tid / kPfxCH] = h2f((uint16_t)rw.sc);
     }
   };
 
@@ -1537,23 +1541,26 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     }
   };
 
-  // ---- pipeline: LDS buffers alternate, raw stages ra / rb two ahead ----
-  PfxRaw<KV> ra, rb;
-  gload(ra, 0);
-  gload(rb, 1);
-  lwrite(0, ra);
-  gload(ra, 2);
-  __syncthreads();
-  for (int st = 0; st < nst; st += 2) {
-    compute(0, st);
-    lwrite(1, rb);       // stage st + 1
-    gload(rb, st + 3);
+  // ---- pipeline: LDS buffers alternate, raw stages ra / rb two ahead (an
+  // empty chunk, nst = 0 for the whole workgroup, writes empty partials) ----
+  if (nst > 0) {
+    PfxRaw<KV> ra, rb;
+    gload(ra, 0);
+    gload(rb, 1);
+    lwrite(0, ra);
+    gload(ra, 2);
     __syncthreads();
-    if (st + 1 >= nst) break;
-    compute(1, st + 1);
-    lwrite(0, ra);       // stage st + 2
-    gload(ra, st + 4);
-    __syncthreads();
+    for (int st = 0; st < nst; st += 2) {
+      compute(0, st);
+      lwrite(1, rb);       // stage st + 1
+      gload(rb, st + 3);
+      __syncthreads();
+      if (st + 1 >= nst) break;
+      compute(1, st + 1);
+      lwrite(0, ra);       // stage st + 2
+      gload(ra, st + 4);
+      __syncthreads();
+    }
   }
 
   // ---- partials: rows 16 rt + 4g + r, dims 16 nt + n ----
