@@ -763,8 +763,8 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
 
 namespace {
 
-constexpr int kPfxRowsPerGroup = 256;  // query rows per workgroup of the shared-prefix pass (8 waves of 32)
-constexpr int kPfxThreads = 512;
+constexpr int kPfxRowsPerGroup = 256;  // query rows per workgroup of the shared-prefix pass (16 waves of 16)
+constexpr int kPfxThreads = 1024;
 
 struct TreePlan {
   const int32_t* bt;

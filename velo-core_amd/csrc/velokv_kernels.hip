@@ -1215,9 +1215,11 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
 // dense product per KV head: all S * n_nodes * G query rows against the same
 // keys. The prefix tiles are then read and converted once per workgroup of 256
 // rows instead of once per (sequence, KV head). Workgroup (row tile, KV head,
-// prefix chunk): 8 waves of 32 rows (two 16-row tiles). Each stage of 4 blocks
-// is loaded by all 512 threads, converted to fp16 (int8 codes become 1152 + c
-// exactly, as in attn_piece) and written to LDS; each wave then runs its score
+// prefix chunk): 16 waves of one 16-row tile, four per SIMD (at 128 registers:
+// with two waves per SIMD the chain scores -> softmax -> values of each wave
+// left the matrix cores idle 70 % of the time). Each stage of 4 blocks is
+// loaded by the first 8 waves, converted to fp16 (int8 codes become 1152 + c
+// exactly, as in attn_piece) and written to LDS; every wave then runs its score
 // and value products on the matrix cores against the staged tiles, two blocks
 // at a time, with the lazy running max of attn_piece. Row r of sequence s sees
 // prefix positions below prefix_tokens_of(ctx_s, pb). The chunk's unnormalised
@@ -1233,8 +1235,9 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
 //   softmax y = S a + c with a = scale_log2 * k_scale and c = -(1152 sum q) a - M
 //           folded per block, p = 2^y; l and the int8 bias term sum over the
 //           fp16 p pairs with v_dot2 (p~ = p * v_scale in fp16).
-// LDS (two stage buffers, one barrier per stage, global loads two stages
-// ahead). gfx950 serves a 16-byte read for lanes {0-7, 16-23} (then
+// LDS: two stage buffers, one barrier per stage; a loader thread holds the
+// next stage's raw bytes in registers while the current one is consumed.
+// gfx950 serves a 16-byte read for lanes {0-7, 16-23} (then
 // {8-15, 24-31}, ...) in one pass over 64 four-byte banks: with lane (n, g)
 // reading row n at word 4g, rows must start 8 (mod 16) words apart for the
 // 16 lanes to cover the 64 banks once (measured: 72-word rows 0 conflict
@@ -1245,8 +1248,10 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
 //     g = 0..3, tokens 4g..4g+3 of u0 then of u1, so that a lane's 8 token slots
 //     are one 16-byte read. The loader writes 8 bytes (one dim, four tokens of
 //     one block) per lane, gathered from two token-pair rows of the pool tile.
-constexpr int kPfxWaves = 8;
-constexpr int kPfxRows = 32 * kPfxWaves;  // query rows per workgroup
+constexpr int kPfxRT = 1;                 // 16-row tiles per wave
+constexpr int kPfxWaves = 16;             // four per SIMD (at most 128 registers)
+constexpr int kPfxRows = 16 * kPfxRT * kPfxWaves;  // query rows per workgroup
+constexpr int kPfxLoadThreads = 512;      // the first 8 waves load the stages
 constexpr int kPfxCH = 4;                 // blocks per stage (two pairs)
 constexpr int kPfxKPitch = HD + 16;       // fp16 per staged K row (72 words)
 constexpr int kPfxVPitch = 2 * BS + 16;   // fp16 per staged V dim row of a block pair (24 words)
@@ -1260,6 +1265,7 @@ struct PfxRaw {  // this thread's share of one stage
 
 template <int KV, int G, int QT>
 DEV void tree_prefix_mfma(const DecodeParams& P) {
+  constexpr int RT = kPfxRT;
   constexpr bool I8 = (KV == KV_I8_BLK);
   constexpr int ESZ = Esz<KV>::v;
   constexpr float kBias = 1152.0f;
@@ -1276,7 +1282,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   const int N = P.n_nodes, H = P.n_heads;
   const int RS = N * G;  // rows of one sequence for this KV head
   const int R = P.n_seqs * RS;
-  const int wrow0 = (int)blockIdx.x * kPfxRows + wave * 32;
+  const int wrow0 = (int)blockIdx.x * kPfxRows + wave * 16 * RT;
   const int PB = P.prefix_blocks;
   const int per = (PB + nchunks - 1) / nchunks;
   const int cb0 = min(PB, chunk * per), cb1 = min(PB, cb0 + per);
@@ -1290,11 +1296,11 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   };
 
   // ---- q^T operands of rows wrow0 + 16 rt + n, and the prefix each row sees ----
-  half8 qa[2][4];
-  float qb[2];
-  int lim[2];
+  half8 qa[RT][4];
+  float qb[RT];
+  int lim[RT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const int r = wrow0 + 16 * rt + n;
     const bool valid = r < R;
     const int64_t qoff = (valid ? out_row(r) : 0) * HD + 8 * g;
@@ -1327,19 +1333,21 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     lim[rt] = valid ? prefix_tokens_of(max(0, min(P.context_lens[r / RS], P.cap_tokens)), PB) : PB * BS;
   }
   // blocks below every row's limit need no mask (wave-uniform)
-  const int minlim = __builtin_amdgcn_readfirstlane((int)(-wave_max(-(float)min(lim[0], lim[1]))));
+  int lmin = lim[0];
+  for (int rt = 1; rt < RT; ++rt) lmin = min(lmin, lim[rt]);
+  const int minlim = __builtin_amdgcn_readfirstlane((int)(-wave_max(-(float)lmin)));
 
-  float M[2], lrun[2], psum[2];
-  float4v acc[2][8];
+  float M[RT], lrun[RT], psum[RT];
+  float4v acc[RT][8];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     M[rt] = kNegInf; lrun[rt] = 0.f; psum[rt] = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- stage loader: every thread reads 4 dims of K token kt and 4 tokens of V
-  // dim vd (token group vq) of each block ----
+  // ---- stage loader (threads 0..511): a thread reads 4 dims of K token kt and
+  // 4 tokens of V dim vd (token group vq) of each block ----
   const int kt = tid >> 5, kd = (tid & 31) * 4;
   const int vd = tid & (HD - 1), vq = tid >> 7;
   // byte offset of K dims kd..kd+3 of token kt: int8 tiles hold dims 32c + 16h + j
@@ -1412,22 +1420,30 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // hidden gets -inf in the score offset, and the per-token mask runs only when
   // some lane sees part of its four tokens (one block per row at most).
   auto pair_body = [&](int buf, int up, int b0, bool has1, bool plain) {
-    half8 kop[2][4];
     float a[2], vs[2];
+    float4v scv[RT][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const _Float16* kb = &kl[buf][up + j][n * kPfxKPitch + 8 * g];
+      half8 kop[4];
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) kop[j][kc] = *reinterpret_cast<const half8*>(kb + 32 * kc);
+      for (int kc = 0; kc < 4; ++kc) kop[kc] = *reinterpret_cast<const half8*>(kb + 32 * kc);
       a[j] = P.scale_log2 * (I8 ? sl[buf][up + j][0] : 1.f);
       vs[j] = I8 ? sl[buf][up + j][1] : 1.f;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        float4v sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kc], qa[rt][kc], sc, 0, 0, 0);
+        scv[rt][j] = sc;
+      }
     }
-    int vis[2][2];
-    float hide[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    int vis[RT][2];
+    float hide[RT][2] = {};
     bool partial = false;
     if (!plain) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           vis[rt][j] = (j == 0 || has1) ? lim[rt] - (b0 + j) * BS - 4 * g : 0;
@@ -1436,32 +1452,28 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         }
     }
     // scores relative to the running max: y = S a + c - M (log2 units)
-    float y[2][2][4];
+    float y[RT][2][4];
     bool need = false;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
-      const float thr = (M[rt] == kNegInf) ? kNegInf : kRescaleThreshold;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        float4v sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[j][kc], qa[rt][kc], sc, 0, 0, 0);
         const float c = (I8 ? fmaf(-qb[rt], a[j], -Ms) : -Ms) + hide[rt][j];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) y[rt][j][r] = fmaf(sc[r], a[j], c);
+        for (int r = 0; r < 4; ++r) y[rt][j][r] = fmaf(scv[rt][j][r], a[j], c);
       }
     }
     if (__builtin_amdgcn_ballot_w64(partial) != 0) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int r = 0; r < 4; ++r) y[rt][j][r] = (r < vis[rt][j]) ? y[rt][j][r] : kNegInf;
     }
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const float thr = (M[rt] == kNegInf) ? kNegInf : kRescaleThreshold;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -1471,7 +1483,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     // lazy running max of row n (rare after the first blocks)
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
         float m = y[rt][0][0];
 #pragma unroll
@@ -1499,9 +1511,9 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       }
     }
     // p = 2^y in fp16 pairs; l += sum p; p~ = p * v_scale is the A operand
-    half8 pa[2];
+    half8 pa[RT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       uint32_t pw[4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -1526,7 +1538,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     for (int nt = 0; nt < 8; ++nt) {
       const half8 vop = *reinterpret_cast<const half8*>(vb + 16 * nt * kPfxVPitch);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
         acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vop, acc[rt][nt], 0, 0, 0);
     }
   };
@@ -1541,31 +1553,28 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     }
   };
 
-  // ---- pipeline: LDS buffers alternate, raw stages ra / rb two ahead (an
-  // empty chunk, nst = 0 for the whole workgroup, writes empty partials) ----
+  // ---- pipeline: LDS buffers alternate; ra holds the raw bytes of the stage
+  // after the one being computed (an empty chunk, nst = 0 for the whole
+  // workgroup, writes empty partials) ----
   if (nst > 0) {
-    PfxRaw<KV> ra, rb;
-    gload(ra, 0);
-    gload(rb, 1);
-    lwrite(0, ra);
-    gload(ra, 2);
+    PfxRaw<KV> ra;
+    const bool ld = tid < kPfxLoadThreads;
+    if (ld) { gload(ra, 0); lwrite(0, ra); gload(ra, 1); }
     __syncthreads();
     for (int st = 0; st < nst; st += 2) {
       compute(0, st);
-      lwrite(1, rb);       // stage st + 1
-      gload(rb, st + 3);
+      if (ld) { lwrite(1, ra); gload(ra, st + 2); }
       __syncthreads();
       if (st + 1 >= nst) break;
       compute(1, st + 1);
-      lwrite(0, ra);       // stage st + 2
-      gload(ra, st + 4);
+      if (ld) { lwrite(0, ra); gload(ra, st + 3); }
       __syncthreads();
     }
   }
 
   // ---- partials: rows 16 rt + 4g + r, dims 16 nt + n ----
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     float l = lrun[rt], ps = psum[rt];
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
@@ -2288,8 +2297,8 @@ VK_TREE_KV(3, VK_TWO_WAVES)
 
 // Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
 #define VK_TREE_PFX(KV, G, QT)                                                      \
-  extern "C" __global__ void __launch_bounds__(64 * kPfxWaves) VK_TWO_WAVES         \
-      vk_tree_pfx_kv##KV##_g##G##_q##QT(const DecodeParams P) {                     \
+  extern "C" __global__ void __launch_bounds__(64 * kPfxWaves)                      \
+      __attribute__((amdgpu_waves_per_eu(4))) vk_tree_pfx_kv##KV##_g##G##_q##QT(const DecodeParams P) { \
     tree_prefix_mfma<KV, G, QT>(P);                                                 \
   }
 #define VK_TREE_PFX_G(KV, QT) \
