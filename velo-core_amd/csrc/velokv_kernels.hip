@@ -2080,7 +2080,8 @@ __device__ void nixl_copy_kernel(const NixlParams& P) {
 
 // ---- accepted-path commit of a draft tree -----------------------------------
 // grid (sequence, KV head, group of kCommitLayers layers), wave 0 = K, wave 1 =
-// V, lane = dims 2l, 2l+1. The row is validated once; then per layer every moved
+// V, lane = two dims (2l, 2l+1, or for int8 K the pair stored at byte 2l of the
+// token's two 64-byte runs). The row is validated once; then per layer every moved
 // token is read (raw element bytes and its scale, 8 tokens' loads in flight at a
 // time) into LDS before any write, so a write never changes a source still to
 // be read; then the tokens are written in order: rows and per-token scales as
@@ -2097,7 +2098,7 @@ DEV void tree_commit(const CommitParams& P) {
   const int l0 = P.layer0 + (int)blockIdx.z * kCommitLayers;
   const int l1 = min(l0 + kCommitLayers, P.layer0 + P.n_layers);
   const int w = threadIdx.x / WAVE;
-  const bool is_v = w != 0;
+  const bool is_v = __builtin_amdgcn_readfirstlane(w) != 0;  // wave-uniform
   const int lane = lane_id();
   const int ctx = P.context_lens[s];
   const int na = P.n_accept[s];
@@ -2117,7 +2118,11 @@ DEV void tree_commit(const CommitParams& P) {
   const int blk_l = lane < nb ? bt[b_first + lane] : 0;
   if (__builtin_amdgcn_ballot_w64(lane < nb && (blk_l < 0 || blk_l >= P.g.n_blocks)) != 0) return;
   const int Hkv = P.g.n_kv_heads;
-  const int c0 = 2 * lane;
+  // the lane's two dims: 2 lane, 2 lane + 1; for int8 K the two dims whose codes
+  // sit at bytes 1024 (lane / 32) + 64 t + 2 (lane % 32) of the tile (the 16-byte
+  // piece layout), so that a wave reads and writes two contiguous 64-byte runs
+  // per token (every per-dim step below is independent of which dims a lane has)
+  const int c0 = (ESZ == 1 && !is_v) ? 32 * ((lane & 31) >> 3) + 16 * (lane >> 5) + 2 * (lane & 7) : 2 * lane;
   auto blk_of = [&](int pos) -> int64_t { return readlane_i(blk_l, pos / BS - b_first); };
   for (int layer = l0; layer < l1; ++layer) {
     uint8_t* L = P.base + (uint64_t)layer * P.g.layer_stride;
