@@ -1,8 +1,8 @@
-"""The weighted stream-K split (velokv_params.h sk_split / sk_begin /
-sk_worker_of), shared by the decode kernel and its merge, compiled for the host
-with g++ and checked by brute force: contiguous non-empty ranges of at most 255
-blocks, weights honoured, and the merge's block -> worker map the exact inverse
-of the kernel's worker -> range map."""
+"""The stream-K split (velokv_params.h sk_split / sk_begin / sk_worker_of),
+shared by the decode kernel and its merge, compiled for the host with g++ and
+checked by brute force: contiguous non-empty ranges within one block of each
+other, and the merge's block -> worker map the exact inverse of the kernel's
+worker -> range map."""
 import os
 import shutil
 import subprocess

@@ -536,7 +536,6 @@ struct DecodePlan {
   int32_t max_parts;
   bool stream_k;
   int32_t n_workers;
-  int32_t sk_fast, sk_wf, sk_ws;  // weighted stream-K split (velokv_params.h sk_split)
   int32_t wg_waves;  // > 0: workgroup-split kernel with this many waves per (sequence, KV head)
   std::string kernel;
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
@@ -558,12 +557,6 @@ void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args*
               (sched == VK_SCHED_STREAM || (sched == VK_SCHED_AUTO && !uniform));
   *mfma = *stream_k || (fast && (kind == VK_DECODE_MFMA || (kind == VK_DECODE_AUTO && d.kv_type != VK_KV_F16)));
 }
-
-// Stream-K weights at two waves per SIMD: the first-dispatched wave of a SIMD
-// streamed its range in 0.85 of the time the second one took (INT8 decode,
-// uniform and ragged batches, MI355X), so it is given proportionally more blocks.
-constexpr int32_t kSkWeightFast = 117;
-constexpr int32_t kSkWeightSlow = 100;
 
 // Smallest partition (256..4096 tokens) whose units fit in one round of resident
 // waves; longer contexts get 4096-token partitions.
@@ -603,8 +596,6 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   decode_choice(ctx, pool, a, &pl->stream_k, &mfma);
   pl->acc_bytes = pl->ml_bytes = pl->prefix_bytes = 0;
   pl->n_workers = 0;
-  pl->sk_fast = 0;
-  pl->sk_wf = pl->sk_ws = 1;
   pl->wg_waves = 0;
   if (pl->stream_k) {
     pl->kernel = decode_sk_name(d.kv_type, G);
@@ -614,11 +605,6 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     const int64_t nw = std::max<int64_t>(1, std::max(waves, (blocks_max + 255) / 256));
     if (nw > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "grid too large");
     pl->n_workers = (int32_t)nw;
-    // one round of two waves per SIMD: the first half of the grid is the faster half
-    const bool two_per_simd = ctx && ctx->n_cu > 0 && waves == 8LL * ctx->n_cu && nw == waves;
-    pl->sk_fast = two_per_simd ? (int32_t)(nw / 2) : 0;
-    pl->sk_wf = kSkWeightFast;
-    pl->sk_ws = kSkWeightSlow;
     pl->part_tokens = kMaxPartTokens;  // unused by the stream-K kernels
     pl->max_parts = 1;
     const uint64_t prow = (uint64_t)nw * 2 * G;
@@ -723,9 +709,6 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.n_nodes = 1;
   p.n_rgroups = 1;
   p.n_workers = pl.n_workers;
-  p.sk_fast = pl.sk_fast;
-  p.sk_wf = pl.sk_wf;
-  p.sk_ws = pl.sk_ws;
   p.scale_log2 = scale * 1.4426950408889634f;
 
   MergeParams m{};
@@ -741,9 +724,6 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   m.cap_tokens = p.cap_tokens;
   m.sk_prefix = p.sk_prefix;
   m.n_workers = pl.n_workers;
-  m.sk_fast = pl.sk_fast;
-  m.sk_wf = pl.sk_wf;
-  m.sk_ws = pl.sk_ws;
   m.n_kv_heads = d.n_kv_heads;
   m.n_seqs = a->n_seqs;
   const dim3 merge_grid((unsigned)((m.n_rows + 3) / 4));

@@ -1068,7 +1068,7 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
 // ---- stream-K decode -------------------------------------------------------
 // The blocks of all (sequence, KV head) segments in order form one range of
 // W = sum_s Hkv * ceil(ctx_s / 16) blocks; worker w (one wave) takes the w-th
-// range of the (weighted) stream-K split, sk_split in velokv_params.h. A
+// range of the stream-K split (sk_split in velokv_params.h). A
 // segment inside one worker's range is written directly; a split segment leaves
 // one partial per worker: slot 1 for the worker where it starts, slot 0 for the
 // workers that continue it. vk_decode_merge_sk combines them. Worker 0 also
@@ -1118,7 +1118,7 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     if (lane == 0) P.sk_prefix[S] = W;
   }
   if (W == 0) return;
-  const SkSplit sp = sk_split(W, nw, P.sk_fast, P.sk_wf, P.sk_ws);
+  const SkSplit sp = sk_split(W, nw);
   if (w >= sp.nw) return;  // workers past the split have no blocks
   const int64_t b0 = sk_begin(sp, w), b1 = sk_begin(sp, w + 1);
   // the sequence holding block b0 and its first global block
@@ -1681,7 +1681,7 @@ __device__ void decode_merge_sk(const MergeParams& P) {
     return;
   }
   const int64_t W = P.sk_prefix[P.n_seqs];
-  const SkSplit sp = sk_split(W, P.n_workers, P.sk_fast, P.sk_wf, P.sk_ws);
+  const SkSplit sp = sk_split(W, P.n_workers);
   const int64_t S0 = (int64_t)P.sk_prefix[s] + (int64_t)kvh * nb;
   const int w_lo = sk_worker_of(sp, S0);
   const int w_hi = sk_worker_of(sp, S0 + nb - 1);

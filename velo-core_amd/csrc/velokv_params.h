@@ -84,7 +84,6 @@ struct DecodeParams {
   int32_t n_nodes;          // query rows per (sequence, head): 1 for decode
   int32_t n_rgroups;        // row groups per (sequence, KV head) in the grid (tree kernels)
   int32_t n_workers;        // stream-K: workers in the grid
-  int32_t sk_fast, sk_wf, sk_ws;  // stream-K: the first sk_fast workers weigh sk_wf, the rest sk_ws
   int32_t* sk_prefix;       // stream-K: [S + 1] first global block of each sequence, then W
   float scale_log2;         // softmax scale * log2(e)
   // tree verify with a shared prefix: the first prefix_blocks pages of every
@@ -156,51 +155,24 @@ struct MergeParams {
   // stream-K merge (vk_decode_merge_sk): partials indexed by (worker, slot, row of the group)
   const int32_t* sk_prefix;
   int32_t n_workers, n_kv_heads, n_seqs;
-  int32_t sk_fast, sk_wf, sk_ws;
   int32_t prefix_blocks, prefix_chunks;  // tree verify with a shared prefix (DecodeParams)
 };
 
-// Stream-K split of W blocks over nw workers of one wave each. Workgroups are
-// dispatched in id order, so at two waves per SIMD the first half of the grid
-// holds the first-dispatched wave of every SIMD, which streams faster than the
-// second one for the whole launch. The first nf workers therefore weigh wf and
-// the others ws: worker w takes blocks [begin(w), begin(w + 1)) with
-// begin(w) = W cum(w) / cum(nw), cum(w) the weight of workers 0..w-1. The
-// weights apply while every range keeps 2..255 blocks (W >= 4 nw and
-// W max(wf, ws) <= 255 cum(nw)); otherwise the split is even over min(nw, W)
+// Stream-K split of W blocks over nw workers of one wave each: worker w takes
+// blocks [begin(w), begin(w + 1)), begin(w) = w W / nwe over nwe = min(nw, W)
 // workers, so that no range is empty. The attention kernel and the merge
-// derive ranges from the same functions.
+// derive ranges from these functions.
 struct SkSplit {
   int64_t W;
-  int32_t nw, nf, wf, ws;
+  int32_t nw;  // workers with blocks
 };
-VK_HD inline int64_t sk_cum(const SkSplit& s, int32_t w) {
-  const int32_t a = w < s.nf ? w : s.nf;
-  const int32_t b = w > s.nf ? w - s.nf : 0;
-  return (int64_t)s.wf * a + (int64_t)s.ws * b;
-}
-VK_HD inline SkSplit sk_split(int64_t W, int32_t nw, int32_t nf, int32_t wf, int32_t ws) {
-  SkSplit s{W, nw, nf, wf, ws};
-  const bool weighted = nf > 0 && nf < nw && wf > 0 && ws > 0 && W >= 4 * (int64_t)nw;
-  if (weighted && W * (wf > ws ? wf : ws) <= 255 * sk_cum(s, nw)) return s;
-  s.nw = (int32_t)(W < nw ? W : nw);
-  s.nf = 0;
-  s.wf = s.ws = 1;
-  return s;
-}
+VK_HD inline SkSplit sk_split(int64_t W, int32_t nw) { return SkSplit{W, (int32_t)(W < nw ? W : nw)}; }
 // First block of worker w (w <= nw; requires W > 0).
-VK_HD inline int64_t sk_begin(const SkSplit& s, int32_t w) { return s.W * sk_cum(s, w) / sk_cum(s, s.nw); }
+VK_HD inline int64_t sk_begin(const SkSplit& s, int32_t w) { return (int64_t)w * s.W / s.nw; }
 // The worker whose range holds block x (0 <= x < W): the largest w with
-// begin(w) <= x, estimated from the running weight at x and then settled.
+// begin(w) <= x, i.e. ceil((x + 1) nw / W) - 1.
 VK_HD inline int32_t sk_worker_of(const SkSplit& s, int64_t x) {
-  const int64_t c = x * sk_cum(s, s.nw) / s.W;
-  const int64_t cf = (int64_t)s.wf * s.nf;
-  int64_t w = c < cf ? c / s.wf : s.nf + (c - cf) / s.ws;
-  if (w > s.nw - 1) w = s.nw - 1;
-  if (w < 0) w = 0;
-  while (w + 1 < s.nw && sk_begin(s, (int32_t)w + 1) <= x) ++w;
-  while (w > 0 && sk_begin(s, (int32_t)w) > x) --w;
-  return (int32_t)w;
+  return (int32_t)(((x + 1) * s.nw + s.W - 1) / s.W) - 1;
 }
 
 struct FillParams {
