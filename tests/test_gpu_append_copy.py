@@ -118,6 +118,42 @@ def test_append_blk_runs_with_padding_windows(ctx, gap):
     assert_layer_equal(pool, 0, ref)
 
 
+@pytest.mark.parametrize("kv", KV_ALL)
+def test_append_large_call_windows(ctx, kv):
+    """A call of ~9000 tokens over 8 KV heads, so that each workgroup covers a
+    window of several tokens (36 here): runs of every length that start and end
+    anywhere relative to the windows, sprinkled padding slots, and an existing
+    partial block that a run continues (its stored scale applies)."""
+    print(f"append large call kv={kv}", flush=True)
+    rng = synth.rng(808)
+    lens = rng.integers(1, 200, 80)
+    case = make_case(kv, [int(L) + 16 for L in lens], n_kv_heads=8, n_heads=32, seed=808, outlier_scale=8.0)
+    bt = case.block_tables
+    # first call: a few tokens per sequence (partial blocks); second call: the rest
+    first = np.minimum(lens, rng.integers(0, 9, len(lens)))
+    ref = O.Layer(case.n_blocks, 8, BS, HD, kv)
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, 8, HD, kv)
+    for part in (0, 1):
+        sl, kk, vv = [], [], []
+        for s_, L in enumerate(lens):
+            lo, hi = (0, int(first[s_])) if part == 0 else (int(first[s_]), int(L))
+            if hi <= lo:
+                continue
+            pos = np.arange(lo, hi)
+            sl.append(synth.slots_for_positions(bt, pos, BS, np.full(len(pos), s_)))
+            kk.append(case.k[s_][lo:hi])
+            vv.append(case.v[s_][lo:hi])
+        sl, kk, vv = np.concatenate(sl), np.concatenate(kk), np.concatenate(vv)
+        if part == 1:  # padding slots at random places (tokens of one block stay adjacent in the call)
+            pad = rng.random(len(sl)) < 0.05
+            sl = sl.copy()
+            sl[pad] = -1
+        O.append(ref, kk, vv, sl)
+        ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
+        ctx.sync()
+    assert_layer_equal(pool, 0, ref)
+
+
 def test_append_skips_negative_slots_and_layers_are_separate(ctx):
     print("append negative slots / layers", flush=True)
     case = make_case(O.I8_BLK, [20], seed=105)

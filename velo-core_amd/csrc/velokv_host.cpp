@@ -425,6 +425,16 @@ extern "C" int vk_slot_mapping(vk_ctx* ctx, vk_pool* pool, const int32_t* block_
   return launch(ctx, "vk_slot_mapping", dim3((n_tok + 255) / 256), dim3(256), p, stream);
 }
 
+namespace {
+// Tokens per append workgroup: enough workgroups to spread the runs over the GPU
+// (about 2048 per call), at most 64 (one slot load per lane); a workgroup per
+// token for small calls.
+int append_tok_per_wg(int32_t n_tok, int32_t n_kv_heads) {
+  const int64_t t = ((int64_t)n_tok * n_kv_heads + 2047) / 2048;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(64, t));
+}
+}  // namespace
+
 extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* k, const void* v, int32_t in_dtype,
                          const int64_t* slot_mapping, int32_t n_tok, void* stream) {
   int rc = check_pool(ctx, pool);
@@ -443,9 +453,11 @@ extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* 
   p.v = v;
   p.slot_mapping = slot_mapping;
   p.n_tok = n_tok;
+  p.tok_per_wg = append_tok_per_wg(n_tok, pool->desc.n_kv_heads);
   const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
   if ((rc = set_device(ctx))) return rc;
-  return launch(ctx, name.c_str(), dim3((unsigned)n_tok, (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
+  return launch(ctx, name.c_str(), dim3((unsigned)((n_tok + p.tok_per_wg - 1) / p.tok_per_wg),
+                                        (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
 }
 
 extern "C" int vk_rope_table(float* out, int32_t n_pos, int32_t head_dim, float freq_base) {
@@ -496,9 +508,11 @@ extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q
   p.q = q;
   p.q_dtype = q_dtype;
   const unsigned rows = (unsigned)pool->desc.n_kv_heads + (q ? (unsigned)((n_heads + 1) / 2) : 0u);
+  p.tok_per_wg = append_tok_per_wg(n_tok, (int32_t)rows);
   const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
   if ((rc = set_device(ctx))) return rc;
-  return launch(ctx, name.c_str(), dim3((unsigned)n_tok, rows), dim3(128), p, stream);
+  return launch(ctx, name.c_str(), dim3((unsigned)((n_tok + p.tok_per_wg - 1) / p.tok_per_wg), rows), dim3(128), p,
+                stream);
 }
 
 namespace {

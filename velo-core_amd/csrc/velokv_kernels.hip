@@ -1804,29 +1804,35 @@ DEV void blk_put(int (&cd)[BS][2], int o, float& s_old, uint16_t& s_bits, float 
 }
 
 // VK_KV_I8_BLK: per-(block, head) fp16 scale, round-half-even codes clamped to +-127.
-// A run = consecutive tokens of the call that fall in one block; the run's first
-// token does the work for all of them, in order, keeping the block's codes in
-// registers:
+// A run = consecutive tokens of the call that fall in one block (padding slots
+// in between skipped); the wave that holds the run's first token does the work
+// for all of them, in order, keeping the block's codes in registers:
 //   s_old = (offset == 0) ? 0 : stored scale
 //   s_new = max(s_old, fp16(amax / 127))
 //   if s_new > s_old: c' = clamp(rne((c * s_old) / s_new)) for tokens before offset
 //   c = s_new > 0 ? clamp(rne(x / s_new)) : 0
-template <bool IS_V>
-DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales) {
+// Slots are read 64 tokens at a time (lane j: token base + j) and runs are found
+// with ballots; the K/V rows of up to 16 members are loaded together before the
+// rule runs over them.
+
+// Block of the nearest non-padding token before token n of the call, or -1.
+DEV int prev_block(const AppendParams& P, int n) {
   const int lane = lane_id();
-  const int n = blockIdx.x, h = blockIdx.y;
-  const int64_t slot = token_slot(P, n);
-  if (slot < 0) return;
-  const int bs = BS;
-  const int64_t b = slot / bs;
-  // Not the first token of its run when the previous non-padding token of the
-  // call is in the same block (padding slots are negative).
-  for (int m = n - 1; m >= 0; --m) {
-    const int64_t prev = token_slot(P, m);
-    if (prev < 0) continue;
-    if (prev / bs == b) return;
-    break;
+  for (int top = n - 1; top >= 0; top -= WAVE) {
+    const int m = top - lane;
+    const int64_t ps = m >= 0 ? token_slot(P, m) : -1;
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(ps >= 0);
+    if (mask != 0) return readlane_i((int)(ps / BS), __builtin_ctzll(mask));
   }
+  return -1;
+}
+
+// The run that starts at token n (slot `slot`), for KV head h.
+template <bool IS_V>
+DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales, int n, int64_t slot,
+                        int h) {
+  const int lane = lane_id();
+  const int64_t b = slot / BS;
   if (b >= P.g.n_blocks) return;
   const int Hkv = P.g.n_kv_heads;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
@@ -1839,23 +1845,54 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
     cd[u][0] = (int8_t)tile[tile_elem<IS_V>(u, d0, 1)];
     cd[u][1] = (int8_t)tile[tile_elem<IS_V>(u, d0 + 1, 1)];
   }
-  int o = (int)(slot % bs);
-  float s_old = (o == 0) ? 0.f : h2f(*sp);
-  uint16_t s_bits = (o == 0) ? (uint16_t)0 : *sp;
+  const uint16_t stored = *sp;
+  float s_old = 0.f;
+  uint16_t s_bits = 0;
   int hi_written = -1;
-  for (int m = n; m < P.n_tok;) {
-    float x0, x1;
-    load_kv(P, src, IS_V, m, h, x0, x1);
-    blk_put(cd, o, s_old, s_bits, x0, x1);
-    hi_written = max(hi_written, o);
-    // next token of the run (padding slots in between are skipped)
-    ++m;
-    while (m < P.n_tok && token_slot(P, m) < 0) ++m;
-    if (m >= P.n_tok) break;
-    const int64_t ns = token_slot(P, m);
-    if (ns / bs != b) break;
-    o = (int)(ns % bs);
-    if (o == 0) { s_old = 0.f; s_bits = 0; }
+  bool first = true;
+  for (int base = n; base < P.n_tok; base += WAVE) {
+    const int m = base + lane;
+    const int64_t ms = m < P.n_tok ? token_slot(P, m) : -1;
+    // the run ends at the first non-padding token of another block
+    const uint64_t other = __builtin_amdgcn_ballot_w64(ms >= 0 && ms / BS != b);
+    const int stop = other ? __builtin_ctzll(other) : WAVE;
+    uint64_t mem = __builtin_amdgcn_ballot_w64(ms >= 0 && lane < stop);
+    const int moff = (int)(ms >= 0 ? ms % BS : 0);
+    while (mem != 0) {
+      // up to 16 members: their rows loaded together, then the rule in order
+      constexpr int kBatch = 16;
+      int idx[kBatch];
+      float xs[kBatch][2];
+      int cnt = 0;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        idx[k] = mem != 0 ? __builtin_ctzll(mem) : 0;
+        if (mem != 0) {
+          mem &= mem - 1;
+          cnt = k + 1;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (k < cnt) load_kv(P, src, IS_V, base + idx[k], h, xs[k][0], xs[k][1]);
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        if (k < cnt) {
+          const int o = readlane_i(moff, idx[k]);
+          if (first) {
+            s_old = (o == 0) ? 0.f : h2f(stored);
+            s_bits = (o == 0) ? (uint16_t)0 : stored;
+            first = false;
+          } else if (o == 0) {
+            s_old = 0.f;
+            s_bits = 0;
+          }
+          blk_put(cd, o, s_old, s_bits, xs[k][0], xs[k][1]);
+          hi_written = max(hi_written, o);
+        }
+      }
+    }
+    if (other != 0) break;
   }
 #pragma unroll
   for (int u = 0; u < BS; ++u) {
@@ -1867,12 +1904,38 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
   if (lane == 0) *sp = s_bits;
 }
 
+// The runs that start inside tokens [w0, w0 + T) of the call, in order. A token
+// starts a run when it is not padding and the nearest non-padding token before
+// it is in another block (or there is none).
+template <bool IS_V>
+DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales, int w0, int T) {
+  const int lane = lane_id();
+  const int h = blockIdx.y;
+  const int m = w0 + lane;
+  const int64_t ms = (lane < T && m < P.n_tok) ? token_slot(P, m) : -1;
+  const int mb = ms >= 0 ? (int)(ms / BS) : -1;
+  const uint64_t valid = __builtin_amdgcn_ballot_w64(ms >= 0);
+  if (valid == 0) return;
+  const int before = prev_block(P, w0);
+  const uint64_t low = valid & ((1ull << lane) - 1ull);
+  const int pl = low ? 63 - __builtin_clzll(low) : 0;
+  const int pb = __shfl(mb, pl, WAVE);
+  const int prevb = low ? pb : before;
+  uint64_t starts = __builtin_amdgcn_ballot_w64(ms >= 0 && prevb != mb);
+  while (starts != 0) {
+    const int j = __builtin_ctzll(starts);
+    starts &= starts - 1;
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ms, j);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)ms >> 32), j);
+    append_blk_run<IS_V>(P, src, codes, scales, w0 + j, (int64_t)(((uint64_t)hi << 32) | lo), h);
+  }
+}
+
 // VK_KV_I8_REF: per-(token, head) fp32 scale = amax/127, codes = trunc(x * (127/amax)).
 template <bool IS_V>
-DEV void append_ref(const AppendParams& P, const void* src, uint8_t* codes, float* scales) {
+DEV void append_ref(const AppendParams& P, const void* src, uint8_t* codes, float* scales, int n, int64_t slot) {
   const int lane = lane_id();
-  const int n = blockIdx.x, h = blockIdx.y;
-  const int64_t slot = token_slot(P, n);
+  const int h = blockIdx.y;
   if (slot < 0) return;
   const int64_t b = slot / BS;
   const int o = (int)(slot % BS);
@@ -1892,10 +1955,9 @@ DEV void append_ref(const AppendParams& P, const void* src, uint8_t* codes, floa
 
 // VK_KV_F16 / VK_KV_F32: plain copy (with RNE conversion to fp16 when needed).
 template <bool IS_V, int ESZ>
-DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes) {
+DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes, int n, int64_t slot) {
   const int lane = lane_id();
-  const int n = blockIdx.x, h = blockIdx.y;
-  const int64_t slot = token_slot(P, n);
+  const int h = blockIdx.y;
   if (slot < 0) return;
   const int64_t b = slot / BS;
   const int o = (int)(slot % BS);
@@ -1922,20 +1984,25 @@ DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes) {
 
 template <int KV>
 DEV void append_kernel(const AppendParams& P) {
-  if ((int)blockIdx.y >= P.g.n_kv_heads) {  // RoPE of two query heads of token blockIdx.x
-    const int n = blockIdx.x;
+  const int T = P.tok_per_wg;
+  const int w0 = (int)blockIdx.x * T;
+  const int w1 = min(w0 + T, P.n_tok);
+  if ((int)blockIdx.y >= P.g.n_kv_heads) {  // RoPE of two query heads of the window's tokens
     const int head = 2 * ((int)blockIdx.y - P.g.n_kv_heads) + (int)(threadIdx.x / WAVE);
-    const int pos = P.positions[n];
-    if (head >= P.n_heads || pos < 0 || pos >= P.n_pos) return;
-    const int64_t off = ((int64_t)n * P.n_heads + head) * HD + 2 * lane_id();
-    float x0, x1;
-    load_x2(P.q, P.q_dtype, off, x0, x1);
-    rope_rotate(P.rope, P.cos_sin, pos, x0, x1);
-    if (P.q_dtype == DT_F16) {
-      reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(P.q) + off)[0] =
-          (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
-    } else {
-      reinterpret_cast<float2*>(reinterpret_cast<float*>(P.q) + off)[0] = make_float2(x0, x1);
+    if (head >= P.n_heads) return;
+    for (int n = w0; n < w1; ++n) {
+      const int pos = P.positions[n];
+      if (pos < 0 || pos >= P.n_pos) continue;
+      const int64_t off = ((int64_t)n * P.n_heads + head) * HD + 2 * lane_id();
+      float x0, x1;
+      load_x2(P.q, P.q_dtype, off, x0, x1);
+      rope_rotate(P.rope, P.cos_sin, pos, x0, x1);
+      if (P.q_dtype == DT_F16) {
+        reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(P.q) + off)[0] =
+            (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+      } else {
+        reinterpret_cast<float2*>(reinterpret_cast<float*>(P.q) + off)[0] = make_float2(x0, x1);
+      }
     }
     return;
   }
@@ -1945,14 +2012,23 @@ DEV void append_kernel(const AppendParams& P) {
   uint8_t* codes = L + (is_v ? P.g.v_off : P.g.k_off);
   if constexpr (KV == KV_I8_BLK) {
     uint16_t* sc = reinterpret_cast<uint16_t*>(L + (is_v ? P.g.vs_off : P.g.ks_off));
-    if (is_v) append_blk<true>(P, src, codes, sc); else append_blk<false>(P, src, codes, sc);
-  } else if constexpr (KV == KV_I8_REF) {
-    float* sc = reinterpret_cast<float*>(L + (is_v ? P.g.vs_off : P.g.ks_off));
-    if (is_v) append_ref<true>(P, src, codes, sc); else append_ref<false>(P, src, codes, sc);
-  } else if constexpr (KV == KV_F16) {
-    if (is_v) append_plain<true, 2>(P, src, codes); else append_plain<false, 2>(P, src, codes);
-  } else {
-    if (is_v) append_plain<true, 4>(P, src, codes); else append_plain<false, 4>(P, src, codes);
+    if (is_v) append_blk<true>(P, src, codes, sc, w0, T); else append_blk<false>(P, src, codes, sc, w0, T);
+    return;
+  }
+  // one token at a time; the window's slots are read at once (lane j: token w0 + j)
+  const int64_t ms = w0 + lane_id() < w1 ? token_slot(P, w0 + lane_id()) : -1;
+  for (int n = w0; n < w1; ++n) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ms, n - w0);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)ms >> 32), n - w0);
+    const int64_t slot = (int64_t)(((uint64_t)hi << 32) | lo);
+    if constexpr (KV == KV_I8_REF) {
+      float* sc = reinterpret_cast<float*>(L + (is_v ? P.g.vs_off : P.g.ks_off));
+      if (is_v) append_ref<true>(P, src, codes, sc, n, slot); else append_ref<false>(P, src, codes, sc, n, slot);
+    } else if constexpr (KV == KV_F16) {
+      if (is_v) append_plain<true, 2>(P, src, codes, n, slot); else append_plain<false, 2>(P, src, codes, n, slot);
+    } else {
+      if (is_v) append_plain<true, 4>(P, src, codes, n, slot); else append_plain<false, 4>(P, src, codes, n, slot);
+    }
   }
 }
 

@@ -27,9 +27,10 @@ struct PoolGeom {
 
 enum RopeStyle : int32_t { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
 
-// Append of n_tok tokens; grid (n_tok, Hkv + ceil(n_heads / 2)): rows y < Hkv
-// write K (wave 0) and V (wave 1) of KV head y; with RoPE, rows y >= Hkv rotate
-// query heads 2(y - Hkv) and 2(y - Hkv) + 1 in place.
+// Append of n_tok tokens; grid (ceil(n_tok / tok_per_wg), Hkv + ceil(n_heads / 2)):
+// workgroup x covers tokens [x T, x T + T) of the call, T = tok_per_wg; rows
+// y < Hkv write K (wave 0) and V (wave 1) of KV head y; with RoPE, rows y >= Hkv
+// rotate query heads 2(y - Hkv) and 2(y - Hkv) + 1 in place.
 struct AppendParams {
   uint8_t* base;            // pool base (all layers)
   PoolGeom g;
@@ -46,6 +47,7 @@ struct AppendParams {
   int32_t n_heads;          // query heads rotated in place (0 = none)
   void* q;                  // [n_tok][n_heads][D] of q_dtype
   int32_t q_dtype;
+  int32_t tok_per_wg;       // tokens per workgroup (1..64)
 };
 
 struct SlotMapParams {
