@@ -1838,12 +1838,16 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
   uint16_t* sp = scales + (uint64_t)b * Hkv + h;
   const int d0 = 2 * lane;
+  // element (u, d) sits at tile_elem(u, 0) + tile_elem(0, d) in both layouts:
+  // two lane pointers and constant offsets per token
+  uint8_t* const lp0 = tile + tile_elem<IS_V>(0, d0, 1);
+  uint8_t* const lp1 = tile + tile_elem<IS_V>(0, d0 + 1, 1);
 
   int cd[BS][2];
 #pragma unroll
   for (int u = 0; u < BS; ++u) {
-    cd[u][0] = (int8_t)tile[tile_elem<IS_V>(u, d0, 1)];
-    cd[u][1] = (int8_t)tile[tile_elem<IS_V>(u, d0 + 1, 1)];
+    cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1)];
+    cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1)];
   }
   const uint16_t stored = *sp;
   float s_old = 0.f;
@@ -1860,35 +1864,44 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
     const int moff = (int)(ms >= 0 ? ms % BS : 0);
     while (mem != 0) {
       // up to 16 members: their rows loaded together, then the rule in order
+      // (a rolled loop over xs[0], the rows shifted down one per member, so
+      // that the rule is instantiated once and the kernel stays near 128
+      // registers: four waves per SIMD)
       constexpr int kBatch = 16;
-      int idx[kBatch];
       float xs[kBatch][2];
-      int cnt = 0;
+      uint64_t batch = 0;
+      {
+        uint64_t rest = mem;
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        idx[k] = mem != 0 ? __builtin_ctzll(mem) : 0;
-        if (mem != 0) {
-          mem &= mem - 1;
-          cnt = k + 1;
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kBatch; ++k)
-        if (k < cnt) load_kv(P, src, IS_V, base + idx[k], h, xs[k][0], xs[k][1]);
-#pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        if (k < cnt) {
-          const int o = readlane_i(moff, idx[k]);
-          if (first) {
-            s_old = (o == 0) ? 0.f : h2f(stored);
-            s_bits = (o == 0) ? (uint16_t)0 : stored;
-            first = false;
-          } else if (o == 0) {
-            s_old = 0.f;
-            s_bits = 0;
+        for (int k = 0; k < kBatch; ++k) {
+          if (rest != 0) {
+            const int j = __builtin_ctzll(rest);
+            rest &= rest - 1;
+            batch |= 1ull << j;
+            load_kv(P, src, IS_V, base + j, h, xs[k][0], xs[k][1]);
           }
-          blk_put(cd, o, s_old, s_bits, xs[k][0], xs[k][1]);
-          hi_written = max(hi_written, o);
+        }
+        mem = rest;
+      }
+#pragma unroll 1
+      while (batch != 0) {
+        const int j = __builtin_ctzll(batch);
+        batch &= batch - 1;
+        const int o = readlane_i(moff, j);
+        if (first) {
+          s_old = (o == 0) ? 0.f : h2f(stored);
+          s_bits = (o == 0) ? (uint16_t)0 : stored;
+          first = false;
+        } else if (o == 0) {
+          s_old = 0.f;
+          s_bits = 0;
+        }
+        blk_put(cd, o, s_old, s_bits, xs[0][0], xs[0][1]);
+        hi_written = max(hi_written, o);
+#pragma unroll
+        for (int k = 0; k + 1 < kBatch; ++k) {
+          xs[k][0] = xs[k + 1][0];
+          xs[k][1] = xs[k + 1][1];
         }
       }
     }
@@ -1897,8 +1910,8 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
 #pragma unroll
   for (int u = 0; u < BS; ++u) {
     if (u <= hi_written) {
-      tile[tile_elem<IS_V>(u, d0, 1)] = (uint8_t)(int8_t)cd[u][0];
-      tile[tile_elem<IS_V>(u, d0 + 1, 1)] = (uint8_t)(int8_t)cd[u][1];
+      lp0[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][0];
+      lp1[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][1];
     }
   }
   if (lane == 0) *sp = s_bits;
@@ -1913,10 +1926,10 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
   const int h = blockIdx.y;
   const int m = w0 + lane;
   const int64_t ms = (lane < T && m < P.n_tok) ? token_slot(P, m) : -1;
+  const int before = prev_block(P, w0);  // loads issued beside the window's
   const int mb = ms >= 0 ? (int)(ms / BS) : -1;
   const uint64_t valid = __builtin_amdgcn_ballot_w64(ms >= 0);
   if (valid == 0) return;
-  const int before = prev_block(P, w0);
   const uint64_t low = valid & ((1ull << lane) - 1ull);
   const int pl = low ? 63 - __builtin_clzll(low) : 0;
   const int pb = __shfl(mb, pl, WAVE);
@@ -2388,7 +2401,8 @@ VK_TREE_PFX_G(1, 0) VK_TREE_PFX_G(1, 1) VK_TREE_PFX_G(3, 0) VK_TREE_PFX_G(3, 1)
 
 
 #define VK_APPEND(KV) \
-  extern "C" __global__ void __launch_bounds__(128) vk_append_kv##KV(const AppendParams P) { append_kernel<KV>(P); }
+  extern "C" __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(4)))                         \
+      vk_append_kv##KV(const AppendParams P) { append_kernel<KV>(P); }
 VK_APPEND(0) VK_APPEND(1) VK_APPEND(2) VK_APPEND(3)
 
 extern "C" __global__ void __launch_bounds__(256) vk_slot_mapping(const SlotMapParams P) { slot_mapping_kernel(P); }
