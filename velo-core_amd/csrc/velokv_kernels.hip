@@ -2178,6 +2178,129 @@ __device__ void nixl_copy_kernel(const NixlParams& P) {
 // put through the append rule (blk_put), one destination block at a time.
 constexpr int kMaxCommit = 32;
 constexpr int kCommitLayers = 8;
+
+// One wave's share of a commit (K when IS_V is false, V when true): layers
+// [l0, l1) of KV head h of sequence s, accepted tokens a (lane i: node of the
+// i-th accepted token), d0 the first moved one, blocks blk_l (lane i: the i-th
+// destination block from b_first).
+template <int KV, bool IS_V>
+DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE * Esz<KV>::v], float (&xsc)[kMaxCommit],
+                     int h, int l0, int l1, int ctx, int na, int a, int d0, int blk_l, int b_first) {
+  constexpr int ESZ = Esz<KV>::v;
+  const int lane = lane_id();
+  const int Hkv = P.g.n_kv_heads;
+  // the lane's two dims: 2 lane, 2 lane + 1; for int8 K the two dims whose codes
+  // sit at bytes 1024 (lane / 32) + 64 t + 2 (lane % 32) of the tile (the 16-byte
+  // piece layout), so that a wave reads and writes two contiguous 64-byte runs
+  // per token (every per-dim step below is independent of which dims a lane has)
+  const int c0 = (ESZ == 1 && !IS_V) ? 32 * ((lane & 31) >> 3) + 16 * (lane >> 5) + 2 * (lane & 7) : 2 * lane;
+  // element (u, d) of a tile sits at tile_elem(u, 0) + tile_elem(0, d)
+  const uint32_t off0 = tile_elem<IS_V>(0, c0, ESZ), off1 = tile_elem<IS_V>(0, c0 + 1, ESZ);
+  auto blk_of = [&](int pos) -> int64_t { return readlane_i(blk_l, pos / BS - b_first); };
+  for (int layer = l0; layer < l1; ++layer) {
+    uint8_t* L = P.base + (uint64_t)layer * P.g.layer_stride;
+    uint8_t* codes = L + (IS_V ? P.g.v_off : P.g.k_off);
+    uint8_t* scales = L + (IS_V ? P.g.vs_off : P.g.ks_off);
+    // ---- read every moved token ----
+    constexpr int RC = 8;
+    for (int d = d0; d < na; d += RC) {
+      uint32_t e[RC][2];
+      float sv[RC];
+#pragma unroll
+      for (int k = 0; k < RC; ++k) {
+        const int q = ctx + readlane_i(a, min(d + k, na - 1));  // past na: a valid token, result dropped
+        const int64_t blk = blk_of(q);
+        const uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes + tile_elem<IS_V>(q % BS, 0, ESZ);
+        if constexpr (ESZ == 4) {
+          e[k][0] = *reinterpret_cast<const uint32_t*>(t + off0);
+          e[k][1] = *reinterpret_cast<const uint32_t*>(t + off1);
+        } else if constexpr (ESZ == 2) {
+          e[k][0] = *reinterpret_cast<const uint16_t*>(t + off0);
+          e[k][1] = *reinterpret_cast<const uint16_t*>(t + off1);
+        } else {
+          e[k][0] = t[off0];
+          e[k][1] = t[off1];
+        }
+        sv[k] = 0.f;
+        if constexpr (KV == KV_I8_BLK) sv[k] = h2f(reinterpret_cast<const uint16_t*>(scales)[(uint64_t)blk * Hkv + h]);
+        if constexpr (KV == KV_I8_REF) sv[k] = reinterpret_cast<const float*>(scales)[((uint64_t)blk * Hkv + h) * BS + q % BS];
+      }
+#pragma unroll
+      for (int k = 0; k < RC; ++k) {
+        if (d + k < na) {
+          uint8_t* r = &raw[d + k][2 * lane * ESZ];
+          if constexpr (ESZ == 4) *reinterpret_cast<uint2*>(r) = make_uint2(e[k][0], e[k][1]);
+          else if constexpr (ESZ == 2) *reinterpret_cast<uint32_t*>(r) = e[k][0] | (e[k][1] << 16);
+          else *reinterpret_cast<uint16_t*>(r) = (uint16_t)(e[k][0] | (e[k][1] << 8));
+          if (ESZ == 1 && lane == 0) xsc[d + k] = sv[k];
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // ---- write them at context_len + d ----
+    if constexpr (KV != KV_I8_BLK) {
+      for (int d = d0; d < na; ++d) {
+        const int p = ctx + d;
+        const int64_t blk = blk_of(p);
+        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes + tile_elem<IS_V>(p % BS, 0, ESZ);
+        const uint8_t* r = &raw[d][2 * lane * ESZ];
+        if constexpr (ESZ == 4) {
+          *reinterpret_cast<uint32_t*>(t + off0) = reinterpret_cast<const uint32_t*>(r)[0];
+          *reinterpret_cast<uint32_t*>(t + off1) = reinterpret_cast<const uint32_t*>(r)[1];
+        } else if constexpr (ESZ == 2) {
+          *reinterpret_cast<uint16_t*>(t + off0) = reinterpret_cast<const uint16_t*>(r)[0];
+          *reinterpret_cast<uint16_t*>(t + off1) = reinterpret_cast<const uint16_t*>(r)[1];
+        } else {
+          t[off0] = r[0];
+          t[off1] = r[1];
+        }
+        if constexpr (KV == KV_I8_REF) {
+          if (lane == 0) reinterpret_cast<float*>(scales)[((uint64_t)blk * Hkv + h) * BS + p % BS] = xsc[d];
+        }
+      }
+    } else {
+      // one run per destination block: [ctx + d, ctx + dend)
+      int d = d0;
+      while (d < na) {
+        const int p = ctx + d;
+        const int dend = min(na, (p / BS + 1) * BS - ctx);
+        const int64_t blk = blk_of(p);
+        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
+        uint8_t* const lp0 = t + off0;
+        uint8_t* const lp1 = t + off1;
+        uint16_t* sp = reinterpret_cast<uint16_t*>(scales) + (uint64_t)blk * Hkv + h;
+        int cd[BS][2];
+#pragma unroll
+        for (int u = 0; u < BS; ++u) {
+          cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1)];
+          cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1)];
+        }
+        const int o0 = p % BS;
+        const uint16_t stored = *sp;
+        float s_old = (o0 == 0) ? 0.f : h2f(stored);
+        uint16_t s_bits = (o0 == 0) ? (uint16_t)0 : stored;
+#pragma unroll 1
+        for (int e = d; e < dend; ++e) {
+          const uint8_t* r = &raw[e][2 * lane];
+          const float sc = xsc[e];
+          blk_put(cd, (ctx + e) % BS, s_old, s_bits, (float)(int8_t)r[0] * sc, (float)(int8_t)r[1] * sc);
+        }
+        const int hi_written = (ctx + dend - 1) % BS;
+#pragma unroll
+        for (int u = 0; u < BS; ++u) {
+          if (u <= hi_written) {
+            lp0[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][0];
+            lp1[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][1];
+          }
+        }
+        if (lane == 0) *sp = s_bits;
+        d = dend;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  }
+}
+
 template <int KV>
 DEV void tree_commit(const CommitParams& P) {
   constexpr int ESZ = Esz<KV>::v;
@@ -2186,8 +2309,7 @@ DEV void tree_commit(const CommitParams& P) {
   const int s = blockIdx.x, h = blockIdx.y;
   const int l0 = P.layer0 + (int)blockIdx.z * kCommitLayers;
   const int l1 = min(l0 + kCommitLayers, P.layer0 + P.n_layers);
-  const int w = threadIdx.x / WAVE;
-  const bool is_v = __builtin_amdgcn_readfirstlane(w) != 0;  // wave-uniform
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x / WAVE);  // 0: K, 1: V (wave-uniform)
   const int lane = lane_id();
   const int ctx = P.context_lens[s];
   const int na = P.n_accept[s];
@@ -2206,107 +2328,8 @@ DEV void tree_commit(const CommitParams& P) {
   const int b_first = (ctx + d0) / BS, nb = last / BS - b_first + 1;  // at most 3 blocks
   const int blk_l = lane < nb ? bt[b_first + lane] : 0;
   if (__builtin_amdgcn_ballot_w64(lane < nb && (blk_l < 0 || blk_l >= P.g.n_blocks)) != 0) return;
-  const int Hkv = P.g.n_kv_heads;
-  // the lane's two dims: 2 lane, 2 lane + 1; for int8 K the two dims whose codes
-  // sit at bytes 1024 (lane / 32) + 64 t + 2 (lane % 32) of the tile (the 16-byte
-  // piece layout), so that a wave reads and writes two contiguous 64-byte runs
-  // per token (every per-dim step below is independent of which dims a lane has)
-  const int c0 = (ESZ == 1 && !is_v) ? 32 * ((lane & 31) >> 3) + 16 * (lane >> 5) + 2 * (lane & 7) : 2 * lane;
-  auto blk_of = [&](int pos) -> int64_t { return readlane_i(blk_l, pos / BS - b_first); };
-  for (int layer = l0; layer < l1; ++layer) {
-    uint8_t* L = P.base + (uint64_t)layer * P.g.layer_stride;
-    uint8_t* codes = L + (is_v ? P.g.v_off : P.g.k_off);
-    uint8_t* scales = L + (is_v ? P.g.vs_off : P.g.ks_off);
-    // ---- read every moved token ----
-    constexpr int RC = 8;
-    for (int d = d0; d < na; d += RC) {
-      uint32_t e[RC][2];
-      float sv[RC];
-#pragma unroll
-      for (int k = 0; k < RC; ++k) {
-        const int q = ctx + readlane_i(a, min(d + k, na - 1));  // past na: a valid token, result dropped
-        const int64_t blk = blk_of(q);
-        const uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
-        const int o = q % BS;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint32_t off = is_v ? tile_elem<true>(o, c0 + c, ESZ) : tile_elem<false>(o, c0 + c, ESZ);
-          if constexpr (ESZ == 4) e[k][c] = *reinterpret_cast<const uint32_t*>(t + off);
-          else if constexpr (ESZ == 2) e[k][c] = *reinterpret_cast<const uint16_t*>(t + off);
-          else e[k][c] = t[off];
-        }
-        sv[k] = 0.f;
-        if constexpr (KV == KV_I8_BLK) sv[k] = h2f(reinterpret_cast<const uint16_t*>(scales)[(uint64_t)blk * Hkv + h]);
-        if constexpr (KV == KV_I8_REF) sv[k] = reinterpret_cast<const float*>(scales)[((uint64_t)blk * Hkv + h) * BS + o];
-      }
-#pragma unroll
-      for (int k = 0; k < RC; ++k) {
-        if (d + k < na) {
-          uint8_t* r = &raw[w][d + k][2 * lane * ESZ];
-          if constexpr (ESZ == 4) *reinterpret_cast<uint2*>(r) = make_uint2(e[k][0], e[k][1]);
-          else if constexpr (ESZ == 2) *reinterpret_cast<uint32_t*>(r) = e[k][0] | (e[k][1] << 16);
-          else *reinterpret_cast<uint16_t*>(r) = (uint16_t)(e[k][0] | (e[k][1] << 8));
-          if (ESZ == 1 && lane == 0) xsc[w][d + k] = sv[k];
-        }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    // ---- write them at context_len + d ----
-    if constexpr (KV != KV_I8_BLK) {
-      for (int d = d0; d < na; ++d) {
-        const int p = ctx + d;
-        const int64_t blk = blk_of(p);
-        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
-        const int o = p % BS;
-        const uint8_t* r = &raw[w][d][2 * lane * ESZ];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint32_t off = is_v ? tile_elem<true>(o, c0 + c, ESZ) : tile_elem<false>(o, c0 + c, ESZ);
-          if constexpr (ESZ == 4) *reinterpret_cast<uint32_t*>(t + off) = reinterpret_cast<const uint32_t*>(r)[c];
-          else if constexpr (ESZ == 2) *reinterpret_cast<uint16_t*>(t + off) = reinterpret_cast<const uint16_t*>(r)[c];
-          else t[off] = r[c];
-        }
-        if constexpr (KV == KV_I8_REF) {
-          if (lane == 0) reinterpret_cast<float*>(scales)[((uint64_t)blk * Hkv + h) * BS + o] = xsc[w][d];
-        }
-      }
-    } else {
-      // one run per destination block: [ctx + d, ctx + dend)
-      int d = d0;
-      while (d < na) {
-        const int p = ctx + d;
-        const int dend = min(na, (p / BS + 1) * BS - ctx);
-        const int64_t blk = blk_of(p);
-        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
-        uint16_t* sp = reinterpret_cast<uint16_t*>(scales) + (uint64_t)blk * Hkv + h;
-        int cd[BS][2];
-#pragma unroll
-        for (int u = 0; u < BS; ++u) {
-          cd[u][0] = (int8_t)t[is_v ? tile_elem<true>(u, c0, 1) : tile_elem<false>(u, c0, 1)];
-          cd[u][1] = (int8_t)t[is_v ? tile_elem<true>(u, c0 + 1, 1) : tile_elem<false>(u, c0 + 1, 1)];
-        }
-        const int o0 = p % BS;
-        float s_old = (o0 == 0) ? 0.f : h2f(*sp);
-        uint16_t s_bits = (o0 == 0) ? (uint16_t)0 : *sp;
-        for (int e = d; e < dend; ++e) {
-          const uint8_t* r = &raw[w][e][2 * lane];
-          const float sc = xsc[w][e];
-          blk_put(cd, (ctx + e) % BS, s_old, s_bits, (float)(int8_t)r[0] * sc, (float)(int8_t)r[1] * sc);
-        }
-        const int hi_written = (ctx + dend - 1) % BS;
-#pragma unroll
-        for (int u = 0; u < BS; ++u) {
-          if (u <= hi_written) {
-            t[is_v ? tile_elem<true>(u, c0, 1) : tile_elem<false>(u, c0, 1)] = (uint8_t)(int8_t)cd[u][0];
-            t[is_v ? tile_elem<true>(u, c0 + 1, 1) : tile_elem<false>(u, c0 + 1, 1)] = (uint8_t)(int8_t)cd[u][1];
-          }
-        }
-        if (lane == 0) *sp = s_bits;
-        d = dend;
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  }
+  if (w == 0) commit_wave<KV, false>(P, raw[0], xsc[0], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
+  else commit_wave<KV, true>(P, raw[1], xsc[1], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
 }
 
 DEV uint64_t splitmix64(uint64_t x) {
@@ -2413,6 +2436,7 @@ extern "C" __global__ void __launch_bounds__(256) vk_decode_merge_sk(const Merge
 extern "C" __global__ void __launch_bounds__(256) vk_nixl_check(const NixlParams P) { nixl_check_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_nixl_copy(const NixlParams P) { nixl_copy_kernel(P); }
 #define VK_COMMIT(KV) \
-  extern "C" __global__ void __launch_bounds__(128) vk_tree_commit_kv##KV(const CommitParams P) { tree_commit<KV>(P); }
+  extern "C" __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(4)))                         \
+      vk_tree_commit_kv##KV(const CommitParams P) { tree_commit<KV>(P); }
 VK_COMMIT(0) VK_COMMIT(1) VK_COMMIT(2) VK_COMMIT(3)
 
