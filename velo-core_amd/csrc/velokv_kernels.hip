@@ -1827,10 +1827,12 @@ DEV int prev_block(const AppendParams& P, int n) {
   return -1;
 }
 
-// The run that starts at token n (slot `slot`), for KV head h.
+// The run that starts at token w0 + j (slot `slot`), for KV head h; ms0 holds
+// the slots of tokens w0 .. w0 + 63 (lane i: token w0 + i, -1 past the end), so
+// the first step of the run's forward scan needs no load.
 template <bool IS_V>
-DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales, int n, int64_t slot,
-                        int h) {
+DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales, int w0, int j,
+                        int64_t slot, int64_t ms0, int h) {
   const int lane = lane_id();
   const int64_t b = slot / BS;
   if (b >= P.g.n_blocks) return;
@@ -1854,9 +1856,10 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
   uint16_t s_bits = 0;
   int hi_written = -1;
   bool first = true;
-  for (int base = n; base < P.n_tok; base += WAVE) {
+  for (int base = w0; base < P.n_tok; base += WAVE) {
     const int m = base + lane;
-    const int64_t ms = m < P.n_tok ? token_slot(P, m) : -1;
+    // tokens before the run's first (lanes below j of the first window) are not part of it
+    const int64_t ms = base == w0 ? (lane >= j ? ms0 : -1) : (m < P.n_tok ? token_slot(P, m) : -1);
     // the run ends at the first non-padding token of another block
     const uint64_t other = __builtin_amdgcn_ballot_w64(ms >= 0 && ms / BS != b);
     const int stop = other ? __builtin_ctzll(other) : WAVE;
@@ -1925,7 +1928,9 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
   const int lane = lane_id();
   const int h = blockIdx.y;
   const int m = w0 + lane;
-  const int64_t ms = (lane < T && m < P.n_tok) ? token_slot(P, m) : -1;
+  // slots of 64 tokens from w0: the window's T and what follows (reused by the runs' forward scans)
+  const int64_t ms64 = m < P.n_tok ? token_slot(P, m) : -1;
+  const int64_t ms = lane < T ? ms64 : -1;
   const int before = prev_block(P, w0);  // loads issued beside the window's
   const int mb = ms >= 0 ? (int)(ms / BS) : -1;
   const uint64_t valid = __builtin_amdgcn_ballot_w64(ms >= 0);
@@ -1940,7 +1945,7 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
     starts &= starts - 1;
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ms, j);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)ms >> 32), j);
-    append_blk_run<IS_V>(P, src, codes, scales, w0 + j, (int64_t)(((uint64_t)hi << 32) | lo), h);
+    append_blk_run<IS_V>(P, src, codes, scales, w0, j, (int64_t)(((uint64_t)hi << 32) | lo), ms64, h);
   }
 }
 
