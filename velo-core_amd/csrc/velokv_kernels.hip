@@ -937,10 +937,11 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     }
   };
 
-  if constexpr (I8 && !TREE) {
+  if constexpr (BLK && !TREE) {
     // three-stage pipeline: two stages in flight while one is consumed (the tree
     // kernels read mostly cached prefix pages and keep two stages so that two
-    // waves fit per SIMD)
+    // waves fit per SIMD; an I8_REF stage also carries the per-token scales, and
+    // a third one would not fit in 256 registers)
     MStage<KV> sc2;
     mstage_load<KV>(sb, P, bw, 1, nblk, kvh, n, g);
     for (int b = 0; b < nbatch; b += 3) {
