@@ -68,6 +68,8 @@ def parse():
     ap.add_argument("--kv-heads", type=int, default=8)
     ap.add_argument("--pool-blocks", type=int, default=40000)
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = auto)")
+    ap.add_argument("--q-dtype", choices=["fp16", "fp32"], default="fp16",
+                    help="decode query dtype (fp32: the reference kernels' float q)")
     ap.add_argument("--ragged", action="store_true", help="context lengths U[1024, ctx] (configs 2/3)")
     ap.add_argument("--decode", choices=["auto", "mfma", "valu"], default="auto",
                     help="decode kernel family (vk_ctx_set_decode_kernel)")
@@ -91,7 +93,7 @@ def parse():
     return ap.parse_args()
 
 
-def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride: int) -> int:
+def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride: int, q_esz: int = 2) -> int:
     """Algorithmic HBM bytes of one decode call: each K/V element of every context
     token read once, its scales, q, the output and the block-table entries used."""
     tok = int(lens.sum())
@@ -102,7 +104,7 @@ def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride:
         kvb += 2 * blocks * Hkv * 2
     elif kv == velokv.KV_I8_REF:
         kvb += 2 * tok * Hkv * 4
-    return kvb + S * H * HD * 2 + S * H * HD * 4 + blocks * 4 + S * 4
+    return kvb + S * H * HD * q_esz + S * H * HD * 4 + blocks * 4 + S * 4
 
 
 def append_bytes(kv: int, S: int, Hkv: int) -> int:
@@ -160,9 +162,13 @@ def run_gpu(ctx, args, kv_name: str):
     R = 4
     new_slots = ctx.upload(synth.slots_for_positions(bt, lens.astype(np.int64) - 1, BS))
     qs, ks, vs = [], [], []
+    qdt = velokv.DT_F32 if args.q_dtype == "fp32" else velokv.DT_F16
     for r in range(R):
-        q = ctx.alloc(S * H * HD * 2)
-        ctx.fill_normal_f16(q, S * H * HD, 7000 + r, H * HD)
+        if qdt == velokv.DT_F32:  # seeded normals made on the host (1 MB per set at the headline shape)
+            q = ctx.upload(synth.rng(7000 + r).standard_normal(S * H * HD).astype(np.float32))
+        else:
+            q = ctx.alloc(S * H * HD * 2)
+            ctx.fill_normal_f16(q, S * H * HD, 7000 + r, H * HD)
         k = ctx.alloc(S * Hkv * HD * 2)
         ctx.fill_normal_f16(k, S * Hkv * HD, 8000 + r, Hkv * HD, outlier)
         v = ctx.alloc(S * Hkv * HD * 2)
@@ -185,14 +191,14 @@ def run_gpu(ctx, args, kv_name: str):
                 app_evs[layer][0].record(stream)
             if rope:
                 ctx.append_rope(pool, layer, ks[r], vs[r], velokv.DT_F16, d_pos, new_slots, S, d_table, n_pos, rope,
-                                q=qs[r], q_dtype=velokv.DT_F16, n_heads=H, stream=stream)
+                                q=qs[r], q_dtype=qdt, n_heads=H, stream=stream)
             else:
                 ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
             if app_evs is not None:
                 app_evs[layer][1].record(stream)
             if evs is not None:
                 evs[layer][0].record(stream)
-            ctx.paged_decode(pool, layer, qs[r], velokv.DT_F16, out, d_lens, S, H, int(lens.max()),
+            ctx.paged_decode(pool, layer, qs[r], qdt, out, d_lens, S, H, int(lens.max()),
                              block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
                              stream=stream, sum_context_len=int(lens.sum()))
             if evs is not None:
@@ -221,15 +227,15 @@ def run_gpu(ctx, args, kv_name: str):
     app_ms = [app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]
 
     ms_step = total_ms / args.steps
-    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1])
+    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1], 4 if qdt == velokv.DT_F32 else 2)
     abytes = append_bytes(kv, S, Hkv)
     if rope:  # q read and written (fp16), positions, one table row (D/2 cos, sin pairs) per token
-        abytes += 2 * S * H * HD * 2 + S * 4 + S * HD * 4
+        abytes += 2 * S * H * HD * (4 if qdt == velokv.DT_F32 else 2) + S * 4 + S * HD * 4
     step_bytes = NL * (dbytes + abytes)
     dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
     kname = ctx.decode_kernel_name(pool, S, H, int(lens.max()), bt_stride=bt.shape[1],
-                                   partition_tokens=args.partition, sum_context_len=int(lens.sum()))
+                                   partition_tokens=args.partition, q_dtype=qdt, sum_context_len=int(lens.sum()))
     res = {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
         "ms_per_step": round(ms_step, 4),

@@ -204,11 +204,14 @@ def test_decode_workspace_reuse_across_layouts(ctx, impl):
 
 @pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("shape", ["mixed", "many_small", "wide"])
-def test_decode_streamk_worker_boundaries(ctx, kv, shape):
+@pytest.mark.parametrize("qd", [np.float16, np.float32])
+def test_decode_streamk_worker_boundaries(ctx, kv, shape, qd):
     """Stream-K ranges that split segments at arbitrary blocks, cross several
     sequences, skip empty contexts, and (many_small) leave fewer blocks than
     workers; more than 64 sequences exercise the chunked prefix scan."""
-    print(f"decode stream-K kv={kv} shape={shape}", flush=True)
+    print(f"decode stream-K kv={kv} shape={shape} q={np.dtype(qd).name}", flush=True)
+    if qd == np.float32 and kv == O.F16:
+        pytest.skip("fp32 queries over fp16 KV run the fp32 VALU kernels, not stream-K")
     ctx.set_decode_kernel(velokv.DECODE_MFMA)
     ctx.set_decode_schedule(velokv.SCHED_STREAM)
     try:
@@ -223,9 +226,12 @@ def test_decode_streamk_worker_boundaries(ctx, kv, shape):
         ref_layer = oracle_layer(case)
         pool = gpu_pool(ctx, case)
         case.ctx_lens = np.asarray(lens, np.int32)
-        got = run_decode(ctx, pool, case)
-        ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
-        check(got, ref, f"stream-K {shape}")
+        name = ctx.decode_kernel_name(pool, len(lens), 8, int(max(lens)), bt_stride=case.block_tables.shape[1],
+                                      q_dtype=velokv.DT_F32 if qd == np.float32 else velokv.DT_F16)
+        assert name.startswith(f"vk_decode_sk_kv{kv}_g4"), name
+        got = run_decode(ctx, pool, case, q_dtype=qd)
+        ref = O.paged_decode(ref_layer, case.q.astype(qd), case.block_tables, case.ctx_lens)
+        check(got, ref, f"stream-K {shape} q={np.dtype(qd).name}")
         assert np.all(got[np.asarray(lens) == 0] == 0.0)
     finally:
         ctx.set_decode_kernel(velokv.DECODE_AUTO)
@@ -234,7 +240,8 @@ def test_decode_streamk_worker_boundaries(ctx, kv, shape):
 
 @pytest.mark.parametrize("kv", [O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("S,G,nw", [(256, 4, 1), (128, 4, 2), (64, 4, 4), (32, 8, 8)])
-def test_decode_workgroup_split(ctx, kv, S, G, nw):
+@pytest.mark.parametrize("qd", [np.float16, np.float32])
+def test_decode_workgroup_split(ctx, kv, S, G, nw, qd):
     """The workgroup-split kernel (one workgroup of nw waves per (sequence, KV
     head), partials combined in LDS) on ragged contexts, including empty and
     one-token ones and waves whose share is empty."""
@@ -251,13 +258,15 @@ def test_decode_workgroup_split(ctx, kv, S, G, nw):
     ctx.set_decode_kernel(velokv.DECODE_MFMA)
     ctx.set_decode_schedule(velokv.SCHED_SPLIT)
     try:
-        name = ctx.decode_kernel_name(pool, S, Hkv * G, int(lens.max()), bt_stride=case.block_tables.shape[1])
-        assert name == f"vk_decode_wg_kv{kv}_g{G}", name
+        qdt = velokv.DT_F32 if qd == np.float32 else velokv.DT_F16
+        name = ctx.decode_kernel_name(pool, S, Hkv * G, int(lens.max()), bt_stride=case.block_tables.shape[1],
+                                      q_dtype=qdt)
+        assert name == f"vk_decode_wg_kv{kv}_g{G}" + ("_q0" if qd == np.float32 else ""), name
         assert ctx.decode_workspace_bytes(pool, S, Hkv * G, int(lens.max()),
-                                          bt_stride=case.block_tables.shape[1]) == 0
-        got = run_decode(ctx, pool, case)
-        ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens)
-        check(got, ref, f"workgroup split S={S} G={G}")
+                                          bt_stride=case.block_tables.shape[1], q_dtype=qdt) == 0
+        got = run_decode(ctx, pool, case, q_dtype=qd)
+        ref = O.paged_decode(ref_layer, case.q.astype(qd), case.block_tables, case.ctx_lens)
+        check(got, ref, f"workgroup split S={S} G={G} q={np.dtype(qd).name}")
         assert np.all(got[lens == 0] == 0.0)
     finally:
         ctx.set_decode_kernel(velokv.DECODE_AUTO)

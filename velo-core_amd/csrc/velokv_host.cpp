@@ -127,14 +127,17 @@ const char* const kKernelNames[] = {
 std::string decode_name(int kv, int g, int qt) {
   return "vk_decode_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
 }
-std::string decode_mfma_name(int kv, int g) {
-  return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g);
+// Matrix-core decode kernels: fp16 q, or (int8 KV only, suffix _q0) fp32 q split
+// into fp16 hi + lo parts.
+std::string q0_suffix(int qt) { return qt == VK_DT_F32 ? "_q0" : ""; }
+std::string decode_mfma_name(int kv, int g, int qt = VK_DT_F16) {
+  return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
-std::string decode_wg_name(int kv, int g) {
-  return "vk_decode_wg_kv" + std::to_string(kv) + "_g" + std::to_string(g);
+std::string decode_wg_name(int kv, int g, int qt = VK_DT_F16) {
+  return "vk_decode_wg_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
-std::string decode_sk_name(int kv, int g) {
-  return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g);
+std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16) {
+  return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
 std::string tree_pfx_name(int kv, int g, int qt) {
   return "vk_tree_pfx_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
@@ -159,16 +162,18 @@ int launch(const vk_ctx* ctx, const char* name, dim3 grid, dim3 block, const P& 
   return VK_OK;
 }
 
-// Waves of a one-wave-per-workgroup kernel that fit on the device at once.
-int64_t resident_waves(vk_ctx* ctx, const std::string& name) {
-  auto it = ctx->resident.find(name);
+// Waves of a kernel that fit on the device at once, launched with workgroups of
+// `block` threads (one wave each by default).
+int64_t resident_waves(vk_ctx* ctx, const std::string& name, int block = 64) {
+  const std::string key = name + "/" + std::to_string(block);
+  auto it = ctx->resident.find(key);
   if (it != ctx->resident.end()) return it->second;
   int64_t waves = 2048;
   hipFunction_t f = ctx->fn(name);
   int per_cu = 0;
-  if (f && hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64, 0) == hipSuccess && per_cu > 0)
-    waves = (int64_t)per_cu * ctx->n_cu;
-  ctx->resident[name] = waves;
+  if (f && hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, block, 0) == hipSuccess && per_cu > 0)
+    waves = (int64_t)per_cu * (block / 64) * ctx->n_cu;
+  ctx->resident[key] = waves;
   return waves;
 }
 
@@ -222,7 +227,12 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
       if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
       if (kv != VK_KV_F32) names.push_back(decode_sk_name(kv, g));
-      if (kv == VK_KV_I8_REF || kv == VK_KV_I8_BLK) names.push_back(decode_wg_name(kv, g));
+      if (kv == VK_KV_I8_REF || kv == VK_KV_I8_BLK) {
+        names.push_back(decode_wg_name(kv, g));
+        names.push_back(decode_wg_name(kv, g, VK_DT_F32));
+        names.push_back(decode_sk_name(kv, g, VK_DT_F32));
+        names.push_back(decode_mfma_name(kv, g, VK_DT_F32));
+      }
       if (kv != VK_KV_F32)
         for (int rt : {1, 2})
           for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
@@ -542,6 +552,8 @@ int split_workspace(vk_ctx* ctx, void* given, uint64_t given_bytes, uint64_t nee
   return VK_OK;
 }
 
+constexpr int kWgMaxWaves = 8;  // waves per workgroup of vk_decode_wg_* at most (velokv_kernels.hip)
+
 struct DecodePlan {
   const int32_t* bt;
   int32_t bt_stride;
@@ -555,14 +567,17 @@ struct DecodePlan {
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
 };
 
-// Schedule and kernel family for these arguments. fp32 queries or fp32 KV take
-// the fp32 VALU kernel with fixed partitions. Otherwise stream-K (matrix cores)
-// when requested, or under AUTO unless the batch is known to be uniform or the
-// VALU family was requested; fixed partitions run the matrix cores for int8 KV
-// and the dot2 kernel for fp16 KV under AUTO (measured faster for each).
+// Schedule and kernel family for these arguments. fp32 KV, and fp32 queries over
+// fp16 KV, take the VALU kernels with fixed partitions (fp32 arithmetic).
+// Otherwise (fp16 queries, or fp32 queries over int8 KV, split into fp16 hi + lo
+// for the matrix cores) stream-K when requested, or under AUTO unless the batch
+// is known to be uniform or the VALU family was requested; fixed partitions run
+// the matrix cores for int8 KV and the dot2 kernel for fp16 KV under AUTO
+// (measured faster for each).
 void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, bool* stream_k, bool* mfma) {
   const vk_pool_desc& d = pool->desc;
-  const bool fast = a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32;
+  const bool i8 = d.kv_type == VK_KV_I8_REF || d.kv_type == VK_KV_I8_BLK;
+  const bool fast = (a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32) || (a->q_dtype == VK_DT_F32 && i8);
   const int kind = ctx ? ctx->decode_kind : VK_DECODE_AUTO;
   const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
   const bool uniform = a->sum_context_len > 0 &&
@@ -612,7 +627,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   pl->n_workers = 0;
   pl->wg_waves = 0;
   if (pl->stream_k) {
-    pl->kernel = decode_sk_name(d.kv_type, G);
+    pl->kernel = decode_sk_name(d.kv_type, G, a->q_dtype);
     // one wave per resident slot, and at most 256 blocks (four id windows) per worker
     const int64_t blocks_max = (int64_t)a->n_seqs * d.n_kv_heads * ((a->max_context_len + d.block_size - 1) / d.block_size);
     const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
@@ -633,20 +648,20 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     // whose workgroups fill one round of resident waves, when each wave's share
     // fits its four block-id windows (256 blocks).
     const int64_t pairs = (int64_t)a->n_seqs * d.n_kv_heads;
-    const int64_t waves = ctx ? resident_waves(ctx, decode_mfma_name(d.kv_type, G)) : 2048;
+    const int64_t waves = ctx ? resident_waves(ctx, decode_wg_name(d.kv_type, G, a->q_dtype), 64 * kWgMaxWaves) : 2048;
     int nw = 1;
     while (nw < 8 && pairs * nw < waves) nw *= 2;
     const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
     if (pairs > 0 && pairs * nw >= waves && (nb + nw - 1) / nw <= kMaxPartTokens / d.block_size &&
         pairs <= 0x7FFFFFFF) {
       pl->wg_waves = nw;
-      pl->kernel = decode_wg_name(d.kv_type, G);
+      pl->kernel = decode_wg_name(d.kv_type, G, a->q_dtype);
       pl->part_tokens = kMaxPartTokens;
       pl->max_parts = 1;
       return VK_OK;
     }
   }
-  pl->kernel = mfma ? decode_mfma_name(d.kv_type, G) : decode_name(d.kv_type, G, a->q_dtype);
+  pl->kernel = mfma ? decode_mfma_name(d.kv_type, G, a->q_dtype) : decode_name(d.kv_type, G, a->q_dtype);
   if (P == 0) P = auto_partition(a, d, ctx ? resident_waves(ctx, pl->kernel) : 2048);
   pl->part_tokens = P;
   pl->max_parts = std::max(1, (a->max_context_len + P - 1) / P);

@@ -746,9 +746,15 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   mstage_load<KV>(sa, P, bw, 0, nblk, kvh, n, g);
 
   // q^T as the B operand: row n of each tile (rows >= nrows are zero and their
-  // results are dropped), dims 32g..32g+31 in 4 chunks
+  // results are dropped), dims 32g..32g+31 in 4 chunks. An fp32 q of the decode
+  // kernels is split as q = hi + lo, hi = fp16(q), lo = fp16(q - hi), and each
+  // score takes two products (hi, then lo, into the same accumulator), so the
+  // scores see q to about 2^-22 instead of fp16's 2^-11; the tree kernels
+  // round an fp32 q to fp16.
+  constexpr bool QSPLIT = (QT == DT_F32) && !TREE;
   half8 qa[RT][4];
-  float qb[RT];        // int8 KV: 1152 * sum_d q[row n][d]
+  half8 qlo[RT][4];
+  float qb[RT];        // int8 KV: 1152 * sum_d q[row n][d] (of hi + lo when split)
   uint32_t mrow[RT];   // tree: mask row of row n's node
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -757,20 +763,26 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     const int64_t qoff = out_row(R) * HD + 32 * g;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
-      uint4 v = make_uint4(0, 0, 0, 0);
+      uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
       if (R < nrows) {
         if constexpr (QT == DT_F32) {
           const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff) + 2 * kc;
           const float4 x0 = q32[0], x1 = q32[1];
           v = make_uint4(pack_h2(x0.x, x0.y), pack_h2(x0.z, x0.w), pack_h2(x1.x, x1.y), pack_h2(x1.z, x1.w));
+          if constexpr (QSPLIT) {
+            const half8 h = bitcast<half8>(v);
+            vlo = make_uint4(pack_h2(x0.x - (float)h[0], x0.y - (float)h[1]), pack_h2(x0.z - (float)h[2], x0.w - (float)h[3]),
+                             pack_h2(x1.x - (float)h[4], x1.y - (float)h[5]), pack_h2(x1.z - (float)h[6], x1.w - (float)h[7]));
+          }
         } else {
           v = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qoff)[kc];
         }
       }
       qa[rt][kc] = bitcast<half8>(v);
+      qlo[rt][kc] = bitcast<half8>(vlo);
       if constexpr (I8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qsum += (float)qa[rt][kc][j];
+        for (int j = 0; j < 8; ++j) qsum += QSPLIT ? (float)qa[rt][kc][j] + (float)qlo[rt][kc][j] : (float)qa[rt][kc][j];
       }
     }
     qb[rt] = 0.f;
@@ -817,6 +829,11 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
           sc[rt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<half8>(kbv), qa[rt][kc], sc[rt][u], 0, 0, 0);
+        if constexpr (QSPLIT) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            sc[rt][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<half8>(kbv), qlo[rt][kc], sc[rt][u], 0, 0, 0);
+        }
       }
     }
     // ---- scaled scores (log2 units) of tokens 4g..4g+3, row n ----
@@ -937,11 +954,11 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     }
   };
 
-  if constexpr (BLK && !TREE) {
+  if constexpr (BLK && !TREE && !QSPLIT) {
     // three-stage pipeline: two stages in flight while one is consumed (the tree
     // kernels read mostly cached prefix pages and keep two stages so that two
     // waves fit per SIMD; an I8_REF stage also carries the per-token scales, and
-    // a third one would not fit in 256 registers)
+    // the lo parts of a split fp32 q take the registers of a third stage)
     MStage<KV> sc2;
     mstage_load<KV>(sb, P, bw, 1, nblk, kvh, n, g);
     for (int b = 0; b < nbatch; b += 3) {
@@ -1096,7 +1113,7 @@ DEV int seq_blocks(const DecodeParams& P, int s) {
   return (max(0, min(P.context_lens[s], P.cap_tokens)) + BS - 1) / BS;
 }
 
-template <int KV, int G>
+template <int KV, int G, int QT = DT_F16>
 DEV void attn_streamk_mfma(const DecodeParams& P) {
   const int lane = lane_id();
   const int w = blockIdx.x;
@@ -1149,8 +1166,8 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     const int o0 = rel - kvh * nb;
     const int o1 = (int)min((int64_t)nb, (int64_t)o0 + (b1 - x));
     const int slot = o0 > 0 ? 0 : 1;
-    attn_piece<KV, G, 1, false, DT_F16>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                        ((int64_t)w * 2 + slot) * G, 1, P.part_acc, P.part_ml);
+    attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
+                                    ((int64_t)w * 2 + slot) * G, 1, P.part_acc, P.part_ml);
     x += o1 - o0;
     if (o1 == nb && kvh == Hkv - 1) {
       pre += Hkv * nb;
@@ -1167,7 +1184,7 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
 //   out = sum_w 2^(M_w - M) acc_w / sum_w 2^(M_w - M) l_w,  M = max_w M_w,
 // so a uniform batch needs no partials in HBM and no merge launch.
 constexpr int kWgMaxWaves = 8;
-template <int KV, int G>
+template <int KV, int G, int QT = DT_F16>
 DEV void attn_wg_mfma(const DecodeParams& P) {
   __shared__ float wacc[kWgMaxWaves][G][HD];
   __shared__ float wml[kWgMaxWaves][G][2];
@@ -1186,8 +1203,8 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   const int per = (nb + nw - 1) / nw;
   const int b0 = min(nb, w * per), b1 = min(nb, b0 + per);
   if (b0 < b1) {
-    attn_piece<KV, G, 1, false, DT_F16>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
-                                        &wml[w][0][0]);
+    attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
+                                    &wml[w][0][0]);
   } else if (lane < G) {
     wml[w][lane][0] = kNegInf;
     wml[w][lane][1] = 0.f;
@@ -2382,6 +2399,15 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
   }
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
 VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
+// fp32 q (split into fp16 hi + lo) over int8 KV: suffix _q0
+#define VK_DECODE_MFMA_Q0(KV, G)                                                    \
+  extern "C" __global__ void __launch_bounds__(64)                                  \
+      vk_decode_mfma_kv##KV##_g##G##_q0(const DecodeParams P) {                     \
+    attn_unit_mfma<KV, G, 1, false, DT_F32>(P);                                     \
+  }
+#define VK_DECODE_MFMA_Q0_G(KV) \
+  VK_DECODE_MFMA_Q0(KV, 1) VK_DECODE_MFMA_Q0(KV, 2) VK_DECODE_MFMA_Q0(KV, 4) VK_DECODE_MFMA_Q0(KV, 8)
+VK_DECODE_MFMA_Q0_G(2) VK_DECODE_MFMA_Q0_G(3)
 
 // Workgroup-split decode: up to kWgMaxWaves waves of 64 per workgroup.
 #define VK_DECODE_WG(KV, G)                                                         \
@@ -2391,6 +2417,13 @@ VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
   }
 #define VK_DECODE_WG_G(KV) VK_DECODE_WG(KV, 1) VK_DECODE_WG(KV, 2) VK_DECODE_WG(KV, 4) VK_DECODE_WG(KV, 8)
 VK_DECODE_WG_G(2) VK_DECODE_WG_G(3)
+#define VK_DECODE_WG_Q0(KV, G)                                                      \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves)                    \
+      vk_decode_wg_kv##KV##_g##G##_q0(const DecodeParams P) {                       \
+    attn_wg_mfma<KV, G, DT_F32>(P);                                                 \
+  }
+#define VK_DECODE_WG_Q0_G(KV) VK_DECODE_WG_Q0(KV, 1) VK_DECODE_WG_Q0(KV, 2) VK_DECODE_WG_Q0(KV, 4) VK_DECODE_WG_Q0(KV, 8)
+VK_DECODE_WG_Q0_G(2) VK_DECODE_WG_Q0_G(3)
 
 // Two waves per SIMD (at most 256 registers).
 #define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
@@ -2401,6 +2434,13 @@ VK_DECODE_WG_G(2) VK_DECODE_WG_G(3)
   }
 #define VK_DECODE_SK_G(KV) VK_DECODE_SK(KV, 1) VK_DECODE_SK(KV, 2) VK_DECODE_SK(KV, 4) VK_DECODE_SK(KV, 8)
 VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
+#define VK_DECODE_SK_Q0(KV, G)                                                      \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
+      vk_decode_sk_kv##KV##_g##G##_q0(const DecodeParams P) {                       \
+    attn_streamk_mfma<KV, G, DT_F32>(P);                                            \
+  }
+#define VK_DECODE_SK_Q0_G(KV) VK_DECODE_SK_Q0(KV, 1) VK_DECODE_SK_Q0(KV, 2) VK_DECODE_SK_Q0(KV, 4) VK_DECODE_SK_Q0(KV, 8)
+VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
 
 // Tree verify: RT tiles of 16 (node, head) rows per wave. Over int8 pools the
 // kernels are held to 256 registers (two waves per SIMD) without spills; the fp16
