@@ -227,6 +227,10 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
       if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
       if (kv != VK_KV_F32) names.push_back(decode_sk_name(kv, g));
+      if (kv == VK_KV_F16) {
+        names.push_back(decode_sk_name(kv, g, VK_DT_F32));
+        names.push_back(decode_mfma_name(kv, g, VK_DT_F32));
+      }
       if (kv == VK_KV_I8_REF || kv == VK_KV_I8_BLK) {
         names.push_back(decode_wg_name(kv, g));
         names.push_back(decode_wg_name(kv, g, VK_DT_F32));
@@ -567,17 +571,15 @@ struct DecodePlan {
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
 };
 
-// Schedule and kernel family for these arguments. fp32 KV, and fp32 queries over
-// fp16 KV, take the VALU kernels with fixed partitions (fp32 arithmetic).
-// Otherwise (fp16 queries, or fp32 queries over int8 KV, split into fp16 hi + lo
+// Schedule and kernel family for these arguments. fp32 KV takes the fp32 VALU
+// kernel with fixed partitions. Otherwise (an fp32 q is split into fp16 hi + lo
 // for the matrix cores) stream-K when requested, or under AUTO unless the batch
 // is known to be uniform or the VALU family was requested; fixed partitions run
-// the matrix cores for int8 KV and the dot2 kernel for fp16 KV under AUTO
-// (measured faster for each).
+// the matrix cores for int8 KV and the VALU kernel for fp16 KV under AUTO
+// (measured faster for each; the VALU kernels compute an fp32 q in fp32).
 void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, bool* stream_k, bool* mfma) {
   const vk_pool_desc& d = pool->desc;
-  const bool i8 = d.kv_type == VK_KV_I8_REF || d.kv_type == VK_KV_I8_BLK;
-  const bool fast = (a->q_dtype == VK_DT_F16 && d.kv_type != VK_KV_F32) || (a->q_dtype == VK_DT_F32 && i8);
+  const bool fast = d.kv_type != VK_KV_F32;
   const int kind = ctx ? ctx->decode_kind : VK_DECODE_AUTO;
   const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
   const bool uniform = a->sum_context_len > 0 &&

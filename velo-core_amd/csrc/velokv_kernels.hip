@@ -653,7 +653,9 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 template <int KV>
 struct MStage {
   static constexpr int ESZ = Esz<KV>::v;
-  static constexpr int CH = 2;  // blocks per pipeline stage
+  // blocks per pipeline stage: two int8 blocks or one fp16 block (the same 8 KB
+  // of K and V per stage)
+  static constexpr int CH = ESZ == 1 ? 2 : 1;
   DW<8 * ESZ> k[CH];     // token n, dims 32g..32g+31
   DW<4 * ESZ> v[CH][2];  // token pairs 2g, 2g+1; dims 8n..8n+7
   float4 ks[CH];         // VK_KV_I8_REF: scales of tokens 4g..4g+3
@@ -2399,7 +2401,7 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
   }
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
 VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
-// fp32 q (split into fp16 hi + lo) over int8 KV: suffix _q0
+// fp32 q (split into fp16 hi + lo) over fp16 / int8 KV: suffix _q0
 #define VK_DECODE_MFMA_Q0(KV, G)                                                    \
   extern "C" __global__ void __launch_bounds__(64)                                  \
       vk_decode_mfma_kv##KV##_g##G##_q0(const DecodeParams P) {                     \
@@ -2407,7 +2409,7 @@ VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
   }
 #define VK_DECODE_MFMA_Q0_G(KV) \
   VK_DECODE_MFMA_Q0(KV, 1) VK_DECODE_MFMA_Q0(KV, 2) VK_DECODE_MFMA_Q0(KV, 4) VK_DECODE_MFMA_Q0(KV, 8)
-VK_DECODE_MFMA_Q0_G(2) VK_DECODE_MFMA_Q0_G(3)
+VK_DECODE_MFMA_Q0_G(1) VK_DECODE_MFMA_Q0_G(2) VK_DECODE_MFMA_Q0_G(3)
 
 // Workgroup-split decode: up to kWgMaxWaves waves of 64 per workgroup.
 #define VK_DECODE_WG(KV, G)                                                         \
@@ -2440,7 +2442,7 @@ VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
     attn_streamk_mfma<KV, G, DT_F32>(P);                                            \
   }
 #define VK_DECODE_SK_Q0_G(KV) VK_DECODE_SK_Q0(KV, 1) VK_DECODE_SK_Q0(KV, 2) VK_DECODE_SK_Q0(KV, 4) VK_DECODE_SK_Q0(KV, 8)
-VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
+VK_DECODE_SK_Q0_G(1) VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
 
 // Tree verify: RT tiles of 16 (node, head) rows per wave. Over int8 pools the
 // kernels are held to 256 registers (two waves per SIMD) without spills; the fp16
