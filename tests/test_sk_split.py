@@ -1,8 +1,11 @@
-"""The stream-K split (velokv_params.h sk_split / sk_begin / sk_worker_of),
-shared by the decode kernel and its merge, compiled for the host with g++ and
-checked by brute force: contiguous non-empty ranges within one block of each
-other, and the merge's block -> worker map the exact inverse of the kernel's
-worker -> range map."""
+"""The stream-K split (velokv_params.h sk_split / sk_begin / sk_worker_of,
+sk_piece / sk_segment_workers), shared by the decode kernel and its merge,
+compiled for the host with g++ and checked by brute force: contiguous non-empty
+ranges within one unit of each other, the merge's unit -> worker map the exact
+inverse of the kernel's worker -> range map, and, on random segment lists and
+per-segment penalties, the kernel's walk over each worker's units runs every
+block exactly once while the merge finds exactly the partials that cover each
+split segment (slot 1 of its first worker, slot 0 of the rest, in order)."""
 import os
 import shutil
 import subprocess

@@ -558,6 +558,12 @@ int split_workspace(vk_ctx* ctx, void* given, uint64_t given_bytes, uint64_t nee
 
 constexpr int kWgMaxWaves = 8;  // waves per workgroup of vk_decode_wg_* at most (velokv_kernels.hip)
 
+// Stream-K cost units charged to each segment ahead of its blocks, for what a
+// worker spends starting a second piece (per-wave traces on config 3: ~5 us).
+// Measured on configs 2 and 3 with 0, 4, 8, 12, 16, 24: 8 was fastest (config 3
+// 110.7 -> 109.2 us per call, config 2 208 -> 206 us).
+constexpr int kSkPenalty = 8;
+
 struct DecodePlan {
   const int32_t* bt;
   int32_t bt_stride;
@@ -630,10 +636,13 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   pl->wg_waves = 0;
   if (pl->stream_k) {
     pl->kernel = decode_sk_name(d.kv_type, G, a->q_dtype);
-    // one wave per resident slot, and at most 256 blocks (four id windows) per worker
-    const int64_t blocks_max = (int64_t)a->n_seqs * d.n_kv_heads * ((a->max_context_len + d.block_size - 1) / d.block_size);
+    // one wave per resident slot, and at most 256 blocks (four id windows) per
+    // worker: a worker's blocks are at most its units, ceil(units / nw)
+    const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads *
+                              ((a->max_context_len + d.block_size - 1) / d.block_size + kSkPenalty);
     const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
-    const int64_t nw = std::max<int64_t>(1, std::max(waves, (blocks_max + 255) / 256));
+    const int64_t nw = std::max<int64_t>(1, std::max(waves, (units_max + 255) / 256));
+    if (units_max > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "batch too large for the stream-K schedule");
     if (nw > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "grid too large");
     pl->n_workers = (int32_t)nw;
     pl->part_tokens = kMaxPartTokens;  // unused by the stream-K kernels
@@ -740,6 +749,7 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.n_nodes = 1;
   p.n_rgroups = 1;
   p.n_workers = pl.n_workers;
+  p.sk_penalty = pl.stream_k ? kSkPenalty : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
 
   MergeParams m{};
@@ -755,6 +765,7 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   m.cap_tokens = p.cap_tokens;
   m.sk_prefix = p.sk_prefix;
   m.n_workers = pl.n_workers;
+  m.sk_penalty = p.sk_penalty;
   m.n_kv_heads = d.n_kv_heads;
   m.n_seqs = a->n_seqs;
   const dim3 merge_grid((unsigned)((m.n_rows + 3) / 4));

@@ -1086,13 +1086,17 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
 }
 
 // ---- stream-K decode -------------------------------------------------------
-// The blocks of all (sequence, KV head) segments in order form one range of
-// W = sum_s Hkv * ceil(ctx_s / 16) blocks; worker w (one wave) takes the w-th
-// range of the stream-K split (sk_split in velokv_params.h). A
-// segment inside one worker's range is written directly; a split segment leaves
-// one partial per worker: slot 1 for the worker where it starts, slot 0 for the
-// workers that continue it. vk_decode_merge_sk combines them. Worker 0 also
-// stores the per-sequence block prefix and W for the merge.
+// The (sequence, KV head) segments in order form one range of cost units: a
+// segment of nb > 0 blocks takes pen + nb units, pen units that stand for the
+// cost of starting a piece and then one per block (sk_penalty; traces showed a
+// worker whose range starts a second segment ending later by about that many
+// blocks' time). Worker w (one wave) takes the w-th range of the stream-K split
+// of all units (sk_split, velokv_params.h) and runs the blocks in it
+// (sk_piece). A segment inside one worker's range is written directly; a
+// split segment leaves one partial per worker: slot 1 for the worker where it
+// starts, slot 0 for the workers that continue it. vk_decode_merge_sk combines
+// them. Worker 0 also stores the per-sequence unit prefix and the total for
+// the merge.
 DEV int wave_sum_i(int x) {
   x += __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR1, 0xF, 0xF, false);
   x += __builtin_amdgcn_update_dpp(0, x, DPP_QUAD_XOR2, 0xF, 0xF, false);
@@ -1115,64 +1119,73 @@ DEV int seq_blocks(const DecodeParams& P, int s) {
   return (max(0, min(P.context_lens[s], P.cap_tokens)) + BS - 1) / BS;
 }
 
+// Cost units of sequence s: Hkv segments of pen + nb units (none when empty).
+DEV int seq_units(const DecodeParams& P, int s) {
+  const int nb = seq_blocks(P, s);
+  return nb > 0 ? P.n_kv_heads * (nb + P.sk_penalty) : 0;
+}
+
 template <int KV, int G, int QT = DT_F16>
 DEV void attn_streamk_mfma(const DecodeParams& P) {
   const int lane = lane_id();
   const int w = blockIdx.x;
   const int nw = P.n_workers;
-  const int S = P.n_seqs, Hkv = P.n_kv_heads;
+  const int S = P.n_seqs, Hkv = P.n_kv_heads, pen = P.sk_penalty;
   int W = 0;
   for (int b = 0; b < S; b += WAVE) {
     const int s = b + lane;
-    W += wave_sum_i(s < S ? Hkv * seq_blocks(P, s) : 0);
+    W += wave_sum_i(s < S ? seq_units(P, s) : 0);
   }
-  if (w == 0) {  // block prefix per sequence for the merge
+  if (w == 0) {  // unit prefix per sequence for the merge
     int off = 0;
     for (int b = 0; b < S; b += WAVE) {
       const int s = b + lane;
-      const int nb = s < S ? Hkv * seq_blocks(P, s) : 0;
-      const int incl = wave_incl_scan_i(nb);
-      if (s < S) P.sk_prefix[s] = off + incl - nb;
+      const int nu = s < S ? seq_units(P, s) : 0;
+      const int incl = wave_incl_scan_i(nu);
+      if (s < S) P.sk_prefix[s] = off + incl - nu;
       off += readlane_i(incl, WAVE - 1);
     }
     if (lane == 0) P.sk_prefix[S] = W;
   }
   if (W == 0) return;
   const SkSplit sp = sk_split(W, nw);
-  if (w >= sp.nw) return;  // workers past the split have no blocks
-  const int64_t b0 = sk_begin(sp, w), b1 = sk_begin(sp, w + 1);
-  // the sequence holding block b0 and its first global block
+  if (w >= sp.nw) return;  // workers past the split have no units
+  const int64_t c0 = sk_begin(sp, w), c1 = sk_begin(sp, w + 1);
+  // the sequence holding unit c0 and its first unit
   int s = -1, pre = 0;
   {
     int off = 0;
     for (int b = 0; b < S && s < 0; b += WAVE) {
       const int sl = b + lane;
-      const int nb = sl < S ? Hkv * seq_blocks(P, sl) : 0;
-      const int incl = wave_incl_scan_i(nb);
-      const uint64_t m = __builtin_amdgcn_ballot_w64(off + incl > b0);
+      const int nu = sl < S ? seq_units(P, sl) : 0;
+      const int incl = wave_incl_scan_i(nu);
+      const uint64_t m = __builtin_amdgcn_ballot_w64(off + incl > c0);
       if (m != 0) {
         const int l = __builtin_ctzll(m);
         s = b + l;
-        pre = off + readlane_i(incl - nb, l);
+        pre = off + readlane_i(incl - nu, l);
       }
       off += readlane_i(incl, WAVE - 1);
     }
   }
-  int64_t x = b0;
-  while (x < b1 && s < S) {
+  int64_t x = c0;  // next unit to cover
+  while (x < c1 && s < S) {
     const int ctx_s = max(0, min(P.context_lens[s], P.cap_tokens));
     const int nb = (ctx_s + BS - 1) / BS;
     if (nb == 0) { ++s; continue; }
-    const int rel = (int)(x - pre);
-    const int kvh = rel / nb;
-    const int o0 = rel - kvh * nb;
-    const int o1 = (int)min((int64_t)nb, (int64_t)o0 + (b1 - x));
-    const int slot = o0 > 0 ? 0 : 1;
-    attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                    ((int64_t)w * 2 + slot) * G, 1, P.part_acc, P.part_ml);
-    x += o1 - o0;
-    if (o1 == nb && kvh == Hkv - 1) {
-      pre += Hkv * nb;
+    const int su = nb + pen;  // units per segment of this sequence
+    const int kvh = (int)(x - pre) / su;
+    const int64_t seg0 = pre + (int64_t)kvh * su;
+    int o0, o1;
+    sk_piece(seg0, nb, pen, x, c1, &o0, &o1);
+    if (o0 < o1) {
+      const int slot = o0 > 0 ? 0 : 1;
+      attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
+                                      ((int64_t)w * 2 + slot) * G, 1, P.part_acc, P.part_ml);
+    }
+    x = seg0 + su;
+    if (kvh == Hkv - 1) {
+      pre += Hkv * su;
       ++s;
     }
   }
@@ -1683,10 +1696,10 @@ __device__ void decode_merge(const MergeParams& P) {
   merge_row(P, r, np, [&](int k) -> int64_t { return base + k; });
 }
 
-// Stream-K merge: one wave per (sequence, head). The segment (s, kvh) covers
-// global blocks [S0, S1); workers w_lo..w_hi touched it: w_lo left slot 1, the
-// others slot 0. Unsplit segments were written by their worker; empty contexts
-// get zeros.
+// Stream-K merge: one wave per (sequence, head). The segment (s, kvh) starts at
+// unit seg0 (its blocks after sk_penalty units); workers w_lo..w_hi hold its
+// blocks: w_lo left slot 1, the others slot 0. Unsplit segments were written by
+// their worker; empty contexts get zeros.
 __device__ void decode_merge_sk(const MergeParams& P) {
   const int lane = lane_id();
   const int r = blockIdx.x * (blockDim.x / WAVE) + (threadIdx.x / WAVE);
@@ -1702,9 +1715,9 @@ __device__ void decode_merge_sk(const MergeParams& P) {
   }
   const int64_t W = P.sk_prefix[P.n_seqs];
   const SkSplit sp = sk_split(W, P.n_workers);
-  const int64_t S0 = (int64_t)P.sk_prefix[s] + (int64_t)kvh * nb;
-  const int w_lo = sk_worker_of(sp, S0);
-  const int w_hi = sk_worker_of(sp, S0 + nb - 1);
+  const int64_t seg0 = (int64_t)P.sk_prefix[s] + (int64_t)kvh * (nb + P.sk_penalty);
+  int w_lo, w_hi;
+  sk_segment_workers(sp, seg0, nb, P.sk_penalty, &w_lo, &w_hi);
   if (w_lo == w_hi) return;
   merge_row(P, r, w_hi - w_lo + 1, [&](int k) -> int64_t {
     return ((int64_t)(w_lo + k) * 2 + (k == 0 ? 1 : 0)) * G + gi;

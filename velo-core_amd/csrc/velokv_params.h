@@ -86,7 +86,8 @@ struct DecodeParams {
   int32_t n_nodes;          // query rows per (sequence, head): 1 for decode
   int32_t n_rgroups;        // row groups per (sequence, KV head) in the grid (tree kernels)
   int32_t n_workers;        // stream-K: workers in the grid
-  int32_t* sk_prefix;       // stream-K: [S + 1] first global block of each sequence, then W
+  int32_t* sk_prefix;       // stream-K: [S + 1] first cost unit of each sequence, then the total C
+  int32_t sk_penalty;       // stream-K: cost units charged to each segment ahead of its blocks
   float scale_log2;         // softmax scale * log2(e)
   // tree verify with a shared prefix: the first prefix_blocks pages of every
   // table row are the same pages; partial slots 0..prefix_chunks-1 of a row hold
@@ -157,13 +158,17 @@ struct MergeParams {
   // stream-K merge (vk_decode_merge_sk): partials indexed by (worker, slot, row of the group)
   const int32_t* sk_prefix;
   int32_t n_workers, n_kv_heads, n_seqs;
+  int32_t sk_penalty;                    // stream-K cost units per segment (DecodeParams)
   int32_t prefix_blocks, prefix_chunks;  // tree verify with a shared prefix (DecodeParams)
 };
 
-// Stream-K split of W blocks over nw workers of one wave each: worker w takes
-// blocks [begin(w), begin(w + 1)), begin(w) = w W / nwe over nwe = min(nw, W)
-// workers, so that no range is empty. The attention kernel and the merge
-// derive ranges from these functions.
+// Stream-K split of W cost units over nw workers of one wave each: worker w
+// takes units [begin(w), begin(w + 1)), begin(w) = w W / nwe over
+// nwe = min(nw, W) workers, so that no range is empty. A segment (sequence, KV
+// head) of nb > 0 blocks occupies pen + nb units, its blocks after pen units
+// that stand for the cost of starting a piece (a worker that starts a new
+// segment gets that many fewer blocks); with pen = 0 units are blocks. The
+// attention kernel and the merge derive ranges from these functions.
 struct SkSplit {
   int64_t W;
   int32_t nw;  // workers with blocks
@@ -175,6 +180,20 @@ VK_HD inline int64_t sk_begin(const SkSplit& s, int32_t w) { return (int64_t)w *
 // begin(w) <= x, i.e. ceil((x + 1) nw / W) - 1.
 VK_HD inline int32_t sk_worker_of(const SkSplit& s, int64_t x) {
   return (int32_t)(((x + 1) * s.nw + s.W - 1) / s.W) - 1;
+}
+
+// Blocks [lo, hi) of the segment whose units start at seg0 (nb blocks, pen
+// units ahead of them) that fall in the unit range [c0, c1); lo >= hi: none.
+VK_HD inline void sk_piece(int64_t seg0, int32_t nb, int32_t pen, int64_t c0, int64_t c1, int32_t* lo, int32_t* hi) {
+  const int64_t a = c0 - seg0 - pen, b = c1 - seg0 - pen;
+  *lo = (int32_t)(a > 0 ? a : 0);
+  *hi = (int32_t)(b < nb ? b : nb);
+}
+// The first and last worker holding blocks of that segment.
+VK_HD inline void sk_segment_workers(const SkSplit& s, int64_t seg0, int32_t nb, int32_t pen, int32_t* w_lo,
+                                     int32_t* w_hi) {
+  *w_lo = sk_worker_of(s, seg0 + pen);
+  *w_hi = sk_worker_of(s, seg0 + pen + nb - 1);
 }
 
 struct FillParams {
