@@ -91,10 +91,10 @@ int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
 /* Kernel family of vk_paged_decode over fp16/int8 KV: VK_DECODE_MFMA (QK and
  * PV on v_mfma_f32_16x16x{32,16}_f16; an fp32 q is split into fp16 hi + lo
  * parts), VK_DECODE_VALU (v_dot2_f32_f16, or fp32 arithmetic for an fp32 q, on
- * the vector ALUs) or VK_DECODE_AUTO (MFMA for int8 KV, VALU for fp16 KV with
- * fixed partitions: the faster one on MI355X for each; stream-K batches run on
- * the matrix cores). fp32 KV always uses the fp32 VALU kernel. No reference
- * counterpart. */
+ * the vector ALUs) or VK_DECODE_AUTO (MFMA for int8 KV and for fp32 queries,
+ * VALU for fp16 queries over fp16 KV with fixed partitions: the faster one on
+ * MI355X for each; stream-K batches run on the matrix cores). fp32 KV always
+ * uses the fp32 VALU kernel. No reference counterpart. */
 #define VK_DECODE_AUTO 0
 #define VK_DECODE_VALU 1
 #define VK_DECODE_MFMA 2
@@ -224,8 +224,8 @@ typedef struct vk_decode_args {
   const void* q;              /* dev [S][n_heads][head_dim] of q_dtype         */
   int32_t q_dtype;            /* VK_DT_F16: fp16 q. VK_DT_F32: the matrix-core
                                  kernels split q into fp16 hi + lo (scores see q
-                                 to ~2^-22); the VALU kernels (fp32 KV, uniform
-                                 fp16-KV batches, VK_DECODE_VALU) use fp32 math */
+                                 to ~2^-22); the VALU kernels (fp32 KV,
+                                 VK_DECODE_VALU) use fp32 math */
   float* out;                 /* dev fp32 [S][n_heads][head_dim]               */
   const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = the pool's slot table */
   int32_t bt_stride;          /* ignored when block_tables is NULL             */

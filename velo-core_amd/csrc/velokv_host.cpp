@@ -581,8 +581,9 @@ struct DecodePlan {
 // kernel with fixed partitions. Otherwise (an fp32 q is split into fp16 hi + lo
 // for the matrix cores) stream-K when requested, or under AUTO unless the batch
 // is known to be uniform or the VALU family was requested; fixed partitions run
-// the matrix cores for int8 KV and the VALU kernel for fp16 KV under AUTO
-// (measured faster for each; the VALU kernels compute an fp32 q in fp32).
+// the matrix cores for int8 KV and for fp32 queries, and the dot2 VALU kernel
+// for fp16 queries over fp16 KV under AUTO (measured faster for each; the VALU
+// kernels compute an fp32 q in fp32 and at GQA 8 spill).
 void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, bool* stream_k, bool* mfma) {
   const vk_pool_desc& d = pool->desc;
   const bool fast = d.kv_type != VK_KV_F32;
@@ -592,7 +593,8 @@ void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args*
                        (double)a->sum_context_len >= 0.97 * (double)a->n_seqs * (double)a->max_context_len;
   *stream_k = fast && a->partition_tokens == 0 && kind != VK_DECODE_VALU &&
               (sched == VK_SCHED_STREAM || (sched == VK_SCHED_AUTO && !uniform));
-  *mfma = *stream_k || (fast && (kind == VK_DECODE_MFMA || (kind == VK_DECODE_AUTO && d.kv_type != VK_KV_F16)));
+  *mfma = *stream_k || (fast && (kind == VK_DECODE_MFMA ||
+                                 (kind == VK_DECODE_AUTO && (d.kv_type != VK_KV_F16 || a->q_dtype == VK_DT_F32))));
 }
 
 // Smallest partition (256..4096 tokens) whose units fit in one round of resident
