@@ -343,9 +343,13 @@ def run_tree(ctx, args):
     mask = np.tile(velokv.branching_tree([2, 2, 2, 2, 2], N).ancestor_mask(), S)
     R = 2
     qs, ks, vs = [], [], []
+    qdt = velokv.DT_F32 if args.q_dtype == "fp32" else velokv.DT_F16
     for r in range(R):
-        q = ctx.alloc(S * N * H * HD * 2)
-        ctx.fill_normal_f16(q, S * N * H * HD, 7100 + r, H * HD)
+        if qdt == velokv.DT_F32:  # seeded normals made on the host
+            q = ctx.upload(synth.rng(7100 + r).standard_normal(S * N * H * HD).astype(np.float32))
+        else:
+            q = ctx.alloc(S * N * H * HD * 2)
+            ctx.fill_normal_f16(q, S * N * H * HD, 7100 + r, H * HD)
         k = ctx.alloc(S * N * Hkv * HD * 2)
         ctx.fill_normal_f16(k, S * N * Hkv * HD, 8100 + r, Hkv * HD, outlier)
         v = ctx.alloc(S * N * Hkv * HD * 2)
@@ -377,7 +381,7 @@ def run_tree(ctx, args):
                 app_evs[layer][1].record(stream)
             if evs is not None:
                 evs[layer][0].record(stream)
-            ctx.tree_verify(pool, layer, qs[r], velokv.DT_F16, out, d_committed, d_mask, S, N, H,
+            ctx.tree_verify(pool, layer, qs[r], qdt, out, d_committed, d_mask, S, N, H,
                             int(committed.max()), block_tables=d_bt, bt_stride=stride,
                             partition_tokens=args.partition, stream=stream, shared_blocks=shared_blocks)
             if evs is not None:
@@ -416,7 +420,7 @@ def run_tree(ctx, args):
     uniq_blk = pblocks + int(sum(-(-int(t) // BS) - pblocks for t in total))
     logical_tok = int(total.sum())
     logical_blk = int(sum(-(-int(t) // BS) for t in total))
-    qo = S * N * H * HD * (2 + 4) + S * N * 4 + S * 4 + logical_blk * 4
+    qo = S * N * H * HD * ((4 if qdt == velokv.DT_F32 else 2) + 4) + S * N * 4 + S * 4 + logical_blk * 4
     uniq = 2 * uniq_tok * Hkv * HD * esz + 2 * uniq_blk * Hkv * sc + qo
     logical = 2 * logical_tok * Hkv * HD * esz + 2 * logical_blk * Hkv * sc + qo
     G = H // Hkv
@@ -430,12 +434,13 @@ def run_tree(ctx, args):
     tv_mean = float(np.mean(tv_ms))
     ach = uniq / (tv_mean * 1e-3) / 1e9
     rt = 2 if N * G > 16 else 1
-    kname = "vk_tree_kv%d_g%d_r%d_q1" % (kv, G, rt)
+    qsfx = 0 if qdt == velokv.DT_F32 else 1
+    kname = "vk_tree_kv%d_g%d_r%d_q%d" % (kv, G, rt, qsfx)
     call_kernels = [kname, "vk_decode_merge"]
     if shared_blocks and kv in (velokv.KV_I8_BLK, velokv.KV_F16):
         # the rest of each context runs in one partition (no merge) while it fits 4096 tokens
         rest = max(int(committed.max()) - shared_blocks * BS, BS - 1) + N
-        call_kernels = ["vk_tree_pfx_kv%d_g%d_q1" % (kv, G), kname] + (["vk_decode_merge"] if rest > 4096 else [])
+        call_kernels = ["vk_tree_pfx_kv%d_g%d_q%d" % (kv, G, qsfx), kname] + (["vk_decode_merge"] if rest > 4096 else [])
     tflops = flops / (tv_mean * 1e-3) / 1e12
     return {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
