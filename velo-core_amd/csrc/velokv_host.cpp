@@ -98,6 +98,7 @@ struct vk_ctx {
   int decode_kind = VK_DECODE_AUTO;
   int decode_sched = VK_SCHED_AUTO;
   int n_cu = 256;
+  std::mutex res_mu;                                   // guards resident
   std::unordered_map<std::string, int64_t> resident;  // kernel -> resident waves
 
   hipFunction_t fn(const std::string& name) const {
@@ -166,6 +167,7 @@ int launch(const vk_ctx* ctx, const char* name, dim3 grid, dim3 block, const P& 
 // `block` threads (one wave each by default).
 int64_t resident_waves(vk_ctx* ctx, const std::string& name, int block = 64) {
   const std::string key = name + "/" + std::to_string(block);
+  std::lock_guard<std::mutex> lk(ctx->res_mu);  // planners may run on several host threads
   auto it = ctx->resident.find(key);
   if (it != ctx->resident.end()) return it->second;
   int64_t waves = 2048;
