@@ -175,8 +175,9 @@ int vk_slot_mapping(vk_ctx* ctx, vk_pool* pool, const int32_t* block_tables,
                     int64_t* slot_mapping_out, void* stream);
 
 /* Append n_tok new tokens of one layer: k, v are dev [n_tok][n_kv_heads][head_dim]
- * of type in_dtype (VK_DT_*); slot_mapping is dev int64 [n_tok] (negative =
- * skip). Quantizes on the way in for the I8 types.
+ * of type in_dtype (VK_DT_*); slot_mapping is dev int64 [n_tok] (negative, or
+ * at or past n_blocks * block_size = skip). Quantizes on the way in for the I8
+ * types.
  * kv_update (kernels.metal:619-645) and kv_update_int8 (kernels.metal:753-802),
  * dispatched at metal/model.rs:399-434.
  * Order rule: tokens of one call are applied in index order. For VK_KV_I8_BLK a

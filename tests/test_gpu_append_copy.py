@@ -171,6 +171,26 @@ def test_append_skips_negative_slots_and_layers_are_separate(ctx):
         assert not got["k"].any() and not got["ks"].any()
 
 
+@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+def test_append_skips_slots_past_the_pool(ctx, kv):
+    """A slot at or past n_blocks * block_size is padding, also in the middle
+    of a block's run (the run continues across it)."""
+    print(f"append slots past the pool kv={kv}", flush=True)
+    case = make_case(kv, [40], seed=106, outlier_scale=8.0)
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, 8, HD, kv)
+    sl, kk, vv = case.prefill_slots()
+    bad = sl.copy()
+    end = case.n_blocks * BS
+    bad[5], bad[6], bad[21] = end, end + 17, 2 ** 40
+    ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(bad), len(bad))
+    ctx.sync()
+    ref_sl = sl.copy()
+    ref_sl[[5, 6, 21]] = -1
+    ref = O.Layer(case.n_blocks, 8, BS, HD, kv)
+    O.append(ref, kk, vv, ref_sl)
+    assert_layer_equal(pool, 0, ref)
+
+
 def test_slot_mapping_kernel(ctx):
     print("slot mapping", flush=True)
     case = make_case(O.F16, [50, 90, 3], seed=106)

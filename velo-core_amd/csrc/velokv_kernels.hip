@@ -1773,11 +1773,11 @@ DEV void rope_rotate(int style, const float* cos_sin, int pos, float& x0, float&
   }
 }
 
-// Flat slot of token m, or -1 when it is padding (negative slot) or, with RoPE,
-// its position is outside the table.
+// Flat slot of token m, or -1 when it is padding (a negative slot, or one at or
+// past the end of the pool) or, with RoPE, its position is outside the table.
 DEV int64_t token_slot(const AppendParams& P, int m) {
   const int64_t slot = P.slot_mapping[m];
-  if (slot < 0) return -1;
+  if (slot < 0 || slot >= (int64_t)P.g.n_blocks * BS) return -1;
   if (P.rope != ROPE_NONE) {
     const int pos = P.positions[m];
     if (pos < 0 || pos >= P.n_pos) return -1;
