@@ -20,6 +20,15 @@
  *    call vk_stream_sync().
  *  - The compute path is HIP only. There is no CPU fallback: a context whose
  *    code object is missing fails vk_ctx_create with VK_ERR_NOT_WIRED.
+ *  - Threading: a context, its pools and block managers may be used from several
+ *    host threads. Planning state (occupancy cache, workspace growth) is guarded
+ *    inside the context. Compute calls on one pool that overlap in time (on
+ *    different streams) must touch disjoint pages and, when they need split-K
+ *    scratch, pass their own workspace: the context-owned one is shared, and
+ *    overlapping calls that use it race on its contents (never on its lifetime:
+ *    a workspace the context outgrows is freed only by vk_ctx_destroy). Block
+ *    managers and radix caches are not internally locked: serialise calls on
+ *    one of them, as the reference does with its mutexes (metal/backend.rs:142-144).
  *
  * Layout of one layer of a pool in HBM ("build layout"; the reference layout
  * is [blk][tok][head][D(+4)], kernels.metal:474,700):
@@ -326,7 +335,8 @@ int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* src_dst_pairs,
  * d < n_accept[s]. All pointers are device pointers; accept is
  * [n_seqs][accept_stride], each row strictly increasing with accept[s][d] >= d
  * and < 32. A row that breaks this, or whose positions fall outside its block
- * table row or the pool, is left untouched. Leading nodes already in place
+ * table row or the pool, is left untouched and reported in status (dev int32
+ * [n_seqs], VK_COMMIT_*; NULL = not reported). Leading nodes already in place
  * (accept[s][d] == d) are not rewritten. The blocks written must belong to one
  * sequence only (copy-on-write before appending the tree makes them private).
  * F32 / F16 / I8_REF: the token rows (with their per-token scales) move
@@ -338,11 +348,15 @@ int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* src_dst_pairs,
  * Completes the tree-verify step: verify_tree (speculative.rs:217-242) accepts
  * a root-to-node path of SpeculativeTree (speculative.rs:48-130) whose K/V
  * were appended at context_len + node by the draft pass. */
+#define VK_COMMIT_OK          0  /* committed (or nothing to move)                     */
+#define VK_COMMIT_BAD_ROW     1  /* n_accept / accept row malformed, or context_len < 0 */
+#define VK_COMMIT_PAST_TABLE  2  /* a position past the block-table row                */
+#define VK_COMMIT_BAD_PAGE    3  /* a page id outside the pool                         */
 int vk_tree_commit(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
                    const int32_t* block_tables, int32_t bt_stride,
                    const int32_t* context_lens, const int32_t* accept,
                    int32_t accept_stride, const int32_t* n_accept,
-                   int32_t n_seqs, void* stream);
+                   int32_t n_seqs, int32_t* status, void* stream);
 
 /* ---- NIXL wire records of KV pages ------------------------------------------
  * Wire format of nixl.rs:24-61 (serialize_block / deserialize_block): a record

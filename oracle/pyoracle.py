@@ -144,7 +144,7 @@ def append(layer: Layer, k, v, slot_mapping):
     s = layer.struct()
     rc = lib().vko_append(C.byref(s), _ptr(k), _ptr(v), _in_dtype(k), _ptr(sm), C.c_int(len(sm)))
     if rc != 0:
-        raise ValueError("slot outside the pool")
+        raise RuntimeError(f"vko_append failed ({rc})")
 
 
 def paged_decode(layer: Layer, q, block_tables, ctx_lens, scale=None):

@@ -324,17 +324,18 @@ static void quant_ref_one(vko_layer* L, int is_v, int64_t blk, int h, int off, c
   memcpy((is_v ? L->vs : L->ks) + (((uint64_t)blk * L->n_kv_heads + h) * L->block_size + off) * 4, &scale, 4);
 }
 
-/* Append n_tok tokens (k, v: [n_tok][Hkv][D] of in_dtype) at flat slots
- * (negative = skip), in index order. Returns 0, or -1 for a slot outside the pool. */
+/* Append n_tok tokens (k, v: [n_tok][Hkv][D] of in_dtype) at flat slots, in
+ * index order. A slot that is negative, or at or past n_blocks * block_size, is
+ * padding and skipped (the reference's kv_update writes wherever the looked-up
+ * block points, kernels.metal:637; the build's append treats both as padding). */
 int vko_append(vko_layer* L, const void* k, const void* v, int in_dtype, const int64_t* slot_mapping, int n_tok) {
   const int D = L->head_dim, Hkv = L->n_kv_heads, bs = L->block_size;
   float* x = (float*)malloc(sizeof(float) * D);
   for (int n = 0; n < n_tok; ++n) {
     const int64_t slot = slot_mapping[n];
-    if (slot < 0) continue;
+    if (slot < 0 || slot >= (int64_t)L->n_blocks * bs) continue;
     const int64_t blk = slot / bs;
     const int off = (int)(slot % bs);
-    if (blk >= L->n_blocks) { free(x); return -1; }
     for (int is_v = 0; is_v < 2; ++is_v) {
       const void* src = is_v ? v : k;
       for (int h = 0; h < Hkv; ++h) {

@@ -85,3 +85,15 @@ def tol_check(got, ref, atol=2e-3, rtol=1e-2):
     bound = atol + rtol * np.abs(ref.astype(np.float64))
     bad = err > bound
     return (not bad.any()), float(err.max(initial=0.0)), int(bad.sum())
+
+
+def ref_codes_closed_form(x):
+    """kv_update_int8's codes restated in numpy fp32 (kernels.metal:783-797):
+    inv = 127 / amax rounded to fp32 once, each x * inv rounded to fp32, then the
+    (char) cast truncates toward zero. No step is shared with the C oracle."""
+    x32 = np.asarray(x, np.float32)
+    amax = np.max(np.abs(x32), axis=-1, keepdims=True)
+    with np.errstate(divide="ignore"):
+        inv = np.where(amax > 0, np.float32(127) / amax, np.float32(0)).astype(np.float32)
+    prod = (x32 * inv).astype(np.float32)
+    return np.trunc(prod).astype(np.int8), (amax[..., 0] / np.float32(127)).astype(np.float32)

@@ -6,7 +6,7 @@ import pytest
 
 import pyoracle as O
 import velokv
-from cases import BS, HD, make_case, oracle_layer
+from cases import BS, HD, make_case, oracle_layer, ref_codes_closed_form
 from velokv import synth
 
 pytestmark = pytest.mark.gpu
@@ -184,11 +184,42 @@ def test_append_skips_slots_past_the_pool(ctx, kv):
     bad[5], bad[6], bad[21] = end, end + 17, 2 ** 40
     ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(bad), len(bad))
     ctx.sync()
-    ref_sl = sl.copy()
-    ref_sl[[5, 6, 21]] = -1
     ref = O.Layer(case.n_blocks, 8, BS, HD, kv)
-    O.append(ref, kk, vv, ref_sl)
+    O.append(ref, kk, vv, bad)  # the oracle skips the same slots
     assert_layer_equal(pool, 0, ref)
+
+
+@pytest.mark.parametrize("in_dt", [np.float32, np.float16])
+def test_append_ref_codes_equal_truncating_closed_form(ctx, in_dt):
+    """The GPU REF append against the numpy fp32 statement of kv_update_int8
+    (truncating cast, kernels.metal:783-797) directly, not only through the
+    oracle: 1024 tokens x 8 heads, one per slot of a 64-block pool in random
+    order, row magnitudes spread so truncation and rounding differ often."""
+    print(f"append REF closed form in={np.dtype(in_dt).name}", flush=True)
+    r = np.random.default_rng(12)
+    n_blocks, Hkv = 64, 8
+    n_tok = n_blocks * BS
+    k = (r.standard_normal((n_tok, Hkv, HD)) * r.uniform(0.01, 50, (n_tok, Hkv, 1))).astype(in_dt)
+    v = (r.standard_normal((n_tok, Hkv, HD)) * r.uniform(0.01, 50, (n_tok, Hkv, 1))).astype(in_dt)
+    k[::7, :, 3] *= 8
+    slots = r.permutation(n_tok).astype(np.int64)
+    pool = velokv.Pool(ctx, 1, n_blocks, BS, Hkv, HD, O.I8_REF)
+    ctx.append(pool, 0, ctx.upload(k), ctx.upload(v), velokv.DT_F16 if in_dt == np.float16 else velokv.DT_F32,
+               ctx.upload(slots), n_tok)
+    ctx.sync()
+    got = pool.download_layer(0)
+    lay = O.Layer(n_blocks, Hkv, BS, HD, O.I8_REF)
+    lay.k[:], lay.v[:], lay.ks[:], lay.vs[:] = got["k"], got["v"], got["ks"], got["vs"]
+    for is_v, src, sc in ((0, k, got["ks"]), (1, v, got["vs"])):
+        want_c, want_s = ref_codes_closed_form(src.astype(np.float32))
+        scales = sc.view(np.float32).reshape(n_blocks, Hkv, BS)
+        for blk in range(n_blocks):
+            for h in range(Hkv):
+                tile = lay.tile_codes(is_v, blk, h)  # [BS][HD] int8
+                toks = np.nonzero(slots // BS == blk)[0]
+                offs = slots[toks] % BS
+                assert np.array_equal(tile[offs], want_c[toks, h]), f"codes is_v={is_v} blk={blk} h={h}"
+                assert np.array_equal(scales[blk, h, offs], want_s[toks, h]), f"scales is_v={is_v} blk={blk}"
 
 
 def test_slot_mapping_kernel(ctx):

@@ -221,20 +221,26 @@ def commit_case(ctx, kv, ctxs, n_nodes, n_layer, seed, spread=True):
     return pool, layers, bt
 
 
-def run_commit(ctx, pool, layers, bt, ctxs, accepts, stride=32, layer0=0, n_layers=None):
+def run_commit(ctx, pool, layers, bt, ctxs, accepts, stride=32, layer0=0, n_layers=None, n_accept=None):
+    """Commit on the GPU and in the oracle; returns the GPU's per-sequence status."""
     S = len(ctxs)
     acc = np.full((S, stride), -1, np.int32)
     na = np.zeros(S, np.int32)
     for s, a in enumerate(accepts):
         acc[s, :len(a)] = a
         na[s] = len(a)
+    if n_accept is not None:
+        na = np.asarray(n_accept, np.int32)
+    status = ctx.upload(np.full(S, -7, np.int32))
     ctx.tree_commit(pool, ctx.upload(bt), bt.shape[1], ctx.upload(np.asarray(ctxs, np.int32)), ctx.upload(acc),
-                    stride, ctx.upload(na), S, layer0=layer0, n_layers=n_layers)
+                    stride, ctx.upload(na), S, layer0=layer0, n_layers=n_layers, status=status)
     ctx.sync()
     n_layers = len(layers) - layer0 if n_layers is None else n_layers
     for L in layers[layer0:layer0 + n_layers]:
         for s, a in enumerate(accepts):
-            O.tree_commit(L, bt[s], ctxs[s], a)
+            if n_accept is None or n_accept[s] == len(a):
+                O.tree_commit(L, bt[s], ctxs[s], a)
+    return status.download((S,), np.int32)
 
 
 @pytest.mark.parametrize("kv", KV_ALL)
@@ -251,8 +257,9 @@ def test_tree_commit_bit_exact(ctx, kv):
     accepts[1] = [3]              # one node, moved
     accepts[2] = [1, 2, 3, 4, 5, 6, 7]
     accepts[3] = [0, 2, 4, 6]     # crosses a block boundary
-    run_commit(ctx, pool, layers, bt, ctxs, accepts)
+    st = run_commit(ctx, pool, layers, bt, ctxs, accepts)
     assert_pool_equal(pool, layers)
+    assert np.all(st == velokv.COMMIT_OK), st
 
 
 def test_tree_commit_invalid_rows_and_layer_range(ctx):
@@ -261,8 +268,30 @@ def test_tree_commit_invalid_rows_and_layer_range(ctx):
     ctxs = [20, 40, 60, 80, 100]
     pool, layers, bt = commit_case(ctx, kv, ctxs, 8, 3, seed=93)
     accepts = [[0, 3, 3], [2, 1], [0, 40], [], [0, 2, 5]]  # three rejected rows, one empty, one good
-    run_commit(ctx, pool, layers, bt, ctxs, accepts, layer0=1, n_layers=1)
+    st = run_commit(ctx, pool, layers, bt, ctxs, accepts, layer0=1, n_layers=1)
     assert_pool_equal(pool, layers)
+    assert st.tolist() == [velokv.COMMIT_BAD_ROW] * 3 + [velokv.COMMIT_OK] * 2, st
+
+
+def test_tree_commit_status_past_table_bad_page_and_counts(ctx):
+    """Each rejection reason is reported per sequence and leaves the pool
+    untouched: a path past the block-table row, a page id outside the pool, a
+    negative n_accept, an n_accept above 32 and a negative context."""
+    print("tree commit statuses", flush=True)
+    kv = O.I8_BLK
+    ctxs = [20, 40, 60, 80, 100, 30]
+    pool, layers, bt = commit_case(ctx, kv, ctxs, 8, 1, seed=96)
+    bt = bt.copy()
+    ctxs[0] = bt.shape[1] * BS - 3          # accepted node 5 lands past the row
+    bt[1, (40 + 2) // BS] = pool.n_blocks + 5   # the destination page of sequence 1 is outside the pool
+    accepts = [[0, 5], [0, 2], [1], [1], [1], [0, 1, 3]]
+    na = [2, 2, -1, 33, 1, 3]
+    ctxs[4] = -4
+    # the GPU pool's table rows are the caller's; the oracle sees the same rejected rows untouched
+    status = run_commit(ctx, pool, layers, bt, ctxs, accepts, n_accept=na)
+    assert_pool_equal(pool, layers)
+    assert status.tolist() == [velokv.COMMIT_PAST_TABLE, velokv.COMMIT_BAD_PAGE, velokv.COMMIT_BAD_ROW,
+                               velokv.COMMIT_BAD_ROW, velokv.COMMIT_BAD_ROW, velokv.COMMIT_OK], status
 
 
 def test_tree_commit_then_decode_matches_oracle(ctx):

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from cases import BS, HD, make_case, oracle_layer
+from cases import BS, HD, make_case, oracle_layer, ref_codes_closed_form
 from velokv import synth
 
 
@@ -115,6 +115,34 @@ def test_ref_int8_invariants():
         assert np.array_equal(c3, c) and s3 == s * 4
     c, s = _ref_quant_row(np.zeros(HD, np.float32))
     assert s == 0.0 and not c.any()
+
+
+def test_ref_int8_codes_equal_truncating_closed_form():
+    """Over 10^4 random rows the REF quantizer's codes equal the numpy fp32
+    closed form with truncation. The rows are drawn so that many products have
+    fractional parts above 0.5 (where truncation and rounding differ) and so that
+    the fp32 rounding of 127/amax sends some absmax elements to 126."""
+    r = np.random.default_rng(11)
+    n_rows = 10_000
+    x = (r.standard_normal((n_rows, HD)) * r.uniform(0.01, 50, (n_rows, 1))).astype(np.float32)
+    x[: n_rows // 10, 5] *= np.float32(8)  # outlier channel, as in config 3
+    want_c, want_s = ref_codes_closed_form(x)
+    got_c = np.empty((n_rows, HD), np.int8)
+    got_s = np.empty(n_rows, np.float32)
+    for i in range(n_rows):
+        got_c[i], got_s[i] = _ref_quant_row(x[i])
+    assert np.array_equal(got_c, want_c)
+    assert np.array_equal(got_s, want_s)
+    # the rows do separate truncation from round-to-nearest ...
+    prod = (x * (np.float32(127) / np.max(np.abs(x), axis=1, keepdims=True)).astype(np.float32)).astype(np.float32)
+    frac = np.abs(prod) - np.floor(np.abs(prod))
+    assert int((frac > 0.5).sum()) > n_rows * HD // 4
+    assert not np.array_equal(np.rint(prod).astype(np.int8), got_c)
+    # ... and reach both absmax outcomes of the fp32 operation order
+    imax = np.argmax(np.abs(x), axis=1)
+    top = np.abs(got_c[np.arange(n_rows), imax].astype(int))
+    assert (top == 126).any() and (top == 127).any()
+    assert set(np.unique(top)) <= {126, 127}
 
 
 def test_ref_layout_build_layout_agree_for_ref_int8():

@@ -95,6 +95,10 @@ struct vk_ctx {
   std::mutex ws_mu;
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
+  // Buffers the context's workspace outgrew: a call on another host thread may
+  // still have kernels queued that use one, so they are freed only by
+  // vk_ctx_destroy (growth is rare: once per new largest shape).
+  std::vector<void*> ws_retired;
   int decode_kind = VK_DECODE_AUTO;
   int decode_sched = VK_SCHED_AUTO;
   int n_cu = 256;
@@ -262,9 +266,10 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
 extern "C" int vk_ctx_destroy(vk_ctx* ctx) {
   if (!ctx) return VK_OK;
   hipSetDevice(ctx->device);
-  if (ctx->ws) {
+  if (ctx->ws || !ctx->ws_retired.empty()) {
     hipDeviceSynchronize();
-    hipFree(ctx->ws);
+    if (ctx->ws) hipFree(ctx->ws);
+    for (void* p : ctx->ws_retired) hipFree(p);
   }
   if (ctx->module) hipModuleUnload(ctx->module);
   delete ctx;
@@ -545,13 +550,11 @@ int split_workspace(vk_ctx* ctx, void* given, uint64_t given_bytes, uint64_t nee
   }
   std::lock_guard<std::mutex> lk(ctx->ws_mu);
   if (ctx->ws_bytes < need) {
-    if (ctx->ws) {
-      HIP_TRY(hipDeviceSynchronize());
-      HIP_TRY(hipFree(ctx->ws));
-      ctx->ws = nullptr;
-      ctx->ws_bytes = 0;
-    }
-    HIP_TRY(hipMalloc(&ctx->ws, need));
+    // never freed here: work queued by another thread may still use the old one
+    void* grown = nullptr;
+    HIP_TRY(hipMalloc(&grown, need));
+    if (ctx->ws) ctx->ws_retired.push_back(ctx->ws);
+    ctx->ws = grown;
     ctx->ws_bytes = need;
   }
   *out = reinterpret_cast<uint8_t*>(ctx->ws);
@@ -1012,7 +1015,7 @@ extern "C" int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* pairs, 
 extern "C" int vk_tree_commit(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers,
                               const int32_t* block_tables, int32_t bt_stride, const int32_t* context_lens,
                               const int32_t* accept, int32_t accept_stride, const int32_t* n_accept, int32_t n_seqs,
-                              void* stream) {
+                              int32_t* status, void* stream) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
   const vk_pool_desc& d = pool->desc;
@@ -1029,6 +1032,7 @@ extern "C" int vk_tree_commit(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_
   p.context_lens = context_lens;
   p.accept = accept;
   p.n_accept = n_accept;
+  p.status = status;
   p.bt_stride = bt_stride;
   p.accept_stride = accept_stride;
   p.n_seqs = n_seqs;

@@ -2349,23 +2349,33 @@ DEV void tree_commit(const CommitParams& P) {
   const int l1 = min(l0 + kCommitLayers, P.layer0 + P.n_layers);
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x / WAVE);  // 0: K, 1: V (wave-uniform)
   const int lane = lane_id();
+  // the status of the row is reported once, by wave 0 of (s, KV head 0, layer group 0)
+  const bool reporter = P.status && h == 0 && blockIdx.z == 0 && w == 0 && lane == 0;
+  auto report = [&](int st) {
+    if (reporter) P.status[s] = st;
+  };
   const int ctx = P.context_lens[s];
   const int na = P.n_accept[s];
-  if (ctx < 0 || na <= 0 || na > min(P.accept_stride, kMaxCommit)) return;
+  if (ctx < 0 || na < 0 || na > min(P.accept_stride, kMaxCommit)) { report(COMMIT_BAD_ROW); return; }
+  if (na == 0) { report(COMMIT_OK); return; }
   const int32_t* acc = P.accept + (int64_t)s * P.accept_stride;
   const int a = lane < na ? acc[lane] : 0;
   const int prev = __shfl_up(a, 1, WAVE);
   const bool bad = lane < na && (a < lane || a >= kMaxCommit || (lane > 0 && a <= prev));
-  if (__builtin_amdgcn_ballot_w64(bad) != 0) return;
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) { report(COMMIT_BAD_ROW); return; }
   const uint64_t moved = __builtin_amdgcn_ballot_w64(lane < na && a != lane);
-  if (moved == 0) return;  // every accepted node is already in place
+  if (moved == 0) { report(COMMIT_OK); return; }  // every accepted node is already in place
   const int d0 = __builtin_ctzll(moved);
   const int last = ctx + readlane_i(a, na - 1);
-  if ((int64_t)last >= (int64_t)P.bt_stride * BS) return;
+  if ((int64_t)last >= (int64_t)P.bt_stride * BS) { report(COMMIT_PAST_TABLE); return; }
   const int32_t* bt = P.block_tables + (int64_t)s * P.bt_stride;
   const int b_first = (ctx + d0) / BS, nb = last / BS - b_first + 1;  // at most 3 blocks
   const int blk_l = lane < nb ? bt[b_first + lane] : 0;
-  if (__builtin_amdgcn_ballot_w64(lane < nb && (blk_l < 0 || blk_l >= P.g.n_blocks)) != 0) return;
+  if (__builtin_amdgcn_ballot_w64(lane < nb && (blk_l < 0 || blk_l >= P.g.n_blocks)) != 0) {
+    report(COMMIT_BAD_PAGE);
+    return;
+  }
+  report(COMMIT_OK);
   if (w == 0) commit_wave<KV, false>(P, raw[0], xsc[0], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
   else commit_wave<KV, true>(P, raw[1], xsc[1], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
 }

@@ -143,8 +143,12 @@ struct CommitParams {
   const int32_t* context_lens;
   const int32_t* accept;
   const int32_t* n_accept;
+  int32_t* status;          // [n_seqs] commit status per sequence, or null
   int32_t bt_stride, accept_stride, n_seqs, layer0, n_layers;
 };
+
+// Per-sequence status of a tree commit (include/velokv.h VK_COMMIT_*).
+enum CommitStatus : int32_t { COMMIT_OK = 0, COMMIT_BAD_ROW = 1, COMMIT_PAST_TABLE = 2, COMMIT_BAD_PAGE = 3 };
 
 struct MergeParams {
   const float* part_acc;

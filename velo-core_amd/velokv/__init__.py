@@ -13,7 +13,7 @@ from ._capi import (  # noqa: F401
     ERR_BAD_ARG, ERR_INVALID_BLOCK_SIZE, ERR_OUT_OF_PAGES, ERR_TOO_MANY_PAGES, ERR_NO_FREE_SLOTS,
     ERR_NOT_WIRED, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_UNKNOWN_HANDLE,
     NIXL_HEADER_BYTES, NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH,
-    NIXL_BAD_PAGE, ROPE_HALF, ROPE_INTERLEAVED,
+    NIXL_BAD_PAGE, ROPE_HALF, ROPE_INTERLEAVED, COMMIT_OK, COMMIT_BAD_ROW, COMMIT_PAST_TABLE, COMMIT_BAD_PAGE,
 )
 from .runtime import (  # noqa: F401
     BlockManager, CacheLookup, CachedSequence, Context, DeviceBuffer, Event, HipMemoryRuntime, KvCacheType,

@@ -41,6 +41,8 @@ DT_F32, DT_F16 = 0, 1
 NIXL_HEADER_BYTES = 16
 ROPE_INTERLEAVED, ROPE_HALF = 1, 2
 NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH, NIXL_BAD_PAGE = range(6)
+# per-sequence status of vk_tree_commit
+COMMIT_OK, COMMIT_BAD_ROW, COMMIT_PAST_TABLE, COMMIT_BAD_PAGE = range(4)
 
 
 class VkError(RuntimeError):
@@ -119,7 +121,7 @@ PROTOTYPES = {
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
     "vk_tree_mask": [PI32, I32, PU32],
     "vk_copy_blocks": [P, P, PI32, I32, P],
-    "vk_tree_commit": [P, P, I32, I32, P, I32, P, P, I32, P, I32, P],
+    "vk_tree_commit": [P, P, I32, I32, P, I32, P, P, I32, P, I32, P, P],
     "vk_nixl_payload_bytes": [P, I32, U32, C.POINTER(U64)],
     "vk_nixl_pack": [P, P, I32, I32, C.POINTER(NixlItem), I32, P, I32, P, U64, P, P],
     "vk_nixl_unpack": [P, P, I32, I32, C.POINTER(NixlItem), I32, P, I32, P, U64, P, P],

@@ -171,12 +171,13 @@ class Context:
                                    _sptr(stream)))
 
     def tree_commit(self, pool: "Pool", block_tables, bt_stride: int, context_lens, accept, accept_stride: int,
-                    n_accept, n_seqs: int, layer0: int = 0, n_layers: int | None = None, stream=None):
-        """vk_tree_commit: move the accepted path's K/V to context_len + d (device arrays)."""
+                    n_accept, n_seqs: int, layer0: int = 0, n_layers: int | None = None, status=None, stream=None):
+        """vk_tree_commit: move the accepted path's K/V to context_len + d (device arrays); status
+        (optional device int32 [n_seqs]) receives COMMIT_* per sequence."""
         n_layers = pool.n_layer - layer0 if n_layers is None else n_layers
         check(lib().vk_tree_commit(self.h, pool.h, layer0, n_layers, _bptr(block_tables), bt_stride,
                                    _bptr(context_lens), _bptr(accept), accept_stride, _bptr(n_accept), n_seqs,
-                                   _sptr(stream)))
+                                   _bptr(status), _sptr(stream)))
 
     @staticmethod
     def _nixl_items(items):
