@@ -90,6 +90,9 @@ def parse():
                     help="tree: do not pass the radix cache's shared prefix to vk_tree_verify (shared_blocks = 0)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one vk_copy_blocks of known size (HBM counter calibration)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="decode workload: skip the configurations reported beside the headline in detail "
+                         "(configs 2 and 3 with ragged contexts, and the headline with fp32 queries)")
     return ap.parse_args()
 
 
@@ -252,6 +255,9 @@ def run_gpu(ctx, args, kv_name: str):
                      "launch_ms_mean": round(dec_mean_ms, 5), "launch_ms_min": round(float(np.min(dec_ms)), 5),
                      "launches": len(dec_ms)},
         "pool_gb": round(pool.nbytes / 1e9, 2),
+        "workload": "S=%d, L=%s, H=%d/Hkv=%d, %s KV, q %s" % (S, "U[1024,%d]" % L if args.ragged else str(L), H, Hkv,
+                                                               kv_name, args.q_dtype),
+        "sum_context_len": int(lens.sum()),
     }
     if args.calibrate:
         # plain copy of known size: n_pairs blocks x all layers x (K + V codes and scales)
@@ -663,6 +669,18 @@ def main():
     also = None
     if args.also != "none" and args.also != args.kv:
         also = run_gpu(ctx, args, args.also)
+    configs = {}
+    if not args.no_configs and not args.ragged and args.kv == "int8" and args.q_dtype == "fp16":
+        # BASELINE configs 2 (fp16) and 3 (INT8 with outliers): the same shapes with
+        # L ~ U[1024, ctx]; and the headline with the reference kernels' fp32 q
+        import copy
+        rag = copy.copy(args)
+        rag.ragged, rag.steps, rag.warmup = True, min(args.steps, 10), min(args.warmup, 2)
+        configs["config2_fp16_ragged"] = run_gpu(ctx, rag, "fp16")
+        configs["config3_int8_ragged"] = run_gpu(ctx, rag, "int8")
+        f32 = copy.copy(args)
+        f32.q_dtype, f32.steps, f32.warmup = "fp32", min(args.steps, 10), min(args.warmup, 2)
+        configs["headline_int8_fp32q"] = run_gpu(ctx, f32, "int8")
     cpu = None if args.no_cpu else cpu_baseline(args)
     workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=128, bs=16, %s KV, %d layers, %sappend+decode per layer, pool %d blocks" %
                 (args.seqs, "U[1024,%d]" % args.ctx if args.ragged else str(args.ctx), args.heads, args.kv_heads,
@@ -678,7 +696,7 @@ def main():
         "tokens_per_s": head["tokens_per_s"], "frac_of_peak": head["frac_of_peak"],
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
-        "detail": {args.kv: head, **({args.also: also} if also else {})},
+        "detail": {args.kv: head, **({args.also: also} if also else {}), **configs},
     }
     print(json.dumps(line))
 

@@ -97,6 +97,21 @@ int vk_ctx_destroy(vk_ctx* ctx);
 /* Name of the GPU architecture the context runs on (e.g. "gfx950"). */
 int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
 
+/* Misuse the kernels detect without trapping. The work still completes on the
+ * clamped input, a flag is or-ed into the context's device error word, and the
+ * next vk_stream_sync or vk_ctx_check returns VK_ERR_BAD_ARG naming it (and
+ * clears the word). The reference rejects the host-visible cases of the same
+ * kind before dispatch (metal/runtime.rs:296-302); these inputs live in device
+ * memory. Calls overlapping on several streams share the word; a flag is
+ * reported by whichever check reads it first. */
+#define VK_MISUSE_PAGE_OUT_OF_POOL 1u  /* an attention call read a block-table page id
+                                          outside [0, n_blocks) (clamped into the pool) */
+#define VK_MISUSE_BLK_SPLIT_RUN    2u  /* an I8_BLK append had tokens of one block that
+                                          were not adjacent in the call               */
+/* Waits for all work of the context's device, then reports and clears the misuse
+ * flags (*flags = the flags read; NULL to skip): VK_OK when none were set. */
+int vk_ctx_check(vk_ctx* ctx, uint32_t* flags);
+
 /* Kernel family of vk_paged_decode over fp16/int8 KV: VK_DECODE_MFMA (QK and
  * PV on v_mfma_f32_16x16x{32,16}_f16; an fp32 q is split into fp16 hi + lo
  * parts), VK_DECODE_VALU (v_dot2_f32_f16, or fp32 arithmetic for an fp32 q, on
@@ -117,9 +132,9 @@ int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
  * workgroup per pair instead, its waves splitting the context and combining in
  * LDS, with no merge launch and no workspace), VK_SCHED_STREAM (stream-K on the matrix cores: one
  * wave per resident slot, each taking an equal share of all (sequence, KV head)
- * blocks, so ragged batches stay balanced) or VK_SCHED_AUTO (stream-K unless
- * vk_decode_args.sum_context_len says the batch is uniform, or the VALU family
- * was requested). A nonzero partition_tokens always uses fixed partitions. No
+ * blocks, so ragged batches stay balanced; the split segments are combined by a
+ * merge launch) or VK_SCHED_AUTO (stream-K unless vk_decode_args.sum_context_len
+ * says the batch is uniform, or the VALU family was requested). A nonzero partition_tokens always uses fixed partitions. No
  * reference counterpart. */
 #define VK_SCHED_AUTO 0
 #define VK_SCHED_SPLIT 1
@@ -193,7 +208,8 @@ int vk_slot_mapping(vk_ctx* ctx, vk_pool* pool, const int32_t* block_tables,
  * token at block offset 0 starts a fresh block scale; a later token whose absmax
  * needs a larger scale re-quantizes the codes already in the block. Tokens of
  * one call that fall in the same block must be adjacent in the call (padding
- * slots may sit between them) and in increasing offset order. */
+ * slots may sit between them) and in increasing offset order; a call that
+ * breaks adjacency is reported as VK_MISUSE_BLK_SPLIT_RUN. */
 int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* k,
               const void* v, int32_t in_dtype, const int64_t* slot_mapping,
               int32_t n_tok, void* stream);
@@ -263,6 +279,22 @@ int vk_paged_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint
  * (for profiling and reports). No reference counterpart. */
 int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args* a, char* buf, size_t cap);
 
+/* The schedule vk_paged_decode would run for these arguments (for tests,
+ * profiling and reports). No reference counterpart. */
+#define VK_SCHED_WORKGROUP 3   /* schedule value reported for the workgroup split */
+typedef struct vk_decode_plan {
+  char kernel[64];             /* attention kernel name                                */
+  int32_t schedule;            /* VK_SCHED_SPLIT, _STREAM or _WORKGROUP                */
+  int32_t wg_waves;            /* workgroup split: waves per (sequence, KV head)       */
+  int32_t partition_tokens;    /* fixed partitions: tokens per partition               */
+  int32_t max_partitions;      /* fixed partitions: partitions of the longest context  */
+  int32_t n_workers;           /* stream-K: workers (one wave each)                    */
+  int32_t max_blocks_per_wave; /* the most blocks one wave can walk (<= 256)           */
+  uint64_t workspace_bytes;    /* split-K scratch the call needs                       */
+  int32_t merge_launch;        /* 1 when a merge launch follows the attention kernel   */
+} vk_decode_plan;
+int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a, vk_decode_plan* out);
+
 /* Single-query paged decode attention for S sequences, with split-K over
  * context partitions and an online-softmax merge (a second launch, skipped
  * when every sequence fits one partition).
@@ -270,6 +302,7 @@ int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args* a, char* b
  * (kernels.metal:672-732); GQA map kv_head = h / (H / Hkv) (kernels.metal:456);
  * math of llama_cpu.rs:251-284. */
 int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream);
+
 
 typedef struct vk_tree_args {
   int32_t layer;
@@ -503,6 +536,7 @@ int vk_memcpy_d2h(vk_ctx* ctx, void* dst, const void* src, uint64_t bytes);
 int vk_memset_d(vk_ctx* ctx, void* dst, int value, uint64_t bytes);
 int vk_stream_create(vk_ctx* ctx, void** out);
 int vk_stream_destroy(vk_ctx* ctx, void* stream);
+/* Waits for the stream, then reports misuse flags as vk_ctx_check does. */
 int vk_stream_sync(vk_ctx* ctx, void* stream);
 int vk_event_create(vk_ctx* ctx, void** out);
 int vk_event_destroy(vk_ctx* ctx, void* ev);

@@ -16,7 +16,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "build", "libvelokv_oracle.so")
+# VELOKV_SANITIZE=1 selects the AddressSanitizer + UBSan build (make asan)
+LIB_PATH = os.path.join(HERE, "build", "libvelokv_oracle_asan.so" if os.environ.get("VELOKV_SANITIZE") == "1"
+                        else "libvelokv_oracle.so")
 
 F32, F16, I8_REF, I8_BLK = 0, 1, 2, 3
 ESZ = {F32: 4, F16: 2, I8_REF: 1, I8_BLK: 1}

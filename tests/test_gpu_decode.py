@@ -84,7 +84,8 @@ def test_decode_gqa_groups_ragged(ctx, impl, kv, G):
 @pytest.mark.parametrize("P", [16, 256, 1024, 2048, 4096, 0])
 def test_decode_split_k_partitions(ctx, impl, kv, P):
     print(f"decode split impl={impl} kv={kv} P={P}", flush=True)
-    lens = [3000, 1024, 2049, 777]
+    # 4095 / 4096 / 4097: a 256-block unit at P = 4096 (the last block-id window) and its edges
+    lens = [3000, 1024, 2049, 777, 4095, 4096, 4097]
     case = make_case(kv, lens, seed=210, outlier_scale=8.0)
     ref_layer = oracle_layer(case)
     pool = gpu_pool(ctx, case)

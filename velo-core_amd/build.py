@@ -43,10 +43,14 @@ def build_code_object():
     return out
 
 
-def build_host_library():
-    out = os.path.join(PKG, "libvelokv.so")
+def build_host_library(sanitize: bool = False):
+    """libvelokv.so (or, with sanitize, libvelokv_asan.so: the host C++ under
+    AddressSanitizer + UndefinedBehaviorSanitizer, for the CPU test suite)."""
+    out = os.path.join(PKG, "libvelokv_asan.so" if sanitize else "libvelokv.so")
     tmp = out + ".tmp"
-    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-Wno-unused-parameter",
+    san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-g"] if sanitize else []
+    _run(["g++", "-O1" if sanitize else "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+          "-Wno-unused-parameter", *san,
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{INCLUDE}", f"-I{CSRC}",
           os.path.join(CSRC, "velokv_host.cpp"), os.path.join(CSRC, "velokv_radix.cpp"), "-o", tmp,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
@@ -60,6 +64,33 @@ def build():
     return co, so
 
 
+def sanitizer_runtime():
+    """LD_PRELOAD value for a Python process that loads the sanitized libraries
+    (the interpreter itself is not instrumented, so the runtimes come first)."""
+    libs = []
+    for name in ("libasan.so", "libubsan.so"):
+        p = subprocess.run(["g++", f"-print-file-name={name}"], stdout=subprocess.PIPE, text=True).stdout.strip()
+        libs.append(os.path.realpath(p))
+    return ":".join(libs)
+
+
+def build_sanitized(run_tests: bool = False) -> int:
+    """Host library and oracle under AddressSanitizer + UndefinedBehaviorSanitizer
+    (host code only; the GPU code object is not involved), then optionally the
+    CPU test suite (pytest -m "not gpu") loading them."""
+    build_host_library(sanitize=True)
+    _run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle"), "asan"])
+    if not run_tests:
+        return 0
+    env = dict(os.environ, VELOKV_SANITIZE="1", LD_PRELOAD=sanitizer_runtime(),
+               ASAN_OPTIONS="detect_leaks=0:abort_on_error=1:halt_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    return subprocess.run([sys.executable, "-m", "pytest", os.path.join(ROOT, "tests"), "-q", "-m", "not gpu",
+                           "-p", "no:cacheprovider"], env=env, cwd=ROOT).returncode
+
+
 if __name__ == "__main__":
+    if "--sanitize" in sys.argv:
+        sys.exit(build_sanitized(run_tests="--run-tests" in sys.argv))
     for p in build():
         print(p)

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -99,6 +100,7 @@ struct vk_ctx {
   // still have kernels queued that use one, so they are freed only by
   // vk_ctx_destroy (growth is rare: once per new largest shape).
   std::vector<void*> ws_retired;
+  uint32_t* err_word = nullptr;  // device: misuse flags (VK_MISUSE_*) or-ed by the kernels
   int decode_kind = VK_DECODE_AUTO;
   int decode_sched = VK_SCHED_AUTO;
   int n_cu = 256;
@@ -119,6 +121,15 @@ struct vk_pool {
   uint64_t bytes = 0;
   int32_t* table = nullptr;  // [max_slots][max_pages_per_slot]
   uint64_t table_bytes = 0;
+  // I8_BLK: per block, (epoch << 32 | first token) of the last append run on it,
+  // so that a call with two runs on one block is reported (VK_MISUSE_BLK_SPLIT_RUN)
+  unsigned long long* claim = nullptr;
+  std::atomic<uint32_t> epoch{0};
+  uint32_t next_epoch() {
+    uint32_t e = ++epoch;
+    while (e == 0) e = ++epoch;  // 0 marks a never-claimed block
+    return e;
+  }
 };
 
 namespace {
@@ -144,6 +155,7 @@ std::string decode_wg_name(int kv, int g, int qt = VK_DT_F16) {
 std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16) {
   return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
+
 std::string tree_pfx_name(int kv, int g, int qt) {
   return "vk_tree_pfx_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
 }
@@ -259,6 +271,14 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
     }
     ctx->fns[nm] = f;
   }
+  e = hipMalloc(reinterpret_cast<void**>(&ctx->err_word), 256);
+  if (e == hipSuccess) e = hipMemset(ctx->err_word, 0, 256);
+  if (e != hipSuccess) {
+    if (ctx->err_word) hipFree(ctx->err_word);
+    hipModuleUnload(ctx->module);
+    delete ctx;
+    return fail(VK_ERR_HIP, "error word allocation failed: %s", hipGetErrorString(e));
+  }
   *out = ctx;
   return VK_OK;
 }
@@ -266,11 +286,10 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
 extern "C" int vk_ctx_destroy(vk_ctx* ctx) {
   if (!ctx) return VK_OK;
   hipSetDevice(ctx->device);
-  if (ctx->ws || !ctx->ws_retired.empty()) {
-    hipDeviceSynchronize();
-    if (ctx->ws) hipFree(ctx->ws);
-    for (void* p : ctx->ws_retired) hipFree(p);
-  }
+  hipDeviceSynchronize();
+  if (ctx->ws) hipFree(ctx->ws);
+  for (void* p : ctx->ws_retired) hipFree(p);
+  if (ctx->err_word) hipFree(ctx->err_word);
   if (ctx->module) hipModuleUnload(ctx->module);
   delete ctx;
   return VK_OK;
@@ -348,10 +367,15 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
     e = hipMalloc(reinterpret_cast<void**>(&p->table), p->table_bytes);
     if (e == hipSuccess) e = hipMemset(p->table, 0, p->table_bytes);
   }
+  if (e == hipSuccess && d->kv_type == VK_KV_I8_BLK) {
+    e = hipMalloc(reinterpret_cast<void**>(&p->claim), (uint64_t)d->n_blocks * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemset(p->claim, 0, (uint64_t)d->n_blocks * sizeof(unsigned long long));
+  }
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     hipFree(p->base);
     if (p->table) hipFree(p->table);
+    if (p->claim) hipFree(p->claim);
     delete p;
     return fail(VK_ERR_HIP, "pool initialisation failed: %s", hipGetErrorString(e));
   }
@@ -365,6 +389,7 @@ extern "C" int vk_pool_destroy(vk_pool* pool) {
   hipDeviceSynchronize();
   hipFree(pool->base);
   if (pool->table) hipFree(pool->table);
+  if (pool->claim) hipFree(pool->claim);
   delete pool;
   return VK_OK;
 }
@@ -475,6 +500,9 @@ extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* 
   p.slot_mapping = slot_mapping;
   p.n_tok = n_tok;
   p.tok_per_wg = append_tok_per_wg(n_tok, pool->desc.n_kv_heads);
+  p.err = ctx->err_word;
+  p.claim = pool->claim;
+  p.epoch = pool->claim ? pool->next_epoch() : 0u;
   const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
   if ((rc = set_device(ctx))) return rc;
   return launch(ctx, name.c_str(), dim3((unsigned)((n_tok + p.tok_per_wg - 1) / p.tok_per_wg),
@@ -530,6 +558,9 @@ extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q
   p.q_dtype = q_dtype;
   const unsigned rows = (unsigned)pool->desc.n_kv_heads + (q ? (unsigned)((n_heads + 1) / 2) : 0u);
   p.tok_per_wg = append_tok_per_wg(n_tok, (int32_t)rows);
+  p.err = ctx->err_word;
+  p.claim = pool->claim;
+  p.epoch = pool->claim ? pool->next_epoch() : 0u;
   const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
   if ((rc = set_device(ctx))) return rc;
   return launch(ctx, name.c_str(), dim3((unsigned)((n_tok + p.tok_per_wg - 1) / p.tok_per_wg), rows), dim3(128), p,
@@ -708,6 +739,36 @@ extern "C" int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args*
   return VK_OK;
 }
 
+extern "C" int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a, vk_decode_plan* out) {
+  if (!pool || !a || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  DecodePlan pl;
+  int rc = plan_decode(pool->ctx, pool, a, &pl);
+  if (rc) return rc;
+  const vk_pool_desc& d = pool->desc;
+  memset(out, 0, sizeof *out);
+  snprintf(out->kernel, sizeof out->kernel, "%s", pl.kernel.c_str());
+  const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
+  out->workspace_bytes = pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes;
+  if (pl.stream_k) {
+    const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads * (nb + kSkPenalty);
+    out->schedule = VK_SCHED_STREAM;
+    out->n_workers = pl.n_workers;
+    out->max_blocks_per_wave = (int32_t)std::min<int64_t>(nb, (units_max + pl.n_workers - 1) / pl.n_workers);
+    out->merge_launch = 1;
+  } else if (pl.wg_waves) {
+    out->schedule = VK_SCHED_WORKGROUP;
+    out->wg_waves = pl.wg_waves;
+    out->max_blocks_per_wave = (int32_t)((nb + pl.wg_waves - 1) / pl.wg_waves);
+  } else {
+    out->schedule = VK_SCHED_SPLIT;
+    out->partition_tokens = pl.part_tokens;
+    out->max_partitions = pl.max_parts;
+    out->max_blocks_per_wave = (int32_t)std::min<int64_t>(nb, pl.part_tokens / d.block_size);
+    out->merge_launch = pl.max_parts > 1 ? 1 : 0;
+  }
+  return VK_OK;
+}
+
 extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
@@ -758,6 +819,7 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.n_workers = pl.n_workers;
   p.sk_penalty = pl.stream_k ? kSkPenalty : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
+  p.err = ctx->err_word;
 
   MergeParams m{};
   m.part_acc = p.part_acc;
@@ -942,6 +1004,7 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   p.scale_log2 = scale * 1.4426950408889634f;
   p.prefix_blocks = pl.prefix_blocks;
   p.prefix_chunks = pl.prefix_chunks;
+  p.err = ctx->err_word;
   const uint64_t units = (uint64_t)a->n_seqs * (pl.max_parts - pl.prefix_chunks) * d.n_kv_heads * pl.n_rgroups;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
   if (pl.prefix_chunks > 0 &&
@@ -1371,12 +1434,40 @@ extern "C" int vk_stream_destroy(vk_ctx* ctx, void* stream) {
   HIP_TRY(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)));
   return VK_OK;
 }
+namespace {
+// Reads and clears the context's misuse word; VK_ERR_BAD_ARG naming the misuse
+// when a kernel set a flag since the last read.
+int take_misuse(vk_ctx* ctx, uint32_t* flags_out) {
+  uint32_t flags = 0;
+  HIP_TRY(hipMemcpy(&flags, ctx->err_word, sizeof flags, hipMemcpyDeviceToHost));
+  if (flags_out) *flags_out = flags;
+  if (flags == 0) return VK_OK;
+  const uint32_t zero = 0;
+  HIP_TRY(hipMemcpy(ctx->err_word, &zero, sizeof zero, hipMemcpyHostToDevice));
+  std::string what;
+  if (flags & VK_MISUSE_PAGE_OUT_OF_POOL)
+    what += "a block table handed to an attention call held a page id outside the pool (clamped into the pool); ";
+  if (flags & VK_MISUSE_BLK_SPLIT_RUN)
+    what += "an INT8 per-block append had tokens of one block that were not adjacent in the call "
+            "(its codes are not defined); ";
+  return fail(VK_ERR_BAD_ARG, "misuse reported by the kernels (flags 0x%x): %s", flags, what.c_str());
+}
+}  // namespace
+
 extern "C" int vk_stream_sync(vk_ctx* ctx, void* stream) {
   if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
   int rc = set_device(ctx);
   if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
-  return VK_OK;
+  return take_misuse(ctx, nullptr);
+}
+
+extern "C" int vk_ctx_check(vk_ctx* ctx, uint32_t* flags) {
+  if (!ctx) return fail(VK_ERR_BAD_ARG, "null context");
+  int rc = set_device(ctx);
+  if (rc) return rc;
+  HIP_TRY(hipDeviceSynchronize());
+  return take_misuse(ctx, flags);
 }
 extern "C" int vk_event_create(vk_ctx* ctx, void** out) {
   if (!ctx || !out) return fail(VK_ERR_BAD_ARG, "null argument");

@@ -166,6 +166,12 @@ DEV void write_zero_rows(const DecodeParams& P, int s, int kvh) {
   for (int g = 0; g < G; ++g) reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (HD / 2) + lane_id()] = make_float2(0.f, 0.f);
 }
 
+// Misuse is reported, not trapped: the kernel or-s a flag into the context's
+// error word (a vector atomic) and carries on with the clamped input.
+DEV void flag_misuse(uint32_t* err, uint32_t bit) {
+  if (err) __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 constexpr float kRescaleThreshold = 4.0f;  // log2 units
 // Block ids (and per-(block, head) scales) of a unit, held one per lane in up to
 // kWin windows of 64 blocks: partitions of up to 256 blocks (4096 tokens).
@@ -175,9 +181,12 @@ struct BlockIds {
   float ks[kWin];
   float vs[kWin];
 };
+// A page id outside [0, n_blocks) is clamped into the pool (the read stays in
+// bounds) and reported as MISUSE_PAGE_OUT_OF_POOL.
 template <bool BLK>
 DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, int blk0, int nblk, int kvh) {
   const int lane = lane_id();
+  bool bad = false;
 #pragma unroll
   for (int k = 0; k < kWin; ++k) {
     w.b[k] = 0;
@@ -185,13 +194,16 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
     w.vs[k] = 1.f;
     const int idx = 64 * k + lane;
     if (idx < nblk) {
-      w.b[k] = min(max(bt[blk0 + idx], 0), P.n_blocks - 1);
+      const int raw = bt[blk0 + idx];
+      bad |= raw < 0 || raw >= P.n_blocks;
+      w.b[k] = min(max(raw, 0), P.n_blocks - 1);
       if constexpr (BLK) {
         w.ks[k] = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
         w.vs[k] = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
       }
     }
   }
+  if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) flag_misuse(P.err, MISUSE_PAGE_OUT_OF_POOL);
 }
 // Value of block i (wave-uniform) from a per-lane window array: each window is
 // read at lane i % 64 and the window i / 64 is selected among the (scalar)
@@ -1400,7 +1412,9 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     for (int u = 0; u < kPfxCH; ++u) {
       int b = cb0 + st * kPfxCH + u;
       b = (st < nst && b < cb1) ? b : cb0;
-      blk[u] = min(max(bt[b], 0), P.n_blocks - 1);
+      const int raw = bt[b];
+      if ((raw < 0 || raw >= P.n_blocks) && tid == 0) flag_misuse(P.err, MISUSE_PAGE_OUT_OF_POOL);
+      blk[u] = min(max(raw, 0), P.n_blocks - 1);
       const uint64_t tix = (uint64_t)blk[u] * P.n_kv_heads + kvh;
       const uint8_t* kt_ = P.kc + tix * P.tile_bytes;
       const uint8_t* vt_ = P.vc + tix * P.tile_bytes;
@@ -1978,7 +1992,16 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
     starts &= starts - 1;
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ms, j);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)ms >> 32), j);
-    append_blk_run<IS_V>(P, src, codes, scales, w0, j, (int64_t)(((uint64_t)hi << 32) | lo), ms64, h);
+    const int64_t slot = (int64_t)(((uint64_t)hi << 32) | lo);
+    if (!IS_V && h == 0 && lane == 0 && P.claim) {
+      // one run per block and call: a second run of this call on the same block
+      // (its tokens not adjacent in the call) would requantize it concurrently
+      const unsigned long long me = ((unsigned long long)P.epoch << 32) | (uint32_t)(w0 + j);
+      const unsigned long long old =
+          __hip_atomic_exchange(&P.claim[slot / BS], me, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((uint32_t)(old >> 32) == P.epoch && old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
+    }
+    append_blk_run<IS_V>(P, src, codes, scales, w0, j, slot, ms64, h);
   }
 }
 

@@ -27,6 +27,10 @@ struct PoolGeom {
 
 enum RopeStyle : int32_t { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
 
+// Misuse flags or-ed into a context's device error word (include/velokv.h
+// VK_MISUSE_*); the kernels still run to completion on the clamped input.
+enum Misuse : uint32_t { MISUSE_PAGE_OUT_OF_POOL = 1u, MISUSE_BLK_SPLIT_RUN = 2u };
+
 // Append of n_tok tokens; grid (ceil(n_tok / tok_per_wg), Hkv + ceil(n_heads / 2)):
 // workgroup x covers tokens [x T, x T + T) of the call, T = tok_per_wg; rows
 // y < Hkv write K (wave 0) and V (wave 1) of KV head y; with RoPE, rows y >= Hkv
@@ -48,6 +52,9 @@ struct AppendParams {
   void* q;                  // [n_tok][n_heads][D] of q_dtype
   int32_t q_dtype;
   int32_t tok_per_wg;       // tokens per workgroup (1..64)
+  uint32_t* err;            // the context's misuse word
+  unsigned long long* claim;// I8_BLK: [n_blocks] (epoch << 32 | first token) of the last run per block
+  uint32_t epoch;           // I8_BLK: this call's epoch (never 0)
 };
 
 struct SlotMapParams {
@@ -93,6 +100,7 @@ struct DecodeParams {
   // table row are the same pages; partial slots 0..prefix_chunks-1 of a row hold
   // the prefix pass, the partitions of the rest of the context follow
   int32_t prefix_blocks, prefix_chunks;
+  uint32_t* err;            // the context's misuse word (page ids outside the pool)
 };
 
 constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)

@@ -10,7 +10,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libvelokv.so")
+# VELOKV_SANITIZE=1 selects the host library built under AddressSanitizer + UBSan
+# (velo-core_amd/build.py --sanitize; CPU tests only)
+LIB_PATH = os.path.join(HERE, "libvelokv_asan.so" if os.environ.get("VELOKV_SANITIZE") == "1" else "libvelokv.so")
 CODE_OBJECT_PATH = os.path.join(HERE, "velokv_gfx950.co")
 
 # status codes (velokv.h)
@@ -37,10 +39,13 @@ STATUS_NAMES = {
 KV_F32, KV_F16, KV_I8_REF, KV_I8_BLK = 0, 1, 2, 3
 DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
 SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM = 0, 1, 2
+SCHED_WORKGROUP = 3  # reported by vk_paged_decode_plan for the workgroup split
 DT_F32, DT_F16 = 0, 1
 NIXL_HEADER_BYTES = 16
 ROPE_INTERLEAVED, ROPE_HALF = 1, 2
 NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH, NIXL_BAD_PAGE = range(6)
+# misuse flags reported by vk_stream_sync / vk_ctx_check
+MISUSE_PAGE_OUT_OF_POOL, MISUSE_BLK_SPLIT_RUN = 1, 2
 # per-sequence status of vk_tree_commit
 COMMIT_OK, COMMIT_BAD_ROW, COMMIT_PAST_TABLE, COMMIT_BAD_PAGE = range(4)
 
@@ -71,6 +76,12 @@ class DecodeArgs(C.Structure):
                 ("context_lens", C.c_void_p), ("n_seqs", C.c_int32), ("n_heads", C.c_int32),
                 ("max_context_len", C.c_int32), ("scale", C.c_float), ("partition_tokens", C.c_int32),
                 ("workspace", C.c_void_p), ("workspace_bytes", C.c_uint64), ("sum_context_len", C.c_int64)]
+
+
+class DecodePlan(C.Structure):
+    _fields_ = [("kernel", C.c_char * 64), ("schedule", C.c_int32), ("wg_waves", C.c_int32),
+                ("partition_tokens", C.c_int32), ("max_partitions", C.c_int32), ("n_workers", C.c_int32),
+                ("max_blocks_per_wave", C.c_int32), ("workspace_bytes", C.c_uint64), ("merge_launch", C.c_int32)]
 
 
 class TreeArgs(C.Structure):
@@ -117,6 +128,7 @@ PROTOTYPES = {
     "vk_paged_decode_workspace": [P, C.POINTER(DecodeArgs), C.POINTER(U64)],
     "vk_paged_decode": [P, P, C.POINTER(DecodeArgs), P],
     "vk_paged_decode_kernel": [P, C.POINTER(DecodeArgs), C.c_char_p, C.c_size_t],
+    "vk_paged_decode_plan": [P, C.POINTER(DecodeArgs), C.POINTER(DecodePlan)],
     "vk_tree_verify_workspace": [P, C.POINTER(TreeArgs), C.POINTER(U64)],
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
     "vk_tree_mask": [PI32, I32, PU32],
@@ -154,6 +166,7 @@ PROTOTYPES = {
     "vk_stream_create": [P, PP],
     "vk_stream_destroy": [P, P],
     "vk_stream_sync": [P, P],
+    "vk_ctx_check": [P, C.POINTER(U32)],
     "vk_event_create": [P, PP],
     "vk_event_destroy": [P, P],
     "vk_event_record": [P, P, P],

@@ -99,7 +99,15 @@ class Context:
         return b
 
     def sync(self, stream=None):
+        """vk_stream_sync: raises VkError (ERR_BAD_ARG) when a kernel reported misuse."""
         check(lib().vk_stream_sync(self.h, _sptr(stream)))
+
+    def check_misuse(self) -> int:
+        """vk_ctx_check: waits for the device, returns the misuse flags read (and clears
+        them) without raising."""
+        f = C.c_uint32()
+        lib().vk_ctx_check(self.h, C.byref(f))
+        return f.value
 
     # ---- hot path ----
     def slot_mapping(self, pool: "Pool", positions, block_tables=None, bt_stride=0, seq_rows=None,
@@ -129,6 +137,18 @@ class Context:
                              _bptr(context_lens), n_seqs, n_heads, max_context_len, scale, partition_tokens,
                              _bptr(workspace), workspace_bytes, sum_context_len)
         check(lib().vk_paged_decode(self.h, pool.h, C.byref(a), _sptr(stream)))
+
+    def decode_plan(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0, partition_tokens=0,
+                    q_dtype=DT_F16, sum_context_len=0) -> dict:
+        """vk_paged_decode_plan as a dict (kernel, schedule, waves, partitions, blocks per wave, workspace)."""
+        a = _capi.DecodeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None,
+                             n_seqs, n_heads, max_context_len, 0.0, partition_tokens, None, 0, sum_context_len)
+        p = _capi.DecodePlan()
+        check(lib().vk_paged_decode_plan(pool.h, C.byref(a), C.byref(p)))
+        return {"kernel": p.kernel.decode(), "schedule": p.schedule, "wg_waves": p.wg_waves,
+                "partition_tokens": p.partition_tokens, "max_partitions": p.max_partitions,
+                "n_workers": p.n_workers, "max_blocks_per_wave": p.max_blocks_per_wave,
+                "workspace_bytes": p.workspace_bytes, "merge_launch": bool(p.merge_launch)}
 
     def decode_workspace_bytes(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0,
                                partition_tokens=0, q_dtype=DT_F16, sum_context_len=0) -> int:
