@@ -303,6 +303,19 @@ int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a, vk_decode
  * math of llama_cpu.rs:251-284. */
 int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream);
 
+/* vk_paged_decode that allocates nothing. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops or harnesses that forbid hipMalloc). The split-K scratch comes
+ * from a fixed array of VK_NOALLOC_SCRATCH_BYTES that the library holds on each
+ * GPU it runs on until the process ends (its device address is resolved once
+ * per device when a context is created); a->workspace must be NULL and
+ * a->workspace_bytes 0. A call whose scratch would exceed the array fails with
+ * VK_ERR_BAD_ARG (vk_paged_decode_plan reports the bytes a call needs). Every
+ * call on one GPU shares that GPU's array and nothing in it needs clearing
+ * between calls; calls that overlap in time on one GPU race on it. */
+#define VK_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int vk_paged_decode_noalloc(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream);
+
 
 typedef struct vk_tree_args {
   int32_t layer;

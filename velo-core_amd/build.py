@@ -43,16 +43,31 @@ def build_code_object():
     return out
 
 
+OBJ_DIR = os.path.join(HERE, "_build")
+
+
+def build_noalloc_object():
+    """velokv_noalloc.hip: host code plus the per-device scratch array of
+    vk_paged_decode_noalloc (a gfx950 fat binary linked into libvelokv.so)."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    out = os.path.join(OBJ_DIR, "velokv_noalloc.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-c",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument",
+          f"-I{CSRC}", f"-I{INCLUDE}", os.path.join(CSRC, "velokv_noalloc.hip"), "-o", out])
+    return out
+
+
 def build_host_library(sanitize: bool = False):
     """libvelokv.so (or, with sanitize, libvelokv_asan.so: the host C++ under
     AddressSanitizer + UndefinedBehaviorSanitizer, for the CPU test suite)."""
     out = os.path.join(PKG, "libvelokv_asan.so" if sanitize else "libvelokv.so")
     tmp = out + ".tmp"
+    noalloc = build_noalloc_object()
     san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-g"] if sanitize else []
     _run(["g++", "-O1" if sanitize else "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
           "-Wno-unused-parameter", *san,
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{INCLUDE}", f"-I{CSRC}",
-          os.path.join(CSRC, "velokv_host.cpp"), os.path.join(CSRC, "velokv_radix.cpp"), "-o", tmp,
+          os.path.join(CSRC, "velokv_host.cpp"), os.path.join(CSRC, "velokv_radix.cpp"), noalloc, "-o", tmp,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl"])
     os.replace(tmp, out)
     return out

@@ -82,11 +82,16 @@ std::string default_code_object_path() {
 }  // namespace
 
 // Error channel shared with the other translation units of the library
-// (velokv_radix.cpp): sets the calling thread's vk_last_error() message.
+// (velokv_radix.cpp, velokv_noalloc.hip): sets the calling thread's
+// vk_last_error() message.
 int vk_internal_set_error(int code, const char* msg) {
   g_last_error = msg ? msg : "";
   return code;
 }
+
+// Resolves the no-alloc scratch of `device` (velokv_noalloc.hip); the device
+// must be current.
+int vk_internal_noalloc_init(int device);
 
 struct vk_ctx {
   int device = 0;
@@ -279,9 +284,16 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
     delete ctx;
     return fail(VK_ERR_HIP, "error word allocation failed: %s", hipGetErrorString(e));
   }
+  // the no-alloc entry point's scratch: a failure here fails that entry point
+  // (with this message), not the context
+  vk_internal_noalloc_init(device);
+  g_last_error.clear();
   *out = ctx;
   return VK_OK;
 }
+
+// Device index of a context (velokv_noalloc.hip).
+int vk_internal_ctx_device(const vk_ctx* ctx) { return ctx ? ctx->device : -1; }
 
 extern "C" int vk_ctx_destroy(vk_ctx* ctx) {
   if (!ctx) return VK_OK;

@@ -138,6 +138,17 @@ class Context:
                              _bptr(workspace), workspace_bytes, sum_context_len)
         check(lib().vk_paged_decode(self.h, pool.h, C.byref(a), _sptr(stream)))
 
+    def paged_decode_noalloc(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, n_seqs: int,
+                             n_heads: int, max_context_len: int, block_tables=None, bt_stride: int = 0,
+                             seq_rows=None, scale: float = 0.0, partition_tokens: int = 0, stream=None,
+                             sum_context_len: int = 0):
+        """vk_paged_decode_noalloc: the same decode with its split-K scratch in the library's
+        per-device array (allocates nothing)."""
+        a = _capi.DecodeArgs(layer, _bptr(q), q_dtype, _bptr(out), _bptr(block_tables), bt_stride, _bptr(seq_rows),
+                             _bptr(context_lens), n_seqs, n_heads, max_context_len, scale, partition_tokens,
+                             None, 0, sum_context_len)
+        check(lib().vk_paged_decode_noalloc(self.h, pool.h, C.byref(a), _sptr(stream)))
+
     def decode_plan(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0, partition_tokens=0,
                     q_dtype=DT_F16, sum_context_len=0) -> dict:
         """vk_paged_decode_plan as a dict (kernel, schedule, waves, partitions, blocks per wave, workspace)."""
