@@ -73,7 +73,7 @@ def parse():
     ap.add_argument("--ragged", action="store_true", help="context lengths U[1024, ctx] (configs 2/3)")
     ap.add_argument("--decode", choices=["auto", "mfma", "valu"], default="auto",
                     help="decode kernel family (vk_ctx_set_decode_kernel)")
-    ap.add_argument("--sched", choices=["auto", "split", "stream"], default="auto",
+    ap.add_argument("--sched", choices=["auto", "split", "stream", "packed"], default="auto",
                     help="decode work schedule (vk_ctx_set_decode_schedule)")
     ap.add_argument("--rope", choices=["none", "interleaved", "half"], default="none",
                     help="decode step: fused RoPE + append (vk_append_rope: K rotated before quantization, "
@@ -187,6 +187,9 @@ def run_gpu(ctx, args, kv_name: str):
         d_table = ctx.upload(velokv.rope_table(n_pos, HD, 500000.0))
         d_pos = ctx.upload(lens.astype(np.int32) - 1)
 
+    plan = ctx.decode_plan(pool, S, H, int(lens.max()), bt_stride=bt.shape[1], partition_tokens=args.partition,
+                           q_dtype=qdt, sum_context_len=int(lens.sum()))
+
     def step(i, evs=None, app_evs=None):
         r = i % R
         for layer in range(NL):
@@ -237,8 +240,7 @@ def run_gpu(ctx, args, kv_name: str):
     step_bytes = NL * (dbytes + abytes)
     dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
-    kname = ctx.decode_kernel_name(pool, S, H, int(lens.max()), bt_stride=bt.shape[1],
-                                   partition_tokens=args.partition, q_dtype=qdt, sum_context_len=int(lens.sum()))
+    kname = plan["kernel"]
     res = {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
         "ms_per_step": round(ms_step, 4),
@@ -246,8 +248,10 @@ def run_gpu(ctx, args, kv_name: str):
         "frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "decode_bytes_per_launch": dbytes,
         "append_bytes_per_launch": abytes,
-        "append": {"kernel": "vk_append_kv%d" % kv, "rope": args.rope, "ms_mean": round(float(np.mean(app_ms)), 5),
+        "append": {"kernel": "vk_append_kv%d" % kv, "call": "vk_append_rope" if rope else "vk_append",
+                   "rope": args.rope, "ms_mean": round(float(np.mean(app_ms)), 5),
                    "q_rotated_heads": S * H if rope else 0},
+        "plan": plan,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(kname, S, L, H, Hkv, args.ragged),
@@ -640,7 +644,7 @@ def main():
     ctx.set_decode_kernel({"auto": velokv.DECODE_AUTO, "mfma": velokv.DECODE_MFMA,
                            "valu": velokv.DECODE_VALU}[args.decode])
     ctx.set_decode_schedule({"auto": velokv.SCHED_AUTO, "split": velokv.SCHED_SPLIT,
-                             "stream": velokv.SCHED_STREAM}[args.sched])
+                             "stream": velokv.SCHED_STREAM, "packed": velokv.SCHED_PACKED}[args.sched])
     if args.workload == "tree":
         if args.seqs == 64 and "--seqs" not in sys.argv:
             args.seqs = 256

@@ -133,12 +133,18 @@ int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
  * LDS, with no merge launch and no workspace), VK_SCHED_STREAM (stream-K on the matrix cores: one
  * wave per resident slot, each taking an equal share of all (sequence, KV head)
  * blocks, so ragged batches stay balanced; the split segments are combined by a
- * merge launch) or VK_SCHED_AUTO (stream-K unless vk_decode_args.sum_context_len
- * says the batch is uniform, or the VALU family was requested). A nonzero partition_tokens always uses fixed partitions. No
+ * merge launch), VK_SCHED_PACKED (one workgroup of 8 waves per resident slot; the
+ * (sequence, KV head) pairs, longest first, are dealt to the workgroups in snake
+ * order so each gets a nearly equal share of blocks, and the waves of a workgroup
+ * split its blocks evenly and combine split pairs in LDS: no merge launch and no
+ * workspace; at most 256 sequences, else stream-K) or VK_SCHED_AUTO (stream-K
+ * unless vk_decode_args.sum_context_len says the batch is uniform, or the VALU
+ * family was requested). A nonzero partition_tokens always uses fixed partitions. No
  * reference counterpart. */
 #define VK_SCHED_AUTO 0
 #define VK_SCHED_SPLIT 1
 #define VK_SCHED_STREAM 2
+#define VK_SCHED_PACKED 4  /* packed workgroup split (see below) */
 int vk_ctx_set_decode_schedule(vk_ctx* ctx, int schedule);
 
 /* ---- pools ---------------------------------------------------------------- */
@@ -284,11 +290,11 @@ int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args* a, char* b
 #define VK_SCHED_WORKGROUP 3   /* schedule value reported for the workgroup split */
 typedef struct vk_decode_plan {
   char kernel[64];             /* attention kernel name                                */
-  int32_t schedule;            /* VK_SCHED_SPLIT, _STREAM or _WORKGROUP                */
-  int32_t wg_waves;            /* workgroup split: waves per (sequence, KV head)       */
+  int32_t schedule;            /* VK_SCHED_SPLIT, _STREAM, _WORKGROUP or _PACKED       */
+  int32_t wg_waves;            /* workgroup / packed split: waves per workgroup        */
   int32_t partition_tokens;    /* fixed partitions: tokens per partition               */
   int32_t max_partitions;      /* fixed partitions: partitions of the longest context  */
-  int32_t n_workers;           /* stream-K: workers (one wave each)                    */
+  int32_t n_workers;           /* stream-K: workers (one wave each); packed: workgroups */
   int32_t max_blocks_per_wave; /* the most blocks one wave can walk (<= 256)           */
   uint64_t workspace_bytes;    /* split-K scratch the call needs                       */
   int32_t merge_launch;        /* 1 when a merge launch follows the attention kernel   */
@@ -303,6 +309,23 @@ int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a, vk_decode
  * math of llama_cpu.rs:251-284. */
 int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream);
 
+/* One decode step of a layer: the new token of every sequence appended, then
+ * decode attention over the context including it. k_new, v_new are dev
+ * [S][n_kv_heads][head_dim] of in_dtype (VK_DT_*); the token of sequence s goes
+ * to position min(context_lens[s], max_context_len) - 1 of its block-table row
+ * (slot = table[row][pos / bs] * bs + pos % bs, as kv_update derives it,
+ * kernels.metal:637-640, 770-774); a sequence with context 0 appends nothing,
+ * and a page id outside the pool stores nothing (the decode reports it,
+ * VK_MISUSE_PAGE_OUT_OF_POOL). The result equals vk_append of those slots
+ * followed by vk_paged_decode, bit for bit: the append is a launch of the append
+ * kernel with the slots derived in the kernel, then the decode (an append fused
+ * into the decode launch measured slower: its chain of dependent loads waits
+ * behind the decode's streaming loads).
+ * The reference runs kv_update then the attention kernel per layer
+ * (metal/model.rs:399-471). */
+int vk_append_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new, int32_t in_dtype,
+                     const vk_decode_args* a, void* stream);
+
 /* vk_paged_decode that allocates nothing. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops or harnesses that forbid hipMalloc). The split-K scratch comes
@@ -315,7 +338,6 @@ int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* s
  * between calls; calls that overlap in time on one GPU race on it. */
 #define VK_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int vk_paged_decode_noalloc(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream);
-
 
 typedef struct vk_tree_args {
   int32_t layer;

@@ -168,9 +168,14 @@ def test_decode_rejects_bad_arguments(ctx):
     pool = gpu_pool(ctx, case)
     with pytest.raises(velokv.VkError) as e:
         ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
-                         ctx.upload(case.ctx_lens), 1, 24, 20, block_tables=ctx.upload(case.block_tables),
+                         ctx.upload(case.ctx_lens), 1, 264, 20, block_tables=ctx.upload(case.block_tables),
                          bt_stride=case.block_tables.shape[1])
-    assert e.value.code == velokv.ERR_UNSUPPORTED  # 24 / 8 = 3 is not a supported group size
+    assert e.value.code == velokv.ERR_UNSUPPORTED  # 264 / 8 = 33 query heads per KV head: beyond 32
+    with pytest.raises(velokv.VkError) as e:
+        ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
+                         ctx.upload(case.ctx_lens), 1, 28, 20, block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1])
+    assert e.value.code == velokv.ERR_BAD_ARG  # 28 is not a multiple of 8 KV heads
     with pytest.raises(velokv.VkError) as e:
         ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, ctx.alloc(32 * HD * 4),
                          ctx.upload(case.ctx_lens), 1, 32, 10 ** 6, block_tables=ctx.upload(case.block_tables),

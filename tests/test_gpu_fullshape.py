@@ -124,7 +124,7 @@ def run_variants(ctx, pool, bt, lens, H, q, lay, cbt, sample, variants):
 
 MFMA, VALU = velokv.DECODE_MFMA, velokv.DECODE_VALU
 AUTO_K, AUTO_S = velokv.DECODE_AUTO, velokv.SCHED_AUTO
-SPLIT, STREAM = velokv.SCHED_SPLIT, velokv.SCHED_STREAM
+SPLIT, STREAM, PACKED = velokv.SCHED_SPLIT, velokv.SCHED_STREAM, velokv.SCHED_PACKED
 
 
 @pytest.fixture(scope="module")
@@ -204,7 +204,8 @@ def test_headline_b64_ctx8k(ctx, kv):
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
 def test_config2_3_full_batch_auto(ctx, kv):
     """Configs 2 (fp16) and 3 (INT8, 1 % outlier channels x8): 64 sequences with
-    L ~ U[1024, 8192] in a 40k-block pool, AUTO (stream-K + merge at full batch)."""
+    L ~ U[1024, 8192] in a 40k-block pool: AUTO (stream-K + merge at full batch)
+    and the packed workgroup split."""
     print(f"config2/3 full batch kv={kv}", flush=True)
     r = synth.rng(303)
     lens = r.integers(1024, 8193, 64).astype(np.int32)
@@ -217,11 +218,17 @@ def test_config2_3_full_batch_auto(ctx, kv):
         check_pool_bytes(pool, kv, 8, bt, lens, lay, cbt, sample)
         q = synth.normals_f16(64 * 32 * HD, 5701).reshape(64, 32, HD)
 
+        def pk(pl):
+            assert pl["schedule"] == velokv.SCHED_PACKED and not pl["merge_launch"], pl
+            assert pl["workspace_bytes"] == 0 and pl["max_blocks_per_wave"] <= 256, pl
+
         def sk(pl):
             assert pl["schedule"] == velokv.SCHED_STREAM and pl["merge_launch"], pl
         run_variants(ctx, pool, bt, lens, 32, q, lay, cbt, sample, [
             ("AUTO fp16 q", AUTO_K, AUTO_S, 0, np.float16, f"vk_decode_sk_kv{kv}_g4", sk),
             ("AUTO fp32 q", AUTO_K, AUTO_S, 0, np.float32, f"vk_decode_sk_kv{kv}_g4_q0", sk),
+            ("packed fp16 q", MFMA, PACKED, 0, np.float16, f"vk_decode_pk_kv{kv}_g4", pk),
+            ("packed fp32 q", MFMA, PACKED, 0, np.float32, f"vk_decode_pk_kv{kv}_g4_q0", pk),
         ])
     finally:
         pool.close()

@@ -28,14 +28,15 @@ def expect_misuse(ctx, flag):
     assert ctx.check_misuse() == 0
 
 
-@pytest.mark.parametrize("impl", ["wg", "streamk", "split-mfma", "split-valu"])
+@pytest.mark.parametrize("impl", ["wg", "packed", "streamk", "split-mfma", "split-valu"])
 def test_decode_page_outside_pool_is_reported(ctx, impl):
     print(f"misuse: decode page outside the pool impl={impl}", flush=True)
     kind, sched, P = {"wg": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 0),
+                      "packed": (velokv.DECODE_MFMA, velokv.SCHED_PACKED, 0),  # forced
                       "streamk": (velokv.DECODE_MFMA, velokv.SCHED_STREAM, 0),
                       "split-mfma": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 64),
                       "split-valu": (velokv.DECODE_VALU, velokv.SCHED_SPLIT, 64)}[impl]
-    S = 64 if impl == "wg" else 3  # the workgroup split needs a batch that fills the GPU
+    S = 64 if impl in ("wg", "packed") else 3  # the workgroup splits need a batch that fills the GPU
     lens = [40 + 7 * i for i in range(S)]
     case = make_case(O.I8_BLK, lens, seed=701)
     pool = gpu_pool(ctx, case)
@@ -50,9 +51,9 @@ def test_decode_page_outside_pool_is_reported(ctx, impl):
         ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, out, ctx.upload(case.ctx_lens), S, 32,
                          int(max(lens)), **dict(args, block_tables=ctx.upload(bt)))
         ctx.sync()
-        if impl == "wg":
+        if impl in ("wg", "packed"):
             name = ctx.decode_kernel_name(pool, S, 32, int(max(lens)), bt_stride=bt.shape[1])
-            assert name.startswith("vk_decode_wg_"), name
+            assert name.startswith("vk_decode_wg_" if impl == "wg" else "vk_decode_pk_"), name
         bt[1, 2] = pool.n_blocks + 7
         ctx.paged_decode(pool, 0, ctx.upload(case.q), velokv.DT_F16, out, ctx.upload(case.ctx_lens), S, 32,
                          int(max(lens)), **dict(args, block_tables=ctx.upload(bt)))

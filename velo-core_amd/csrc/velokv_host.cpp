@@ -145,6 +145,13 @@ const char* const kKernelNames[] = {
     "vk_tree_commit_kv0", "vk_tree_commit_kv1", "vk_tree_commit_kv2", "vk_tree_commit_kv3",
 };
 
+// GQA group sizes with kernels of their own; any other size up to kMaxGroup
+// runs the "_gx" kernels, which take the size at run time.
+bool fixed_group(int g) { return g == 1 || g == 2 || g == 4 || g == 8; }
+constexpr int kMaxGroupTile = 16;  // one 16-row matrix-core tile
+constexpr int kMaxGroup = 32;      // two tiles (split-K decode; tree verify takes any)
+std::string gtag(int g) { return fixed_group(g) ? "_g" + std::to_string(g) : std::string("_gx"); }
+
 std::string decode_name(int kv, int g, int qt) {
   return "vk_decode_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
 }
@@ -152,21 +159,23 @@ std::string decode_name(int kv, int g, int qt) {
 // into fp16 hi + lo parts.
 std::string q0_suffix(int qt) { return qt == VK_DT_F32 ? "_q0" : ""; }
 std::string decode_mfma_name(int kv, int g, int qt = VK_DT_F16) {
-  return "vk_decode_mfma_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
+  const std::string t = fixed_group(g) ? gtag(g) : (g > kMaxGroupTile ? "_gx2" : "_gx");
+  return "vk_decode_mfma_kv" + std::to_string(kv) + t + q0_suffix(qt);
 }
 std::string decode_wg_name(int kv, int g, int qt = VK_DT_F16) {
-  return "vk_decode_wg_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
+  return "vk_decode_wg_kv" + std::to_string(kv) + gtag(g) + q0_suffix(qt);
 }
 std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16) {
-  return "vk_decode_sk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
+  return "vk_decode_sk_kv" + std::to_string(kv) + gtag(g) + q0_suffix(qt);
 }
-
+std::string decode_pk_name(int kv, int g, int qt = VK_DT_F16) {
+  return "vk_decode_pk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
+}
 std::string tree_pfx_name(int kv, int g, int qt) {
-  return "vk_tree_pfx_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_q" + std::to_string(qt);
+  return "vk_tree_pfx_kv" + std::to_string(kv) + gtag(g) + "_q" + std::to_string(qt);
 }
 std::string tree_name(int kv, int g, int rt, int qt) {
-  return "vk_tree_kv" + std::to_string(kv) + "_g" + std::to_string(g) + "_r" + std::to_string(rt) + "_q" +
-         std::to_string(qt);
+  return "vk_tree_kv" + std::to_string(kv) + gtag(g) + "_r" + std::to_string(rt) + "_q" + std::to_string(qt);
 }
 
 int set_device(const vk_ctx* ctx) {
@@ -245,11 +254,25 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
     return fail(VK_ERR_NOT_WIRED, "hipModuleLoad(%s) failed: %s", path.c_str(), hipGetErrorString(e));
   }
   std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
+  for (int kv = 1; kv < 4; ++kv) {  // the runtime-group-size ("_gx") kernels
+    for (int qt : {VK_DT_F16, VK_DT_F32}) {
+      names.push_back(decode_mfma_name(kv, 3, qt));
+      names.push_back(decode_mfma_name(kv, kMaxGroup, qt));
+      names.push_back(decode_sk_name(kv, 3, qt));
+      if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, 3, qt));
+      if (kv != VK_KV_I8_REF) names.push_back(tree_pfx_name(kv, 3, qt));
+      for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt));
+    }
+  }
   for (int kv = 0; kv < 4; ++kv)
     for (int g : {1, 2, 4, 8}) {
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
       if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
       if (kv != VK_KV_F32) names.push_back(decode_sk_name(kv, g));
+      if (kv != VK_KV_F32) {
+        names.push_back(decode_pk_name(kv, g));
+        names.push_back(decode_pk_name(kv, g, VK_DT_F32));
+      }
       if (kv == VK_KV_F16) {
         names.push_back(decode_sk_name(kv, g, VK_DT_F32));
         names.push_back(decode_mfma_name(kv, g, VK_DT_F32));
@@ -317,7 +340,8 @@ extern "C" int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind) {
 
 extern "C" int vk_ctx_set_decode_schedule(vk_ctx* ctx, int schedule) {
   if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
-  if (schedule != VK_SCHED_AUTO && schedule != VK_SCHED_SPLIT && schedule != VK_SCHED_STREAM)
+  if (schedule != VK_SCHED_AUTO && schedule != VK_SCHED_SPLIT && schedule != VK_SCHED_STREAM &&
+      schedule != VK_SCHED_PACKED)
     return fail(VK_ERR_BAD_ARG, "unknown decode schedule %d", schedule);
   ctx->decode_sched = schedule;
   return VK_OK;
@@ -604,7 +628,9 @@ int split_workspace(vk_ctx* ctx, void* given, uint64_t given_bytes, uint64_t nee
   return VK_OK;
 }
 
-constexpr int kWgMaxWaves = 8;  // waves per workgroup of vk_decode_wg_* at most (velokv_kernels.hip)
+constexpr int kWgMaxWaves = 8;  // waves per workgroup of vk_decode_wg_* / vk_decode_pk_* at most (velokv_kernels.hip)
+constexpr int kPkMaxSeqs = 256;  // sequences a vk_decode_pk_* workgroup ranks
+constexpr int kPkMaxRounds = 16; // items per vk_decode_pk_* workgroup
 
 // Stream-K cost units charged to each segment ahead of its blocks, for what a
 // worker spends starting a second piece (per-wave traces on config 3: ~5 us).
@@ -619,8 +645,10 @@ struct DecodePlan {
   int32_t part_tokens;
   int32_t max_parts;
   bool stream_k;
+  bool packed;       // packed workgroup split: n_workers workgroups of kWgMaxWaves waves
   int32_t n_workers;
   int32_t wg_waves;  // > 0: workgroup-split kernel with this many waves per (sequence, KV head)
+  int32_t max_wave_blocks;  // packed: bound on the blocks of one wave's range
   std::string kernel;
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
 };
@@ -639,9 +667,13 @@ void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args*
   const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
   const bool uniform = a->sum_context_len > 0 &&
                        (double)a->sum_context_len >= 0.97 * (double)a->n_seqs * (double)a->max_context_len;
-  *stream_k = fast && a->partition_tokens == 0 && kind != VK_DECODE_VALU &&
-              (sched == VK_SCHED_STREAM || (sched == VK_SCHED_AUTO && !uniform));
-  *mfma = *stream_k || (fast && (kind == VK_DECODE_MFMA ||
+  const int G = a->n_heads / d.n_kv_heads;
+  // the VALU kernels exist for group sizes 1, 2, 4, 8 only: other sizes always
+  // take the matrix cores, and beyond one 16-row tile only fixed partitions
+  const bool valu_ok = fixed_group(G);
+  *stream_k = fast && a->partition_tokens == 0 && (kind != VK_DECODE_VALU || !valu_ok) && G <= kMaxGroupTile &&
+              (sched == VK_SCHED_STREAM || sched == VK_SCHED_PACKED || (sched == VK_SCHED_AUTO && !uniform));
+  *mfma = *stream_k || (fast && (!valu_ok || kind == VK_DECODE_MFMA ||
                                  (kind == VK_DECODE_AUTO && (d.kv_type != VK_KV_F16 || a->q_dtype == VK_DT_F32))));
 }
 
@@ -662,7 +694,9 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   if (a->n_seqs < 0 || a->n_heads <= 0 || a->max_context_len < 0) return fail(VK_ERR_BAD_ARG, "bad sizes");
   if (a->n_heads % d.n_kv_heads) return fail(VK_ERR_BAD_ARG, "n_heads %d not a multiple of n_kv_heads %d", a->n_heads, d.n_kv_heads);
   const int G = a->n_heads / d.n_kv_heads;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (supported 1, 2, 4, 8)", G);
+  if (G > kMaxGroup) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (decode supports up to %d)", G, kMaxGroup);
+  if (!fixed_group(G) && d.kv_type == VK_KV_F32)
+    return fail(VK_ERR_UNSUPPORTED, "GQA group size %d over fp32 KV (the fp32 kernels take 1, 2, 4, 8)", G);
   if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
   pl->bt = a->block_tables;
   pl->bt_stride = a->bt_stride;
@@ -684,6 +718,32 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   pl->acc_bytes = pl->ml_bytes = pl->prefix_bytes = 0;
   pl->n_workers = 0;
   pl->wg_waves = 0;
+  pl->packed = false;
+  pl->max_wave_blocks = 0;
+  const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
+  if (pl->stream_k && sched == VK_SCHED_PACKED && fixed_group(G) && a->n_seqs > 0 && a->n_seqs <= kPkMaxSeqs) {
+    // Packed workgroup split: one workgroup per resident slot (n_workers bins), the
+    // batch's (sequence, KV head) items dealt to them longest first in snake
+    // order, so that they fill the GPU, each workgroup gets at most kPkMaxRounds
+    // items and no wave's range can pass 256 blocks (four block-id windows).
+    const std::string name = decode_pk_name(d.kv_type, G, a->q_dtype);
+    const int64_t wgs = std::max<int64_t>(1, (ctx ? resident_waves(ctx, name, 64 * kWgMaxWaves) : 2048) / kWgMaxWaves);
+    const int64_t items = (int64_t)a->n_seqs * d.n_kv_heads;
+    const int64_t bins = std::min(wgs, items);
+    const int64_t rounds = (items + bins - 1) / bins;
+    const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
+    const int64_t wave_units = (rounds * (nb + kSkPenalty) + kWgMaxWaves - 1) / kWgMaxWaves;
+    if (rounds <= kPkMaxRounds && wave_units <= kMaxPartTokens / d.block_size) {
+      pl->stream_k = false;
+      pl->packed = true;
+      pl->kernel = name;
+      pl->n_workers = (int32_t)bins;
+      pl->part_tokens = kMaxPartTokens;
+      pl->max_parts = 1;
+      pl->max_wave_blocks = (int32_t)std::min<int64_t>(nb, wave_units);
+      return VK_OK;
+    }
+  }
   if (pl->stream_k) {
     pl->kernel = decode_sk_name(d.kv_type, G, a->q_dtype);
     // one wave per resident slot, and at most 256 blocks (four id windows) per
@@ -704,7 +764,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     return VK_OK;
   }
   pl->wg_waves = 0;
-  if (mfma && P == 0 && (d.kv_type == VK_KV_I8_REF || d.kv_type == VK_KV_I8_BLK)) {
+  if (mfma && P == 0 && G <= kMaxGroupTile && (d.kv_type == VK_KV_I8_REF || d.kv_type == VK_KV_I8_BLK)) {
     // Workgroup split: NW waves per (sequence, KV head), the smallest power of two
     // whose workgroups fill one round of resident waves, when each wave's share
     // fits its four block-id windows (256 blocks).
@@ -761,7 +821,12 @@ extern "C" int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a
   snprintf(out->kernel, sizeof out->kernel, "%s", pl.kernel.c_str());
   const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
   out->workspace_bytes = pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes;
-  if (pl.stream_k) {
+  if (pl.packed) {
+    out->schedule = VK_SCHED_PACKED;
+    out->wg_waves = kWgMaxWaves;
+    out->n_workers = pl.n_workers;
+    out->max_blocks_per_wave = pl.max_wave_blocks;
+  } else if (pl.stream_k) {
     const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads * (nb + kSkPenalty);
     out->schedule = VK_SCHED_STREAM;
     out->n_workers = pl.n_workers;
@@ -781,7 +846,41 @@ extern "C" int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a
   return VK_OK;
 }
 
-extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
+namespace {
+
+// The new token of every sequence (k_new / v_new rows [S][Hkv][D] of in_dtype)
+// appended at position context_len - 1 of its table row by the append kernel,
+// slots derived in the kernel (the unfused half of vk_append_decode).
+int append_new_tokens(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, const DecodePlan& pl, const void* k_new,
+                      const void* v_new, int in_dtype, void* stream) {
+  AppendParams p{};
+  p.base = pool->base;
+  p.g = pool->geom;
+  p.layer = a->layer;
+  p.in_dtype = in_dtype;
+  p.k = k_new;
+  p.v = v_new;
+  p.slot_mapping = nullptr;
+  p.block_tables = pl.bt;
+  p.seq_rows = a->seq_rows;
+  p.context_lens = a->context_lens;
+  p.bt_stride = pl.bt_stride;
+  p.bt_rows = pl.bt_rows;
+  p.cap_tokens = a->max_context_len;
+  p.n_tok = a->n_seqs;
+  p.tok_per_wg = append_tok_per_wg(a->n_seqs, pool->desc.n_kv_heads);
+  p.err = ctx->err_word;
+  p.claim = pool->claim;
+  p.epoch = pool->claim ? pool->next_epoch() : 0u;
+  const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
+  return launch(ctx, name.c_str(), dim3((unsigned)((a->n_seqs + p.tok_per_wg - 1) / p.tok_per_wg),
+                                        (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
+}
+
+// vk_paged_decode, and with k_new the append of vk_append_decode as a launch
+// before it.
+int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream, const void* k_new,
+               const void* v_new, int in_dtype) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
   DecodePlan pl;
@@ -789,6 +888,7 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
+  if (k_new && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
   uint8_t* ws = nullptr;
   if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes, &ws)))
     return rc;
@@ -822,14 +922,14 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   p.part_tokens = pl.part_tokens;
   // stream-K: contexts are clamped to max_context_len, which bounds every worker's
   // range to 256 blocks (the planner sized the grid for it)
-  p.cap_tokens = pl.stream_k ? a->max_context_len
+  p.cap_tokens = (pl.stream_k || pl.packed) ? a->max_context_len
                 : pl.wg_waves ? a->max_context_len  // bounds every wave's share to 256 blocks (planner)
                               : (int32_t)std::min<int64_t>((int64_t)pl.max_parts * pl.part_tokens,
                                                            (int64_t)pl.bt_stride * d.block_size);
   p.n_nodes = 1;
   p.n_rgroups = 1;
   p.n_workers = pl.n_workers;
-  p.sk_penalty = pl.stream_k ? kSkPenalty : 0;
+  p.sk_penalty = (pl.stream_k || pl.packed) ? kSkPenalty : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.err = ctx->err_word;
 
@@ -854,6 +954,8 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
     if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64), p, stream))) return rc;
     return launch(ctx, "vk_decode_merge_sk", merge_grid, dim3(256), m, stream);
   }
+  if (pl.packed)
+    return launch(ctx, pl.kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64 * kWgMaxWaves), p, stream);
   if (pl.wg_waves)
     return launch(ctx, pl.kernel.c_str(), dim3((unsigned)(a->n_seqs * d.n_kv_heads)), dim3(64 * (unsigned)pl.wg_waves),
                   p, stream);
@@ -862,6 +964,20 @@ extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args*
   if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
   if (pl.max_parts == 1) return VK_OK;  // every sequence was finished by the decode kernel
   return launch(ctx, "vk_decode_merge", merge_grid, dim3(256), m, stream);
+}
+
+}  // namespace
+
+extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
+  return run_decode(ctx, pool, a, stream, nullptr, nullptr, VK_DT_F16);
+}
+
+extern "C" int vk_append_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new, int32_t in_dtype,
+                                const vk_decode_args* a, void* stream) {
+  if (in_dtype != VK_DT_F32 && in_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "in_dtype %d", in_dtype);
+  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
+  if (a->n_seqs > 0 && (!k_new || !v_new)) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  return run_decode(ctx, pool, a, stream, k_new, v_new, in_dtype);
 }
 
 namespace {
@@ -887,8 +1003,7 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
   if (a->n_nodes < 1 || a->n_nodes > kMaxTreeNodes)
     return fail(VK_ERR_BAD_ARG, "n_nodes %d out of range [1, %d]", a->n_nodes, kMaxTreeNodes);
   if (a->n_heads % d.n_kv_heads) return fail(VK_ERR_BAD_ARG, "n_heads %d not a multiple of n_kv_heads %d", a->n_heads, d.n_kv_heads);
-  const int G = a->n_heads / d.n_kv_heads;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (supported 1, 2, 4, 8)", G);
+  const int G = a->n_heads / d.n_kv_heads;  // any group size: rows of (node, head) in 16-row tiles
   if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
   if (d.kv_type == VK_KV_F32) return fail(VK_ERR_UNSUPPORTED, "tree verify reads fp16 or int8 KV pools, not fp32");
   pl->bt = a->block_tables;

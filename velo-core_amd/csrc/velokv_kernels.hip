@@ -166,6 +166,19 @@ DEV void write_zero_rows(const DecodeParams& P, int s, int kvh) {
   for (int g = 0; g < G; ++g) reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (HD / 2) + lane_id()] = make_float2(0.f, 0.f);
 }
 
+// GQA group size of a kernel: the template's G, or for G == 0 (the "_gx" kernels
+// that serve any other ratio) the runtime n_heads / n_kv_heads.
+template <int G>
+DEV int group_size(const DecodeParams& P) { return G > 0 ? G : P.n_heads / P.n_kv_heads; }
+// Rows of one (sequence, KV head) a workgroup holds in LDS for group size G:
+// runtime group sizes are at most 16 (one 16-row tile).
+template <int G>
+constexpr int lds_rows() { return G > 0 ? G : 16; }
+DEV void write_zero_rows_n(const DecodeParams& P, int s, int kvh, int g_n) {
+  const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * g_n;
+  for (int g = 0; g < g_n; ++g) reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (HD / 2) + lane_id()] = make_float2(0.f, 0.f);
+}
+
 // Misuse is reported, not trapped: the kernel or-s a flag into the context's
 // error word (a vector atomic) and carries on with the clamped input.
 DEV void flag_misuse(uint32_t* err, uint32_t bit) {
@@ -747,11 +760,12 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   const int nblk = (end - start + BS - 1) / BS;
   const int blk0 = start / BS;
   const int nbatch = (nblk + CH - 1) / CH;
-  const int nrows = N * G;
+  const int Gn = group_size<G>(P);
+  const int nrows = N * Gn;
   const int row0 = rg * 16 * RT;
   const int plain_end = min(end, ctx_c);  // tokens below this need no validity or mask test
   // output row of row R of this (sequence, KV head) pair
-  auto out_row = [&](int R) -> int64_t { return ((int64_t)s * N + R / G) * H + (int64_t)kvh * G + R % G; };
+  auto out_row = [&](int R) -> int64_t { return ((int64_t)s * N + R / Gn) * H + (int64_t)kvh * Gn + R % Gn; };
 
   BlockIds bw;
   load_block_ids<BLK>(bw, P, bt, blk0, nblk, kvh);
@@ -807,7 +821,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     }
     mrow[rt] = 0u;
     if constexpr (TREE) {
-      if (R < nrows) mrow[rt] = P.tree_mask[(int64_t)s * N + R / G];
+      if (R < nrows) mrow[rt] = P.tree_mask[(int64_t)s * N + R / Gn];
     }
   }
 
@@ -1083,13 +1097,14 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   const int start = pre + part * P.part_tokens;
   if (start >= ctx) {
     if constexpr (!TREE) {
-      if (part == 0) write_zero_rows<G>(P, s, kvh);
+      if (part == 0) write_zero_rows_n(P, s, kvh, group_size<G>(P));
     }
     return;
   }
   const int end = min(start + P.part_tokens, ctx);
   const int nparts = C0 + (ctx - pre + P.part_tokens - 1) / P.part_tokens;
-  const int64_t pbase = TREE ? C0 + part : ((int64_t)s * P.n_heads + (int64_t)kvh * G) * P.max_parts + part;
+  const int64_t pbase =
+      TREE ? C0 + part : ((int64_t)s * P.n_heads + (int64_t)kvh * group_size<G>(P)) * P.max_parts + part;
   // the rest of a context in one partition after a shared prefix writes the
   // output itself, folding in the prefix partials
   const bool fold = C0 > 0 && nparts == C0 + 1;
@@ -1193,7 +1208,7 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     if (o0 < o1) {
       const int slot = o0 > 0 ? 0 : 1;
       attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                      ((int64_t)w * 2 + slot) * G, 1, P.part_acc, P.part_ml);
+                                      ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc, P.part_ml);
     }
     x = seg0 + su;
     if (kvh == Hkv - 1) {
@@ -1213,8 +1228,10 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
 constexpr int kWgMaxWaves = 8;
 template <int KV, int G, int QT = DT_F16>
 DEV void attn_wg_mfma(const DecodeParams& P) {
-  __shared__ float wacc[kWgMaxWaves][G][HD];
-  __shared__ float wml[kWgMaxWaves][G][2];
+  constexpr int GM = lds_rows<G>();
+  __shared__ float wacc[kWgMaxWaves][GM][HD];
+  __shared__ float wml[kWgMaxWaves][GM][2];
+  const int Gn = group_size<G>(P);
   const int nw = (int)blockDim.x / WAVE;
   const int w = (int)threadIdx.x / WAVE;
   const int lane = lane_id();
@@ -1223,7 +1240,7 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   if (s >= P.n_seqs) return;  // the whole workgroup
   const int ctx = max(0, min(P.context_lens[s], P.cap_tokens));
   if (ctx == 0) {
-    if (w == 0) write_zero_rows<G>(P, s, kvh);
+    if (w == 0) write_zero_rows_n(P, s, kvh, Gn);
     return;
   }
   const int nb = (ctx + BS - 1) / BS;
@@ -1232,13 +1249,13 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   if (b0 < b1) {
     attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
                                     &wml[w][0][0]);
-  } else if (lane < G) {
+  } else if (lane < Gn) {
     wml[w][lane][0] = kNegInf;
     wml[w][lane][1] = 0.f;
   }
   __syncthreads();
-  const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * G;
-  for (int i = (int)threadIdx.x; i < G * HD; i += (int)blockDim.x) {
+  const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * Gn;
+  for (int i = (int)threadIdx.x; i < Gn * HD; i += (int)blockDim.x) {
     const int r = i / HD, d = i - r * HD;
     float M = kNegInf;
     for (int v = 0; v < nw; ++v) M = fmaxf(M, wml[v][r][0]);
@@ -1251,6 +1268,117 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
       o = fmaf(e, wacc[v][r][d], o);
     }
     P.out[(hrow0 + r) * HD + d] = L > 0.f ? o / L : 0.f;
+  }
+}
+
+// ---- packed workgroup split (ragged batches) ---------------------------------
+// The (sequence, KV head) items of the batch, longest first, are dealt to the B
+// workgroups of the grid in snake order: item i goes to workgroup i mod B in even
+// rounds r = i / B and to B - 1 - (i mod B) in odd ones, so a workgroup gets one
+// of the longest items with one of the shortest, and so on, and the workgroups'
+// sums of blocks come out nearly equal without a host round trip or an extra
+// launch. Each workgroup ranks the sequences itself (rank of s = the sequences
+// with more blocks, ties by index). Inside the workgroup the NW waves split the
+// concatenated blocks of its items evenly, as stream-K does (sk_split over cost
+// units: sk_penalty per item, then one per block). An item inside one wave's
+// range is written directly; a split item leaves one partial per wave in LDS
+// (slot 1 in the wave where it starts, slot 0 in the waves that continue it),
+// combined into the output after one barrier. No partials in HBM, no merge
+// launch. The host keeps every wave's range within 256 blocks.
+constexpr int kPkMaxSeqs = 256;  // sequences a workgroup ranks (LDS)
+constexpr int kPkMaxRounds = 16; // items per workgroup at most
+
+template <int KV, int G, int QT = DT_F16>
+DEV void attn_pk_mfma(const DecodeParams& P) {
+  __shared__ int nb_l[kPkMaxSeqs];
+  __shared__ int seq_at[kPkMaxSeqs];
+  __shared__ float wacc[kWgMaxWaves][2][G][HD];
+  __shared__ float wml[kWgMaxWaves][2][G][2];
+  const int nw = (int)blockDim.x / WAVE;
+  const int w = (int)threadIdx.x / WAVE;
+  const int S = P.n_seqs, Hkv = P.n_kv_heads, pen = P.sk_penalty;
+  const int B = (int)gridDim.x, bin = (int)blockIdx.x;
+  const int NI = S * Hkv;
+  for (int s = (int)threadIdx.x; s < S; s += (int)blockDim.x) nb_l[s] = seq_blocks(P, s);
+  __syncthreads();
+  for (int s = (int)threadIdx.x; s < S; s += (int)blockDim.x) {
+    const int ns = nb_l[s];
+    int r = 0;
+    for (int t = 0; t < S; ++t) {
+      const int nt = nb_l[t];
+      r += (nt > ns) || (nt == ns && t < s);
+    }
+    seq_at[r] = s;
+  }
+  __syncthreads();
+  // item of this workgroup in round r (or -1 past the last item)
+  auto item = [&](int r) -> int {
+    const int i = r * B + ((r & 1) ? B - 1 - bin : bin);
+    return i < NI ? i : -1;
+  };
+  int T = 0;  // cost units of the workgroup's items
+  for (int r = 0; r < kPkMaxRounds; ++r) {
+    const int i = item(r);
+    if (i < 0) break;
+    const int nb = nb_l[seq_at[i / Hkv]];
+    T += nb > 0 ? nb + pen : 0;
+  }
+  if (T > 0) {
+    const SkSplit sp = sk_split(T, nw);
+    if (w < sp.nw) {
+      const int64_t c0 = sk_begin(sp, w), c1 = sk_begin(sp, w + 1);
+      int64_t u = 0;  // first unit of the current item
+      for (int r = 0; r < kPkMaxRounds && u < c1; ++r) {
+        const int i = item(r);
+        if (i < 0) break;
+        const int s = seq_at[i / Hkv], kvh = i % Hkv;
+        const int nb = nb_l[s];
+        if (nb == 0) continue;
+        int o0, o1;
+        sk_piece(u, nb, pen, c0, c1, &o0, &o1);
+        if (o0 < o1) {
+          const int ctx_s = max(0, min(P.context_lens[s], P.cap_tokens));
+          const int slot = o0 > 0 ? 0 : 1;
+          attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb, 0,
+                                          1, &wacc[w][slot][0][0], &wml[w][slot][0][0]);
+        }
+        u += nb + pen;
+      }
+    }
+  }
+  __syncthreads();
+  // split items: combine their pieces; empty items: zero rows
+  int64_t u = 0;
+  const SkSplit sp = sk_split(T > 0 ? T : 1, nw);
+  for (int r = 0; r < kPkMaxRounds; ++r) {
+    const int i = item(r);
+    if (i < 0) break;
+    const int s = seq_at[i / Hkv], kvh = i % Hkv;
+    const int nb = nb_l[s];
+    const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * G;
+    if (nb == 0) {
+      for (int e = (int)threadIdx.x; e < G * HD; e += (int)blockDim.x) P.out[hrow0 * HD + e] = 0.f;
+      continue;
+    }
+    int w_lo, w_hi;
+    sk_segment_workers(sp, u, nb, pen, &w_lo, &w_hi);
+    u += nb + pen;
+    if (w_lo == w_hi) continue;  // written by its wave
+    for (int e = (int)threadIdx.x; e < G * HD; e += (int)blockDim.x) {
+      const int g = e / HD, d = e - g * HD;
+      float M = kNegInf;
+      for (int v = w_lo; v <= w_hi; ++v) M = fmaxf(M, wml[v][v == w_lo ? 1 : 0][g][0]);
+      float L = 0.f, o = 0.f;
+      for (int v = w_lo; v <= w_hi; ++v) {
+        const int sl = v == w_lo ? 1 : 0;
+        const float mv = wml[v][sl][g][0];
+        if (mv == kNegInf) continue;
+        const float ev = __builtin_amdgcn_exp2f(mv - M);
+        L = fmaf(ev, wml[v][sl][g][1], L);
+        o = fmaf(ev, wacc[v][sl][g][d], o);
+      }
+      P.out[(hrow0 + g) * HD + d] = L > 0.f ? o / L : 0.f;
+    }
   }
 }
 
@@ -1325,7 +1453,8 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   const int kvh = (int)blockIdx.y;
   const int chunk = (int)blockIdx.z, nchunks = (int)gridDim.z;
   const int N = P.n_nodes, H = P.n_heads;
-  const int RS = N * G;  // rows of one sequence for this KV head
+  const int Gn = group_size<G>(P);
+  const int RS = N * Gn;  // rows of one sequence for this KV head
   const int R = P.n_seqs * RS;
   const int wrow0 = (int)blockIdx.x * kPfxRows + wave * 16 * RT;
   const int PB = P.prefix_blocks;
@@ -1337,7 +1466,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   const int32_t* bt = P.block_tables + (int64_t)prow * P.bt_stride;
   auto out_row = [&](int r) -> int64_t {
     const int s = r / RS, rem = r - s * RS;
-    return ((int64_t)s * N + rem / G) * H + (int64_t)kvh * G + rem % G;
+    return ((int64_t)s * N + rem / Gn) * H + (int64_t)kvh * Gn + rem % Gn;
   };
 
   // ---- q^T operands of rows wrow0 + 16 rt + n, and the prefix each row sees ----
@@ -1790,7 +1919,16 @@ DEV void rope_rotate(int style, const float* cos_sin, int pos, float& x0, float&
 // Flat slot of token m, or -1 when it is padding (a negative slot, or one at or
 // past the end of the pool) or, with RoPE, its position is outside the table.
 DEV int64_t token_slot(const AppendParams& P, int m) {
-  const int64_t slot = P.slot_mapping[m];
+  int64_t slot;
+  if (P.slot_mapping) {
+    slot = P.slot_mapping[m];
+  } else {  // the new token of sequence m, at its last context position (kernels.metal:770-774)
+    const int pos = min(P.context_lens[m], P.cap_tokens) - 1;
+    if (pos < 0 || pos / BS >= P.bt_stride) return -1;
+    int row = P.seq_rows ? P.seq_rows[m] : m;
+    if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
+    slot = (int64_t)P.block_tables[(int64_t)row * P.bt_stride + pos / BS] * BS + pos % BS;
+  }
   if (slot < 0 || slot >= (int64_t)P.g.n_blocks * BS) return -1;
   if (P.rope != ROPE_NONE) {
     const int pos = P.positions[m];
@@ -2473,6 +2611,17 @@ VK_DECODE_WG_G(2) VK_DECODE_WG_G(3)
 #define VK_DECODE_WG_Q0_G(KV) VK_DECODE_WG_Q0(KV, 1) VK_DECODE_WG_Q0(KV, 2) VK_DECODE_WG_Q0(KV, 4) VK_DECODE_WG_Q0(KV, 8)
 VK_DECODE_WG_Q0_G(2) VK_DECODE_WG_Q0_G(3)
 
+// Packed workgroup split (ragged batches): up to kWgMaxWaves waves of 64.
+#define VK_DECODE_PK(KV, G, QT, SUF)                                                \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves)                    \
+      vk_decode_pk_kv##KV##_g##G##SUF(const DecodeParams P) {                       \
+    attn_pk_mfma<KV, G, QT>(P);                                                     \
+  }
+#define VK_DECODE_PK_G(KV, QT, SUF) \
+  VK_DECODE_PK(KV, 1, QT, SUF) VK_DECODE_PK(KV, 2, QT, SUF) VK_DECODE_PK(KV, 4, QT, SUF) VK_DECODE_PK(KV, 8, QT, SUF)
+VK_DECODE_PK_G(1, DT_F16, ) VK_DECODE_PK_G(2, DT_F16, ) VK_DECODE_PK_G(3, DT_F16, )
+VK_DECODE_PK_G(1, DT_F32, _q0) VK_DECODE_PK_G(2, DT_F32, _q0) VK_DECODE_PK_G(3, DT_F32, _q0)
+
 // Two waves per SIMD (at most 256 registers).
 #define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
 #define VK_DECODE_SK(KV, G)                                                         \
@@ -2506,6 +2655,44 @@ VK_TREE_KV(1, )
 VK_TREE_KV(2, VK_TWO_WAVES)
 VK_TREE_KV(3, VK_TWO_WAVES)
 
+// Any other GQA group size ("_gx"): the group size is n_heads / n_kv_heads at run
+// time, at most 16 rows per tile (decode), two tiles ("_gx2", split-K) up to 32.
+#define VK_GX_DECODE(KV)                                                                                        \
+  extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx(const DecodeParams P) {           \
+    attn_unit_mfma<KV, 0, 1, false>(P);                                                                        \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx_q0(const DecodeParams P) {        \
+    attn_unit_mfma<KV, 0, 1, false, DT_F32>(P);                                                                \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx2(const DecodeParams P) {          \
+    attn_unit_mfma<KV, 0, 2, false>(P);                                                                        \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx2_q0(const DecodeParams P) {       \
+    attn_unit_mfma<KV, 0, 2, false, DT_F32>(P);                                                                \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx(const DecodeParams P) { \
+    attn_streamk_mfma<KV, 0>(P);                                                                               \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_q0(const DecodeParams P) { \
+    attn_streamk_mfma<KV, 0, DT_F32>(P);                                                                       \
+  }
+VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
+#define VK_GX_WG(KV)                                                                                            \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx(const DecodeParams P) { \
+    attn_wg_mfma<KV, 0>(P);                                                                                    \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_q0(const DecodeParams P) { \
+    attn_wg_mfma<KV, 0, DT_F32>(P);                                                                            \
+  }
+VK_GX_WG(2) VK_GX_WG(3)
+#define VK_GX_TREE(KV, RT, QT, ATTR)                                                                            \
+  extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_r##RT##_q##QT(const DecodeParams P) { \
+    attn_unit_mfma<KV, 0, RT, true, QT>(P);                                                                    \
+  }
+#define VK_GX_TREE_KV(KV, ATTR) \
+  VK_GX_TREE(KV, 1, 0, ATTR) VK_GX_TREE(KV, 1, 1, ATTR) VK_GX_TREE(KV, 2, 0, ATTR) VK_GX_TREE(KV, 2, 1, ATTR)
+VK_GX_TREE_KV(1, ) VK_GX_TREE_KV(2, VK_TWO_WAVES) VK_GX_TREE_KV(3, VK_TWO_WAVES)
+
 // Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
 #define VK_TREE_PFX(KV, G, QT)                                                      \
   extern "C" __global__ void __launch_bounds__(64 * kPfxWaves)                      \
@@ -2515,6 +2702,12 @@ VK_TREE_KV(3, VK_TWO_WAVES)
 #define VK_TREE_PFX_G(KV, QT) \
   VK_TREE_PFX(KV, 1, QT) VK_TREE_PFX(KV, 2, QT) VK_TREE_PFX(KV, 4, QT) VK_TREE_PFX(KV, 8, QT)
 VK_TREE_PFX_G(1, 0) VK_TREE_PFX_G(1, 1) VK_TREE_PFX_G(3, 0) VK_TREE_PFX_G(3, 1)
+#define VK_GX_TREE_PFX(KV, QT)                                                      \
+  extern "C" __global__ void __launch_bounds__(64 * kPfxWaves)                      \
+      __attribute__((amdgpu_waves_per_eu(4))) vk_tree_pfx_kv##KV##_gx_q##QT(const DecodeParams P) { \
+    tree_prefix_mfma<KV, 0, QT>(P);                                                 \
+  }
+VK_GX_TREE_PFX(1, 0) VK_GX_TREE_PFX(1, 1) VK_GX_TREE_PFX(3, 0) VK_GX_TREE_PFX(3, 1)
 
 
 #define VK_APPEND(KV) \

@@ -55,6 +55,12 @@ struct AppendParams {
   uint32_t* err;            // the context's misuse word
   unsigned long long* claim;// I8_BLK: [n_blocks] (epoch << 32 | first token) of the last run per block
   uint32_t epoch;           // I8_BLK: this call's epoch (never 0)
+  // slot_mapping == null: token m is the new token of sequence m, at position
+  // min(context_lens[m], cap_tokens) - 1 of table row seq_rows[m] (or m)
+  const int32_t* block_tables;
+  const int32_t* seq_rows;
+  const int32_t* context_lens;
+  int32_t bt_stride, bt_rows, cap_tokens;
 };
 
 struct SlotMapParams {

@@ -9,7 +9,7 @@ tree, and NIXL wire-record pack/unpack of KV pages. Every compute call goes to t
 code object through libvelokv.so.
 """
 from ._capi import (  # noqa: F401
-    DT_F16, DT_F32, DECODE_AUTO, DECODE_MFMA, DECODE_VALU, SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM, SCHED_WORKGROUP, NOALLOC_SCRATCH_BYTES, KV_F16, KV_F32, KV_I8_BLK, KV_I8_REF, VkError,
+    DT_F16, DT_F32, DECODE_AUTO, DECODE_MFMA, DECODE_VALU, SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM, SCHED_WORKGROUP, SCHED_PACKED, NOALLOC_SCRATCH_BYTES, KV_F16, KV_F32, KV_I8_BLK, KV_I8_REF, VkError,
     ERR_BAD_ARG, ERR_INVALID_BLOCK_SIZE, ERR_OUT_OF_PAGES, ERR_TOO_MANY_PAGES, ERR_NO_FREE_SLOTS,
     ERR_NOT_WIRED, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_UNKNOWN_HANDLE,
     NIXL_HEADER_BYTES, NIXL_OK, NIXL_SHORT_HEADER, NIXL_TRUNCATED, NIXL_HANDLE_MISMATCH, NIXL_LENGTH_MISMATCH,

@@ -40,6 +40,7 @@ KV_F32, KV_F16, KV_I8_REF, KV_I8_BLK = 0, 1, 2, 3
 DECODE_AUTO, DECODE_VALU, DECODE_MFMA = 0, 1, 2
 SCHED_AUTO, SCHED_SPLIT, SCHED_STREAM = 0, 1, 2
 SCHED_WORKGROUP = 3  # reported by vk_paged_decode_plan for the workgroup split
+SCHED_PACKED = 4
 NOALLOC_SCRATCH_BYTES = 64 << 20  # VK_NOALLOC_SCRATCH_BYTES
 DT_F32, DT_F16 = 0, 1
 NIXL_HEADER_BYTES = 16
@@ -131,6 +132,7 @@ PROTOTYPES = {
     "vk_paged_decode_kernel": [P, C.POINTER(DecodeArgs), C.c_char_p, C.c_size_t],
     "vk_paged_decode_plan": [P, C.POINTER(DecodeArgs), C.POINTER(DecodePlan)],
     "vk_paged_decode_noalloc": [P, P, C.POINTER(DecodeArgs), P],
+    "vk_append_decode": [P, P, P, P, I32, C.POINTER(DecodeArgs), P],
     "vk_tree_verify_workspace": [P, C.POINTER(TreeArgs), C.POINTER(U64)],
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
     "vk_tree_mask": [PI32, I32, PU32],

@@ -138,6 +138,17 @@ class Context:
                              _bptr(workspace), workspace_bytes, sum_context_len)
         check(lib().vk_paged_decode(self.h, pool.h, C.byref(a), _sptr(stream)))
 
+    def append_decode(self, pool: "Pool", layer: int, k_new, v_new, in_dtype: int, q, q_dtype: int, out,
+                      context_lens, n_seqs: int, n_heads: int, max_context_len: int, block_tables=None,
+                      bt_stride: int = 0, seq_rows=None, scale: float = 0.0, partition_tokens: int = 0,
+                      workspace=None, workspace_bytes: int = 0, stream=None, sum_context_len: int = 0):
+        """vk_append_decode: the new token of every sequence appended at context_len - 1, then decode."""
+        a = _capi.DecodeArgs(layer, _bptr(q), q_dtype, _bptr(out), _bptr(block_tables), bt_stride, _bptr(seq_rows),
+                             _bptr(context_lens), n_seqs, n_heads, max_context_len, scale, partition_tokens,
+                             _bptr(workspace), workspace_bytes, sum_context_len)
+        check(lib().vk_append_decode(self.h, pool.h, _bptr(k_new), _bptr(v_new), in_dtype, C.byref(a),
+                                     _sptr(stream)))
+
     def paged_decode_noalloc(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, n_seqs: int,
                              n_heads: int, max_context_len: int, block_tables=None, bt_stride: int = 0,
                              seq_rows=None, scale: float = 0.0, partition_tokens: int = 0, stream=None,
