@@ -57,10 +57,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--kv", choices=["int8", "fp16", "int8ref"], default="int8",
+    ap.add_argument("--kv", choices=["int8", "fp16", "int8ref", "fp32"], default="int8",
                     help="headline KV type (int8: per-(block, head) fp16 scales; int8ref: the reference's "
                          "kv_update_int8 rows, per-(token, head) fp32 scales)")
-    ap.add_argument("--also", choices=["fp16", "int8", "none"], default="fp16", help="second KV type reported beside")
+    ap.add_argument("--also", choices=["fp16", "int8", "fp32", "none"], default="fp16",
+                    help="second KV type reported beside")
     ap.add_argument("--seqs", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=8192)
     ap.add_argument("--layers", type=int, default=32)
@@ -135,7 +136,7 @@ def measured_traffic(kernel: str, S: int, L: int, H: int, Hkv: int, ragged: bool
 
 
 def run_gpu(ctx, args, kv_name: str):
-    kv = {"int8": velokv.KV_I8_BLK, "int8ref": velokv.KV_I8_REF}.get(kv_name, velokv.KV_F16)
+    kv = {"int8": velokv.KV_I8_BLK, "int8ref": velokv.KV_I8_REF, "fp32": velokv.KV_F32}.get(kv_name, velokv.KV_F16)
     S, H, Hkv, L, NL = args.seqs, args.heads, args.kv_heads, args.ctx, args.layers
     if args.ragged:
         lens = synth.rng(2024).integers(1024, L + 1, S).astype(np.int32)
@@ -272,7 +273,7 @@ def run_gpu(ctx, args, kv_name: str):
         pairs = pairs[:len(free) // 2] if len(free) < 2 * n else pairs
         ctx.copy_blocks(pool, pairs.astype(np.int32))
         ctx.sync()
-        desc_tile = HD * BS * {velokv.KV_F16: 2}.get(kv, 1)
+        desc_tile = HD * BS * {velokv.KV_F16: 2, velokv.KV_F32: 4}.get(kv, 1)
         sc = {velokv.KV_I8_BLK: 2}.get(kv, 0)
         res["calibration_copy_bytes_read"] = int(len(pairs) * NL * 2 * Hkv * (desc_tile + sc))
     del pool
@@ -685,16 +686,19 @@ def main():
         f32 = copy.copy(args)
         f32.q_dtype, f32.steps, f32.warmup = "fp32", min(args.steps, 10), min(args.warmup, 2)
         configs["headline_int8_fp32q"] = run_gpu(ctx, f32, "int8")
+        # the reference's default cache type (fp32 K/V, fp32 q) at the headline shape
+        configs["config1_fp32_kv"] = run_gpu(ctx, f32, "fp32")
     cpu = None if args.no_cpu else cpu_baseline(args)
     workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=128, bs=16, %s KV, %d layers, %sappend+decode per layer, pool %d blocks" %
                 (args.seqs, "U[1024,%d]" % args.ctx if args.ragged else str(args.ctx), args.heads, args.kv_heads,
-                 {"int8": "INT8 per-(block,head) fp16-scale", "int8ref": "INT8 per-(token,head) fp32-scale (reference rows)"}.get(args.kv, "fp16"), args.layers,
+                 {"int8": "INT8 per-(block,head) fp16-scale", "int8ref": "INT8 per-(token,head) fp32-scale (reference rows)",
+                  "fp32": "fp32"}.get(args.kv, "fp16"), args.layers,
                  "" if args.rope == "none" else "RoPE(%s)+" % args.rope, args.pool_blocks))
     line = {
         "metric": "paged decode-attn achieved HBM GB/s (% peak) + tokens/s, B=64 ctx=8k, fp16/INT8 KV",
         "value": head["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "i8" if args.kv.startswith("int8") else "f16",
+        "dtype": "i8" if args.kv.startswith("int8") else {"fp32": "f32"}.get(args.kv, "f16"),
         "data": "synthetic (seeded SplitMix64 normals, 1% outlier channels x8 for INT8, random block scatter)",
         "config": {"workload": workload, "global_batch": args.seqs, "seq_len": args.ctx, "parallelism": "single GPU"},
         "tokens_per_s": head["tokens_per_s"], "frac_of_peak": head["frac_of_peak"],

@@ -112,22 +112,23 @@ int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
  * flags (*flags = the flags read; NULL to skip): VK_OK when none were set. */
 int vk_ctx_check(vk_ctx* ctx, uint32_t* flags);
 
-/* Kernel family of vk_paged_decode over fp16/int8 KV: VK_DECODE_MFMA (QK and
- * PV on v_mfma_f32_16x16x{32,16}_f16; an fp32 q is split into fp16 hi + lo
- * parts), VK_DECODE_VALU (v_dot2_f32_f16, or fp32 arithmetic for an fp32 q, on
- * the vector ALUs) or VK_DECODE_AUTO (MFMA for int8 KV and for fp32 queries,
- * VALU for fp16 queries over fp16 KV with fixed partitions: the faster one on
- * MI355X for each; stream-K batches run on the matrix cores). fp32 KV always
- * uses the fp32 VALU kernel. No reference counterpart. */
+/* Kernel family of vk_paged_decode: VK_DECODE_MFMA (QK and PV on
+ * v_mfma_f32_16x16x{32,16}_f16 over fp16 / int8 KV, where an fp32 q is split
+ * into fp16 hi + lo parts; on v_mfma_f32_16x16x4_f32 in fp32 throughout over
+ * fp32 KV), VK_DECODE_VALU (v_dot2_f32_f16, or fp32 arithmetic for an fp32 q or
+ * fp32 KV, on the vector ALUs; GQA group sizes 1, 2, 4, 8) or VK_DECODE_AUTO
+ * (MFMA for int8 and fp32 KV and for fp32 queries, VALU for fp16 queries over
+ * fp16 KV with fixed partitions: the faster one on MI355X for each; stream-K
+ * batches run on the matrix cores). No reference counterpart. */
 #define VK_DECODE_AUTO 0
 #define VK_DECODE_VALU 1
 #define VK_DECODE_MFMA 2
 int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
 
-/* Work schedule of vk_paged_decode for fp16 queries over fp16 / int8 KV when
- * partition_tokens is 0: VK_SCHED_SPLIT (units = fixed context partitions, sized
- * to fill one round of resident waves; kernel family per
- * vk_ctx_set_decode_kernel; over int8 KV with the matrix cores, a batch whose
+/* Work schedule of vk_paged_decode when partition_tokens is 0: VK_SCHED_SPLIT
+ * (units = fixed context partitions, sized to fill one round of resident waves;
+ * kernel family per vk_ctx_set_decode_kernel; over int8 or fp32 KV with the
+ * matrix cores, a batch whose
  * (sequence, KV head) pairs fill the GPU with at most 8 waves each runs one
  * workgroup per pair instead, its waves splitting the context and combining in
  * LDS, with no merge launch and no workspace), VK_SCHED_STREAM (stream-K on the matrix cores: one
@@ -137,7 +138,7 @@ int vk_ctx_set_decode_kernel(vk_ctx* ctx, int kind);
  * (sequence, KV head) pairs, longest first, are dealt to the workgroups in snake
  * order so each gets a nearly equal share of blocks, and the waves of a workgroup
  * split its blocks evenly and combine split pairs in LDS: no merge launch and no
- * workspace; at most 256 sequences, else stream-K) or VK_SCHED_AUTO (stream-K
+ * workspace; fp16 / int8 KV, at most 256 sequences, else stream-K) or VK_SCHED_AUTO (stream-K
  * unless vk_decode_args.sum_context_len says the batch is uniform, or the VALU
  * family was requested). A nonzero partition_tokens always uses fixed partitions. No
  * reference counterpart. */
@@ -254,10 +255,10 @@ int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q, int32_t q
 typedef struct vk_decode_args {
   int32_t layer;
   const void* q;              /* dev [S][n_heads][head_dim] of q_dtype         */
-  int32_t q_dtype;            /* VK_DT_F16: fp16 q. VK_DT_F32: the matrix-core
-                                 kernels split q into fp16 hi + lo (scores see q
-                                 to ~2^-22); the VALU kernels (fp32 KV,
-                                 VK_DECODE_VALU) use fp32 math */
+  int32_t q_dtype;            /* VK_DT_F16: fp16 q. VK_DT_F32: over fp16 / int8
+                                 KV the matrix-core kernels split q into fp16
+                                 hi + lo (scores see q to ~2^-22); over fp32 KV
+                                 and in the VALU kernels fp32 math */
   float* out;                 /* dev fp32 [S][n_heads][head_dim]               */
   const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = the pool's slot table */
   int32_t bt_stride;          /* ignored when block_tables is NULL             */
@@ -342,7 +343,9 @@ int vk_paged_decode_noalloc(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a,
 typedef struct vk_tree_args {
   int32_t layer;
   const void* q;              /* dev [S][n_nodes][n_heads][head_dim] of q_dtype */
-  int32_t q_dtype;            /* VK_DT_F16, or VK_DT_F32 (rounded to fp16 for the matrix cores) */
+  int32_t q_dtype;            /* VK_DT_F16, or VK_DT_F32 (rounded to fp16 for the
+                                 fp16 / int8 matrix-core kernels, kept in fp32
+                                 over fp32 KV) */
   float* out;                 /* dev fp32 [S][n_nodes][n_heads][head_dim]       */
   const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = slot table        */
   int32_t bt_stride;
@@ -371,7 +374,7 @@ typedef struct vk_tree_args {
  * one partition covers every sequence). */
 int vk_tree_verify_workspace(const vk_pool* pool, const vk_tree_args* a, uint64_t* bytes);
 
-/* Multi-query tree-verify attention over fp16 or int8 pools: query row (node i,
+/* Multi-query tree-verify attention over fp32, fp16 or int8 pools: query row (node i,
  * head h) attends to the committed context (positions 0..context_len-1) and to
  * the tree nodes j its mask row selects (position context_len + j). Build
  * tree_mask with vk_tree_mask (ancestors and the node itself).

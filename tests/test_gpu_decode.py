@@ -208,7 +208,7 @@ def test_decode_workspace_reuse_across_layouts(ctx, impl):
             check(out.download((S, 32, HD), np.float32), ref[:S], f"S={S} P={P} own_ws={ws is not None}")
 
 
-@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("shape", ["mixed", "many_small", "wide"])
 @pytest.mark.parametrize("qd", [np.float16, np.float32])
 def test_decode_streamk_worker_boundaries(ctx, kv, shape, qd):
@@ -242,7 +242,7 @@ def test_decode_streamk_worker_boundaries(ctx, kv, shape, qd):
         ctx.set_decode_schedule(velokv.SCHED_AUTO)
 
 
-@pytest.mark.parametrize("kv", [O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("kv", [O.F32, O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("S,G,nw", [(256, 4, 1), (128, 4, 2), (64, 4, 4), (32, 8, 8)])
 @pytest.mark.parametrize("qd", [np.float16, np.float32])
 def test_decode_workgroup_split(ctx, kv, S, G, nw, qd):

@@ -39,7 +39,7 @@ def decode(ctx, pool, case, qd, kind, sched, P):
     return pl, out.download((S, H, HD), np.float32)
 
 
-@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("G", [3, 5, 6, 7, 12, 16, 24, 32])
 @pytest.mark.parametrize("qd", [np.float16, np.float32])
 def test_decode_any_group_size(ctx, kv, G, qd):
@@ -87,7 +87,7 @@ def test_decode_any_group_workgroup_split_and_append_decode(ctx, G):
     assert ok, (err, nbad)
 
 
-@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("G,N", [(3, 8), (6, 5), (16, 2), (12, 8), (40, 1)])
 def test_tree_any_group_size(ctx, kv, G, N):
     print(f"gqa tree kv={kv} G={G} N={N}", flush=True)
@@ -146,6 +146,4 @@ def test_group_size_limits(ctx):
         ctx.decode_plan(pool, 1, 66, 40, bt_stride=case.block_tables.shape[1])
     assert e.value.code == velokv.ERR_UNSUPPORTED
     f32 = velokv.Pool(ctx, 1, 8, BS, 2, HD, O.F32)
-    with pytest.raises(velokv.VkError) as e:
-        ctx.decode_plan(f32, 1, 6, 40, bt_stride=4)  # G = 3 over fp32 KV
-    assert e.value.code == velokv.ERR_UNSUPPORTED
+    assert ctx.decode_plan(f32, 1, 6, 40, bt_stride=4)["kernel"].startswith("vk_decode_")  # G = 3 over fp32 KV

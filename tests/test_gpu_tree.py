@@ -14,7 +14,7 @@ from velokv import synth
 
 pytestmark = pytest.mark.gpu
 
-KV_TREE = [O.F16, O.I8_REF, O.I8_BLK]
+KV_TREE = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
 
 
 def run_tree(ctx, pool, case, q, committed, mask, q_dtype=np.float16, partition_tokens=0, block_tables=None,
@@ -92,7 +92,7 @@ def test_tree_row_tiles_and_random_masks(ctx, kv, G, N):
     assert np.all(got[0, 0] == 0.0)
 
 
-@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_BLK])
 @pytest.mark.parametrize("P", [16, 64, 256, 1024, 0])
 def test_tree_split_k(ctx, kv, P):
     print(f"tree split kv={kv} P={P}", flush=True)
@@ -146,11 +146,6 @@ def test_tree_bad_arguments(ctx):
         ctx.tree_verify(pool, 0, q, velokv.DT_F16, out, cl, None, 1, 8, case.n_heads, 10, block_tables=bt,
                         bt_stride=stride)
     assert e.value.code == velokv.ERR_BAD_ARG
-    f32 = velokv.Pool(ctx, 1, 8, BS, case.n_kv_heads, HD, O.F32)
-    with pytest.raises(velokv.VkError) as e:
-        ctx.tree_verify(f32, 0, q, velokv.DT_F16, out, cl, mk, 1, 8, case.n_heads, 10, block_tables=bt,
-                        bt_stride=stride)
-    assert e.value.code == velokv.ERR_UNSUPPORTED
 
 
 def config4_flow(ctx, kv, S, prefix_len, max_suffix, N, seed, Hkv=8, G=4, n_layer=1, layer=0):
@@ -230,7 +225,7 @@ def test_config4_flow_reduced(ctx, kv, prefix_len):
 
 # ---- shared-prefix pass (vk_tree_args.shared_blocks) --------------------------
 
-@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16, O.I8_REF])
+@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16, O.I8_REF, O.F32])
 @pytest.mark.parametrize("prefix_len,S", [(4096, 64), (4100, 16)])
 def test_tree_shared_prefix_flow(ctx, kv, prefix_len, S):
     """Config-4 flow with the shared prefix declared: the prefix pass over the

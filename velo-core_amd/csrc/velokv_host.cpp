@@ -254,38 +254,27 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
     return fail(VK_ERR_NOT_WIRED, "hipModuleLoad(%s) failed: %s", path.c_str(), hipGetErrorString(e));
   }
   std::vector<std::string> names(std::begin(kKernelNames), std::end(kKernelNames));
-  for (int kv = 1; kv < 4; ++kv) {  // the runtime-group-size ("_gx") kernels
+  for (int kv = 0; kv < 4; ++kv) {  // the runtime-group-size ("_gx") kernels
     for (int qt : {VK_DT_F16, VK_DT_F32}) {
       names.push_back(decode_mfma_name(kv, 3, qt));
       names.push_back(decode_mfma_name(kv, kMaxGroup, qt));
       names.push_back(decode_sk_name(kv, 3, qt));
       if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, 3, qt));
-      if (kv != VK_KV_I8_REF) names.push_back(tree_pfx_name(kv, 3, qt));
+      if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt));
       for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt));
     }
   }
   for (int kv = 0; kv < 4; ++kv)
     for (int g : {1, 2, 4, 8}) {
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
-      if (kv != VK_KV_F32) names.push_back(decode_mfma_name(kv, g));
-      if (kv != VK_KV_F32) names.push_back(decode_sk_name(kv, g));
-      if (kv != VK_KV_F32) {
-        names.push_back(decode_pk_name(kv, g));
-        names.push_back(decode_pk_name(kv, g, VK_DT_F32));
+      for (int qt : {VK_DT_F16, VK_DT_F32}) {
+        names.push_back(decode_mfma_name(kv, g, qt));
+        names.push_back(decode_sk_name(kv, g, qt));
+        if (kv != VK_KV_F32) names.push_back(decode_pk_name(kv, g, qt));
+        if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, g, qt));
       }
-      if (kv == VK_KV_F16) {
-        names.push_back(decode_sk_name(kv, g, VK_DT_F32));
-        names.push_back(decode_mfma_name(kv, g, VK_DT_F32));
-      }
-      if (kv == VK_KV_I8_REF || kv == VK_KV_I8_BLK) {
-        names.push_back(decode_wg_name(kv, g));
-        names.push_back(decode_wg_name(kv, g, VK_DT_F32));
-        names.push_back(decode_sk_name(kv, g, VK_DT_F32));
-        names.push_back(decode_mfma_name(kv, g, VK_DT_F32));
-      }
-      if (kv != VK_KV_F32)
-        for (int rt : {1, 2})
-          for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
+      for (int rt : {1, 2})
+        for (int qt = 0; qt < 2; ++qt) names.push_back(tree_name(kv, g, rt, qt));
       if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK)
         for (int qt = 0; qt < 2; ++qt) names.push_back(tree_pfx_name(kv, g, qt));
     }
@@ -653,16 +642,15 @@ struct DecodePlan {
   uint64_t acc_bytes, ml_bytes, prefix_bytes;
 };
 
-// Schedule and kernel family for these arguments. fp32 KV takes the fp32 VALU
-// kernel with fixed partitions. Otherwise (an fp32 q is split into fp16 hi + lo
-// for the matrix cores) stream-K when requested, or under AUTO unless the batch
-// is known to be uniform or the VALU family was requested; fixed partitions run
-// the matrix cores for int8 KV and for fp32 queries, and the dot2 VALU kernel
-// for fp16 queries over fp16 KV under AUTO (measured faster for each; the VALU
-// kernels compute an fp32 q in fp32 and at GQA 8 spill).
+// Schedule and kernel family for these arguments: stream-K when requested, or
+// under AUTO unless the batch is known to be uniform or the VALU family was
+// requested; fixed partitions run the matrix cores for int8 and fp32 KV and for
+// fp32 queries, and the dot2 VALU kernel for fp16 queries over fp16 KV under
+// AUTO (measured faster for each; the VALU kernels compute an fp32 q in fp32
+// and at GQA 8 spill). Over fp16 / int8 KV an fp32 q is split into fp16 hi + lo
+// for the matrix cores; over fp32 KV the matrix cores take q, K, p and V in fp32.
 void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, bool* stream_k, bool* mfma) {
   const vk_pool_desc& d = pool->desc;
-  const bool fast = d.kv_type != VK_KV_F32;
   const int kind = ctx ? ctx->decode_kind : VK_DECODE_AUTO;
   const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
   const bool uniform = a->sum_context_len > 0 &&
@@ -671,10 +659,10 @@ void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args*
   // the VALU kernels exist for group sizes 1, 2, 4, 8 only: other sizes always
   // take the matrix cores, and beyond one 16-row tile only fixed partitions
   const bool valu_ok = fixed_group(G);
-  *stream_k = fast && a->partition_tokens == 0 && (kind != VK_DECODE_VALU || !valu_ok) && G <= kMaxGroupTile &&
+  *stream_k = a->partition_tokens == 0 && (kind != VK_DECODE_VALU || !valu_ok) && G <= kMaxGroupTile &&
               (sched == VK_SCHED_STREAM || sched == VK_SCHED_PACKED || (sched == VK_SCHED_AUTO && !uniform));
-  *mfma = *stream_k || (fast && (!valu_ok || kind == VK_DECODE_MFMA ||
-                                 (kind == VK_DECODE_AUTO && (d.kv_type != VK_KV_F16 || a->q_dtype == VK_DT_F32))));
+  *mfma = *stream_k || !valu_ok || kind == VK_DECODE_MFMA ||
+          (kind == VK_DECODE_AUTO && (d.kv_type != VK_KV_F16 || a->q_dtype == VK_DT_F32));
 }
 
 // Smallest partition (256..4096 tokens) whose units fit in one round of resident
@@ -695,8 +683,6 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   if (a->n_heads % d.n_kv_heads) return fail(VK_ERR_BAD_ARG, "n_heads %d not a multiple of n_kv_heads %d", a->n_heads, d.n_kv_heads);
   const int G = a->n_heads / d.n_kv_heads;
   if (G > kMaxGroup) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (decode supports up to %d)", G, kMaxGroup);
-  if (!fixed_group(G) && d.kv_type == VK_KV_F32)
-    return fail(VK_ERR_UNSUPPORTED, "GQA group size %d over fp32 KV (the fp32 kernels take 1, 2, 4, 8)", G);
   if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
   pl->bt = a->block_tables;
   pl->bt_stride = a->bt_stride;
@@ -721,7 +707,8 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   pl->packed = false;
   pl->max_wave_blocks = 0;
   const int sched = ctx ? ctx->decode_sched : VK_SCHED_AUTO;
-  if (pl->stream_k && sched == VK_SCHED_PACKED && fixed_group(G) && a->n_seqs > 0 && a->n_seqs <= kPkMaxSeqs) {
+  if (pl->stream_k && sched == VK_SCHED_PACKED && fixed_group(G) && d.kv_type != VK_KV_F32 && a->n_seqs > 0 &&
+      a->n_seqs <= kPkMaxSeqs) {
     // Packed workgroup split: one workgroup per resident slot (n_workers bins), the
     // batch's (sequence, KV head) items dealt to them longest first in snake
     // order, so that they fill the GPU, each workgroup gets at most kPkMaxRounds
@@ -764,7 +751,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     return VK_OK;
   }
   pl->wg_waves = 0;
-  if (mfma && P == 0 && G <= kMaxGroupTile && (d.kv_type == VK_KV_I8_REF || d.kv_type == VK_KV_I8_BLK)) {
+  if (mfma && P == 0 && G <= kMaxGroupTile && d.kv_type != VK_KV_F16) {
     // Workgroup split: NW waves per (sequence, KV head), the smallest power of two
     // whose workgroups fill one round of resident waves, when each wave's share
     // fits its four block-id windows (256 blocks).
@@ -1005,7 +992,6 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
   if (a->n_heads % d.n_kv_heads) return fail(VK_ERR_BAD_ARG, "n_heads %d not a multiple of n_kv_heads %d", a->n_heads, d.n_kv_heads);
   const int G = a->n_heads / d.n_kv_heads;  // any group size: rows of (node, head) in 16-row tiles
   if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
-  if (d.kv_type == VK_KV_F32) return fail(VK_ERR_UNSUPPORTED, "tree verify reads fp16 or int8 KV pools, not fp32");
   pl->bt = a->block_tables;
   pl->bt_stride = a->bt_stride;
   pl->bt_rows = 0;

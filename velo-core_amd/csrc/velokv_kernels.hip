@@ -1070,6 +1070,227 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   }
 }
 
+// =============================================================================
+// fp32 KV on the matrix cores (v_mfma_f32_16x16x4f32): the unit, partials and
+// schedules of attn_piece, with q, K, p and V in fp32 end to end, as the
+// reference computes over its default fp32 cache (kernels.metal:440-501,
+// llama_cpu.rs:251-284). One block per pipeline stage (8 KB of K, 8 KB of V).
+//   scores  S^T[t][r] in 32 instructions of 4 dims: lane (n, g) feeds K[token n]
+//           and q[row n] at dims 16 j + 4 g + e (instruction 4 j + e), read as 8
+//           16-byte pieces of the token row (the 4 lanes of a token cover 64
+//           contiguous bytes per load), and gets S^T[tokens 4g..4g+3][row n]: the
+//           layout of attn_piece, so the softmax is the same.
+//   values  out[r][d] += sum_t p[r][t] V[t][d] in 4 instructions of 4 tokens per
+//           16-dim tile: instruction i takes tokens 4 g + i, so A = the lane's own
+//           p[row n][token 4 g + i]; B = V[token 4 g + i][dim 16 tile + n], from
+//           the token pairs 2 g and 2 g + 1 (one 8-byte load each per tile, 128
+//           contiguous bytes per 16 lanes); lane (n, g) accumulates rows 4g..4g+3,
+//           dim 16 tile + n.
+// =============================================================================
+struct F32Stage {
+  u32x4 k[8];      // token n, dims 16 j + 4 g .. + 3
+  u32x2 v[8][2];   // tile t, token pair 2 g + r: dim 16 t + n of its two tokens
+};
+
+DEV void f32_stage_load(F32Stage& st, const DecodeParams& P, const BlockIds& bw, int i, int nblk, int kvh, int n,
+                        int g) {
+  const int blk = window_at(bw.b, min(i, nblk - 1));
+  const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
+  const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
+  const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, n * 512 + (4 * j + g) * 16, 0, 0);
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      st.v[t][r] = __builtin_amdgcn_raw_buffer_load_b64(vr, (((2 * g + r) * HD + 16 * t + n) * 2) * 4, 0, kAuxNT);
+}
+
+template <int G, int RT, bool TREE, int QT>
+DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
+                        int64_t pbase, int pstride, float* pacc, float* pml) {
+  const int lane = lane_id();
+  const int n = lane & 15, g = lane >> 4;
+  const int N = TREE ? P.n_nodes : 1;
+  int row = P.seq_rows ? P.seq_rows[s] : s;
+  if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
+  const int32_t* bt = P.block_tables + (int64_t)row * P.bt_stride;
+  const int H = P.n_heads;
+  const int nblk = (end - start + BS - 1) / BS;
+  const int blk0 = start / BS;
+  const int Gn = group_size<G>(P);
+  const int nrows = N * Gn;
+  const int row0 = rg * 16 * RT;
+  const int plain_end = min(end, ctx_c);
+  auto out_row = [&](int R) -> int64_t { return ((int64_t)s * N + R / Gn) * H + (int64_t)kvh * Gn + R % Gn; };
+
+  BlockIds bw;
+  load_block_ids<false>(bw, P, bt, blk0, nblk, kvh);
+  F32Stage sa, sb;
+  f32_stage_load(sa, P, bw, 0, nblk, kvh, n, g);
+
+  // q of row n of each tile at the lane's dims 16 j + 4 g + e (rows past the end are 0)
+  float qf[RT][32];
+  uint32_t mrow[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int R = row0 + 16 * rt + n;
+    const int64_t qoff = (R < nrows ? out_row(R) : 0) * HD + 4 * g;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (R < nrows) {
+        if constexpr (QT == DT_F32) {
+          x = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 16 * j);
+        } else {
+          const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(P.q) + qoff + 16 * j);
+          x = make_float4(half_lo(h.x), half_hi(h.x), half_lo(h.y), half_hi(h.y));
+        }
+      }
+      qf[rt][4 * j] = x.x; qf[rt][4 * j + 1] = x.y; qf[rt][4 * j + 2] = x.z; qf[rt][4 * j + 3] = x.w;
+    }
+    mrow[rt] = 0u;
+    if constexpr (TREE) {
+      if (R < nrows) mrow[rt] = P.tree_mask[(int64_t)s * N + R / Gn];
+    }
+  }
+
+  float M[RT], lrun[RT];
+  float4v acc[RT][8];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    M[rt] = kNegInf; lrun[rt] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[rt][t] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
+  const int last_valid = (end - start) - (nblk - 1) * BS;
+
+  auto compute = [&](const F32Stage& st, int i) {
+    float4v sc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) sc[rt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          sc[rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(bitcast<float>(st.k[j][e]), qf[rt][4 * j + e], sc[rt], 0, 0, 0);
+    const bool plain = (i < nblk) && (start + (i + 1) * BS <= plain_end);
+    float sv[RT][4];
+    bool need = false;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = sc[rt][r] * P.scale_log2;
+        if (!plain) {
+          const int tpos = start + i * BS + 4 * g + r;
+          bool ok = (i < nblk) && tpos < end;
+          if constexpr (TREE) {
+            const int j = tpos - ctx_c;
+            ok = ok && (j < 0 || ((mrow[rt] >> (j & 31)) & 1u));
+          }
+          x = ok ? x : kNegInf;
+        }
+        sv[rt][r] = x;
+        need |= x > M[rt] + kRescaleThreshold;
+      }
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        float m = fmaxf(fmaxf(sv[rt][0], sv[rt][1]), fmaxf(sv[rt][2], sv[rt][3]));
+        m = fmaxf(m, shfl_xor(m, 16));
+        m = fmaxf(m, shfl_xor(m, 32));
+        const float Mn = fmaxf(M[rt], m);
+        const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[rt] - Mn);
+        M[rt] = Mn;
+        lrun[rt] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float ar = __shfl(alpha, 4 * g + r, WAVE);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) acc[rt][t][r] *= ar;
+        }
+      }
+    }
+    float p[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[rt][r] = __builtin_amdgcn_exp2f(sv[rt][r] - Ms);
+        lrun[rt] += p[rt][r];
+      }
+    }
+    if (i < nblk) {
+      const bool partial = (i == nblk - 1) && (last_valid < BS);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        float vv[4] = {bitcast<float>(st.v[t][0].x), bitcast<float>(st.v[t][0].y), bitcast<float>(st.v[t][1].x),
+                       bitcast<float>(st.v[t][1].y)};
+        if (partial) {  // bytes past the context may be anything, NaN included
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vv[r] = (4 * g + r < last_valid) ? vv[r] : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[rt][r], vv[r], acc[rt][t], 0, 0, 0);
+      }
+    }
+  };
+
+  for (int b = 0; b < nblk; b += 2) {
+    f32_stage_load(sb, P, bw, b + 1, nblk, kvh, n, g);
+    compute(sa, b);
+    if (b + 1 >= nblk) break;
+    f32_stage_load(sa, P, bw, b + 2, nblk, kvh, n, g);
+    compute(sb, b + 1);
+  }
+
+  // ---- partials: acc rows 16 rt + 4g + r, dims 16 t + n ----
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float l = lrun[rt];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int src = 4 * g + r;
+      const float lr = __shfl(l, src, WAVE);
+      const float Mr = __shfl(M[rt], src, WAVE);
+      const int R = row0 + 16 * rt + 4 * g + r;
+      if (R < nrows) {
+        const int64_t orow = out_row(R);
+        if (direct) {
+          const float inv = lr > 0.f ? 1.f / lr : 0.f;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) P.out[orow * HD + 16 * t + n] = acc[rt][t][r] * inv;
+        } else {
+          const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) pacc[pr * HD + 16 * t + n] = acc[rt][t][r];
+          if (n == 0) reinterpret_cast<float2*>(pml)[pr] = make_float2(Mr, lr);
+        }
+      }
+    }
+  }
+}
+
+// attn_piece for every KV type: fp32 pools take the fp32 matrix-core piece.
+template <int KV, int G, int RT, bool TREE, int QT>
+DEV void attn_piece_kv(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
+                       int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
+  if constexpr (KV == KV_F32)
+    attn_piece_f32<G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml);
+  else
+    attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
+}
+
 // Split-K entry: unit = (row group, KV head, partition, sequence), kv head
 // fastest. Partitions that start past the context exit; an empty decode context
 // writes zero rows.
@@ -1108,7 +1329,7 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   // the rest of a context in one partition after a shared prefix writes the
   // output itself, folding in the prefix partials
   const bool fold = C0 > 0 && nparts == C0 + 1;
-  attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1 || fold, pbase, P.max_parts, P.part_acc,
+  attn_piece_kv<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1 || fold, pbase, P.max_parts, P.part_acc,
                                   P.part_ml, fold ? C0 : 0);
 }
 
@@ -1207,8 +1428,8 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     sk_piece(seg0, nb, pen, x, c1, &o0, &o1);
     if (o0 < o1) {
       const int slot = o0 > 0 ? 0 : 1;
-      attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                      ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc, P.part_ml);
+      attn_piece_kv<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
+                                         ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc, P.part_ml);
     }
     x = seg0 + su;
     if (kvh == Hkv - 1) {
@@ -1247,8 +1468,8 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   const int per = (nb + nw - 1) / nw;
   const int b0 = min(nb, w * per), b1 = min(nb, b0 + per);
   if (b0 < b1) {
-    attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
-                                    &wml[w][0][0]);
+    attn_piece_kv<KV, G, 1, false, QT>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
+                                       &wml[w][0][0]);
   } else if (lane < Gn) {
     wml[w][lane][0] = kNegInf;
     wml[w][lane][1] = 0.f;
@@ -1339,8 +1560,8 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
         if (o0 < o1) {
           const int ctx_s = max(0, min(P.context_lens[s], P.cap_tokens));
           const int slot = o0 > 0 ? 0 : 1;
-          attn_piece<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb, 0,
-                                          1, &wacc[w][slot][0][0], &wml[w][slot][0][0]);
+          attn_piece_kv<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
+                                             0, 1, &wacc[w][slot][0][0], &wml[w][slot][0][0]);
         }
         u += nb + pen;
       }
@@ -2584,8 +2805,8 @@ VK_DECODE_G(3, 0) VK_DECODE_G(3, 1)
     attn_unit_mfma<KV, G, 1, false>(P);                                             \
   }
 #define VK_DECODE_MFMA_G(KV) VK_DECODE_MFMA(KV, 1) VK_DECODE_MFMA(KV, 2) VK_DECODE_MFMA(KV, 4) VK_DECODE_MFMA(KV, 8)
-VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
-// fp32 q (split into fp16 hi + lo) over fp16 / int8 KV: suffix _q0
+VK_DECODE_MFMA_G(0) VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
+// fp32 q (split into fp16 hi + lo over fp16 / int8 KV, fp32 over fp32 KV): suffix _q0
 #define VK_DECODE_MFMA_Q0(KV, G)                                                    \
   extern "C" __global__ void __launch_bounds__(64)                                  \
       vk_decode_mfma_kv##KV##_g##G##_q0(const DecodeParams P) {                     \
@@ -2593,7 +2814,7 @@ VK_DECODE_MFMA_G(1) VK_DECODE_MFMA_G(2) VK_DECODE_MFMA_G(3)
   }
 #define VK_DECODE_MFMA_Q0_G(KV) \
   VK_DECODE_MFMA_Q0(KV, 1) VK_DECODE_MFMA_Q0(KV, 2) VK_DECODE_MFMA_Q0(KV, 4) VK_DECODE_MFMA_Q0(KV, 8)
-VK_DECODE_MFMA_Q0_G(1) VK_DECODE_MFMA_Q0_G(2) VK_DECODE_MFMA_Q0_G(3)
+VK_DECODE_MFMA_Q0_G(0) VK_DECODE_MFMA_Q0_G(1) VK_DECODE_MFMA_Q0_G(2) VK_DECODE_MFMA_Q0_G(3)
 
 // Workgroup-split decode: up to kWgMaxWaves waves of 64 per workgroup.
 #define VK_DECODE_WG(KV, G)                                                         \
@@ -2602,14 +2823,14 @@ VK_DECODE_MFMA_Q0_G(1) VK_DECODE_MFMA_Q0_G(2) VK_DECODE_MFMA_Q0_G(3)
     attn_wg_mfma<KV, G>(P);                                                         \
   }
 #define VK_DECODE_WG_G(KV) VK_DECODE_WG(KV, 1) VK_DECODE_WG(KV, 2) VK_DECODE_WG(KV, 4) VK_DECODE_WG(KV, 8)
-VK_DECODE_WG_G(2) VK_DECODE_WG_G(3)
+VK_DECODE_WG_G(0) VK_DECODE_WG_G(2) VK_DECODE_WG_G(3)
 #define VK_DECODE_WG_Q0(KV, G)                                                      \
   extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves)                    \
       vk_decode_wg_kv##KV##_g##G##_q0(const DecodeParams P) {                       \
     attn_wg_mfma<KV, G, DT_F32>(P);                                                 \
   }
 #define VK_DECODE_WG_Q0_G(KV) VK_DECODE_WG_Q0(KV, 1) VK_DECODE_WG_Q0(KV, 2) VK_DECODE_WG_Q0(KV, 4) VK_DECODE_WG_Q0(KV, 8)
-VK_DECODE_WG_Q0_G(2) VK_DECODE_WG_Q0_G(3)
+VK_DECODE_WG_Q0_G(0) VK_DECODE_WG_Q0_G(2) VK_DECODE_WG_Q0_G(3)
 
 // Packed workgroup split (ragged batches): up to kWgMaxWaves waves of 64.
 #define VK_DECODE_PK(KV, G, QT, SUF)                                                \
@@ -2630,14 +2851,14 @@ VK_DECODE_PK_G(1, DT_F32, _q0) VK_DECODE_PK_G(2, DT_F32, _q0) VK_DECODE_PK_G(3, 
     attn_streamk_mfma<KV, G>(P);                                                    \
   }
 #define VK_DECODE_SK_G(KV) VK_DECODE_SK(KV, 1) VK_DECODE_SK(KV, 2) VK_DECODE_SK(KV, 4) VK_DECODE_SK(KV, 8)
-VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
+VK_DECODE_SK_G(0) VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
 #define VK_DECODE_SK_Q0(KV, G)                                                      \
   extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
       vk_decode_sk_kv##KV##_g##G##_q0(const DecodeParams P) {                       \
     attn_streamk_mfma<KV, G, DT_F32>(P);                                            \
   }
 #define VK_DECODE_SK_Q0_G(KV) VK_DECODE_SK_Q0(KV, 1) VK_DECODE_SK_Q0(KV, 2) VK_DECODE_SK_Q0(KV, 4) VK_DECODE_SK_Q0(KV, 8)
-VK_DECODE_SK_Q0_G(1) VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
+VK_DECODE_SK_Q0_G(0) VK_DECODE_SK_Q0_G(1) VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
 
 // Tree verify: RT tiles of 16 (node, head) rows per wave. Over int8 pools the
 // kernels are held to 256 registers (two waves per SIMD) without spills; the fp16
@@ -2651,6 +2872,7 @@ VK_DECODE_SK_Q0_G(1) VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
   VK_TREE(KV, 1, RT, QT, ATTR) VK_TREE(KV, 2, RT, QT, ATTR) VK_TREE(KV, 4, RT, QT, ATTR) VK_TREE(KV, 8, RT, QT, ATTR)
 #define VK_TREE_KV(KV, ATTR) \
   VK_TREE_G(KV, 1, 0, ATTR) VK_TREE_G(KV, 1, 1, ATTR) VK_TREE_G(KV, 2, 0, ATTR) VK_TREE_G(KV, 2, 1, ATTR)
+VK_TREE_KV(0, )
 VK_TREE_KV(1, )
 VK_TREE_KV(2, VK_TWO_WAVES)
 VK_TREE_KV(3, VK_TWO_WAVES)
@@ -2676,7 +2898,7 @@ VK_TREE_KV(3, VK_TWO_WAVES)
   extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_q0(const DecodeParams P) { \
     attn_streamk_mfma<KV, 0, DT_F32>(P);                                                                       \
   }
-VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
+VK_GX_DECODE(0) VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
 #define VK_GX_WG(KV)                                                                                            \
   extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx(const DecodeParams P) { \
     attn_wg_mfma<KV, 0>(P);                                                                                    \
@@ -2684,14 +2906,14 @@ VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
   extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_q0(const DecodeParams P) { \
     attn_wg_mfma<KV, 0, DT_F32>(P);                                                                            \
   }
-VK_GX_WG(2) VK_GX_WG(3)
+VK_GX_WG(0) VK_GX_WG(2) VK_GX_WG(3)
 #define VK_GX_TREE(KV, RT, QT, ATTR)                                                                            \
   extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_r##RT##_q##QT(const DecodeParams P) { \
     attn_unit_mfma<KV, 0, RT, true, QT>(P);                                                                    \
   }
 #define VK_GX_TREE_KV(KV, ATTR) \
   VK_GX_TREE(KV, 1, 0, ATTR) VK_GX_TREE(KV, 1, 1, ATTR) VK_GX_TREE(KV, 2, 0, ATTR) VK_GX_TREE(KV, 2, 1, ATTR)
-VK_GX_TREE_KV(1, ) VK_GX_TREE_KV(2, VK_TWO_WAVES) VK_GX_TREE_KV(3, VK_TWO_WAVES)
+VK_GX_TREE_KV(0, ) VK_GX_TREE_KV(1, ) VK_GX_TREE_KV(2, VK_TWO_WAVES) VK_GX_TREE_KV(3, VK_TWO_WAVES)
 
 // Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
 #define VK_TREE_PFX(KV, G, QT)                                                      \
