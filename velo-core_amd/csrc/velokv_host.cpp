@@ -1017,13 +1017,16 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
   int64_t tokens = (int64_t)a->max_context_len + a->n_nodes;
   if (a->shared_blocks > 0 && (d.kv_type == VK_KV_F16 || d.kv_type == VK_KV_I8_BLK)) {
     // One workgroup per (256 query rows, KV head, prefix chunk); the prefix is cut
-    // into chunks of at least 16 pages until the workgroups cover the CUs.
+    // into chunks of at least 16 pages until the workgroups cover the CUs, and of
+    // at most kPfxMaxChunkBlocks pages.
     const int64_t qrows = (int64_t)a->n_seqs * rows;
     pl->pfx_row_tiles = (int32_t)((qrows + kPfxRowsPerGroup - 1) / kPfxRowsPerGroup);
     const int64_t groups = std::max<int64_t>(1, (int64_t)pl->pfx_row_tiles * d.n_kv_heads);
     const int64_t n_cu = ctx ? ctx->n_cu : 256;
     const int64_t max_chunks = std::max(1, a->shared_blocks / 16);
-    pl->prefix_chunks = (int32_t)std::min(max_chunks, std::max<int64_t>(1, (n_cu + groups - 1) / groups));
+    const int64_t min_chunks = (a->shared_blocks + kPfxMaxChunkBlocks - 1) / kPfxMaxChunkBlocks;
+    pl->prefix_chunks = (int32_t)std::max(
+        min_chunks, std::min(max_chunks, std::max<int64_t>(1, (n_cu + groups - 1) / groups)));
     pl->prefix_blocks = a->shared_blocks;
     pl->pfx_kernel = tree_pfx_name(d.kv_type, G, a->q_dtype);
     // the rest of a context: past the prefix, or the last partial page of a

@@ -99,8 +99,12 @@ DEV float dot2(uint32_t a, uint32_t b, float c) {
 DEV float byte_to_f(uint32_t w, int byte) { return (float)(int8_t)((w >> (8 * byte)) & 0xFFu); }
 DEV float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xFFFFu)); }
 DEV float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+// Two fp32 values to an fp16 pair, each rounded to nearest even: one
+// v_cvt_pk_f16_f32.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 DEV uint32_t pack_h2(float a, float b) {
-  return (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+  const f32x2 x = {a, b};
+  return bitcast<uint32_t>(__builtin_convertvector(x, half2v));
 }
 
 template <int KV> struct Esz;
@@ -1623,14 +1627,17 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
 //   scores  16x16x32: A = staged K (token n, dims 32kc + 8g .. +7), B = q^T (row
 //           n, the same dims); lane (n, g) gets row n, tokens 4g..4g+3.
 //   values  16x16x32 over a block pair (u0, u1): the 32 token slots of lane group
-//           g are tokens 4g..4g+3 of u0 then of u1, in A = p~ (row n) and in
+//           g are tokens 4g..4g+3 of u0 then of u1, in A = p (row n) and in
 //           B = staged V (dim 16 nt + n); lane (n, g) accumulates rows 4g..4g+3,
-//           dims 16 nt + n.
+//           dims 16 nt + n. int8 V is staged as fp16 c * v_scale (one rounding),
+//           so the product needs no scale and no bias term.
 //   softmax y = S a + c with a = scale_log2 * k_scale and c = -(1152 sum q) a - M
-//           folded per block, p = 2^y; l and the int8 bias term sum over the
-//           fp16 p pairs with v_dot2 (p~ = p * v_scale in fp16).
+//           folded per block, p = 2^y; l sums the fp16 p pairs with v_dot2.
 // LDS: two stage buffers, one barrier per stage; a loader thread holds the
-// next stage's raw bytes in registers while the current one is consumed.
+// next stage's raw bytes in registers while the current one is consumed. The
+// chunk's page ids and block scales are staged in LDS once at the start, so the
+// loaders take page ids from LDS: a global load of an id would wait for every
+// tile load issued before it (vector loads return in order).
 // gfx950 serves a 16-byte read for lanes {0-7, 16-23} (then
 // {8-15, 24-31}, ...) in one pass over 64 four-byte banks: with lane (n, g)
 // reading row n at word 4g, rows must start 8 (mod 16) words apart for the
@@ -1654,7 +1661,6 @@ template <int KV>
 struct PfxRaw {  // this thread's share of one stage
   uint32_t k[kPfxCH][Esz<KV>::v];  // 4 dims of one K token row (int8: 4 bytes, fp16: 8 bytes)
   uint32_t v[kPfxCH][2];           // tokens 4t..4t+1 and 4t+2..4t+3 of one V dim (int8: 2 bytes each, fp16: 4)
-  uint32_t sc;                     // fp16 bits of a block scale (threads 0 .. 2 kPfxCH - 1, int8 only)
 };
 
 template <int KV, int G, int QT>
@@ -1665,7 +1671,11 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   constexpr float kBias = 1152.0f;
   __shared__ __attribute__((aligned(16))) _Float16 kl[2][kPfxCH][BS * kPfxKPitch];
   __shared__ __attribute__((aligned(16))) _Float16 vl[2][kPfxCH / 2][HD * kPfxVPitch];
-  __shared__ float sl[2][kPfxCH][2];
+  // the chunk's tiles (page id * n_kv_heads + kvh) and (int8) block scales: K
+  // scale times the softmax scale as fp32, V scale as fp16 bits
+  __shared__ uint32_t pid[kPfxMaxChunkBlocks];
+  __shared__ float pks[I8 ? kPfxMaxChunkBlocks : 1];
+  __shared__ uint16_t pvs[I8 ? kPfxMaxChunkBlocks : 1];
 
   const int tid = (int)threadIdx.x;
   const int wave = tid / WAVE;
@@ -1689,6 +1699,26 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     const int s = r / RS, rem = r - s * RS;
     return ((int64_t)s * N + rem / Gn) * H + (int64_t)kvh * Gn + rem % Gn;
   };
+
+  // ---- the chunk's page ids and scales into LDS, once: the stage loads then
+  // take their page ids from LDS, so no global load of an id (which would wait
+  // for every tile load issued before it) sits between the tile loads ----
+  {
+    bool bad = false;
+    for (int i = tid; i < cb1 - cb0; i += (int)blockDim.x) {
+      const int raw = bt[cb0 + i];
+      bad |= raw < 0 || raw >= P.n_blocks;
+      const int b = min(max(raw, 0), P.n_blocks - 1);
+      const uint32_t tix = (uint32_t)b * (uint32_t)P.n_kv_heads + (uint32_t)kvh;
+      pid[i] = tix;
+      if constexpr (I8) {
+        pks[i] = P.scale_log2 * h2f(reinterpret_cast<const uint16_t*>(P.ks)[tix]);
+        pvs[i] = reinterpret_cast<const uint16_t*>(P.vs)[tix];
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) flag_misuse(P.err, MISUSE_PAGE_OUT_OF_POOL);
+  }
+  __syncthreads();
 
   // ---- q^T operands of rows wrow0 + 16 rt + n, and the prefix each row sees ----
   half8 qa[RT][4];
@@ -1732,17 +1762,18 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   for (int rt = 1; rt < RT; ++rt) lmin = min(lmin, lim[rt]);
   const int minlim = __builtin_amdgcn_readfirstlane((int)(-wave_max(-(float)lmin)));
 
-  float M[RT], lrun[RT], psum[RT];
+  float M[RT], lrun[RT];
   float4v acc[RT][8];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    M[rt] = kNegInf; lrun[rt] = 0.f; psum[rt] = 0.f;
+    M[rt] = kNegInf; lrun[rt] = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
   // ---- stage loader (threads 0..511): a thread reads 4 dims of K token kt and
-  // 4 tokens of V dim vd (token group vq) of each block ----
+  // 4 tokens of V dim vd (token group vq) of each block; int8 V is staged as
+  // fp16 c * v_scale (the value product then needs no scale and no bias) ----
   const int kt = tid >> 5, kd = (tid & 31) * 4;
   const int vd = tid & (HD - 1), vq = tid >> 7;
   // byte offset of K dims kd..kd+3 of token kt: int8 tiles hold dims 32c + 16h + j
@@ -1757,48 +1788,44 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // the first step of the int8 conversion right behind each load, which turned
   // the two-stage prefetch into waits.)
   auto gload = [&](PfxRaw<KV>& rw, int st) {
-    int blk[kPfxCH];  // wave-uniform page ids of the stage
 #pragma unroll
     for (int u = 0; u < kPfxCH; ++u) {
-      int b = cb0 + st * kPfxCH + u;
-      b = (st < nst && b < cb1) ? b : cb0;
-      const int raw = bt[b];
-      if ((raw < 0 || raw >= P.n_blocks) && tid == 0) flag_misuse(P.err, MISUSE_PAGE_OUT_OF_POOL);
-      blk[u] = min(max(raw, 0), P.n_blocks - 1);
-      const uint64_t tix = (uint64_t)blk[u] * P.n_kv_heads + kvh;
-      const uint8_t* kt_ = P.kc + tix * P.tile_bytes;
-      const uint8_t* vt_ = P.vc + tix * P.tile_bytes;
+      const int b = cb0 + st * kPfxCH + u;
+      const int bi = (st < nst && b < cb1) ? b - cb0 : 0;
+      // wave-uniform tile address (SALU): tile index from LDS, tile bytes fixed;
+      // buffer loads take the lane offsets as 32-bit VGPRs
+      const uint32_t tix = (uint32_t)__builtin_amdgcn_readfirstlane((int)pid[bi]);
+      constexpr uint32_t kTile = (uint32_t)BS * HD * ESZ;
+      const rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.kc + (uint64_t)tix * kTile), 0,
+                                                          (int)kTile, 0x00020000);
+      const rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.vc + (uint64_t)tix * kTile), 0,
+                                                          (int)kTile, 0x00020000);
       if constexpr (ESZ == 1) {
-        rw.k[u][0] = *reinterpret_cast<const uint32_t*>(kt_ + koff);
-        rw.v[u][0] = *reinterpret_cast<const uint16_t*>(vt_ + voff0);
-        rw.v[u][1] = *reinterpret_cast<const uint16_t*>(vt_ + voff1);
+        rw.k[u][0] = __builtin_amdgcn_raw_buffer_load_b32(kr, (int)koff, 0, 0);
+        rw.v[u][0] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff0, 0, 0);
+        rw.v[u][1] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff1, 0, 0);
       } else {
-        const u32x2 x = *reinterpret_cast<const u32x2*>(kt_ + koff);
+        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(kr, (int)koff, 0, 0);
         rw.k[u][0] = x.x; rw.k[u][1] = x.y;
-        rw.v[u][0] = *reinterpret_cast<const uint32_t*>(vt_ + voff0);
-        rw.v[u][1] = *reinterpret_cast<const uint32_t*>(vt_ + voff1);
-      }
-    }
-    rw.sc = 0u;
-    if constexpr (I8) {
-      // threads 0..3: K scales, 4..7: V scales of the stage's blocks, as raw bits
-      // (converting here would wait for the load); the page ids are the
-      // uniform ones above, so no per-lane id load precedes them
-      const int u = tid % kPfxCH;
-      const int bsel = u == 0 ? blk[0] : u == 1 ? blk[1] : u == 2 ? blk[2] : blk[3];
-      if (tid < 2 * kPfxCH) {
-        const uint8_t* sp = (tid < kPfxCH) ? P.ks : P.vs;
-        rw.sc = reinterpret_cast<const uint16_t*>(sp)[(int64_t)bsel * P.n_kv_heads + kvh];
+        rw.v[u][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)voff0, 0, 0);
+        rw.v[u][1] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)voff1, 0, 0);
       }
     }
   };
-  auto lwrite = [&](int buf, const PfxRaw<KV>& rw) {
+  auto lwrite = [&](int buf, int st, const PfxRaw<KV>& rw) {
 #pragma unroll
     for (int u = 0; u < kPfxCH; ++u) {
       uint32_t kw0, kw1, vw0, vw1;
       if constexpr (ESZ == 1) {
         i8x4_to_h2x2_biased(rw.k[u][0], kw0, kw1);
         i8x4_to_h2x2_biased(rw.v[u][0] | (rw.v[u][1] << 16), vw0, vw1);
+        // (1152 + c) - 1152 = c exactly, then one rounding of c * v_scale
+        const int b = cb0 + st * kPfxCH + u;
+        const int bi = (st < nst && b < cb1) ? b - cb0 : 0;
+        const _Float16 vsh = bitcast<_Float16>(pvs[bi]);
+        const half2v vs2 = {vsh, vsh}, bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        vw0 = bitcast<uint32_t>((bitcast<half2v>(vw0) - bias) * vs2);
+        vw1 = bitcast<uint32_t>((bitcast<half2v>(vw1) - bias) * vs2);
       } else {
         kw0 = rw.k[u][0]; kw1 = rw.k[u][1];
         vw0 = rw.v[u][0]; vw1 = rw.v[u][1];
@@ -1806,18 +1833,14 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       *reinterpret_cast<u32x2*>(&kl[buf][u][kt * kPfxKPitch + kd]) = u32x2{kw0, kw1};
       *reinterpret_cast<u32x2*>(&vl[buf][u >> 1][vd * kPfxVPitch + 8 * vq + 4 * (u & 1)]) = u32x2{vw0, vw1};
     }
-    if constexpr (I8) {
-      if (tid < 2 * kPfxCH) sl[buf][tid % kPfxCH][tid / kPfxCH] = h2f((uint16_t)rw.sc);
-    }
   };
-
   const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
   // one block pair (u0 = up, u1 = up + 1) of stage buffer buf. Masks: row n sees
   // tokens 4g + r of block b0 + j for r < vis; a lane whose four tokens are all
   // hidden gets -inf in the score offset, and the per-token mask runs only when
   // some lane sees part of its four tokens (one block per row at most).
   auto pair_body = [&](int buf, int up, int b0, bool has1, bool plain) {
-    float a[2], vs[2];
+    float a[2];
     float4v scv[RT][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -1825,8 +1848,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       half8 kop[4];
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) kop[kc] = *reinterpret_cast<const half8*>(kb + 32 * kc);
-      a[j] = P.scale_log2 * (I8 ? sl[buf][up + j][0] : 1.f);
-      vs[j] = I8 ? sl[buf][up + j][1] : 1.f;
+      a[j] = I8 ? pks[min(b0 + j, cb1 - 1) - cb0] : P.scale_log2;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         float4v sc = {0.f, 0.f, 0.f, 0.f};
@@ -1894,7 +1916,6 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         const float shift = (Mn == kNegInf) ? 0.f : Mn - Ms;
         M[rt] = Mn;
         lrun[rt] *= alpha;
-        psum[rt] *= alpha;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -1907,7 +1928,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         }
       }
     }
-    // p = 2^y in fp16 pairs; l += sum p; p~ = p * v_scale is the A operand
+    // p = 2^y in fp16 pairs (the A operand); l += sum p
     half8 pa[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -1917,15 +1938,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         const uint32_t lo = pack_h2(__builtin_amdgcn_exp2f(y[rt][j][0]), __builtin_amdgcn_exp2f(y[rt][j][1]));
         const uint32_t hi = pack_h2(__builtin_amdgcn_exp2f(y[rt][j][2]), __builtin_amdgcn_exp2f(y[rt][j][3]));
         lrun[rt] = dot2(hi, bitcast<uint32_t>(ones), dot2(lo, bitcast<uint32_t>(ones), lrun[rt]));
-        if constexpr (I8) {
-          const half2v v2 = {(_Float16)vs[j], (_Float16)vs[j]};
-          const uint32_t plo = bitcast<uint32_t>(bitcast<half2v>(lo) * v2);
-          const uint32_t phi = bitcast<uint32_t>(bitcast<half2v>(hi) * v2);
-          psum[rt] = dot2(phi, bitcast<uint32_t>(ones), dot2(plo, bitcast<uint32_t>(ones), psum[rt]));
-          pw[2 * j] = plo; pw[2 * j + 1] = phi;
-        } else {
-          pw[2 * j] = lo; pw[2 * j + 1] = hi;
-        }
+        pw[2 * j] = lo; pw[2 * j + 1] = hi;
       }
       pa[rt] = bitcast<half8>(u32x4{pw[0], pw[1], pw[2], pw[3]});
     }
@@ -1956,15 +1969,15 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   if (nst > 0) {
     PfxRaw<KV> ra;
     const bool ld = tid < kPfxLoadThreads;
-    if (ld) { gload(ra, 0); lwrite(0, ra); gload(ra, 1); }
+    if (ld) { gload(ra, 0); lwrite(0, 0, ra); gload(ra, 1); }
     __syncthreads();
     for (int st = 0; st < nst; st += 2) {
       compute(0, st);
-      if (ld) { lwrite(1, ra); gload(ra, st + 2); }
+      if (ld) { lwrite(1, st + 1, ra); gload(ra, st + 2); }
       __syncthreads();
       if (st + 1 >= nst) break;
       compute(1, st + 1);
-      if (ld) { lwrite(0, ra); gload(ra, st + 3); }
+      if (ld) { lwrite(0, st + 2, ra); gload(ra, st + 3); }
       __syncthreads();
     }
   }
@@ -1972,25 +1985,20 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // ---- partials: rows 16 rt + 4g + r, dims 16 nt + n ----
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    float l = lrun[rt], ps = psum[rt];
+    float l = lrun[rt];
     l += shfl_xor(l, 16);
     l += shfl_xor(l, 32);
-    if constexpr (I8) {
-      ps += shfl_xor(ps, 16);
-      ps += shfl_xor(ps, 32);
-    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int src = 4 * g + r;
       const float lr = __shfl(l, src, WAVE);
-      const float psr = I8 ? __shfl(ps, src, WAVE) : 0.f;
       const float Mr = __shfl(M[rt], src, WAVE);
       const int row = wrow0 + 16 * rt + 4 * g + r;
       if (row < R) {
         const int64_t pr = out_row(row) * P.max_parts + chunk;
         float* dst = P.part_acc + pr * HD + n;
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) dst[16 * nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
+        for (int nt = 0; nt < 8; ++nt) dst[16 * nt] = acc[rt][nt][r];
         if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(Mr, lr);
       }
     }

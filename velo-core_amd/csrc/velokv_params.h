@@ -110,6 +110,10 @@ struct DecodeParams {
 };
 
 constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)
+// Shared-prefix pass of tree verify: pages per prefix chunk, whose page ids and
+// block scales one workgroup stages in LDS (the host cuts longer prefixes into
+// more chunks).
+constexpr int kPfxMaxChunkBlocks = 1024;
 struct CopyParams {
   uint8_t* base;
   PoolGeom g;
