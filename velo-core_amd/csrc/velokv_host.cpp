@@ -969,8 +969,8 @@ extern "C" int vk_append_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, c
 
 namespace {
 
-constexpr int kPfxRowsPerGroup = 256;  // query rows per workgroup of the shared-prefix pass (16 waves of 16)
-constexpr int kPfxThreads = 1024;
+constexpr int kPfxRowsPerGroup = kPfxRows;  // query rows per workgroup of the shared-prefix pass
+constexpr int kPfxThreads = 64 * kPfxWaves;
 
 struct TreePlan {
   const int32_t* bt;

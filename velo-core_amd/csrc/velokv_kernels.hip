@@ -1649,9 +1649,6 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
 //     g = 0..3, tokens 4g..4g+3 of u0 then of u1, so that a lane's 8 token slots
 //     are one 16-byte read. The loader writes 8 bytes (one dim, four tokens of
 //     one block) per lane, gathered from two token-pair rows of the pool tile.
-constexpr int kPfxRT = 1;                 // 16-row tiles per wave
-constexpr int kPfxWaves = 16;             // four per SIMD (at most 128 registers)
-constexpr int kPfxRows = 16 * kPfxRT * kPfxWaves;  // query rows per workgroup
 constexpr int kPfxLoadThreads = 512;      // the first 8 waves load the stages
 constexpr int kPfxCH = 4;                 // blocks per stage (two pairs)
 constexpr int kPfxKPitch = HD + 16;       // fp16 per staged K row (72 words)
@@ -2926,7 +2923,7 @@ VK_GX_TREE_KV(0, ) VK_GX_TREE_KV(1, ) VK_GX_TREE_KV(2, VK_TWO_WAVES) VK_GX_TREE_
 // Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
 #define VK_TREE_PFX(KV, G, QT)                                                      \
   extern "C" __global__ void __launch_bounds__(64 * kPfxWaves)                      \
-      __attribute__((amdgpu_waves_per_eu(4))) vk_tree_pfx_kv##KV##_g##G##_q##QT(const DecodeParams P) { \
+      __attribute__((amdgpu_waves_per_eu(kPfxWaves / 4))) vk_tree_pfx_kv##KV##_g##G##_q##QT(const DecodeParams P) { \
     tree_prefix_mfma<KV, G, QT>(P);                                                 \
   }
 #define VK_TREE_PFX_G(KV, QT) \
@@ -2934,7 +2931,7 @@ VK_GX_TREE_KV(0, ) VK_GX_TREE_KV(1, ) VK_GX_TREE_KV(2, VK_TWO_WAVES) VK_GX_TREE_
 VK_TREE_PFX_G(1, 0) VK_TREE_PFX_G(1, 1) VK_TREE_PFX_G(3, 0) VK_TREE_PFX_G(3, 1)
 #define VK_GX_TREE_PFX(KV, QT)                                                      \
   extern "C" __global__ void __launch_bounds__(64 * kPfxWaves)                      \
-      __attribute__((amdgpu_waves_per_eu(4))) vk_tree_pfx_kv##KV##_gx_q##QT(const DecodeParams P) { \
+      __attribute__((amdgpu_waves_per_eu(kPfxWaves / 4))) vk_tree_pfx_kv##KV##_gx_q##QT(const DecodeParams P) { \
     tree_prefix_mfma<KV, 0, QT>(P);                                                 \
   }
 VK_GX_TREE_PFX(1, 0) VK_GX_TREE_PFX(1, 1) VK_GX_TREE_PFX(3, 0) VK_GX_TREE_PFX(3, 1)

@@ -114,6 +114,10 @@ constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)
 // block scales one workgroup stages in LDS (the host cuts longer prefixes into
 // more chunks).
 constexpr int kPfxMaxChunkBlocks = 1024;
+// Its workgroup: kPfxWaves waves of kPfxRT 16-row tiles of query rows each.
+constexpr int kPfxRT = 1;
+constexpr int kPfxWaves = 16;
+constexpr int kPfxRows = 16 * kPfxRT * kPfxWaves;  // query rows per workgroup
 struct CopyParams {
   uint8_t* base;
   PoolGeom g;
