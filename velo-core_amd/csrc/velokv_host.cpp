@@ -47,7 +47,8 @@ int fail(int code, const char* fmt, ...) {
       return fail(VK_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));     \
   } while (0)
 
-constexpr int kBS = 16;   // block size the kernels are built for
+constexpr int kBS = 16;   // tokens per tile, the kernels' block
+constexpr int kMaxPageShift = 4;  // pages of up to 16 << 4 = 256 tokens
 constexpr int kHD = 128;  // head_dim the kernels are built for
 constexpr int kMaxPartTokens = 4096;  // 256 blocks: four block-id windows of one wave
 constexpr int kMaxTreeNodes = 32;     // one 32-bit mask row per node
@@ -67,6 +68,18 @@ int kv_stile(int kv, int bs) {
   if (kv == VK_KV_I8_BLK) return 2;
   if (kv == VK_KV_I8_REF) return 4 * bs;
   return 0;
+}
+
+// Page view of a pool's geometry (COW copy, NIXL): one block = one page of
+// 16 << page_shift tokens, its tiles back to back.
+PoolGeom page_geom(const PoolGeom& t) {
+  PoolGeom g = t;
+  g.tile_bytes = t.tile_bytes << t.page_shift;
+  g.stile_bytes = t.stile_bytes << t.page_shift;
+  g.n_blocks = t.n_blocks >> t.page_shift;
+  g.block_size = t.block_size << t.page_shift;
+  g.page_shift = 0;
+  return g;
 }
 
 std::string default_code_object_path() {
@@ -354,25 +367,31 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
       d->max_pages_per_slot < 0)
     return fail(VK_ERR_BAD_ARG, "pool sizes must be positive");
   if (kv_esz(d->kv_type) == 0) return fail(VK_ERR_BAD_ARG, "unknown kv_type %d", d->kv_type);
-  if (d->block_size != kBS || d->head_dim != kHD)
-    return fail(VK_ERR_UNSUPPORTED, "kernels are built for block_size %d and head_dim %d (got %d, %d)", kBS, kHD,
-                d->block_size, d->head_dim);
+  if (d->head_dim != kHD)
+    return fail(VK_ERR_UNSUPPORTED, "kernels are built for head_dim %d (got %d)", kHD, d->head_dim);
+  int ps = 0;  // pages of 16 << ps tokens: 16-token tiles, 2^ps per page
+  while (ps < kMaxPageShift && (kBS << ps) < d->block_size) ++ps;
+  if ((kBS << ps) != d->block_size)
+    return fail(VK_ERR_UNSUPPORTED, "block_size %d: the kernels take pages of 16, 32, 64, 128 or 256 tokens",
+                d->block_size);
+  if (((int64_t)d->n_blocks << ps) > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "pool too large");
   auto* p = new vk_pool();
   p->ctx = ctx;
   p->desc = *d;
   if (p->desc.max_pages_per_slot == 0) p->desc.max_pages_per_slot = d->n_blocks;
   const int esz = kv_esz(d->kv_type);
-  PoolGeom& g = p->geom;
-  g.tile_bytes = (uint32_t)(d->block_size * d->head_dim * esz);
-  g.stile_bytes = (uint32_t)kv_stile(d->kv_type, d->block_size);
-  g.n_blocks = d->n_blocks;
+  PoolGeom& g = p->geom;  // tile view: 16-token tiles, 2^ps per page
+  g.tile_bytes = (uint32_t)(kBS * d->head_dim * esz);
+  g.stile_bytes = (uint32_t)kv_stile(d->kv_type, kBS);
+  g.n_blocks = d->n_blocks << ps;
+  g.page_shift = ps;
   g.n_kv_heads = d->n_kv_heads;
-  g.block_size = d->block_size;
+  g.block_size = kBS;
   g.head_dim = d->head_dim;
   g.kv_type = d->kv_type;
   g.n_layer = d->n_layer;
-  const uint64_t codes = (uint64_t)d->n_blocks * d->n_kv_heads * g.tile_bytes;
-  const uint64_t scales = (uint64_t)d->n_blocks * d->n_kv_heads * g.stile_bytes;
+  const uint64_t codes = (uint64_t)g.n_blocks * d->n_kv_heads * g.tile_bytes;
+  const uint64_t scales = (uint64_t)g.n_blocks * d->n_kv_heads * g.stile_bytes;
   g.k_off = 0;
   g.v_off = align_up(codes, 256);
   g.ks_off = g.v_off + align_up(codes, 256);
@@ -393,8 +412,8 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
     if (e == hipSuccess) e = hipMemset(p->table, 0, p->table_bytes);
   }
   if (e == hipSuccess && d->kv_type == VK_KV_I8_BLK) {
-    e = hipMalloc(reinterpret_cast<void**>(&p->claim), (uint64_t)d->n_blocks * sizeof(unsigned long long));
-    if (e == hipSuccess) e = hipMemset(p->claim, 0, (uint64_t)d->n_blocks * sizeof(unsigned long long));
+    e = hipMalloc(reinterpret_cast<void**>(&p->claim), (uint64_t)g.n_blocks * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemset(p->claim, 0, (uint64_t)g.n_blocks * sizeof(unsigned long long));
   }
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
@@ -697,8 +716,8 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   if ((int64_t)a->max_context_len > (int64_t)pl->bt_stride * d.block_size)
     return fail(VK_ERR_BAD_ARG, "max_context_len %d exceeds the block-table row (%d pages)", a->max_context_len, pl->bt_stride);
   int P = a->partition_tokens;
-  if (P < 0 || P % d.block_size || P > kMaxPartTokens)
-    return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
+  if (P < 0 || P % kBS || P > kMaxPartTokens)
+    return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of 16 in [16, %d]", kMaxPartTokens);
   bool mfma = false;
   decode_choice(ctx, pool, a, &pl->stream_k, &mfma);
   pl->acc_bytes = pl->ml_bytes = pl->prefix_bytes = 0;
@@ -718,9 +737,9 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     const int64_t items = (int64_t)a->n_seqs * d.n_kv_heads;
     const int64_t bins = std::min(wgs, items);
     const int64_t rounds = (items + bins - 1) / bins;
-    const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
+    const int64_t nb = ((int64_t)a->max_context_len + kBS - 1) / kBS;
     const int64_t wave_units = (rounds * (nb + kSkPenalty) + kWgMaxWaves - 1) / kWgMaxWaves;
-    if (rounds <= kPkMaxRounds && wave_units <= kMaxPartTokens / d.block_size) {
+    if (rounds <= kPkMaxRounds && wave_units <= kMaxPartTokens / kBS) {
       pl->stream_k = false;
       pl->packed = true;
       pl->kernel = name;
@@ -736,7 +755,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     // one wave per resident slot, and at most 256 blocks (four id windows) per
     // worker: a worker's blocks are at most its units, ceil(units / nw)
     const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads *
-                              ((a->max_context_len + d.block_size - 1) / d.block_size + kSkPenalty);
+                              ((a->max_context_len + kBS - 1) / kBS + kSkPenalty);
     const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
     const int64_t nw = std::max<int64_t>(1, std::max(waves, (units_max + 255) / 256));
     if (units_max > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "batch too large for the stream-K schedule");
@@ -759,8 +778,8 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     const int64_t waves = ctx ? resident_waves(ctx, decode_wg_name(d.kv_type, G, a->q_dtype), 64 * kWgMaxWaves) : 2048;
     int nw = 1;
     while (nw < 8 && pairs * nw < waves) nw *= 2;
-    const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
-    if (pairs > 0 && pairs * nw >= waves && (nb + nw - 1) / nw <= kMaxPartTokens / d.block_size &&
+    const int64_t nb = ((int64_t)a->max_context_len + kBS - 1) / kBS;
+    if (pairs > 0 && pairs * nw >= waves && (nb + nw - 1) / nw <= kMaxPartTokens / kBS &&
         pairs <= 0x7FFFFFFF) {
       pl->wg_waves = nw;
       pl->kernel = decode_wg_name(d.kv_type, G, a->q_dtype);
@@ -806,7 +825,7 @@ extern "C" int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a
   const vk_pool_desc& d = pool->desc;
   memset(out, 0, sizeof *out);
   snprintf(out->kernel, sizeof out->kernel, "%s", pl.kernel.c_str());
-  const int64_t nb = ((int64_t)a->max_context_len + d.block_size - 1) / d.block_size;
+  const int64_t nb = ((int64_t)a->max_context_len + kBS - 1) / kBS;
   out->workspace_bytes = pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes;
   if (pl.packed) {
     out->schedule = VK_SCHED_PACKED;
@@ -827,7 +846,7 @@ extern "C" int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a
     out->schedule = VK_SCHED_SPLIT;
     out->partition_tokens = pl.part_tokens;
     out->max_partitions = pl.max_parts;
-    out->max_blocks_per_wave = (int32_t)std::min<int64_t>(nb, pl.part_tokens / d.block_size);
+    out->max_blocks_per_wave = (int32_t)std::min<int64_t>(nb, pl.part_tokens / kBS);
     out->merge_launch = pl.max_parts > 1 ? 1 : 0;
   }
   return VK_OK;
@@ -905,6 +924,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   p.n_heads = a->n_heads;
   p.n_kv_heads = d.n_kv_heads;
   p.n_blocks = d.n_blocks;
+  p.page_shift = g.page_shift;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
   // stream-K: contexts are clamped to max_context_len, which bounds every worker's
@@ -1023,25 +1043,26 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
     pl->pfx_row_tiles = (int32_t)((qrows + kPfxRowsPerGroup - 1) / kPfxRowsPerGroup);
     const int64_t groups = std::max<int64_t>(1, (int64_t)pl->pfx_row_tiles * d.n_kv_heads);
     const int64_t n_cu = ctx ? ctx->n_cu : 256;
-    const int64_t max_chunks = std::max(1, a->shared_blocks / 16);
-    const int64_t min_chunks = (a->shared_blocks + kPfxMaxChunkBlocks - 1) / kPfxMaxChunkBlocks;
+    const int32_t tiles = a->shared_blocks << pool->geom.page_shift;  // the prefix in 16-token tiles
+    const int64_t max_chunks = std::max(1, tiles / 16);
+    const int64_t min_chunks = (tiles + kPfxMaxChunkBlocks - 1) / kPfxMaxChunkBlocks;
     pl->prefix_chunks = (int32_t)std::max(
         min_chunks, std::min(max_chunks, std::max<int64_t>(1, (n_cu + groups - 1) / groups)));
-    pl->prefix_blocks = a->shared_blocks;
+    pl->prefix_blocks = tiles;
     pl->pfx_kernel = tree_pfx_name(d.kv_type, G, a->q_dtype);
     // the rest of a context: past the prefix, or the last partial page of a
     // context shorter than the prefix, then the tree nodes
     tokens = std::max<int64_t>((int64_t)a->max_context_len - (int64_t)a->shared_blocks * d.block_size,
-                               d.block_size - 1) + a->n_nodes;
+                               kBS - 1) + a->n_nodes;
   }
   int P = a->partition_tokens;
-  if (P < 0 || P % d.block_size || P > kMaxPartTokens)
-    return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of the block size in [16, %d]", kMaxPartTokens);
+  if (P < 0 || P % kBS || P > kMaxPartTokens)
+    return fail(VK_ERR_BAD_ARG, "partition_tokens must be a multiple of 16 in [16, %d]", kMaxPartTokens);
   if (P == 0 && pl->prefix_chunks > 0 && tokens <= kMaxPartTokens) {
     // after a shared prefix, the rest of each context in one partition: the
     // tree kernel then folds the prefix partials into the output itself and no
     // merge launch follows
-    P = (int)((tokens + d.block_size - 1) / d.block_size * d.block_size);
+    P = (int)((tokens + kBS - 1) / kBS * kBS);
   } else if (P == 0) {
     // Smallest partition with at most four units per resident wave: the tree
     // kernels are bound by issue, not by HBM, and short partitions even out
@@ -1110,9 +1131,10 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   p.n_heads = a->n_heads;
   p.n_kv_heads = d.n_kv_heads;
   p.n_blocks = d.n_blocks;
+  p.page_shift = pool->geom.page_shift;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
-  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.prefix_blocks * d.block_size +
+  p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.prefix_blocks * kBS +
                                                 (int64_t)(pl.max_parts - pl.prefix_chunks) * pl.part_tokens,
                                             (int64_t)pl.bt_stride * d.block_size);
   p.n_nodes = a->n_nodes;
@@ -1181,7 +1203,7 @@ extern "C" int vk_copy_blocks(vk_ctx* ctx, vk_pool* pool, const int32_t* pairs, 
   for (int i0 = 0; i0 < n_pairs; i0 += kMaxCopyPairs) {
     CopyParams p{};
     p.base = pool->base;
-    p.g = pool->geom;
+    p.g = page_geom(pool->geom);
     p.n_pairs = std::min(kMaxCopyPairs, n_pairs - i0);
     memcpy(p.pairs, pairs + 2 * i0, sizeof(int32_t) * 2 * (size_t)p.n_pairs);
     if ((rc = launch(ctx, "vk_copy_blocks", dim3((unsigned)p.n_pairs, (unsigned)pool->desc.n_layer, 2), dim3(256), p,
@@ -1231,7 +1253,8 @@ namespace {
 uint64_t nixl_payload(const vk_pool* pool, int32_t n_layers, uint32_t token_len) {
   const vk_pool_desc& d = pool->desc;
   const uint64_t pages = ((uint64_t)token_len + d.block_size - 1) / d.block_size;
-  return pages * (uint64_t)n_layers * 2 * (uint64_t)d.n_kv_heads * (pool->geom.tile_bytes + pool->geom.stile_bytes);
+  const PoolGeom g = page_geom(pool->geom);
+  return pages * (uint64_t)n_layers * 2 * (uint64_t)d.n_kv_heads * (g.tile_bytes + g.stile_bytes);
 }
 
 int nixl_run(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers, const vk_nixl_item* items,
@@ -1281,12 +1304,13 @@ int nixl_run(vk_ctx* ctx, vk_pool* pool, int32_t layer0, int32_t n_layers, const
       if (spans[i].first < spans[i - 1].second) return fail(VK_ERR_BAD_ARG, "wire records overlap");
   }
   if ((rc = set_device(ctx))) return rc;
-  const uint64_t page_codes = 2ull * (uint64_t)d.n_kv_heads * pool->geom.tile_bytes;  // K + V of one page
+  const PoolGeom pg = page_geom(pool->geom);
+  const uint64_t page_codes = 2ull * (uint64_t)d.n_kv_heads * pg.tile_bytes;  // K + V of one page
   const int32_t n_slices = (int32_t)((page_codes / 16 + kNixlSliceVecs - 1) / kNixlSliceVecs);
   for (int32_t i0 = 0; i0 < n_items;) {
     NixlParams p{};
     p.base = pool->base;
-    p.g = pool->geom;
+    p.g = pg;
     p.pages = pages;
     p.wire = reinterpret_cast<uint8_t*>(const_cast<void*>(wire));
     p.wire_bytes = wire_bytes;

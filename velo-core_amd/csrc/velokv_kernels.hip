@@ -199,10 +199,12 @@ struct BlockIds {
   float vs[kWin];
 };
 // A page id outside [0, n_blocks) is clamped into the pool (the read stays in
-// bounds) and reported as MISUSE_PAGE_OUT_OF_POOL.
+// bounds) and reported as MISUSE_PAGE_OUT_OF_POOL. Tile u of a sequence (tokens
+// 16u .. 16u + 15) is tile u % 2^page_shift of page bt[u >> page_shift].
 template <bool BLK>
 DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, int blk0, int nblk, int kvh) {
   const int lane = lane_id();
+  const int ps = P.page_shift;
   bool bad = false;
 #pragma unroll
   for (int k = 0; k < kWin; ++k) {
@@ -211,9 +213,10 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
     w.vs[k] = 1.f;
     const int idx = 64 * k + lane;
     if (idx < nblk) {
-      const int raw = bt[blk0 + idx];
+      const int u = blk0 + idx;
+      const int raw = bt[u >> ps];
       bad |= raw < 0 || raw >= P.n_blocks;
-      w.b[k] = min(max(raw, 0), P.n_blocks - 1);
+      w.b[k] = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
       if constexpr (BLK) {
         w.ks[k] = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
         w.vs[k] = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
@@ -1703,9 +1706,10 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   {
     bool bad = false;
     for (int i = tid; i < cb1 - cb0; i += (int)blockDim.x) {
-      const int raw = bt[cb0 + i];
+      const int u = cb0 + i, ps = P.page_shift;
+      const int raw = bt[u >> ps];
       bad |= raw < 0 || raw >= P.n_blocks;
-      const int b = min(max(raw, 0), P.n_blocks - 1);
+      const int b = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
       const uint32_t tix = (uint32_t)b * (uint32_t)P.n_kv_heads + (uint32_t)kvh;
       pid[i] = tix;
       if constexpr (I8) {
@@ -2150,10 +2154,11 @@ DEV int64_t token_slot(const AppendParams& P, int m) {
     slot = P.slot_mapping[m];
   } else {  // the new token of sequence m, at its last context position (kernels.metal:770-774)
     const int pos = min(P.context_lens[m], P.cap_tokens) - 1;
-    if (pos < 0 || pos / BS >= P.bt_stride) return -1;
+    const int ps = 4 + P.g.page_shift;  // log2 of the page's tokens
+    if (pos < 0 || (pos >> ps) >= P.bt_stride) return -1;
     int row = P.seq_rows ? P.seq_rows[m] : m;
     if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
-    slot = (int64_t)P.block_tables[(int64_t)row * P.bt_stride + pos / BS] * BS + pos % BS;
+    slot = ((int64_t)P.block_tables[(int64_t)row * P.bt_stride + (pos >> ps)] << ps) + (pos & ((1 << ps) - 1));
   }
   if (slot < 0 || slot >= (int64_t)P.g.n_blocks * BS) return -1;
   if (P.rope != ROPE_NONE) {
@@ -2754,14 +2759,17 @@ DEV void tree_commit(const CommitParams& P) {
   if (moved == 0) { report(COMMIT_OK); return; }  // every accepted node is already in place
   const int d0 = __builtin_ctzll(moved);
   const int last = ctx + readlane_i(a, na - 1);
-  if ((int64_t)last >= (int64_t)P.bt_stride * BS) { report(COMMIT_PAST_TABLE); return; }
+  const int ps = P.g.page_shift;
+  if ((int64_t)last >= ((int64_t)P.bt_stride << (4 + ps))) { report(COMMIT_PAST_TABLE); return; }
   const int32_t* bt = P.block_tables + (int64_t)s * P.bt_stride;
-  const int b_first = (ctx + d0) / BS, nb = last / BS - b_first + 1;  // at most 3 blocks
-  const int blk_l = lane < nb ? bt[b_first + lane] : 0;
-  if (__builtin_amdgcn_ballot_w64(lane < nb && (blk_l < 0 || blk_l >= P.g.n_blocks)) != 0) {
+  const int b_first = (ctx + d0) / BS, nb = last / BS - b_first + 1;  // at most 3 tiles
+  // tile b_first + lane: page bt[tile >> ps], tile (tile % 2^ps) of that page
+  const int pg = lane < nb ? bt[(b_first + lane) >> ps] : 0;
+  if (__builtin_amdgcn_ballot_w64(lane < nb && (pg < 0 || pg >= (P.g.n_blocks >> ps))) != 0) {
     report(COMMIT_BAD_PAGE);
     return;
   }
+  const int blk_l = (pg << ps) | ((b_first + lane) & ((1 << ps) - 1));
   report(COMMIT_OK);
   if (w == 0) commit_wave<KV, false>(P, raw[0], xsc[0], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
   else commit_wave<KV, true>(P, raw[1], xsc[1], h, l0, l1, ctx, na, a, d0, blk_l, b_first);

@@ -15,14 +15,22 @@ namespace velokv {
 enum KvType : int32_t { KV_F32 = 0, KV_F16 = 1, KV_I8_REF = 2, KV_I8_BLK = 3 };
 enum DType : int32_t { DT_F32 = 0, DT_F16 = 1 };
 
-// Geometry of one layer of a pool (see include/velokv.h for the layout).
+// Geometry of one layer of a pool (see include/velokv.h for the layout). The
+// kernels work on blocks of 16 tokens ("tiles"); a pool whose pages hold
+// 16 << page_shift tokens stores page p as tiles p << page_shift ..
+// (p + 1 << page_shift) - 1, back to back, so a flat slot page * page_tokens +
+// offset is also tile * 16 + offset % 16. The tile view (append, decode,
+// commit) has n_blocks = tiles and block_size = 16; the page view (COW copy,
+// NIXL) has n_blocks = pages, block_size = page tokens, page_shift = 0 and the
+// tile sizes of a whole page.
 struct PoolGeom {
   uint64_t layer_stride;   // bytes between layers
   uint64_t k_off, v_off;   // byte offsets of K / V codes inside a layer
   uint64_t ks_off, vs_off; // byte offsets of K / V scales inside a layer
   uint32_t tile_bytes;     // codes of one (block, head): block_size * head_dim * esz
-  uint32_t stile_bytes;    // scales of one (block, head): 2 (I8_BLK), 4*bs (I8_REF), 0
+  uint32_t stile_bytes;    // scales of one (block, head): 2 (I8_BLK, per 16 tokens), 4 per token (I8_REF), 0
   int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
+  int32_t page_shift;      // tile view: log2(page tokens / 16)
 };
 
 enum RopeStyle : int32_t { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
@@ -92,7 +100,9 @@ struct DecodeParams {
   uint32_t stile_bytes;
   int32_t bt_stride;
   int32_t bt_rows;          // rows of the block table when known (pool slot table), else 0
-  int32_t n_seqs, n_heads, n_kv_heads, n_blocks;
+  int32_t n_seqs, n_heads, n_kv_heads;
+  int32_t n_blocks;         // pages in the pool (block-table entries range)
+  int32_t page_shift;       // log2(page tokens / 16): table entry p holds tiles p << page_shift ..
   int32_t max_parts;        // partitions per sequence in the grid
   int32_t part_tokens;      // tokens per partition (multiple of the block size)
   int32_t cap_tokens;       // tokens a table row can address: min(max_parts*part_tokens, bt_stride*bs)
