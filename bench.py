@@ -67,7 +67,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--kv-heads", type=int, default=8)
-    ap.add_argument("--pool-blocks", type=int, default=40000)
+    ap.add_argument("--pool-blocks", type=int, default=40000, help="pool capacity in 16-token blocks")
+    ap.add_argument("--page", type=int, default=16, help="decode workload: tokens per page (16, 32, 64, 128, 256)")
+    ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128], help="decode workload: head_dim")
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = auto)")
     ap.add_argument("--q-dtype", choices=["fp16", "fp32"], default="fp16",
                     help="decode query dtype (fp32: the reference kernels' float q)")
@@ -97,25 +99,28 @@ def parse():
     return ap.parse_args()
 
 
-def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride: int, q_esz: int = 2) -> int:
+def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride: int, q_esz: int = 2,
+                 hd: int = HD) -> int:
     """Algorithmic HBM bytes of one decode call: each K/V element of every context
-    token read once, its scales, q, the output and the block-table entries used."""
+    token read once, its scales, q, the output and the block-table entries used
+    (hd = the caller's head_dim: a head_dim-64 pool also reads its zero upper
+    halves, which these bytes do not count)."""
     tok = int(lens.sum())
     blocks = int(sum(-(-int(L) // BS) for L in lens))
     esz = {velokv.KV_F16: 2, velokv.KV_I8_BLK: 1, velokv.KV_I8_REF: 1, velokv.KV_F32: 4}[kv]
-    kvb = 2 * tok * Hkv * HD * esz
+    kvb = 2 * tok * Hkv * hd * esz
     if kv == velokv.KV_I8_BLK:
         kvb += 2 * blocks * Hkv * 2
     elif kv == velokv.KV_I8_REF:
         kvb += 2 * tok * Hkv * 4
-    return kvb + S * H * HD * q_esz + S * H * HD * 4 + blocks * 4 + S * 4
+    return kvb + S * H * hd * q_esz + S * H * hd * 4 + blocks * 4 + S * 4
 
 
-def append_bytes(kv: int, S: int, Hkv: int) -> int:
+def append_bytes(kv: int, S: int, Hkv: int, hd: int = HD) -> int:
     """New K/V read (fp16), codes written, scales written, slot mapping read."""
     esz = {velokv.KV_F16: 2, velokv.KV_I8_BLK: 1, velokv.KV_I8_REF: 1, velokv.KV_F32: 4}[kv]
     sc = {velokv.KV_I8_BLK: 2, velokv.KV_I8_REF: 4}.get(kv, 0)
-    return 2 * S * Hkv * HD * 2 + 2 * S * Hkv * HD * esz + 2 * S * Hkv * sc + S * 8
+    return 2 * S * Hkv * hd * 2 + 2 * S * Hkv * hd * esz + 2 * S * Hkv * sc + S * 8
 
 
 def measured_traffic(kernel: str, S: int, L: int, H: int, Hkv: int, ragged: bool):
@@ -138,25 +143,27 @@ def measured_traffic(kernel: str, S: int, L: int, H: int, Hkv: int, ragged: bool
 def run_gpu(ctx, args, kv_name: str):
     kv = {"int8": velokv.KV_I8_BLK, "int8ref": velokv.KV_I8_REF, "fp32": velokv.KV_F32}.get(kv_name, velokv.KV_F16)
     S, H, Hkv, L, NL = args.seqs, args.heads, args.kv_heads, args.ctx, args.layers
+    D, PG = args.head_dim, args.page  # head_dim and tokens per page of the pool
+    n_pages = args.pool_blocks * BS // PG
     if args.ragged:
         lens = synth.rng(2024).integers(1024, L + 1, S).astype(np.int32)
     else:
         lens = np.full(S, L, np.int32)
-    pages = [-(-int(x) // BS) for x in lens]
-    bt = synth.scatter_block_tables(args.pool_blocks, pages, seed=11, stride=-(-L // BS))
-    pool = velokv.Pool(ctx, NL, args.pool_blocks, BS, Hkv, HD, kv)
+    pages = [-(-int(x) // PG) for x in lens]
+    bt = synth.scatter_block_tables(n_pages, pages, seed=11, stride=-(-L // PG))
+    pool = velokv.Pool(ctx, NL, n_pages, PG, Hkv, D, kv)
 
     # ---- fill the pool: prefill tokens 0 .. L-2 of every sequence, per layer ----
     n_pre = int((lens - 1).sum())
     rows = np.repeat(np.arange(S), lens - 1)
     pos = np.concatenate([np.arange(int(x) - 1) for x in lens])
-    pre_slots = ctx.upload(synth.slots_for_positions(bt, pos, BS, rows))
-    kbuf = ctx.alloc(n_pre * Hkv * HD * 2)
-    vbuf = ctx.alloc(n_pre * Hkv * HD * 2)
+    pre_slots = ctx.upload(synth.slots_for_positions(bt, pos, PG, rows))
+    kbuf = ctx.alloc(n_pre * Hkv * D * 2)
+    vbuf = ctx.alloc(n_pre * Hkv * D * 2)
     outlier = 8.0 if kv in (velokv.KV_I8_BLK, velokv.KV_I8_REF) else 1.0
     for layer in range(NL):
-        ctx.fill_normal_f16(kbuf, n_pre * Hkv * HD, 1000 + 2 * layer, Hkv * HD, outlier)
-        ctx.fill_normal_f16(vbuf, n_pre * Hkv * HD, 1001 + 2 * layer, Hkv * HD, outlier)
+        ctx.fill_normal_f16(kbuf, n_pre * Hkv * D, 1000 + 2 * layer, Hkv * D, outlier)
+        ctx.fill_normal_f16(vbuf, n_pre * Hkv * D, 1001 + 2 * layer, Hkv * D, outlier)
         ctx.append(pool, layer, kbuf, vbuf, velokv.DT_F16, pre_slots, n_pre)
     ctx.sync()
     kbuf.free()
@@ -164,28 +171,28 @@ def run_gpu(ctx, args, kv_name: str):
 
     # ---- per-step inputs, rotated over R sets so consecutive steps differ ----
     R = 4
-    new_slots = ctx.upload(synth.slots_for_positions(bt, lens.astype(np.int64) - 1, BS))
+    new_slots = ctx.upload(synth.slots_for_positions(bt, lens.astype(np.int64) - 1, PG))
     qs, ks, vs = [], [], []
     qdt = velokv.DT_F32 if args.q_dtype == "fp32" else velokv.DT_F16
     for r in range(R):
         if qdt == velokv.DT_F32:  # seeded normals made on the host (1 MB per set at the headline shape)
-            q = ctx.upload(synth.rng(7000 + r).standard_normal(S * H * HD).astype(np.float32))
+            q = ctx.upload(synth.rng(7000 + r).standard_normal(S * H * D).astype(np.float32))
         else:
-            q = ctx.alloc(S * H * HD * 2)
-            ctx.fill_normal_f16(q, S * H * HD, 7000 + r, H * HD)
-        k = ctx.alloc(S * Hkv * HD * 2)
-        ctx.fill_normal_f16(k, S * Hkv * HD, 8000 + r, Hkv * HD, outlier)
-        v = ctx.alloc(S * Hkv * HD * 2)
-        ctx.fill_normal_f16(v, S * Hkv * HD, 9000 + r, Hkv * HD, outlier)
+            q = ctx.alloc(S * H * D * 2)
+            ctx.fill_normal_f16(q, S * H * D, 7000 + r, H * D)
+        k = ctx.alloc(S * Hkv * D * 2)
+        ctx.fill_normal_f16(k, S * Hkv * D, 8000 + r, Hkv * D, outlier)
+        v = ctx.alloc(S * Hkv * D * 2)
+        ctx.fill_normal_f16(v, S * Hkv * D, 9000 + r, Hkv * D, outlier)
         qs.append(q); ks.append(k); vs.append(v)
-    out = ctx.alloc(S * H * HD * 4)
+    out = ctx.alloc(S * H * D * 4)
     d_lens = ctx.upload(lens)
     d_bt = ctx.upload(bt)
     stream = velokv.Stream(ctx)
     rope = {"none": 0, "interleaved": velokv.ROPE_INTERLEAVED, "half": velokv.ROPE_HALF}[args.rope]
     if rope:
         n_pos = int(lens.max())
-        d_table = ctx.upload(velokv.rope_table(n_pos, HD, 500000.0))
+        d_table = ctx.upload(velokv.rope_table(n_pos, D, 500000.0))
         d_pos = ctx.upload(lens.astype(np.int32) - 1)
 
     plan = ctx.decode_plan(pool, S, H, int(lens.max()), bt_stride=bt.shape[1], partition_tokens=args.partition,
@@ -234,10 +241,10 @@ def run_gpu(ctx, args, kv_name: str):
     app_ms = [app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]
 
     ms_step = total_ms / args.steps
-    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1], 4 if qdt == velokv.DT_F32 else 2)
-    abytes = append_bytes(kv, S, Hkv)
+    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1], 4 if qdt == velokv.DT_F32 else 2, D)
+    abytes = append_bytes(kv, S, Hkv, D)
     if rope:  # q read and written (fp16), positions, one table row (D/2 cos, sin pairs) per token
-        abytes += 2 * S * H * HD * (4 if qdt == velokv.DT_F32 else 2) + S * 4 + S * HD * 4
+        abytes += 2 * S * H * D * (4 if qdt == velokv.DT_F32 else 2) + S * 4 + S * D * 4
     step_bytes = NL * (dbytes + abytes)
     dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
@@ -255,13 +262,14 @@ def run_gpu(ctx, args, kv_name: str):
         "plan": plan,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(kname, S, L, H, Hkv, args.ragged),
+                     "traffic": (measured_traffic(kname, S, L, H, Hkv, args.ragged)
+                                 if (D, PG) == (HD, BS) else None),
                      "kernel": kname,
                      "launch_ms_mean": round(dec_mean_ms, 5), "launch_ms_min": round(float(np.min(dec_ms)), 5),
                      "launches": len(dec_ms)},
         "pool_gb": round(pool.nbytes / 1e9, 2),
-        "workload": "S=%d, L=%s, H=%d/Hkv=%d, %s KV, q %s" % (S, "U[1024,%d]" % L if args.ragged else str(L), H, Hkv,
-                                                               kv_name, args.q_dtype),
+        "workload": "S=%d, L=%s, H=%d/Hkv=%d, D=%d, page %d, %s KV, q %s" % (
+            S, "U[1024,%d]" % L if args.ragged else str(L), H, Hkv, D, PG, kv_name, args.q_dtype),
         "sum_context_len": int(lens.sum()),
     }
     if args.calibrate:
@@ -675,7 +683,8 @@ def main():
     if args.also != "none" and args.also != args.kv:
         also = run_gpu(ctx, args, args.also)
     configs = {}
-    if not args.no_configs and not args.ragged and args.kv == "int8" and args.q_dtype == "fp16":
+    if (not args.no_configs and not args.ragged and args.kv == "int8" and args.q_dtype == "fp16"
+            and (args.page, args.head_dim) == (BS, HD)):
         # BASELINE configs 2 (fp16) and 3 (INT8 with outliers): the same shapes with
         # L ~ U[1024, ctx]; and the headline with the reference kernels' fp32 q
         import copy
@@ -689,11 +698,12 @@ def main():
         # the reference's default cache type (fp32 K/V, fp32 q) at the headline shape
         configs["config1_fp32_kv"] = run_gpu(ctx, f32, "fp32")
     cpu = None if args.no_cpu else cpu_baseline(args)
-    workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=128, bs=16, %s KV, %d layers, %sappend+decode per layer, pool %d blocks" %
+    workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=%d, bs=%d, %s KV, %d layers, %sappend+decode per layer, pool %d blocks" %
                 (args.seqs, "U[1024,%d]" % args.ctx if args.ragged else str(args.ctx), args.heads, args.kv_heads,
+                 args.head_dim, args.page,
                  {"int8": "INT8 per-(block,head) fp16-scale", "int8ref": "INT8 per-(token,head) fp32-scale (reference rows)",
                   "fp32": "fp32"}.get(args.kv, "fp16"), args.layers,
-                 "" if args.rope == "none" else "RoPE(%s)+" % args.rope, args.pool_blocks))
+                 "" if args.rope == "none" else "RoPE(%s)+" % args.rope, args.pool_blocks * BS // args.page))
     line = {
         "metric": "paged decode-attn achieved HBM GB/s (% peak) + tokens/s, B=64 ctx=8k, fp16/INT8 KV",
         "value": head["value"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

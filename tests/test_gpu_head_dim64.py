@@ -1,0 +1,224 @@
+"""GPU parity for head_dim 64 (the reference's kernels take any head_dim up to
+128, kernels.metal:464; the byte formula of model_loader.rs:129-140 scales with
+it). A head_dim-64 pool stores each head in a 128-wide tile whose dims 64..127
+stay zero: appends write the caller's 64-dim rows and zeros, attention reads q
+rows of 64 dims (zero above) and writes 64-dim output rows.
+
+So the pool bytes must equal the oracle's 128-dim layer filled with the same K/V
+padded with zeros (bit for bit, every KV type), and attention must equal the
+oracle's with the softmax scale 1/sqrt(64) (within the north-star tolerance);
+for fp16 / fp32 KV it must also equal the oracle run at head_dim 64 directly,
+which pins the padding itself."""
+import numpy as np
+import pytest
+
+import pyoracle as O
+import velokv
+from cases import BS, HD, make_case, oracle_layer, tol_check
+from test_gpu_append_copy import assert_layer_equal
+from velokv import synth
+
+pytestmark = pytest.mark.gpu
+
+D = 64
+KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
+SCALE = 1.0 / np.sqrt(D)
+
+
+def pad(x):
+    """[..., 64] -> [..., 128] with zeros above."""
+    out = np.zeros(x.shape[:-1] + (HD,), x.dtype)
+    out[..., :D] = x
+    return out
+
+
+def hd64_case(kv, lens, n_kv_heads=2, n_heads=8, seed=1, outlier_scale=8.0):
+    """make_case with 64-dim K, V and q (the 128-dim case's first 64 dims) and the
+    padded copy the 128-dim oracle reads."""
+    c = make_case(kv, lens, n_kv_heads=n_kv_heads, n_heads=n_heads, seed=seed, outlier_scale=outlier_scale)
+    c.k = [pad(np.ascontiguousarray(k[..., :D])) for k in c.k]
+    c.v = [pad(np.ascontiguousarray(v[..., :D])) for v in c.v]
+    c.q = pad(np.ascontiguousarray(c.q[..., :D]))
+    return c
+
+
+def hd64_pool(ctx, case, with_last=True):
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, case.n_kv_heads, D, case.kv_type)
+    parts = [case.prefill_slots()] + ([case.last_slots()] if with_last else [])
+    for sl, kk, vv in parts:
+        if len(sl):
+            ctx.append(pool, 0, ctx.upload(np.ascontiguousarray(kk[..., :D])),
+                       ctx.upload(np.ascontiguousarray(vv[..., :D])), velokv.DT_F16, ctx.upload(sl), len(sl))
+    ctx.sync()
+    return pool
+
+
+def direct_oracle(case):
+    """The oracle at head_dim 64 (fp16 / fp32 KV: its int8 K layout is written for 128)."""
+    L = O.Layer(case.n_blocks, case.n_kv_heads, BS, D, case.kv_type)
+    for sl, kk, vv in (case.prefill_slots(), case.last_slots()):
+        if len(sl):
+            O.append(L, np.ascontiguousarray(kk[..., :D]), np.ascontiguousarray(vv[..., :D]), sl)
+    return L
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+def test_hd64_append_bit_exact(ctx, kv):
+    print(f"hd64 append kv={kv}", flush=True)
+    case = hd64_case(kv, [1, 15, 16, 17, 33, 200, 257], seed=1400)
+    pool = hd64_pool(ctx, case)
+    assert_layer_equal(pool, 0, oracle_layer(case))
+
+
+SCHEDS = {"split": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 0), "split-p64": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 64),
+          "stream": (velokv.DECODE_MFMA, velokv.SCHED_STREAM, 0), "auto": (velokv.DECODE_AUTO, velokv.SCHED_AUTO, 0),
+          "valu-request": (velokv.DECODE_VALU, velokv.SCHED_SPLIT, 0)}
+
+
+@pytest.mark.parametrize("kv", KV_ALL)
+@pytest.mark.parametrize("sched", list(SCHEDS))
+@pytest.mark.parametrize("qd", [np.float16, np.float32])
+def test_hd64_decode(ctx, kv, sched, qd):
+    print(f"hd64 decode kv={kv} sched={sched} q={np.dtype(qd).name}", flush=True)
+    kind, sc, P = SCHEDS[sched]
+    case = hd64_case(kv, [1, 16, 17, 255, 700, 2100], seed=1410 + kv)
+    pool = hd64_pool(ctx, case)
+    q64 = np.ascontiguousarray(case.q[..., :D]).astype(qd)
+    qdt = velokv.DT_F32 if qd == np.float32 else velokv.DT_F16
+    ctx.set_decode_kernel(kind)
+    ctx.set_decode_schedule(sc)
+    try:
+        pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()),
+                             bt_stride=case.block_tables.shape[1], partition_tokens=P, q_dtype=qdt)
+        assert "mfma" in pl["kernel"] or "_sk_" in pl["kernel"] or "_wg_" in pl["kernel"], pl  # no VALU at 64
+        out = ctx.alloc(case.S * case.n_heads * D * 4)
+        ctx.paged_decode(pool, 0, ctx.upload(q64), qdt, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
+                         int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1], partition_tokens=P)
+        ctx.sync()
+    finally:
+        ctx.set_decode_kernel(velokv.DECODE_AUTO)
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)
+    got = out.download((case.S, case.n_heads, D), np.float32)
+    ref = O.paged_decode(oracle_layer(case), pad(q64), case.block_tables, case.ctx_lens, scale=SCALE)
+    assert np.all(ref[..., D:] == 0.0)
+    ok, err, nbad = tol_check(got, ref[..., :D])
+    assert ok, f"max err {err:.3g}, {nbad} out of tolerance ({pl['kernel']})"
+    if kv in (O.F16, O.F32):
+        ref_d = O.paged_decode(direct_oracle(case), q64, case.block_tables, case.ctx_lens)
+        ok, err, nbad = tol_check(got, ref_d)
+        assert ok, f"vs the oracle at head_dim 64: max err {err:.3g}, {nbad} out of tolerance"
+
+
+@pytest.mark.parametrize("kv", [O.F32, O.I8_BLK])
+def test_hd64_workgroup_split_and_append_decode(ctx, kv):
+    print(f"hd64 workgroup split kv={kv}", flush=True)
+    lens = list(synth.rng(1420).integers(2, 500, 64))
+    case = hd64_case(kv, lens, n_kv_heads=8, n_heads=32, seed=1421)
+    pool = hd64_pool(ctx, case, with_last=False)
+    sl, kk, vv = case.last_slots()
+    q64 = np.ascontiguousarray(case.q[..., :D])
+    out = ctx.alloc(case.S * case.n_heads * D * 4)
+    ctx.set_decode_schedule(velokv.SCHED_SPLIT)
+    try:
+        pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1])
+        assert pl["kernel"].startswith(f"vk_decode_wg_kv{kv}_g4"), pl
+        ctx.append_decode(pool, 0, ctx.upload(np.ascontiguousarray(kk[..., :D])),
+                          ctx.upload(np.ascontiguousarray(vv[..., :D])), velokv.DT_F16, ctx.upload(q64),
+                          velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
+                          int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
+                          bt_stride=case.block_tables.shape[1])
+        ctx.sync()
+    finally:
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)
+    ref_layer = oracle_layer(case)
+    assert_layer_equal(pool, 0, ref_layer)
+    got = out.download((case.S, case.n_heads, D), np.float32)
+    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens, scale=SCALE)
+    ok, err, nbad = tol_check(got, ref[..., :D])
+    assert ok, (err, nbad)
+
+
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("shared", [0, 8])
+def test_hd64_tree_verify(ctx, kv, shared):
+    print(f"hd64 tree kv={kv} shared={shared}", flush=True)
+    N, G, Hkv = 8, 4, 2
+    committed = np.array([shared * BS + 3, shared * BS + 60, shared * BS + 200, shared * BS], np.int32)
+    case = hd64_case(kv, committed + N, n_kv_heads=Hkv, n_heads=Hkv * G, seed=1430 + kv)
+    if shared:
+        for s in range(1, case.S):
+            case.k[s][:shared * BS] = case.k[0][:shared * BS]
+            case.v[s][:shared * BS] = case.v[0][:shared * BS]
+    pool = hd64_pool(ctx, case)
+    bt = case.block_tables.copy()
+    if shared:
+        bt[1:, :shared] = bt[0, :shared]
+    q64 = synth.normals_f16(case.S * N * case.n_heads * D, 1431).reshape(case.S, N, case.n_heads, D)
+    mask = np.tile(velokv.branching_tree([2, 2, 2], N).ancestor_mask(), (case.S, 1)).astype(np.uint32)
+    out = ctx.alloc(q64.size * 4)
+    ctx.tree_verify(pool, 0, ctx.upload(q64), velokv.DT_F16, out, ctx.upload(committed), ctx.upload(mask), case.S, N,
+                    case.n_heads, int(committed.max()), block_tables=ctx.upload(bt), bt_stride=bt.shape[1],
+                    shared_blocks=shared)
+    ctx.sync()
+    got = out.download(q64.shape, np.float32)
+    ref = O.tree_verify(oracle_layer(case), pad(q64), bt, committed, mask, scale=SCALE)
+    ok, err, nbad = tol_check(got, ref[..., :D])
+    assert ok, f"max err {err:.3g}, {nbad} out of tolerance"
+
+
+@pytest.mark.parametrize("style", [O.ROPE_INTERLEAVED, O.ROPE_HALF])
+@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
+def test_hd64_append_rope_bit_exact(ctx, kv, style):
+    """RoPE over 64-dim rows (pairs (2i, 2i+1) or (i, i + 32), angles of a 64-dim
+    table) fused into the append: pool bytes and rotated q bit for bit."""
+    print(f"hd64 rope kv={kv} style={style}", flush=True)
+    case = hd64_case(kv, [1, 17, 100, 257], n_kv_heads=2, n_heads=8, seed=1440)
+    rows = np.concatenate([np.full(int(L), s) for s, L in enumerate(case.ctx_lens)])
+    cpos = np.concatenate([np.arange(int(L)) for L in case.ctx_lens])
+    sl = synth.slots_for_positions(case.block_tables, cpos, BS, rows)
+    kk = np.concatenate([case.k[s][..., :D] for s in range(case.S)])
+    vv = np.concatenate([case.v[s][..., :D] for s in range(case.S)])
+    pos = (cpos + 5).astype(np.int32)
+    n_pos = int(pos.max()) + 1
+    table = velokv.rope_table(n_pos, D, 500000.0)
+    q = synth.normals_f16(len(sl) * 8 * D, 1441).reshape(len(sl), 8, D)
+    pool = velokv.Pool(ctx, 1, case.n_blocks, BS, 2, D, kv)
+    dq = ctx.upload(q)
+    ctx.append_rope(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(pos), ctx.upload(sl), len(sl),
+                    ctx.upload(table), n_pos, style, q=dq, q_dtype=velokv.DT_F16, n_heads=8)
+    ctx.sync()
+    kr = O.rope_apply(kk, pos, style, table)          # fp32, 64 dims
+    ref = O.Layer(case.n_blocks, 2, BS, HD, kv)
+    O.append(ref, pad(kr), pad(vv.astype(np.float32)), sl)
+    assert_layer_equal(pool, 0, ref)
+    qr = O.rope_apply(q, pos, style, table).astype(np.float16)
+    assert np.array_equal(dq.download(q.shape, np.float16).view(np.uint16), qr.view(np.uint16))
+
+
+@pytest.mark.parametrize("kv", [O.F32, O.I8_BLK])
+def test_hd64_tree_commit(ctx, kv):
+    print(f"hd64 commit kv={kv}", flush=True)
+    N = 8
+    ctxs = np.array([0, 14, 31, 33, 100], np.int32)
+    case = hd64_case(kv, ctxs + N, seed=1450)
+    pool = hd64_pool(ctx, case)
+    ref = oracle_layer(case)
+    accepts = [[0, 2, 5], [1, 3], [0, 1, 2, 3, 4, 5, 6, 7], [2, 4, 6], [7]]
+    acc = np.full((case.S, 32), -1, np.int32)
+    na = np.array([len(a) for a in accepts], np.int32)
+    for s, a in enumerate(accepts):
+        acc[s, :len(a)] = a
+    ctx.tree_commit(pool, ctx.upload(case.block_tables), case.block_tables.shape[1], ctx.upload(ctxs),
+                    ctx.upload(acc), 32, ctx.upload(na), case.S)
+    ctx.sync()
+    for s, a in enumerate(accepts):
+        O.tree_commit(ref, case.block_tables[s], int(ctxs[s]), a)
+    assert_layer_equal(pool, 0, ref)
+
+
+def test_hd64_limits(ctx):
+    for bad in (32, 96, 256):
+        with pytest.raises(velokv.VkError) as e:
+            velokv.Pool(ctx, 1, 8, BS, 2, bad, O.F16)
+        assert e.value.code == velokv.ERR_UNSUPPORTED, bad

@@ -367,8 +367,8 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
       d->max_pages_per_slot < 0)
     return fail(VK_ERR_BAD_ARG, "pool sizes must be positive");
   if (kv_esz(d->kv_type) == 0) return fail(VK_ERR_BAD_ARG, "unknown kv_type %d", d->kv_type);
-  if (d->head_dim != kHD)
-    return fail(VK_ERR_UNSUPPORTED, "kernels are built for head_dim %d (got %d)", kHD, d->head_dim);
+  if (d->head_dim != kHD && d->head_dim != kHD / 2)
+    return fail(VK_ERR_UNSUPPORTED, "head_dim %d: the kernels take 64 or 128", d->head_dim);
   int ps = 0;  // pages of 16 << ps tokens: 16-token tiles, 2^ps per page
   while (ps < kMaxPageShift && (kBS << ps) < d->block_size) ++ps;
   if ((kBS << ps) != d->block_size)
@@ -381,13 +381,15 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
   if (p->desc.max_pages_per_slot == 0) p->desc.max_pages_per_slot = d->n_blocks;
   const int esz = kv_esz(d->kv_type);
   PoolGeom& g = p->geom;  // tile view: 16-token tiles, 2^ps per page
-  g.tile_bytes = (uint32_t)(kBS * d->head_dim * esz);
+  // tiles are kHD wide; a head_dim-64 pool keeps zeros in dims 64..127
+  g.tile_bytes = (uint32_t)(kBS * kHD * esz);
   g.stile_bytes = (uint32_t)kv_stile(d->kv_type, kBS);
   g.n_blocks = d->n_blocks << ps;
   g.page_shift = ps;
   g.n_kv_heads = d->n_kv_heads;
   g.block_size = kBS;
-  g.head_dim = d->head_dim;
+  g.head_dim = kHD;
+  g.io_hd = d->head_dim;
   g.kv_type = d->kv_type;
   g.n_layer = d->n_layer;
   const uint64_t codes = (uint64_t)g.n_blocks * d->n_kv_heads * g.tile_bytes;
@@ -578,7 +580,6 @@ extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q
   if (in_dtype != VK_DT_F32 && in_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "in_dtype %d", in_dtype);
   if (rope_style != VK_ROPE_INTERLEAVED && rope_style != VK_ROPE_HALF)
     return fail(VK_ERR_BAD_ARG, "rope_style %d (VK_ROPE_INTERLEAVED or VK_ROPE_HALF)", rope_style);
-  if (pool->desc.head_dim != kHD) return fail(VK_ERR_UNSUPPORTED, "head_dim %d", pool->desc.head_dim);
   if (n_tok < 0 || n_pos <= 0) return fail(VK_ERR_BAD_ARG, "n_tok < 0 or n_pos <= 0");
   if (q && (n_heads <= 0 || (q_dtype != VK_DT_F32 && q_dtype != VK_DT_F16)))
     return fail(VK_ERR_BAD_ARG, "q needs n_heads > 0 and q_dtype VK_DT_F32 / VK_DT_F16");
@@ -675,9 +676,9 @@ void decode_choice(const vk_ctx* ctx, const vk_pool* pool, const vk_decode_args*
   const bool uniform = a->sum_context_len > 0 &&
                        (double)a->sum_context_len >= 0.97 * (double)a->n_seqs * (double)a->max_context_len;
   const int G = a->n_heads / d.n_kv_heads;
-  // the VALU kernels exist for group sizes 1, 2, 4, 8 only: other sizes always
+  // the VALU kernels exist for group sizes 1, 2, 4, 8 and head_dim 128 only: the rest always
   // take the matrix cores, and beyond one 16-row tile only fixed partitions
-  const bool valu_ok = fixed_group(G);
+  const bool valu_ok = fixed_group(G) && d.head_dim == kHD;
   *stream_k = a->partition_tokens == 0 && (kind != VK_DECODE_VALU || !valu_ok) && G <= kMaxGroupTile &&
               (sched == VK_SCHED_STREAM || sched == VK_SCHED_PACKED || (sched == VK_SCHED_AUTO && !uniform));
   *mfma = *stream_k || !valu_ok || kind == VK_DECODE_MFMA ||
@@ -904,6 +905,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   const float scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)d.head_dim);
 
   DecodeParams p{};
+  p.io_hd = pool->geom.io_hd;
   p.kc = L + g.k_off;
   p.vc = L + g.v_off;
   p.ks = g.stile_bytes ? L + g.ks_off : nullptr;
@@ -941,6 +943,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   p.err = ctx->err_word;
 
   MergeParams m{};
+  m.io_hd = pool->geom.io_hd;
   m.part_acc = p.part_acc;
   m.part_ml = p.part_ml;
   m.context_lens = a->context_lens;
@@ -1111,6 +1114,7 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   const float scale = a->scale != 0.f ? a->scale : 1.0f / std::sqrt((float)d.head_dim);
 
   DecodeParams p{};
+  p.io_hd = pool->geom.io_hd;
   p.kc = L + g.k_off;
   p.vc = L + g.v_off;
   p.ks = g.stile_bytes ? L + g.ks_off : nullptr;
@@ -1155,6 +1159,7 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   if (pl.max_parts == pl.prefix_chunks + 1) return VK_OK;
 
   MergeParams m{};
+  m.io_hd = pool->geom.io_hd;
   m.part_acc = p.part_acc;
   m.part_ml = p.part_ml;
   m.context_lens = a->context_lens;

@@ -180,7 +180,9 @@ template <int G>
 constexpr int lds_rows() { return G > 0 ? G : 16; }
 DEV void write_zero_rows_n(const DecodeParams& P, int s, int kvh, int g_n) {
   const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * g_n;
-  for (int g = 0; g < g_n; ++g) reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (HD / 2) + lane_id()] = make_float2(0.f, 0.f);
+  if (2 * lane_id() >= P.io_hd) return;
+  for (int g = 0; g < g_n; ++g)
+    reinterpret_cast<float2*>(P.out)[(hrow0 + g) * (P.io_hd / 2) + lane_id()] = make_float2(0.f, 0.f);
 }
 
 // Misuse is reported, not trapped: the kernel or-s a flag into the context's
@@ -795,11 +797,13 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   for (int rt = 0; rt < RT; ++rt) {
     const int R = row0 + 16 * rt + n;
     float qsum = 0.f;
-    const int64_t qoff = out_row(R) * HD + 32 * g;
+    // q rows are io_hd long: dims 32g.. past it are zero
+    const int64_t qoff = out_row(R) * P.io_hd + 32 * g;
+    const bool qin = R < nrows && 32 * g < P.io_hd;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
-      if (R < nrows) {
+      if (qin) {
         if constexpr (QT == DT_F32) {
           const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff) + 2 * kc;
           const float4 x0 = q32[0], x1 = q32[1];
@@ -1062,9 +1066,11 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
             }
           }
           const float inv = L > 0.f ? 1.f / L : 0.f;  // a tree row that sees no token attends to nothing
-          float4* dst = reinterpret_cast<float4*>(P.out + orow * HD + 8 * n);
-          dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-          dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+          if (8 * n < P.io_hd) {
+            float4* dst = reinterpret_cast<float4*>(P.out + orow * P.io_hd + 8 * n);
+            dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+            dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+          }
         } else {
           const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
           float4* dst = reinterpret_cast<float4*>(pacc + pr * HD + 8 * n);
@@ -1143,11 +1149,11 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int R = row0 + 16 * rt + n;
-    const int64_t qoff = (R < nrows ? out_row(R) : 0) * HD + 4 * g;
+    const int64_t qoff = (R < nrows ? out_row(R) : 0) * P.io_hd + 4 * g;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (R < nrows) {
+      if (R < nrows && 16 * j < P.io_hd) {
         if constexpr (QT == DT_F32) {
           x = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 16 * j);
         } else {
@@ -1276,7 +1282,8 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
         if (direct) {
           const float inv = lr > 0.f ? 1.f / lr : 0.f;
 #pragma unroll
-          for (int t = 0; t < 8; ++t) P.out[orow * HD + 16 * t + n] = acc[rt][t][r] * inv;
+          for (int t = 0; t < 8; ++t)
+            if (16 * t < P.io_hd) P.out[orow * P.io_hd + 16 * t + n] = acc[rt][t][r] * inv;
         } else {
           const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
 #pragma unroll
@@ -1483,8 +1490,9 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   }
   __syncthreads();
   const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * Gn;
-  for (int i = (int)threadIdx.x; i < Gn * HD; i += (int)blockDim.x) {
-    const int r = i / HD, d = i - r * HD;
+  const int IO = P.io_hd;  // output dims of a row; the partials are HD wide
+  for (int i = (int)threadIdx.x; i < Gn * IO; i += (int)blockDim.x) {
+    const int r = i / IO, d = i - r * IO;
     float M = kNegInf;
     for (int v = 0; v < nw; ++v) M = fmaxf(M, wml[v][r][0]);
     float L = 0.f, o = 0.f;
@@ -1495,7 +1503,7 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
       L = fmaf(e, wml[v][r][1], L);
       o = fmaf(e, wacc[v][r][d], o);
     }
-    P.out[(hrow0 + r) * HD + d] = L > 0.f ? o / L : 0.f;
+    P.out[(hrow0 + r) * IO + d] = L > 0.f ? o / L : 0.f;
   }
 }
 
@@ -1584,16 +1592,17 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
     const int s = seq_at[i / Hkv], kvh = i % Hkv;
     const int nb = nb_l[s];
     const int64_t hrow0 = (int64_t)s * P.n_heads + (int64_t)kvh * G;
+    const int IO = P.io_hd;  // output dims of a row; the partials are HD wide
     if (nb == 0) {
-      for (int e = (int)threadIdx.x; e < G * HD; e += (int)blockDim.x) P.out[hrow0 * HD + e] = 0.f;
+      for (int e = (int)threadIdx.x; e < G * IO; e += (int)blockDim.x) P.out[hrow0 * IO + e] = 0.f;
       continue;
     }
     int w_lo, w_hi;
     sk_segment_workers(sp, u, nb, pen, &w_lo, &w_hi);
     u += nb + pen;
     if (w_lo == w_hi) continue;  // written by its wave
-    for (int e = (int)threadIdx.x; e < G * HD; e += (int)blockDim.x) {
-      const int g = e / HD, d = e - g * HD;
+    for (int e = (int)threadIdx.x; e < G * IO; e += (int)blockDim.x) {
+      const int g = e / IO, d = e - g * IO;
       float M = kNegInf;
       for (int v = w_lo; v <= w_hi; ++v) M = fmaxf(M, wml[v][v == w_lo ? 1 : 0][g][0]);
       float L = 0.f, o = 0.f;
@@ -1605,7 +1614,7 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
         L = fmaf(ev, wml[v][sl][g][1], L);
         o = fmaf(ev, wacc[v][sl][g][d], o);
       }
-      P.out[(hrow0 + g) * HD + d] = L > 0.f ? o / L : 0.f;
+      P.out[(hrow0 + g) * IO + d] = L > 0.f ? o / L : 0.f;
     }
   }
 }
@@ -1729,12 +1738,12 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   for (int rt = 0; rt < RT; ++rt) {
     const int r = wrow0 + 16 * rt + n;
     const bool valid = r < R;
-    const int64_t qoff = (valid ? out_row(r) : 0) * HD + 8 * g;
+    const int64_t qoff = (valid ? out_row(r) : 0) * P.io_hd + 8 * g;
     float qsum = 0.f;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (valid) {
+      if (valid && 32 * kc < P.io_hd) {
         if constexpr (QT == DT_F32) {
           const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 32 * kc);
           const float4 x0 = q32[0], x1 = q32[1];
@@ -2046,7 +2055,8 @@ DEV void merge_row(const MergeParams& P, int64_t out_row, int np, PR pr) {
   }
   L = wave_sum(L);
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  reinterpret_cast<float2*>(P.out)[out_row * (HD / 2) + lane] = make_float2(o0 * inv, o1 * inv);
+  if (2 * lane < P.io_hd)
+    reinterpret_cast<float2*>(P.out)[out_row * (P.io_hd / 2) + lane] = make_float2(o0 * inv, o1 * inv);
 }
 
 // Split-K merge: one wave per (sequence, row) with partials [row][max_parts]:
@@ -2083,7 +2093,7 @@ __device__ void decode_merge_sk(const MergeParams& P) {
   const int kvh = h / G, gi = h - kvh * G;
   const int nb = (max(0, min(P.context_lens[s], P.cap_tokens)) + BS - 1) / BS;
   if (nb == 0) {
-    reinterpret_cast<float2*>(P.out)[(int64_t)r * (HD / 2) + lane] = make_float2(0.f, 0.f);
+    if (2 * lane < P.io_hd) reinterpret_cast<float2*>(P.out)[(int64_t)r * (P.io_hd / 2) + lane] = make_float2(0.f, 0.f);
     return;
   }
   const int64_t W = P.sk_prefix[P.n_seqs];
@@ -2114,25 +2124,30 @@ DEV void load_x2(const void* src, int in_dtype, int64_t off, float& x0, float& x
 
 // ---- RoPE (fused into the append) --------------------------------------------
 // Pair i of a head row at position p is rotated by the table's (cos, sin) of
-// angle p * base^(-2i/D): ROPE_INTERLEAVED pairs dims (2i, 2i+1)
+// angle p * base^(-2i/D), D the caller's head_dim: ROPE_INTERLEAVED pairs dims (2i, 2i+1)
 // (kernels.metal:103-131), ROPE_HALF pairs dims (i, i + D/2)
 // (llama_cpu.rs:113-131). y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32 with
 // every product and sum rounded separately (no fused multiply-add), the
 // reference's expression order. Lane l holds dims 2l, 2l+1 of the row.
-DEV void rope_rotate(int style, const float* cos_sin, int pos, float& x0, float& x1) {
+// D = 64 or 128: lanes 2l >= D hold zeros and stay zero.
+DEV void rope_rotate(int style, const float* cos_sin, int pos, int D, float& x0, float& x1) {
 #pragma clang fp contract(off)
   const int lane = lane_id();
-  const float* row = cos_sin + (int64_t)pos * HD;  // D/2 pairs of (cos, sin)
+  const float* row = cos_sin + (int64_t)pos * D;  // D/2 pairs of (cos, sin)
+  const int hl = D / 4;                             // lanes of one half of the row
   if (style == ROPE_INTERLEAVED) {
-    const float2 cs = reinterpret_cast<const float2*>(row)[lane];
-    const float y0 = x0 * cs.x - x1 * cs.y;
-    const float y1 = x0 * cs.y + x1 * cs.x;
-    x0 = y0;
-    x1 = y1;
+    if (2 * lane < D) {
+      const float2 cs = reinterpret_cast<const float2*>(row)[lane];
+      const float y0 = x0 * cs.x - x1 * cs.y;
+      const float y1 = x0 * cs.y + x1 * cs.x;
+      x0 = y0;
+      x1 = y1;
+    }
   } else {
-    const float p0 = __shfl_xor(x0, 32, WAVE), p1 = __shfl_xor(x1, 32, WAVE);  // dims d ^ 64
-    const float4 cs = reinterpret_cast<const float4*>(row)[lane & 31];  // pairs 2(l%32), 2(l%32)+1
-    if (lane < 32) {  // first half: y = x c - partner s
+    const float p0 = __shfl_xor(x0, hl, WAVE), p1 = __shfl_xor(x1, hl, WAVE);  // dims d ^ D/2
+    if (2 * lane >= D) return;
+    const float4 cs = reinterpret_cast<const float4*>(row)[lane & (hl - 1)];  // pairs 2(l%hl), 2(l%hl)+1
+    if (lane < hl) {  // first half: y = x c - partner s
       const float y0 = x0 * cs.x - p0 * cs.y;
       const float y1 = x1 * cs.z - p1 * cs.w;
       x0 = y0;
@@ -2169,9 +2184,12 @@ DEV int64_t token_slot(const AppendParams& P, int m) {
 }
 
 // K/V row elements (dims 2l, 2l+1) of token m, head h, rotated for K when RoPE is on.
+// Rows are io_hd long; lanes past it hold zeros (the tile's upper dims).
 DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h, float& x0, float& x1) {
-  load_x2(src, P.in_dtype, ((int64_t)m * P.g.n_kv_heads + h) * HD + 2 * lane_id(), x0, x1);
-  if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, P.positions[m], x0, x1);
+  const int io = P.g.io_hd;
+  x0 = x1 = 0.f;
+  if (2 * lane_id() < io) load_x2(src, P.in_dtype, ((int64_t)m * P.g.n_kv_heads + h) * io + 2 * lane_id(), x0, x1);
+  if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, P.positions[m], io, x0, x1);
 }
 
 // Byte offset inside a (block, head) tile of element (token, dim).
@@ -2408,7 +2426,7 @@ DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes, in
   const int Hkv = P.g.n_kv_heads;
   const int d0 = 2 * lane;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
-  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE)) {
+  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE) && P.g.io_hd == HD) {
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src) + ((int64_t)n * Hkv + h) * HD + d0;
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2)) = s16[0];
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2)) = s16[1];
@@ -2436,10 +2454,12 @@ DEV void append_kernel(const AppendParams& P) {
     for (int n = w0; n < w1; ++n) {
       const int pos = P.positions[n];
       if (pos < 0 || pos >= P.n_pos) continue;
-      const int64_t off = ((int64_t)n * P.n_heads + head) * HD + 2 * lane_id();
-      float x0, x1;
-      load_x2(P.q, P.q_dtype, off, x0, x1);
-      rope_rotate(P.rope, P.cos_sin, pos, x0, x1);
+      const int64_t off = ((int64_t)n * P.n_heads + head) * P.g.io_hd + 2 * lane_id();
+      float x0 = 0.f, x1 = 0.f;
+      const bool in = 2 * lane_id() < P.g.io_hd;
+      if (in) load_x2(P.q, P.q_dtype, off, x0, x1);
+      rope_rotate(P.rope, P.cos_sin, pos, P.g.io_hd, x0, x1);
+      if (!in) continue;
       if (P.q_dtype == DT_F16) {
         reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(P.q) + off)[0] =
             (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
