@@ -31,14 +31,20 @@
  *    one of them, as the reference does with its mutexes (metal/backend.rs:142-144).
  *
  * Layout of one layer of a pool in HBM ("build layout"; the reference layout
- * is [blk][tok][head][D(+4)], kernels.metal:474,700):
- *    K codes   [n_blocks][n_kv_heads][block_size][head_dim] for F32 / F16;
- *              I8_*: [n_blocks][n_kv_heads][2][block_size][head_dim/32][16] (dims
- *              32c..32c+15 of token t at byte (4t + c)*16 of the tile, dims
- *              32c+16..32c+31 at 1024 + (4t + c)*16)
- *    V codes   [n_blocks][n_kv_heads][block_size/2][head_dim][2]   (token pairs interleaved)
- *    K scales  I8_BLK: fp16 [n_blocks][n_kv_heads]; I8_REF: fp32 [n_blocks][n_kv_heads][block_size]
+ * is [blk][tok][head][D(+4)], kernels.metal:474,700). The unit is a tile of 16
+ * tokens and 128 dims per KV head; a page of block_size = 16 << s tokens is the
+ * 2^s tiles n_tiles = page << s .. (page + 1 << s) - 1, so a flat slot
+ * page * block_size + offset is also tile * 16 + offset % 16:
+ *    K codes   [n_tiles][n_kv_heads][16][128] for F32 / F16;
+ *              I8_*: [n_tiles][n_kv_heads][2][16][4][16] (dims 32c..32c+15 of
+ *              token t at byte (4t + c)*16 of the tile, dims 32c+16..32c+31 at
+ *              1024 + (4t + c)*16)
+ *    V codes   [n_tiles][n_kv_heads][8][128][2]   (token pairs interleaved)
+ *    K scales  I8_BLK: fp16 [n_tiles][n_kv_heads] (one scale per 16 tokens and
+ *              head); I8_REF: fp32 [n_tiles][n_kv_heads][16]
  *    V scales  same as K scales
+ * n_tiles = n_blocks * block_size / 16. A head_dim-64 pool stores each head in
+ * dims 0..63 of the tile and zeros in 64..127 (callers pass 64-dim rows).
  * Element size: F32 4, F16 2, I8_* 1 byte.
  */
 #ifndef VELOKV_H
@@ -116,7 +122,8 @@ int vk_ctx_check(vk_ctx* ctx, uint32_t* flags);
  * v_mfma_f32_16x16x{32,16}_f16 over fp16 / int8 KV, where an fp32 q is split
  * into fp16 hi + lo parts; on v_mfma_f32_16x16x4_f32 in fp32 throughout over
  * fp32 KV), VK_DECODE_VALU (v_dot2_f32_f16, or fp32 arithmetic for an fp32 q or
- * fp32 KV, on the vector ALUs; GQA group sizes 1, 2, 4, 8) or VK_DECODE_AUTO
+ * fp32 KV, on the vector ALUs; GQA group sizes 1, 2, 4, 8 and head_dim 128,
+ * else the matrix cores run) or VK_DECODE_AUTO
  * (MFMA for int8 and fp32 KV and for fp32 queries, VALU for fp16 queries over
  * fp16 KV with fixed partitions: the faster one on MI355X for each; stream-K
  * batches run on the matrix cores). No reference counterpart. */
@@ -153,9 +160,12 @@ int vk_ctx_set_decode_schedule(vk_ctx* ctx, int schedule);
 typedef struct vk_pool_desc {
   int32_t n_layer;        /* MemoryRuntimeConfig::n_layer (runtime.rs:55)          */
   int32_t n_blocks;       /* MemoryRuntimeConfig::paged_total_pages (runtime.rs:53) */
-  int32_t block_size;     /* MemoryRuntimeConfig::paged_block_size (runtime.rs:51)  */
+  int32_t block_size;     /* MemoryRuntimeConfig::paged_block_size (runtime.rs:51):
+                             16, 32, 64, 128 or 256 tokens per page; other sizes >
+                             0 are VK_ERR_UNSUPPORTED, 0 VK_ERR_INVALID_BLOCK_SIZE */
   int32_t n_kv_heads;     /* ModelMeta::n_head_kv                                  */
-  int32_t head_dim;       /* ModelMeta::head_dim                                   */
+  int32_t head_dim;       /* ModelMeta::head_dim: 128, or 64 (stored in 128-wide
+                             tiles, so it reads the bytes of 128)                 */
   int32_t kv_type;        /* VK_KV_*  (MemoryRuntimeConfig::kv_type)               */
   int32_t max_slots;      /* MemoryRuntimeConfig::max_slots (runtime.rs:59)        */
   int32_t max_pages_per_slot; /* row length of the slot block table; 0 = n_blocks
