@@ -103,8 +103,7 @@ def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride:
                  hd: int = HD) -> int:
     """Algorithmic HBM bytes of one decode call: each K/V element of every context
     token read once, its scales, q, the output and the block-table entries used
-    (hd = the caller's head_dim: a head_dim-64 pool also reads its zero upper
-    halves, which these bytes do not count)."""
+    (hd = the pool's head_dim)."""
     tok = int(lens.sum())
     blocks = int(sum(-(-int(L) // BS) for L in lens))
     esz = {velokv.KV_F16: 2, velokv.KV_I8_BLK: 1, velokv.KV_I8_REF: 1, velokv.KV_F32: 4}[kv]

@@ -43,8 +43,10 @@
  *    K scales  I8_BLK: fp16 [n_tiles][n_kv_heads] (one scale per 16 tokens and
  *              head); I8_REF: fp32 [n_tiles][n_kv_heads][16]
  *    V scales  same as K scales
- * n_tiles = n_blocks * block_size / 16. A head_dim-64 pool stores each head in
- * dims 0..63 of the tile and zeros in 64..127 (callers pass 64-dim rows).
+ * n_tiles = n_blocks * block_size / 16. A head_dim-64 pool has 64-dim tiles in
+ * the same layouts at D = 64: [16][64] K, [8][64][2] V, and int8 K as
+ * [2][16][2][16] (dims 32c..32c+15 of token t at byte (2t + c)*16, dims
+ * 32c+16..32c+31 at 512 + (2t + c)*16); callers pass 64-dim rows.
  * Element size: F32 4, F16 2, I8_* 1 byte.
  */
 #ifndef VELOKV_H
@@ -164,8 +166,7 @@ typedef struct vk_pool_desc {
                              16, 32, 64, 128 or 256 tokens per page; other sizes >
                              0 are VK_ERR_UNSUPPORTED, 0 VK_ERR_INVALID_BLOCK_SIZE */
   int32_t n_kv_heads;     /* ModelMeta::n_head_kv                                  */
-  int32_t head_dim;       /* ModelMeta::head_dim: 128, or 64 (stored in 128-wide
-                             tiles, so it reads the bytes of 128)                 */
+  int32_t head_dim;       /* ModelMeta::head_dim: 128 or 64                        */
   int32_t kv_type;        /* VK_KV_*  (MemoryRuntimeConfig::kv_type)               */
   int32_t max_slots;      /* MemoryRuntimeConfig::max_slots (runtime.rs:59)        */
   int32_t max_pages_per_slot; /* row length of the slot block table; 0 = n_blocks

@@ -242,7 +242,8 @@ static uint64_t elem_off(const vko_layer* L, int is_v, int64_t blk, int h, int t
   const uint64_t tile = (uint64_t)L->block_size * L->head_dim * esz;
   const uint64_t base = ((uint64_t)blk * L->n_kv_heads + h) * tile;
   /* int8 K: [h][tok][D/32][16], h = (d/16) % 2 (two 16-byte pieces per 32 dims) */
-  if (!is_v && esz == 1) return base + (uint64_t)(((d >> 4) & 1) * (tile / 2) + (4 * tok + (d >> 5)) * 16 + (d & 15));
+  if (!is_v && esz == 1)
+    return base + (uint64_t)(((d >> 4) & 1) * (tile / 2) + (tok * (L->head_dim / 32) + (d >> 5)) * 16 + (d & 15));
   if (!is_v) return base + ((uint64_t)tok * L->head_dim + d) * esz;
   return base + ((uint64_t)((tok >> 1) * L->head_dim + d) * 2 + (tok & 1)) * esz;
 }

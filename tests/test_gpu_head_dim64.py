@@ -1,20 +1,18 @@
 """GPU parity for head_dim 64 (the reference's kernels take any head_dim up to
 128, kernels.metal:464; the byte formula of model_loader.rs:129-140 scales with
-it). A head_dim-64 pool stores each head in a 128-wide tile whose dims 64..127
-stay zero: appends write the caller's 64-dim rows and zeros, attention reads q
-rows of 64 dims (zero above) and writes 64-dim output rows.
+it). A head_dim-64 pool stores 64-dim tiles (16 tokens x 64 dims, the layouts of
+the 128-dim tiles at D = 64), so it holds and reads its own bytes only.
 
-So the pool bytes must equal the oracle's 128-dim layer filled with the same K/V
-padded with zeros (bit for bit, every KV type), and attention must equal the
-oracle's with the softmax scale 1/sqrt(64) (within the north-star tolerance);
-for fp16 / fp32 KV it must also equal the oracle run at head_dim 64 directly,
-which pins the padding itself."""
+The pool bytes must equal the oracle's layer built at head_dim 64 (bit for bit,
+every KV type) and attention must equal the oracle's at head_dim 64 (within the
+north-star tolerance). The oracle at 64 dims is pinned on the CPU against the
+oracle at 128 dims over zero-padded rows (tests/test_oracle.py)."""
 import numpy as np
 import pytest
 
 import pyoracle as O
 import velokv
-from cases import BS, HD, make_case, oracle_layer, tol_check
+from cases import BS, make_case, tol_check
 from test_gpu_append_copy import assert_layer_equal
 from velokv import synth
 
@@ -22,23 +20,14 @@ pytestmark = pytest.mark.gpu
 
 D = 64
 KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
-SCALE = 1.0 / np.sqrt(D)
-
-
-def pad(x):
-    """[..., 64] -> [..., 128] with zeros above."""
-    out = np.zeros(x.shape[:-1] + (HD,), x.dtype)
-    out[..., :D] = x
-    return out
 
 
 def hd64_case(kv, lens, n_kv_heads=2, n_heads=8, seed=1, outlier_scale=8.0):
-    """make_case with 64-dim K, V and q (the 128-dim case's first 64 dims) and the
-    padded copy the 128-dim oracle reads."""
+    """make_case with 64-dim K, V and q (the 128-dim case's first 64 dims)."""
     c = make_case(kv, lens, n_kv_heads=n_kv_heads, n_heads=n_heads, seed=seed, outlier_scale=outlier_scale)
-    c.k = [pad(np.ascontiguousarray(k[..., :D])) for k in c.k]
-    c.v = [pad(np.ascontiguousarray(v[..., :D])) for v in c.v]
-    c.q = pad(np.ascontiguousarray(c.q[..., :D]))
+    c.k = [np.ascontiguousarray(k[..., :D]) for k in c.k]
+    c.v = [np.ascontiguousarray(v[..., :D]) for v in c.v]
+    c.q = np.ascontiguousarray(c.q[..., :D])
     return c
 
 
@@ -47,18 +36,18 @@ def hd64_pool(ctx, case, with_last=True):
     parts = [case.prefill_slots()] + ([case.last_slots()] if with_last else [])
     for sl, kk, vv in parts:
         if len(sl):
-            ctx.append(pool, 0, ctx.upload(np.ascontiguousarray(kk[..., :D])),
-                       ctx.upload(np.ascontiguousarray(vv[..., :D])), velokv.DT_F16, ctx.upload(sl), len(sl))
+            ctx.append(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(sl), len(sl))
     ctx.sync()
     return pool
 
 
-def direct_oracle(case):
-    """The oracle at head_dim 64 (fp16 / fp32 KV: its int8 K layout is written for 128)."""
+def oracle64(case, with_last=True):
+    """The oracle's layer at head_dim 64 with the case's tokens."""
     L = O.Layer(case.n_blocks, case.n_kv_heads, BS, D, case.kv_type)
-    for sl, kk, vv in (case.prefill_slots(), case.last_slots()):
+    parts = [case.prefill_slots()] + ([case.last_slots()] if with_last else [])
+    for sl, kk, vv in parts:
         if len(sl):
-            O.append(L, np.ascontiguousarray(kk[..., :D]), np.ascontiguousarray(vv[..., :D]), sl)
+            O.append(L, kk, vv, sl)
     return L
 
 
@@ -67,7 +56,11 @@ def test_hd64_append_bit_exact(ctx, kv):
     print(f"hd64 append kv={kv}", flush=True)
     case = hd64_case(kv, [1, 15, 16, 17, 33, 200, 257], seed=1400)
     pool = hd64_pool(ctx, case)
-    assert_layer_equal(pool, 0, oracle_layer(case))
+    ref = oracle64(case)
+    # 16 tokens x 64 dims per (page, head): the reference's byte formula at D = 64
+    esz = {O.F32: 4, O.F16: 2}.get(kv, 1)
+    assert pool.download_layer(0)["k"].size == ref.k.size == case.n_blocks * case.n_kv_heads * BS * D * esz
+    assert_layer_equal(pool, 0, ref)
 
 
 SCHEDS = {"split": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 0), "split-p64": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 64),
@@ -100,14 +93,9 @@ def test_hd64_decode(ctx, kv, sched, qd):
         ctx.set_decode_kernel(velokv.DECODE_AUTO)
         ctx.set_decode_schedule(velokv.SCHED_AUTO)
     got = out.download((case.S, case.n_heads, D), np.float32)
-    ref = O.paged_decode(oracle_layer(case), pad(q64), case.block_tables, case.ctx_lens, scale=SCALE)
-    assert np.all(ref[..., D:] == 0.0)
-    ok, err, nbad = tol_check(got, ref[..., :D])
+    ref = O.paged_decode(oracle64(case), q64, case.block_tables, case.ctx_lens)
+    ok, err, nbad = tol_check(got, ref)
     assert ok, f"max err {err:.3g}, {nbad} out of tolerance ({pl['kernel']})"
-    if kv in (O.F16, O.F32):
-        ref_d = O.paged_decode(direct_oracle(case), q64, case.block_tables, case.ctx_lens)
-        ok, err, nbad = tol_check(got, ref_d)
-        assert ok, f"vs the oracle at head_dim 64: max err {err:.3g}, {nbad} out of tolerance"
 
 
 @pytest.mark.parametrize("kv", [O.F32, O.I8_BLK])
@@ -131,11 +119,11 @@ def test_hd64_workgroup_split_and_append_decode(ctx, kv):
         ctx.sync()
     finally:
         ctx.set_decode_schedule(velokv.SCHED_AUTO)
-    ref_layer = oracle_layer(case)
+    ref_layer = oracle64(case)
     assert_layer_equal(pool, 0, ref_layer)
     got = out.download((case.S, case.n_heads, D), np.float32)
-    ref = O.paged_decode(ref_layer, case.q, case.block_tables, case.ctx_lens, scale=SCALE)
-    ok, err, nbad = tol_check(got, ref[..., :D])
+    ref = O.paged_decode(ref_layer, q64, case.block_tables, case.ctx_lens)
+    ok, err, nbad = tol_check(got, ref)
     assert ok, (err, nbad)
 
 
@@ -162,8 +150,8 @@ def test_hd64_tree_verify(ctx, kv, shared):
                     shared_blocks=shared)
     ctx.sync()
     got = out.download(q64.shape, np.float32)
-    ref = O.tree_verify(oracle_layer(case), pad(q64), bt, committed, mask, scale=SCALE)
-    ok, err, nbad = tol_check(got, ref[..., :D])
+    ref = O.tree_verify(oracle64(case), q64, bt, committed, mask)
+    ok, err, nbad = tol_check(got, ref)
     assert ok, f"max err {err:.3g}, {nbad} out of tolerance"
 
 
@@ -189,8 +177,8 @@ def test_hd64_append_rope_bit_exact(ctx, kv, style):
                     ctx.upload(table), n_pos, style, q=dq, q_dtype=velokv.DT_F16, n_heads=8)
     ctx.sync()
     kr = O.rope_apply(kk, pos, style, table)          # fp32, 64 dims
-    ref = O.Layer(case.n_blocks, 2, BS, HD, kv)
-    O.append(ref, pad(kr), pad(vv.astype(np.float32)), sl)
+    ref = O.Layer(case.n_blocks, 2, BS, D, kv)
+    O.append(ref, kr, vv.astype(np.float32), sl)
     assert_layer_equal(pool, 0, ref)
     qr = O.rope_apply(q, pos, style, table).astype(np.float16)
     assert np.array_equal(dq.download(q.shape, np.float16).view(np.uint16), qr.view(np.uint16))
@@ -203,7 +191,7 @@ def test_hd64_tree_commit(ctx, kv):
     ctxs = np.array([0, 14, 31, 33, 100], np.int32)
     case = hd64_case(kv, ctxs + N, seed=1450)
     pool = hd64_pool(ctx, case)
-    ref = oracle_layer(case)
+    ref = oracle64(case)
     accepts = [[0, 2, 5], [1, 3], [0, 1, 2, 3, 4, 5, 6, 7], [2, 4, 6], [7]]
     acc = np.full((case.S, 32), -1, np.int32)
     na = np.array([len(a) for a in accepts], np.int32)

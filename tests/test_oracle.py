@@ -444,22 +444,60 @@ def test_copy_blocks_invariants(kv):
     assert set(changed.tolist()) <= set(dst)
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
-def test_tile_layout_is_a_permutation_with_line_friendly_int8_k(kv):
+def test_tile_layout_is_a_permutation_with_line_friendly_int8_k(kv, D):
     """Every (token, dim) of a tile has its own offset (a permutation of the
-    tile); int8 K puts the 32 codes of dims 32c..32c+31 of token t in two
-    16-byte pieces at (4t + c)*16 and 1024 + (4t + c)*16."""
-    L = O.Layer(1, 1, BS, HD, kv)
+    16 x D tile); int8 K puts the 32 codes of dims 32c..32c+31 of token t in two
+    16-byte pieces at (t D/32 + c)*16 and 8 D + (t D/32 + c)*16."""
+    L = O.Layer(1, 1, BS, D, kv)
     esz = O.ESZ[kv]
     for is_v in (0, 1):
         idx = O._tile_index(L, is_v)
-        assert np.array_equal(np.sort(idx.ravel() // esz), np.arange(BS * HD))
+        assert np.array_equal(np.sort(idx.ravel() // esz), np.arange(BS * D))
     idx = O._tile_index(L, 0)
     if esz == 1:
+        n = D // 32
         for t in (0, 7, 15):
-            for c in range(4):
-                assert list(idx[t, 32 * c:32 * c + 16]) == list(range((4 * t + c) * 16, (4 * t + c) * 16 + 16))
-                assert list(idx[t, 32 * c + 16:32 * c + 32]) == list(range(1024 + (4 * t + c) * 16,
-                                                                          1024 + (4 * t + c) * 16 + 16))
+            for c in range(n):
+                p = (n * t + c) * 16
+                assert list(idx[t, 32 * c:32 * c + 16]) == list(range(p, p + 16))
+                assert list(idx[t, 32 * c + 16:32 * c + 32]) == list(range(8 * D + p, 8 * D + p + 16))
     else:
-        assert np.array_equal(idx, (np.arange(BS)[:, None] * HD + np.arange(HD)[None, :]) * esz)
+        assert np.array_equal(idx, (np.arange(BS)[:, None] * D + np.arange(D)[None, :]) * esz)
+    vidx = O._tile_index(L, 1)  # V: token pairs interleaved, [tok/2][D][2]
+    t = np.arange(BS)[:, None]
+    assert np.array_equal(vidx, (((t >> 1) * D + np.arange(D)[None, :]) * 2 + (t & 1)) * esz)
+
+
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
+def test_head_dim64_layer_equals_zero_padded_128(kv):
+    """The oracle at head_dim 64 (16 x 64 tiles) against the oracle at 128 over
+    the same rows zero-padded: every (token, dim) holds the same code and scale
+    (an int8 scale comes from an absmax, which zero dims do not move), the padded
+    dims stay zero, and attention with the 1/sqrt(64) scale is bit for bit the
+    same (the zero dims add exact zeros)."""
+    D = 64
+    case = make_case(kv, [37, 16, 70], n_kv_heads=2, n_heads=4, seed=23, outlier_scale=8.0)
+    L64 = O.Layer(case.n_blocks, 2, BS, D, kv)
+    L128 = O.Layer(case.n_blocks, 2, BS, HD, kv)
+    for sl, kk, vv in (case.prefill_slots(), case.last_slots()):
+        O.append(L64, np.ascontiguousarray(kk[..., :D]), np.ascontiguousarray(vv[..., :D]), sl)
+        kp, vp = np.zeros_like(kk), np.zeros_like(vv)
+        kp[..., :D], vp[..., :D] = kk[..., :D], vv[..., :D]
+        O.append(L128, kp, vp, sl)
+    used = sorted({int(b) for s in range(case.S) for b in case.block_tables[s, :(int(case.ctx_lens[s]) + BS - 1) // BS]})
+    for b in used:
+        for h in range(2):
+            for is_v in (0, 1):
+                t64, t128 = L64.tile_codes(is_v, b, h), L128.tile_codes(is_v, b, h)
+                assert np.array_equal(t64, t128[:, :D])
+                assert not np.any(t128[:, D:])
+    if L64.ks is not None:
+        assert np.array_equal(L64.ks, L128.ks) and np.array_equal(L64.vs, L128.vs)
+    q64 = np.ascontiguousarray(case.q[..., :D])
+    qp = np.zeros_like(case.q)
+    qp[..., :D] = q64
+    got = O.paged_decode(L64, q64, case.block_tables, case.ctx_lens)
+    ref = O.paged_decode(L128, qp, case.block_tables, case.ctx_lens, scale=1.0 / np.sqrt(D))
+    assert np.array_equal(got, ref[..., :D])

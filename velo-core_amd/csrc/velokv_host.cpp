@@ -82,6 +82,11 @@ PoolGeom page_geom(const PoolGeom& t) {
   return g;
 }
 
+// The append kernel of a pool (the I8_BLK rule has its own build for head_dim 64).
+std::string append_kernel_name(int kv_type, int head_dim) {
+  return "vk_append_kv" + std::to_string(kv_type) + (kv_type == VK_KV_I8_BLK && head_dim != kHD ? "_d64" : "");
+}
+
 std::string default_code_object_path() {
   Dl_info info;
   if (dladdr(reinterpret_cast<void*>(&vk_ctx_create), &info) && info.dli_fname) {
@@ -154,6 +159,7 @@ namespace {
 
 const char* const kKernelNames[] = {
     "vk_decode_merge", "vk_decode_merge_sk", "vk_append_kv0", "vk_append_kv1", "vk_append_kv2", "vk_append_kv3",
+    "vk_append_kv3_d64",
     "vk_slot_mapping", "vk_copy_blocks", "vk_fill_normal_f16", "vk_nixl_check", "vk_nixl_copy",
     "vk_tree_commit_kv0", "vk_tree_commit_kv1", "vk_tree_commit_kv2", "vk_tree_commit_kv3",
 };
@@ -381,14 +387,14 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
   if (p->desc.max_pages_per_slot == 0) p->desc.max_pages_per_slot = d->n_blocks;
   const int esz = kv_esz(d->kv_type);
   PoolGeom& g = p->geom;  // tile view: 16-token tiles, 2^ps per page
-  // tiles are kHD wide; a head_dim-64 pool keeps zeros in dims 64..127
-  g.tile_bytes = (uint32_t)(kBS * kHD * esz);
+  // a tile holds 16 tokens of one head, head_dim wide
+  g.tile_bytes = (uint32_t)(kBS * d->head_dim * esz);
   g.stile_bytes = (uint32_t)kv_stile(d->kv_type, kBS);
   g.n_blocks = d->n_blocks << ps;
   g.page_shift = ps;
   g.n_kv_heads = d->n_kv_heads;
   g.block_size = kBS;
-  g.head_dim = kHD;
+  g.head_dim = d->head_dim;
   g.io_hd = d->head_dim;
   g.kv_type = d->kv_type;
   g.n_layer = d->n_layer;
@@ -549,7 +555,7 @@ extern "C" int vk_append(vk_ctx* ctx, vk_pool* pool, int32_t layer, const void* 
   p.err = ctx->err_word;
   p.claim = pool->claim;
   p.epoch = pool->claim ? pool->next_epoch() : 0u;
-  const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
+  const std::string name = append_kernel_name(pool->desc.kv_type, pool->desc.head_dim);
   if ((rc = set_device(ctx))) return rc;
   return launch(ctx, name.c_str(), dim3((unsigned)((n_tok + p.tok_per_wg - 1) / p.tok_per_wg),
                                         (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
@@ -606,7 +612,7 @@ extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q
   p.err = ctx->err_word;
   p.claim = pool->claim;
   p.epoch = pool->claim ? pool->next_epoch() : 0u;
-  const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
+  const std::string name = append_kernel_name(pool->desc.kv_type, pool->desc.head_dim);
   if ((rc = set_device(ctx))) return rc;
   return launch(ctx, name.c_str(), dim3((unsigned)((n_tok + p.tok_per_wg - 1) / p.tok_per_wg), rows), dim3(128), p,
                 stream);
@@ -879,7 +885,7 @@ int append_new_tokens(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, const
   p.err = ctx->err_word;
   p.claim = pool->claim;
   p.epoch = pool->claim ? pool->next_epoch() : 0u;
-  const std::string name = "vk_append_kv" + std::to_string(pool->desc.kv_type);
+  const std::string name = append_kernel_name(pool->desc.kv_type, pool->desc.head_dim);
   return launch(ctx, name.c_str(), dim3((unsigned)((a->n_seqs + p.tok_per_wg - 1) / p.tok_per_wg),
                                         (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
 }

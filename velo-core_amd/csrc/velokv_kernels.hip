@@ -4,8 +4,11 @@
 // that the host library loads with hipModuleLoad and launches with
 // hipModuleLaunchKernel. Every kernel takes one argument struct (velokv_params.h).
 //
-// Block size 16 and head_dim 128 are compile-time constants of the attention and
-// append kernels; the host rejects other shapes with VK_ERR_UNSUPPORTED.
+// The kernels work on 16-token tiles (a page of 16 << s tokens is 2^s tiles back
+// to back) and 128-dim rows in registers; a head_dim-64 pool stores 64-dim tiles,
+// which the loaders read into the lower half of those rows (the upper half takes
+// a copy of the lower one and meets zero q dims; outputs keep the lower half).
+// The host rejects other shapes with VK_ERR_UNSUPPORTED.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <type_traits>
@@ -696,10 +699,16 @@ struct MStage {
   float4 vs[CH];
 };
 
+// Tiles of a head_dim-64 pool are 64 dims wide: lanes whose 32-dim chunk (K) or
+// 8-dim group (V) lies past dim 63 read the same bytes as the lane 64 dims below
+// (the chunk g & 1, the group n & 7), so a tile is fetched once; those K dims meet
+// zero q dims and those output dims are dropped.
 template <int KV>
 DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, int b, int nblk, int kvh, int n, int g) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr int CH = MStage<KV>::CH;
+  const int D = P.io_hd;
+  const int gk = g & (D / 32 - 1), nv = n & (D / 8 - 1);
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
     const int i = min(b * CH + u, nblk - 1);
@@ -707,16 +716,16 @@ DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, 
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
     const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
     const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
-    if constexpr (ESZ == 1) {  // pieces (4n + g) of the two 1 KB halves (int8 K layout)
-      const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, (4 * n + g) * 16);
-      const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 1024 + (4 * n + g) * 16);
+    if constexpr (ESZ == 1) {  // pieces (n D/32 + g) of the two halves of 8 D bytes (int8 K layout)
+      const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, (n * (D / 32) + gk) * 16);
+      const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 8 * D + (n * (D / 32) + gk) * 16);
 #pragma unroll
       for (int w = 0; w < 4; ++w) { st.k[u].d[w] = lo.d[w]; st.k[u].d[4 + w] = hi.d[w]; }
     } else {
-      st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * HD + 32 * g) * ESZ);
+      st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * D + 32 * gk) * ESZ);
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * HD * 2 + 16 * n) * ESZ);
+    for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * D * 2 + 16 * nv) * ESZ);
     if constexpr (KV == KV_I8_REF) {
       const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
       const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
@@ -1111,13 +1120,21 @@ DEV void f32_stage_load(F32Stage& st, const DecodeParams& P, const BlockIds& bw,
   const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
   const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
   const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+  // K dims 16 j + 4 g .. + 3 of token n at 4 (n D + 16 j + 4 g); V dim 16 t + n of
+  // token pair 2 g + r at 8 ((2 g + r) D + 16 t + n). A 64-dim tile: dims 64 and
+  // up (j, t >= 4) read the bytes of the dims 64 below (they meet zero q dims and
+  // their outputs are dropped). Two base offsets each, so that j and t stay
+  // immediates; the pair r goes in the scalar offset.
+  const int D = P.io_hd;
+  const int k0 = n * 4 * D + 16 * g, k1 = k0 - (D < HD ? 256 : 0);
+  const int v0 = 16 * g * D + 8 * n, v1 = v0 - (D < HD ? 512 : 0);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, n * 512 + (4 * j + g) * 16, 0, 0);
+  for (int j = 0; j < 8; ++j) st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, (j < 4 ? k0 : k1) + 64 * j, 0, 0);
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
     for (int r = 0; r < 2; ++r)
-      st.v[t][r] = __builtin_amdgcn_raw_buffer_load_b64(vr, (((2 * g + r) * HD + 16 * t + n) * 2) * 4, 0, kAuxNT);
+      st.v[t][r] = __builtin_amdgcn_raw_buffer_load_b64(vr, (t < 4 ? v0 : v1) + 128 * t, r * 8 * D, kAuxNT);
 }
 
 template <int G, int RT, bool TREE, int QT>
@@ -1786,12 +1803,17 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // fp16 c * v_scale (the value product then needs no scale and no bias) ----
   const int kt = tid >> 5, kd = (tid & 31) * 4;
   const int vd = tid & (HD - 1), vq = tid >> 7;
+  // A head_dim-64 tile is 64 dims wide: dims 64 and up are read from the dims 64
+  // below (they meet zero q dims, and those output dims are dropped).
+  const int D = P.io_hd;
+  const int kdt = kd & (D - 1), vdt = vd & (D - 1);
   // byte offset of K dims kd..kd+3 of token kt: int8 tiles hold dims 32c + 16h + j
-  // of token t at byte 1024 h + (4t + c) 16 + j
-  const uint32_t koff = (ESZ == 1) ? (uint32_t)(((kd >> 4) & 1) * 1024 + (4 * kt + (kd >> 5)) * 16 + (kd & 15))
-                                   : (uint32_t)((kt * HD + kd) * 2);
+  // of token t at byte 8 D h + (t D/32 + c) 16 + j
+  const uint32_t koff = (ESZ == 1) ? (uint32_t)(((kdt >> 4) & 1) * 8 * D + (kt * (D >> 5) + (kdt >> 5)) * 16 + (kdt & 15))
+                                   : (uint32_t)((kt * D + kdt) * 2);
   // V token pairs 2 vq and 2 vq + 1 of dim vd ([pair][D][2] tile)
-  const uint32_t voff0 = (uint32_t)(((2 * vq) * HD + vd) * 2 * ESZ), voff1 = voff0 + HD * 2 * ESZ;
+  const uint32_t voff0 = (uint32_t)(((2 * vq) * D + vdt) * 2 * ESZ), voff1 = voff0 + D * 2 * ESZ;
+  const uint32_t tile_b = (uint32_t)__builtin_amdgcn_readfirstlane((int)P.tile_bytes);  // uniform: SGPR descriptors
   // Loads are unconditional: a block past the chunk (or a stage past the last)
   // reads the chunk's first page, a written prefix page, whose tokens the
   // compute then skips or masks. (A zero fill on a branch let the compiler hoist
@@ -1805,11 +1827,13 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       // wave-uniform tile address (SALU): tile index from LDS, tile bytes fixed;
       // buffer loads take the lane offsets as 32-bit VGPRs
       const uint32_t tix = (uint32_t)__builtin_amdgcn_readfirstlane((int)pid[bi]);
-      constexpr uint32_t kTile = (uint32_t)BS * HD * ESZ;
-      const rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.kc + (uint64_t)tix * kTile), 0,
-                                                          (int)kTile, 0x00020000);
-      const rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.vc + (uint64_t)tix * kTile), 0,
-                                                          (int)kTile, 0x00020000);
+      // range: a 128-dim tile (a constant, so the descriptor stays in SGPRs); the
+      // lane offsets stay inside the pool's own tile, 64 dims wide or 128
+      constexpr uint32_t kTileMax = (uint32_t)BS * HD * ESZ;
+      const rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.kc + (uint64_t)tix * tile_b), 0,
+                                                          (int)kTileMax, 0x00020000);
+      const rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.vc + (uint64_t)tix * tile_b), 0,
+                                                          (int)kTileMax, 0x00020000);
       if constexpr (ESZ == 1) {
         rw.k[u][0] = __builtin_amdgcn_raw_buffer_load_b32(kr, (int)koff, 0, 0);
         rw.v[u][0] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff0, 0, 0);
@@ -2192,17 +2216,18 @@ DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h
   if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, P.positions[m], io, x0, x1);
 }
 
-// Byte offset inside a (block, head) tile of element (token, dim).
+// Byte offset inside a (block, head) tile of element (token, dim), D = head_dim
+// (64 or 128):
 //   V: [tok/2][D][2] (token pairs interleaved)
 //   K, fp16 / fp32: [tok][D]
 //   K, int8: [h][tok][D/32][16] with h = (d/16) % 2: the 32 codes of dims
-//     32c..32c+31 of token t are two 16-byte pieces at (4t + c)*16 and
-//     1024 + (4t + c)*16, so one 16-byte load per lane covers whole cache lines
+//     32c..32c+31 of token t are two 16-byte pieces at (t D/32 + c)*16 and
+//     8 D + (t D/32 + c)*16, so one 16-byte load per lane covers whole cache lines
 template <bool IS_V>
-DEV uint32_t tile_elem(int tok, int d, int esz) {
-  if (IS_V) return (uint32_t)(((tok >> 1) * HD + d) * 2 + (tok & 1)) * esz;
-  if (esz == 1) return (uint32_t)(((d >> 4) & 1) * 1024 + (4 * tok + (d >> 5)) * 16 + (d & 15));
-  return (uint32_t)(tok * HD + d) * esz;
+DEV uint32_t tile_elem(int tok, int d, int esz, int D) {
+  if (IS_V) return (uint32_t)(((tok >> 1) * D + d) * 2 + (tok & 1)) * esz;
+  if (esz == 1) return (uint32_t)(((d >> 4) & 1) * 8 * D + (tok * (D >> 5) + (d >> 5)) * 16 + (d & 15));
+  return (uint32_t)(tok * D + d) * esz;
 }
 
 DEV int clamp127(float r) { return (int)fminf(fmaxf(r, -127.f), 127.f); }
@@ -2264,7 +2289,7 @@ DEV int prev_block(const AppendParams& P, int n) {
 // The run that starts at token w0 + j (slot `slot`), for KV head h; ms0 holds
 // the slots of tokens w0 .. w0 + 63 (lane i: token w0 + i, -1 past the end), so
 // the first step of the run's forward scan needs no load.
-template <bool IS_V>
+template <bool IS_V, int D>
 DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales, int w0, int j,
                         int64_t slot, int64_t ms0, int h) {
   const int lane = lane_id();
@@ -2274,16 +2299,20 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
   uint16_t* sp = scales + (uint64_t)b * Hkv + h;
   const int d0 = 2 * lane;
+  // lanes past the row (2 lane >= D) read the codes of the dims D below and never
+  // write them back; their new-token values are zero, so the absmax is the row's
+  const bool din = d0 < D;
+  const int da = d0 & (D - 1);
   // element (u, d) sits at tile_elem(u, 0) + tile_elem(0, d) in both layouts:
   // two lane pointers and constant offsets per token
-  uint8_t* const lp0 = tile + tile_elem<IS_V>(0, d0, 1);
-  uint8_t* const lp1 = tile + tile_elem<IS_V>(0, d0 + 1, 1);
+  uint8_t* const lp0 = tile + tile_elem<IS_V>(0, da, 1, D);
+  uint8_t* const lp1 = tile + tile_elem<IS_V>(0, da + 1, 1, D);
 
   int cd[BS][2];
 #pragma unroll
   for (int u = 0; u < BS; ++u) {
-    cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1)];
-    cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1)];
+    cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1, D)];
+    cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1, D)];
   }
   const uint16_t stored = *sp;
   float s_old = 0.f;
@@ -2346,9 +2375,9 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
   }
 #pragma unroll
   for (int u = 0; u < BS; ++u) {
-    if (u <= hi_written) {
-      lp0[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][0];
-      lp1[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][1];
+    if (din && u <= hi_written) {
+      lp0[tile_elem<IS_V>(u, 0, 1, D)] = (uint8_t)(int8_t)cd[u][0];
+      lp1[tile_elem<IS_V>(u, 0, 1, D)] = (uint8_t)(int8_t)cd[u][1];
     }
   }
   if (lane == 0) *sp = s_bits;
@@ -2357,7 +2386,7 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
 // The runs that start inside tokens [w0, w0 + T) of the call, in order. A token
 // starts a run when it is not padding and the nearest non-padding token before
 // it is in another block (or there is none).
-template <bool IS_V>
+template <bool IS_V, int D>
 DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint16_t* scales, int w0, int T) {
   const int lane = lane_id();
   const int h = blockIdx.y;
@@ -2388,7 +2417,7 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
           __hip_atomic_exchange(&P.claim[slot / BS], me, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if ((uint32_t)(old >> 32) == P.epoch && old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
     }
-    append_blk_run<IS_V>(P, src, codes, scales, w0, j, slot, ms64, h);
+    append_blk_run<IS_V, D>(P, src, codes, scales, w0, j, slot, ms64, h);
   }
 }
 
@@ -2409,8 +2438,11 @@ DEV void append_ref(const AppendParams& P, const void* src, uint8_t* codes, floa
   const float scale = amax / 127.0f;
   const float inv = amax > 0.f ? 127.0f / amax : 0.f;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
-  tile[tile_elem<IS_V>(o, d0, 1)] = (uint8_t)(int8_t)(int)(x0 * inv);
-  tile[tile_elem<IS_V>(o, d0 + 1, 1)] = (uint8_t)(int8_t)(int)(x1 * inv);
+  const int D = P.g.head_dim;
+  if (d0 < D) {
+    tile[tile_elem<IS_V>(o, d0, 1, D)] = (uint8_t)(int8_t)(int)(x0 * inv);
+    tile[tile_elem<IS_V>(o, d0 + 1, 1, D)] = (uint8_t)(int8_t)(int)(x1 * inv);
+  }
   if (lane == 0) scales[((uint64_t)b * Hkv + h) * BS + o] = scale;
 }
 
@@ -2426,24 +2458,28 @@ DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes, in
   const int Hkv = P.g.n_kv_heads;
   const int d0 = 2 * lane;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
-  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE) && P.g.io_hd == HD) {
+  const int D = P.g.head_dim;
+  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE) && D == HD) {
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src) + ((int64_t)n * Hkv + h) * HD + d0;
-    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2)) = s16[0];
-    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2)) = s16[1];
+    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2, HD)) = s16[0];
+    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2, HD)) = s16[1];
     return;
   }
   float x0, x1;
   load_kv(P, src, IS_V, n, h, x0, x1);
+  if (d0 >= D) return;
   if constexpr (ESZ == 2) {
-    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2)) = f2h(x0);
-    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2)) = f2h(x1);
+    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2, D)) = f2h(x0);
+    *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2, D)) = f2h(x1);
   } else {
-    *reinterpret_cast<float*>(tile + tile_elem<IS_V>(o, d0, 4)) = x0;
-    *reinterpret_cast<float*>(tile + tile_elem<IS_V>(o, d0 + 1, 4)) = x1;
+    *reinterpret_cast<float*>(tile + tile_elem<IS_V>(o, d0, 4, D)) = x0;
+    *reinterpret_cast<float*>(tile + tile_elem<IS_V>(o, d0 + 1, 4, D)) = x1;
   }
 }
 
-template <int KV>
+// D: head_dim of the pool for the I8_BLK rule (a compile-time constant, so that
+// the 16 tokens' tile offsets fold into the instructions; vk_append_kv3 / _d64).
+template <int KV, int D = HD>
 DEV void append_kernel(const AppendParams& P) {
   const int T = P.tok_per_wg;
   const int w0 = (int)blockIdx.x * T;
@@ -2475,7 +2511,7 @@ DEV void append_kernel(const AppendParams& P) {
   uint8_t* codes = L + (is_v ? P.g.v_off : P.g.k_off);
   if constexpr (KV == KV_I8_BLK) {
     uint16_t* sc = reinterpret_cast<uint16_t*>(L + (is_v ? P.g.vs_off : P.g.ks_off));
-    if (is_v) append_blk<true>(P, src, codes, sc, w0, T); else append_blk<false>(P, src, codes, sc, w0, T);
+    if (is_v) append_blk<true, D>(P, src, codes, sc, w0, T); else append_blk<false, D>(P, src, codes, sc, w0, T);
     return;
   }
   // one token at a time; the window's slots are read at once (lane j: token w0 + j)
@@ -2633,19 +2669,24 @@ constexpr int kCommitLayers = 8;
 // [l0, l1) of KV head h of sequence s, accepted tokens a (lane i: node of the
 // i-th accepted token), d0 the first moved one, blocks blk_l (lane i: the i-th
 // destination block from b_first).
-template <int KV, bool IS_V>
+template <int KV, bool IS_V, int D>
 DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE * Esz<KV>::v], float (&xsc)[kMaxCommit],
                      int h, int l0, int l1, int ctx, int na, int a, int d0, int blk_l, int b_first) {
   constexpr int ESZ = Esz<KV>::v;
   const int lane = lane_id();
   const int Hkv = P.g.n_kv_heads;
   // the lane's two dims: 2 lane, 2 lane + 1; for int8 K the two dims whose codes
-  // sit at bytes 1024 (lane / 32) + 64 t + 2 (lane % 32) of the tile (the 16-byte
-  // piece layout), so that a wave reads and writes two contiguous 64-byte runs
-  // per token (every per-dim step below is independent of which dims a lane has)
-  const int c0 = (ESZ == 1 && !IS_V) ? 32 * ((lane & 31) >> 3) + 16 * (lane >> 5) + 2 * (lane & 7) : 2 * lane;
+  // sit at bytes 8 D (lane / (D/4)) + (D/2) t + 2 (lane % (D/4)) of the tile (the
+  // 16-byte piece layout), so that a wave reads and writes two contiguous runs of
+  // D/2 bytes per token (every per-dim step below is independent of which dims a
+  // lane has). Lanes 2 lane >= D repeat the lane D/2 below (the same bytes, so
+  // the same absmax) and write nothing.
+  const bool din = 2 * lane < D;
+  const int la = lane & (D / 2 - 1);
+  const int lq = la & (D / 4 - 1), lh = la / (D / 4);
+  const int c0 = (ESZ == 1 && !IS_V) ? 32 * (lq >> 3) + 16 * lh + 2 * (lq & 7) : 2 * la;
   // element (u, d) of a tile sits at tile_elem(u, 0) + tile_elem(0, d)
-  const uint32_t off0 = tile_elem<IS_V>(0, c0, ESZ), off1 = tile_elem<IS_V>(0, c0 + 1, ESZ);
+  const uint32_t off0 = tile_elem<IS_V>(0, c0, ESZ, D), off1 = tile_elem<IS_V>(0, c0 + 1, ESZ, D);
   auto blk_of = [&](int pos) -> int64_t { return readlane_i(blk_l, pos / BS - b_first); };
   for (int layer = l0; layer < l1; ++layer) {
     uint8_t* L = P.base + (uint64_t)layer * P.g.layer_stride;
@@ -2660,7 +2701,7 @@ DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE 
       for (int k = 0; k < RC; ++k) {
         const int q = ctx + readlane_i(a, min(d + k, na - 1));  // past na: a valid token, result dropped
         const int64_t blk = blk_of(q);
-        const uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes + tile_elem<IS_V>(q % BS, 0, ESZ);
+        const uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes + tile_elem<IS_V>(q % BS, 0, ESZ, D);
         if constexpr (ESZ == 4) {
           e[k][0] = *reinterpret_cast<const uint32_t*>(t + off0);
           e[k][1] = *reinterpret_cast<const uint32_t*>(t + off1);
@@ -2692,9 +2733,10 @@ DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE 
       for (int d = d0; d < na; ++d) {
         const int p = ctx + d;
         const int64_t blk = blk_of(p);
-        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes + tile_elem<IS_V>(p % BS, 0, ESZ);
+        uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes + tile_elem<IS_V>(p % BS, 0, ESZ, D);
         const uint8_t* r = &raw[d][2 * lane * ESZ];
-        if constexpr (ESZ == 4) {
+        if (!din) {
+        } else if constexpr (ESZ == 4) {
           *reinterpret_cast<uint32_t*>(t + off0) = reinterpret_cast<const uint32_t*>(r)[0];
           *reinterpret_cast<uint32_t*>(t + off1) = reinterpret_cast<const uint32_t*>(r)[1];
         } else if constexpr (ESZ == 2) {
@@ -2722,8 +2764,8 @@ DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE 
         int cd[BS][2];
 #pragma unroll
         for (int u = 0; u < BS; ++u) {
-          cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1)];
-          cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1)];
+          cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1, D)];
+          cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1, D)];
         }
         const int o0 = p % BS;
         const uint16_t stored = *sp;
@@ -2738,9 +2780,9 @@ DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE 
         const int hi_written = (ctx + dend - 1) % BS;
 #pragma unroll
         for (int u = 0; u < BS; ++u) {
-          if (u <= hi_written) {
-            lp0[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][0];
-            lp1[tile_elem<IS_V>(u, 0, 1)] = (uint8_t)(int8_t)cd[u][1];
+          if (din && u <= hi_written) {
+            lp0[tile_elem<IS_V>(u, 0, 1, D)] = (uint8_t)(int8_t)cd[u][0];
+            lp1[tile_elem<IS_V>(u, 0, 1, D)] = (uint8_t)(int8_t)cd[u][1];
           }
         }
         if (lane == 0) *sp = s_bits;
@@ -2791,8 +2833,14 @@ DEV void tree_commit(const CommitParams& P) {
   }
   const int blk_l = (pg << ps) | ((b_first + lane) & ((1 << ps) - 1));
   report(COMMIT_OK);
-  if (w == 0) commit_wave<KV, false>(P, raw[0], xsc[0], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
-  else commit_wave<KV, true>(P, raw[1], xsc[1], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
+  // D as a constant, so that tile offsets fold into the instructions
+  if (P.g.head_dim == HD) {
+    if (w == 0) commit_wave<KV, false, HD>(P, raw[0], xsc[0], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
+    else commit_wave<KV, true, HD>(P, raw[1], xsc[1], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
+  } else {
+    if (w == 0) commit_wave<KV, false, HD / 2>(P, raw[0], xsc[0], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
+    else commit_wave<KV, true, HD / 2>(P, raw[1], xsc[1], h, l0, l1, ctx, na, a, d0, blk_l, b_first);
+  }
 }
 
 DEV uint64_t splitmix64(uint64_t x) {
@@ -2969,6 +3017,8 @@ VK_GX_TREE_PFX(1, 0) VK_GX_TREE_PFX(1, 1) VK_GX_TREE_PFX(3, 0) VK_GX_TREE_PFX(3,
   extern "C" __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(4)))                         \
       vk_append_kv##KV(const AppendParams P) { append_kernel<KV>(P); }
 VK_APPEND(0) VK_APPEND(1) VK_APPEND(2) VK_APPEND(3)
+extern "C" __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(4)))
+    vk_append_kv3_d64(const AppendParams P) { append_kernel<KV_I8_BLK, HD / 2>(P); }
 
 extern "C" __global__ void __launch_bounds__(256) vk_slot_mapping(const SlotMapParams P) { slot_mapping_kernel(P); }
 extern "C" __global__ void __launch_bounds__(256) vk_copy_blocks(const CopyParams P) { copy_blocks_kernel(P); }

@@ -31,8 +31,8 @@ struct PoolGeom {
   uint32_t stile_bytes;    // scales of one (block, head): 2 (I8_BLK, per 16 tokens), 4 per token (I8_REF), 0
   int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
   int32_t page_shift;      // tile view: log2(page tokens / 16)
-  int32_t io_hd;           // head_dim of the caller's K/V/q/out rows (64 or 128); tiles
-                           // are head_dim wide and hold zeros in dims io_hd and up
+  int32_t io_hd;           // head_dim of the caller's K/V/q/out rows (64 or 128), the
+                           // same as head_dim
 };
 
 enum RopeStyle : int32_t { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
@@ -105,7 +105,7 @@ struct DecodeParams {
   int32_t n_seqs, n_heads, n_kv_heads;
   int32_t n_blocks;         // pages in the pool (block-table entries range)
   int32_t page_shift;       // log2(page tokens / 16): table entry p holds tiles p << page_shift ..
-  int32_t io_hd;            // q / out row length (64 or 128); dims past it are zero in the tiles
+  int32_t io_hd;            // head_dim: q / out row length and tile width (64 or 128)
   int32_t max_parts;        // partitions per sequence in the grid
   int32_t part_tokens;      // tokens per partition (multiple of the block size)
   int32_t cap_tokens;       // tokens a table row can address: min(max_parts*part_tokens, bt_stride*bs)
