@@ -16,9 +16,13 @@ resident in HBM before timing starts.
 value        = algorithmic bytes of a step / step time (GB/s)
 tokens_per_s = 64 / step time (attention-only decode throughput, 32 layers)
 roofline     = one vk_paged_decode call (the decode kernel and, when a sequence
-               spans several partitions, the split-K merge kernel): algorithmic
-               bytes per call / mean call time from HIP events around every call in
-               the timed region, against the 8 TB/s HBM peak.
+               spans several partitions, the merge kernel): algorithmic bytes per
+               call / mean call time, against the 8 TB/s HBM peak. The mean call
+               time is one pair of HIP events around NL x steps back-to-back calls
+               on the bench's stream, divided by their number (an event packet
+               between calls adds its own few microseconds, so per-call event
+               pairs, reported beside it, read high). The timed step loop holds
+               no event packets either: only its start and end are recorded.
 
 --workload tree measures configuration 4 instead: 256 sequences sharing an
 aliased 4096-token prefix, suffixes U[0, 512], copy-on-write of every partial
@@ -139,6 +143,26 @@ def measured_traffic(kernel: str, S: int, L: int, H: int, Hkv: int, ragged: bool
     return None
 
 
+def time_calls(ctx, stream, fn, n: int):
+    """fn(i) for i < n, twice: back to back between one pair of HIP events on
+    `stream` (mean ms per call), then with an event pair around each call
+    (per-call ms, which include the event packets' own overhead)."""
+    s0, s1 = velokv.Event(ctx), velokv.Event(ctx)
+    s0.record(stream)
+    for i in range(n):
+        fn(i)
+    s1.record(stream)
+    stream.sync()
+    block_ms = s0.elapsed_ms(s1) / n
+    evs = [[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(n)]
+    for i in range(n):
+        evs[i][0].record(stream)
+        fn(i)
+        evs[i][1].record(stream)
+    stream.sync()
+    return block_ms, [e[0].elapsed_ms(e[1]) for e in evs]
+
+
 def run_gpu(ctx, args, kv_name: str):
     kv = {"int8": velokv.KV_I8_BLK, "int8ref": velokv.KV_I8_REF, "fp32": velokv.KV_F32}.get(kv_name, velokv.KV_F16)
     S, H, Hkv, L, NL = args.seqs, args.heads, args.kv_heads, args.ctx, args.layers
@@ -197,7 +221,12 @@ def run_gpu(ctx, args, kv_name: str):
     plan = ctx.decode_plan(pool, S, H, int(lens.max()), bt_stride=bt.shape[1], partition_tokens=args.partition,
                            q_dtype=qdt, sum_context_len=int(lens.sum()))
 
-    def step(i, evs=None, app_evs=None):
+    def decode(layer, r):
+        ctx.paged_decode(pool, layer, qs[r], qdt, out, d_lens, S, H, int(lens.max()),
+                         block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
+                         stream=stream, sum_context_len=int(lens.sum()))
+
+    def step(i, app_evs=None):
         r = i % R
         for layer in range(NL):
             if app_evs is not None:
@@ -209,13 +238,7 @@ def run_gpu(ctx, args, kv_name: str):
                 ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
             if app_evs is not None:
                 app_evs[layer][1].record(stream)
-            if evs is not None:
-                evs[layer][0].record(stream)
-            ctx.paged_decode(pool, layer, qs[r], qdt, out, d_lens, S, H, int(lens.max()),
-                             block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
-                             stream=stream, sum_context_len=int(lens.sum()))
-            if evs is not None:
-                evs[layer][1].record(stream)
+            decode(layer, r)
 
     for i in range(args.warmup):
         step(i)
@@ -223,19 +246,19 @@ def run_gpu(ctx, args, kv_name: str):
     ctx.sync()
 
     start, end = velokv.Event(ctx), velokv.Event(ctx)
-    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(args.steps)]
     start.record(stream)
     for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+        step(args.warmup + i)
     end.record(stream)
     stream.sync()
     ctx.sync()
     total_ms = start.elapsed_ms(end)
-    dec_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
+    # decode calls alone: NL x steps back-to-back calls (layers and input sets rotating)
+    dec_mean_ms, dec_ms = time_calls(ctx, stream, lambda i: decode(i % NL, (i // NL) % R), NL * args.steps)
     # append time per layer, from two more (untimed) steps with events around the appends only
     app_evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(2)]
     for i in range(2):
-        step(i, None, app_evs[i])
+        step(i, app_evs[i])
     stream.sync()
     app_ms = [app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]
 
@@ -245,7 +268,6 @@ def run_gpu(ctx, args, kv_name: str):
     if rope:  # q read and written (fp16), positions, one table row (D/2 cos, sin pairs) per token
         abytes += 2 * S * H * D * (4 if qdt == velokv.DT_F32 else 2) + S * 4 + S * D * 4
     step_bytes = NL * (dbytes + abytes)
-    dec_mean_ms = float(np.mean(dec_ms))
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
     kname = plan["kernel"]
     res = {
@@ -265,7 +287,7 @@ def run_gpu(ctx, args, kv_name: str):
                                  if (D, PG) == (HD, BS) else None),
                      "kernel": kname,
                      "launch_ms_mean": round(dec_mean_ms, 5), "launch_ms_min": round(float(np.min(dec_ms)), 5),
-                     "launches": len(dec_ms)},
+                     "launches": len(dec_ms), "call_ms_events_mean": round(float(np.mean(dec_ms)), 5)},
         "pool_gb": round(pool.nbytes / 1e9, 2),
         "workload": "S=%d, L=%s, H=%d/Hkv=%d, D=%d, page %d, %s KV, q %s" % (
             S, "U[1024,%d]" % L if args.ragged else str(L), H, Hkv, D, PG, kv_name, args.q_dtype),
@@ -387,7 +409,12 @@ def run_tree(ctx, args):
     moved_tok = sum(len(a) - next((d for d, x in enumerate(a) if x != d), len(a)) for a in acc_rows)
     stream = velokv.Stream(ctx)
 
-    def step(i, evs=None, app_evs=None):
+    def verify(layer, r):
+        ctx.tree_verify(pool, layer, qs[r], qdt, out, d_committed, d_mask, S, N, H,
+                        int(committed.max()), block_tables=d_bt, bt_stride=stride,
+                        partition_tokens=args.partition, stream=stream, shared_blocks=shared_blocks)
+
+    def step(i, app_evs=None, commit_evs=None):
         r = i % R
         if len(pairs):
             ctx.copy_blocks(pool, pairs, stream=stream)
@@ -397,39 +424,35 @@ def run_tree(ctx, args):
             ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, draft_slots, S * N, stream=stream)
             if app_evs is not None:
                 app_evs[layer][1].record(stream)
-            if evs is not None:
-                evs[layer][0].record(stream)
-            ctx.tree_verify(pool, layer, qs[r], qdt, out, d_committed, d_mask, S, N, H,
-                            int(committed.max()), block_tables=d_bt, bt_stride=stride,
-                            partition_tokens=args.partition, stream=stream, shared_blocks=shared_blocks)
-            if evs is not None:
-                evs[layer][1].record(stream)
+            verify(layer, r)
         # the accepted paths move to committed + 0, 1, ... in every layer
-        if evs is not None:
-            evs[NL][0].record(stream)
+        if commit_evs is not None:
+            commit_evs[0].record(stream)
         ctx.tree_commit(pool, d_bt, stride, d_committed, d_acc, 32, d_nacc, S, stream=stream)
-        if evs is not None:
-            evs[NL][1].record(stream)
+        if commit_evs is not None:
+            commit_evs[1].record(stream)
 
     for i in range(args.warmup):
         step(i)
     stream.sync()
     start, end = velokv.Event(ctx), velokv.Event(ctx)
-    evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL + 1)] for _ in range(args.steps)]
     start.record(stream)
     for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+        step(args.warmup + i)
     end.record(stream)
     stream.sync()
     total_ms = start.elapsed_ms(end)
-    tv_ms = [evs[i][l][0].elapsed_ms(evs[i][l][1]) for i in range(args.steps) for l in range(NL)]
-    commit_ms = float(np.mean([evs[i][NL][0].elapsed_ms(evs[i][NL][1]) for i in range(args.steps)]))
-    # draft-append time per layer, from two more (untimed) steps with events around the appends only
+    # verify calls alone: NL x steps back-to-back calls (layers and input sets rotating)
+    tv_mean, tv_ms = time_calls(ctx, stream, lambda i: verify(i % NL, (i // NL) % R), NL * args.steps)
+    # draft-append time per layer and commit time per step, from two more
+    # (untimed) steps with events around the appends and the commit only
     app_evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(2)]
+    commit_evs = [[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(2)]
     for i in range(2):
-        step(i, None, app_evs[i])
+        step(i, app_evs[i], commit_evs[i])
     stream.sync()
     append_ms = float(np.mean([app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]))
+    commit_ms = float(np.mean([e[0].elapsed_ms(e[1]) for e in commit_evs]))
 
     esz = 1 if kv == velokv.KV_I8_BLK else 2
     sc = 2 if kv == velokv.KV_I8_BLK else 0
@@ -449,7 +472,6 @@ def run_tree(ctx, args):
     commit_bytes = NL * moved_tok * 2 * 2 * Hkv * (HD * esz + sc)
     step_bytes = cow_bytes + commit_bytes + NL * (uniq + append_bytes(kv, S * N, Hkv))
     ms_step = total_ms / args.steps
-    tv_mean = float(np.mean(tv_ms))
     ach = uniq / (tv_mean * 1e-3) / 1e9
     rt = 2 if N * G > 16 else 1
     qsfx = 0 if qdt == velokv.DT_F32 else 1
@@ -486,7 +508,7 @@ def run_tree(ctx, args):
                      "kernel": "vk_tree_verify call: " + " + ".join(call_kernels),
                      "flops_per_launch": int(flops),
                      "launch_ms_mean": round(tv_mean, 5), "launch_ms_min": round(float(np.min(tv_ms)), 5),
-                     "launches": len(tv_ms)},
+                     "launches": len(tv_ms), "call_ms_events_mean": round(float(np.mean(tv_ms)), 5)},
         "roofline_hbm": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4), "bytes_per_launch": uniq},
         "pool_gb": round(pool.nbytes / 1e9, 2),
