@@ -84,6 +84,8 @@ def test_hd64_decode(ctx, kv, sched, qd):
         pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()),
                              bt_stride=case.block_tables.shape[1], partition_tokens=P, q_dtype=qdt)
         assert "mfma" in pl["kernel"] or "_sk_" in pl["kernel"] or "_wg_" in pl["kernel"], pl  # no VALU at 64
+        # int8 and fp16 pools run the 64-dim pieces (2 score and 4 value products per block)
+        assert pl["kernel"].endswith("_d64" + ("_q0" if qd == np.float32 else "")) == (kv != O.F32), pl
         out = ctx.alloc(case.S * case.n_heads * D * 4)
         ctx.paged_decode(pool, 0, ctx.upload(q64), qdt, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
                          int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
@@ -110,7 +112,7 @@ def test_hd64_workgroup_split_and_append_decode(ctx, kv):
     ctx.set_decode_schedule(velokv.SCHED_SPLIT)
     try:
         pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1])
-        assert pl["kernel"].startswith(f"vk_decode_wg_kv{kv}_g4"), pl
+        assert pl["kernel"] == (f"vk_decode_wg_kv{kv}_g4" if kv == O.F32 else f"vk_decode_wg_kv{kv}_gx_d64"), pl
         ctx.append_decode(pool, 0, ctx.upload(np.ascontiguousarray(kk[..., :D])),
                           ctx.upload(np.ascontiguousarray(vv[..., :D])), velokv.DT_F16, ctx.upload(q64),
                           velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
@@ -210,3 +212,67 @@ def test_hd64_limits(ctx):
         with pytest.raises(velokv.VkError) as e:
             velokv.Pool(ctx, 1, 8, BS, 2, bad, O.F16)
         assert e.value.code == velokv.ERR_UNSUPPORTED, bad
+
+
+@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("G", [3, 8, 16])
+@pytest.mark.parametrize("sched", ["split", "stream", "auto"])
+def test_hd64_pieces_group_sizes_and_long_units(ctx, kv, G, sched):
+    """The 64-dim pieces at runtime group sizes (rows padded to one 16-row tile)
+    over units that fill all four block-id windows: contexts of 4095-4097 tokens
+    with 4096-token partitions (split), a ragged batch (stream-K) and a uniform
+    batch under AUTO (the workgroup split for int8 pools)."""
+    print(f"hd64 pieces kv={kv} G={G} sched={sched}", flush=True)
+    kind, sc, P = {"split": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 4096),
+                   "stream": (velokv.DECODE_MFMA, velokv.SCHED_STREAM, 0),
+                   "auto": (velokv.DECODE_AUTO, velokv.SCHED_AUTO, 0)}[sched]
+    lens = {"split": [4095, 4096, 4097, 1, 300], "stream": [4095, 33, 1000, 2500, 17, 4000],
+            "auto": [3000] * 6}[sched]
+    Hkv = 2
+    case = hd64_case(kv, lens, n_kv_heads=Hkv, n_heads=G * Hkv, seed=1450 + 7 * G + kv)
+    pool = hd64_pool(ctx, case)
+    q64 = np.ascontiguousarray(case.q[..., :D]).astype(np.float16)
+    ctx.set_decode_kernel(kind)
+    ctx.set_decode_schedule(sc)
+    try:
+        sum_len = int(sum(lens))
+        pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1],
+                             partition_tokens=P, sum_context_len=sum_len)
+        assert pl["kernel"].endswith("_gx_d64"), pl
+        out = ctx.alloc(case.S * case.n_heads * D * 4)
+        ctx.paged_decode(pool, 0, ctx.upload(q64), velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S,
+                         case.n_heads, int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1], partition_tokens=P, sum_context_len=sum_len)
+        ctx.sync()
+    finally:
+        ctx.set_decode_kernel(velokv.DECODE_AUTO)
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)
+    got = out.download((case.S, case.n_heads, D), np.float32)
+    ref = O.paged_decode(oracle64(case), q64, case.block_tables, case.ctx_lens)
+    ok, err, nbad = tol_check(got, ref)
+    assert ok, f"max err {err:.3g}, {nbad} out of tolerance ({pl['kernel']})"
+
+
+@pytest.mark.parametrize("G", [3, 8])
+def test_hd64_workgroup_split_group_sizes(ctx, G):
+    """The 64-dim workgroup split over an int8 pool at runtime group sizes."""
+    print(f"hd64 workgroup split G={G}", flush=True)
+    lens = list(synth.rng(1470 + G).integers(2, 400, 64))
+    case = hd64_case(O.I8_BLK, lens, n_kv_heads=8, n_heads=8 * G, seed=1471 + G)
+    pool = hd64_pool(ctx, case)
+    q64 = np.ascontiguousarray(case.q[..., :D])
+    out = ctx.alloc(case.S * case.n_heads * D * 4)
+    ctx.set_decode_schedule(velokv.SCHED_SPLIT)
+    try:
+        pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1])
+        assert pl["kernel"] == "vk_decode_wg_kv3_gx_d64", pl
+        ctx.paged_decode(pool, 0, ctx.upload(q64), velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
+                         int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
+                         bt_stride=case.block_tables.shape[1])
+        ctx.sync()
+    finally:
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)
+    got = out.download((case.S, case.n_heads, D), np.float32)
+    ref = O.paged_decode(oracle64(case), q64, case.block_tables, case.ctx_lens)
+    ok, err, nbad = tol_check(got, ref)
+    assert ok, (err, nbad)

@@ -177,16 +177,21 @@ std::string decode_name(int kv, int g, int qt) {
 // Matrix-core decode kernels: fp16 q, or (int8 KV only, suffix _q0) fp32 q split
 // into fp16 hi + lo parts.
 std::string q0_suffix(int qt) { return qt == VK_DT_F32 ? "_q0" : ""; }
-std::string decode_mfma_name(int kv, int g, int qt = VK_DT_F16) {
+// d64: the head_dim-64 kernels (64-dim pieces, runtime group size up to 16)
+std::string decode_mfma_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) {
+  if (d64) return "vk_decode_mfma_kv" + std::to_string(kv) + "_gx_d64" + q0_suffix(qt);
   const std::string t = fixed_group(g) ? gtag(g) : (g > kMaxGroupTile ? "_gx2" : "_gx");
   return "vk_decode_mfma_kv" + std::to_string(kv) + t + q0_suffix(qt);
 }
-std::string decode_wg_name(int kv, int g, int qt = VK_DT_F16) {
-  return "vk_decode_wg_kv" + std::to_string(kv) + gtag(g) + q0_suffix(qt);
+std::string decode_wg_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) {
+  return "vk_decode_wg_kv" + std::to_string(kv) + (d64 ? std::string("_gx_d64") : gtag(g)) + q0_suffix(qt);
 }
-std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16) {
-  return "vk_decode_sk_kv" + std::to_string(kv) + gtag(g) + q0_suffix(qt);
+std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) {
+  return "vk_decode_sk_kv" + std::to_string(kv) + (d64 ? std::string("_gx_d64") : gtag(g)) + q0_suffix(qt);
 }
+// The head_dim-64 kernels serve this pool and group size: int8 and fp16 pools
+// of 64-dim heads, one 16-row tile of query rows per (sequence, KV head).
+bool use_d64(const vk_pool_desc& d, int g) { return d.head_dim == kHD / 2 && d.kv_type != VK_KV_F32 && g <= kMaxGroupTile; }
 std::string decode_pk_name(int kv, int g, int qt = VK_DT_F16) {
   return "vk_decode_pk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
@@ -227,6 +232,7 @@ int64_t resident_waves(vk_ctx* ctx, const std::string& name, int block = 64) {
   ctx->resident[key] = waves;
   return waves;
 }
+
 
 int check_pool(const vk_ctx* ctx, const vk_pool* pool) {
   if (!ctx) return fail(VK_ERR_NOT_WIRED, "context is null");
@@ -281,6 +287,11 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, 3, qt));
       if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt));
       for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt));
+      if (kv != VK_KV_F32) {  // head_dim 64
+        names.push_back(decode_mfma_name(kv, 3, qt, true));
+        names.push_back(decode_sk_name(kv, 3, qt, true));
+        if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, 3, qt, true));
+      }
     }
   }
   for (int kv = 0; kv < 4; ++kv)
@@ -710,6 +721,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
   const int G = a->n_heads / d.n_kv_heads;
   if (G > kMaxGroup) return fail(VK_ERR_UNSUPPORTED, "GQA group size %d (decode supports up to %d)", G, kMaxGroup);
   if (a->q_dtype != VK_DT_F32 && a->q_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "q_dtype %d", a->q_dtype);
+  const bool d64 = use_d64(d, G);
   pl->bt = a->block_tables;
   pl->bt_stride = a->bt_stride;
   pl->bt_rows = 0;
@@ -758,7 +770,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     }
   }
   if (pl->stream_k) {
-    pl->kernel = decode_sk_name(d.kv_type, G, a->q_dtype);
+    pl->kernel = decode_sk_name(d.kv_type, G, a->q_dtype, d64);
     // one wave per resident slot, and at most 256 blocks (four id windows) per
     // worker: a worker's blocks are at most its units, ceil(units / nw)
     const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads *
@@ -782,20 +794,20 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     // whose workgroups fill one round of resident waves, when each wave's share
     // fits its four block-id windows (256 blocks).
     const int64_t pairs = (int64_t)a->n_seqs * d.n_kv_heads;
-    const int64_t waves = ctx ? resident_waves(ctx, decode_wg_name(d.kv_type, G, a->q_dtype), 64 * kWgMaxWaves) : 2048;
+    const int64_t waves = ctx ? resident_waves(ctx, decode_wg_name(d.kv_type, G, a->q_dtype, d64), 64 * kWgMaxWaves) : 2048;
     int nw = 1;
     while (nw < 8 && pairs * nw < waves) nw *= 2;
     const int64_t nb = ((int64_t)a->max_context_len + kBS - 1) / kBS;
     if (pairs > 0 && pairs * nw >= waves && (nb + nw - 1) / nw <= kMaxPartTokens / kBS &&
         pairs <= 0x7FFFFFFF) {
       pl->wg_waves = nw;
-      pl->kernel = decode_wg_name(d.kv_type, G, a->q_dtype);
+      pl->kernel = decode_wg_name(d.kv_type, G, a->q_dtype, d64);
       pl->part_tokens = kMaxPartTokens;
       pl->max_parts = 1;
       return VK_OK;
     }
   }
-  pl->kernel = mfma ? decode_mfma_name(d.kv_type, G, a->q_dtype) : decode_name(d.kv_type, G, a->q_dtype);
+  pl->kernel = mfma ? decode_mfma_name(d.kv_type, G, a->q_dtype, d64) : decode_name(d.kv_type, G, a->q_dtype);
   if (P == 0) P = auto_partition(a, d, ctx ? resident_waves(ctx, pl->kernel) : 2048);
   pl->part_tokens = P;
   pl->max_parts = std::max(1, (a->max_context_len + P - 1) / P);

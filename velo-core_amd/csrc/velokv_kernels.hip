@@ -687,15 +687,20 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
-template <int KV>
+// D: the dims a kernel is built for, 128 or 64. A 64-dim kernel gives each lane
+// half the dims (K: 16 per token, V: 4 per token pair), so a block takes two
+// score and four value products instead of four and eight.
+template <int KV, int D = HD>
 struct MStage {
   static constexpr int ESZ = Esz<KV>::v;
-  // blocks per pipeline stage: two int8 blocks or one fp16 block (the same 8 KB
-  // of K and V per stage)
-  static constexpr int CH = ESZ == 1 ? 2 : 1;
-  DW<8 * ESZ> k[CH];     // token n, dims 32g..32g+31
-  DW<4 * ESZ> v[CH][2];  // token pairs 2g, 2g+1; dims 8n..8n+7
-  float4 ks[CH];         // VK_KV_I8_REF: scales of tokens 4g..4g+3
+  // blocks per pipeline stage: two int8 blocks or one fp16 block at 128 dims (8 KB
+  // of K and V), two blocks at 64 dims (measured: four int8 blocks per stage at
+  // two waves per SIMD lost to two at three waves per SIMD; one fp16 block lost
+  // to two)
+  static constexpr int CH = (ESZ == 1 || D < HD) ? 2 : 1;
+  DW<(D / 16) * ESZ> k[CH];     // token n, dims 32g..32g+31 (D = 64: 16g..16g+15)
+  DW<(D / 32) * ESZ> v[CH][2];  // token pairs 2g, 2g+1; dims 8n..8n+7 (D = 64: 4n..4n+3)
+  float4 ks[CH];                // VK_KV_I8_REF: scales of tokens 4g..4g+3
   float4 vs[CH];
 };
 
@@ -703,11 +708,12 @@ struct MStage {
 // 8-dim group (V) lies past dim 63 read the same bytes as the lane 64 dims below
 // (the chunk g & 1, the group n & 7), so a tile is fetched once; those K dims meet
 // zero q dims and those output dims are dropped.
-template <int KV>
-DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, int b, int nblk, int kvh, int n, int g) {
+template <int KV, int DK = HD>
+DEV void mstage_load(MStage<KV, DK>& st, const DecodeParams& P, const BlockIds& bw, int b, int nblk, int kvh, int n,
+                     int g) {
   constexpr int ESZ = Esz<KV>::v;
-  constexpr int CH = MStage<KV>::CH;
-  const int D = P.io_hd;
+  constexpr int CH = MStage<KV, DK>::CH;
+  const int D = DK == HD ? P.io_hd : DK;
   const int gk = g & (D / 32 - 1), nv = n & (D / 8 - 1);
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
@@ -716,16 +722,28 @@ DEV void mstage_load(MStage<KV>& st, const DecodeParams& P, const BlockIds& bw, 
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
     const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
     const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
-    if constexpr (ESZ == 1) {  // pieces (n D/32 + g) of the two halves of 8 D bytes (int8 K layout)
-      const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, (n * (D / 32) + gk) * 16);
-      const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 8 * D + (n * (D / 32) + gk) * 16);
+    if constexpr (DK == 64) {
+      // K dims 16g..16g+15 of token n: int8 half g & 1 of 32-dim chunk g >> 1
+      // (byte 8 D h + (n D/32 + c) 16), fp16 32 contiguous bytes; V dims
+      // 4n..4n+3 of token pairs 2g + r (8 elements of the pair row)
+      if constexpr (ESZ == 1)
+        st.k[u] = buf_load<4, k_aux<ESZ>()>(kr, (g & 1) * 8 * DK + (n * 2 + (g >> 1)) * 16);
+      else
+        st.k[u] = buf_load<8, k_aux<ESZ>()>(kr, (n * DK + 16 * g) * 2);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) { st.k[u].d[w] = lo.d[w]; st.k[u].d[4 + w] = hi.d[w]; }
+      for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<2 * ESZ>(vr, ((2 * g + r) * DK * 2 + 8 * n) * ESZ);
     } else {
-      st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * D + 32 * gk) * ESZ);
-    }
+      if constexpr (ESZ == 1) {  // pieces (n D/32 + g) of the two halves of 8 D bytes (int8 K layout)
+        const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, (n * (D / 32) + gk) * 16);
+        const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 8 * D + (n * (D / 32) + gk) * 16);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * D * 2 + 16 * nv) * ESZ);
+        for (int w = 0; w < 4; ++w) { st.k[u].d[w] = lo.d[w]; st.k[u].d[4 + w] = hi.d[w]; }
+      } else {
+        st.k[u] = buf_load<8 * ESZ, k_aux<ESZ>()>(kr, (n * D + 32 * gk) * ESZ);
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * D * 2 + 16 * nv) * ESZ);
+    }
     if constexpr (KV == KV_I8_REF) {
       const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
       const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
@@ -757,15 +775,18 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 // normalised rows; otherwise it writes the unnormalised partial (acc, M, l) of
 // row R at index TREE ? out_row(R) * max_parts + pbase : pbase + R * pstride of
 // pacc ([.][HD] fp32) and pml ([.][2] fp32), in HBM or in LDS.
-template <int KV, int G, int RT, bool TREE, int QT>
+template <int KV, int G, int RT, bool TREE, int QT, int D = HD>
 DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                     int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr bool I8 = (ESZ == 1);
   constexpr bool BLK = (KV == KV_I8_BLK);
   constexpr bool REF = (KV == KV_I8_REF);
-  constexpr int CH = MStage<KV>::CH;
+  constexpr int CH = MStage<KV, D>::CH;
   constexpr float kBias = 1152.0f;
+  constexpr int KC = D / 32;   // score products per block (8 dims of each lane group each)
+  constexpr int NT = D / 16;   // value tiles: lane n holds output dims (128 / D) 4 n + nt
+  constexpr int DL = D / 16;   // output dims per lane
 
   const int lane = lane_id();
   const int n = lane & 15;   // K token (A operand) / query row (scores, p) / dim group (values)
@@ -788,18 +809,18 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   BlockIds bw;
   load_block_ids<BLK>(bw, P, bt, blk0, nblk, kvh);
 
-  MStage<KV> sa, sb;
-  mstage_load<KV>(sa, P, bw, 0, nblk, kvh, n, g);
+  MStage<KV, D> sa, sb;
+  mstage_load<KV, D>(sa, P, bw, 0, nblk, kvh, n, g);
 
   // q^T as the B operand: row n of each tile (rows >= nrows are zero and their
-  // results are dropped), dims 32g..32g+31 in 4 chunks. An fp32 q of the decode
+  // results are dropped), dims 32g..32g+31 in 4 chunks (D = 64: 16g..16g+15 in 2). An fp32 q of the decode
   // kernels is split as q = hi + lo, hi = fp16(q), lo = fp16(q - hi), and each
   // score takes two products (hi, then lo, into the same accumulator), so the
   // scores see q to about 2^-22 instead of fp16's 2^-11; the tree kernels
   // round an fp32 q to fp16.
   constexpr bool QSPLIT = (QT == DT_F32) && !TREE;
-  half8 qa[RT][4];
-  half8 qlo[RT][4];
+  half8 qa[RT][KC];
+  half8 qlo[RT][KC];
   float qb[RT];        // int8 KV: 1152 * sum_d q[row n][d] (of hi + lo when split)
   uint32_t mrow[RT];   // tree: mask row of row n's node
 #pragma unroll
@@ -807,10 +828,10 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     const int R = row0 + 16 * rt + n;
     float qsum = 0.f;
     // q rows are io_hd long: dims 32g.. past it are zero
-    const int64_t qoff = out_row(R) * P.io_hd + 32 * g;
-    const bool qin = R < nrows && 32 * g < P.io_hd;
+    const int64_t qoff = out_row(R) * P.io_hd + 8 * KC * g;
+    const bool qin = R < nrows && 8 * KC * g < P.io_hd;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+    for (int kc = 0; kc < KC; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
       if (qin) {
         if constexpr (QT == DT_F32) {
@@ -846,17 +867,17 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   }
 
   float M[RT], lrun[RT], psum[RT];   // state of row n (each lane holds a quarter of the row's sums)
-  float4v acc[RT][8];
+  float4v acc[RT][NT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     M[rt] = kNegInf; lrun[rt] = 0.f; psum[rt] = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
   const int last_valid = (end - start) - (nblk - 1) * BS;
   const half2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  auto compute = [&](const MStage<KV>& st, int b) {
+  auto compute = [&](const MStage<KV, D>& st, int b) {
     // ---- S^T of every block of the stage (independent MFMA chains) ----
     float4v sc[RT][CH];
 #pragma unroll
@@ -864,7 +885,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) sc[rt][u] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
+      for (int kc = 0; kc < KC; ++kc) {
         uint32_t kb[4];
         if constexpr (I8) {
           i8x4_to_h2x2_biased(st.k[u].d[2 * kc], kb[0], kb[1]);
@@ -936,7 +957,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
         for (int r = 0; r < 4; ++r) {
           const float ar = __shfl(alpha, 4 * g + r, WAVE);
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt) acc[rt][nt][r] *= ar;
+          for (int nt = 0; nt < NT; ++nt) acc[rt][nt][r] *= ar;
         }
       }
     }
@@ -971,7 +992,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
       if (i < nblk) {
         const bool partial = (i == nblk - 1) && (last_valid < BS);
 #pragma unroll
-        for (int w = 0; w < 4 * ESZ; w += ESZ) {
+        for (int w = 0; w < KC * ESZ; w += ESZ) {
           uint32_t b0[2], b1[2];   // [pair row] for tiles nt0, nt1
           int nt0, nt1;
           if constexpr (I8) {
@@ -1007,29 +1028,29 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     // kernels read mostly cached prefix pages and keep two stages so that two
     // waves fit per SIMD; an I8_REF stage also carries the per-token scales, and
     // the lo parts of a split fp32 q take the registers of a third stage)
-    MStage<KV> sc2;
-    mstage_load<KV>(sb, P, bw, 1, nblk, kvh, n, g);
+    MStage<KV, D> sc2;
+    mstage_load<KV, D>(sb, P, bw, 1, nblk, kvh, n, g);
     for (int b = 0; b < nbatch; b += 3) {
-      mstage_load<KV>(sc2, P, bw, b + 2, nblk, kvh, n, g);
+      mstage_load<KV, D>(sc2, P, bw, b + 2, nblk, kvh, n, g);
       compute(sa, b);
       if (b + 1 >= nbatch) break;
-      mstage_load<KV>(sa, P, bw, b + 3, nblk, kvh, n, g);
+      mstage_load<KV, D>(sa, P, bw, b + 3, nblk, kvh, n, g);
       compute(sb, b + 1);
       if (b + 2 >= nbatch) break;
-      mstage_load<KV>(sb, P, bw, b + 4, nblk, kvh, n, g);
+      mstage_load<KV, D>(sb, P, bw, b + 4, nblk, kvh, n, g);
       compute(sc2, b + 2);
     }
   } else {
     for (int b = 0; b < nbatch; b += 2) {
-      mstage_load<KV>(sb, P, bw, b + 1, nblk, kvh, n, g);
+      mstage_load<KV, D>(sb, P, bw, b + 1, nblk, kvh, n, g);
       compute(sa, b);
       if (b + 1 >= nbatch) break;
-      mstage_load<KV>(sa, P, bw, b + 2, nblk, kvh, n, g);
+      mstage_load<KV, D>(sa, P, bw, b + 2, nblk, kvh, n, g);
       compute(sb, b + 1);
     }
   }
 
-  // ---- partials: acc rows 16 rt + 4g + r, dims 8n..8n+7 ----
+  // ---- partials: acc rows 16 rt + 4g + r, dims DL n .. DL n + DL - 1 ----
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     float l = lrun[rt], ps = psum[rt];
@@ -1048,9 +1069,9 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
       const int R = row0 + 16 * rt + 4 * g + r;
       if (R < nrows) {
         const int64_t orow = out_row(R);
-        float o[8];
+        float o[DL];
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) o[nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
+        for (int nt = 0; nt < NT; ++nt) o[nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
         if (direct) {
           float L = lr;
           if (npre > 0) {
@@ -1062,29 +1083,33 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
             const float es = (Mr == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(Mr - Mt);
             L = lr * es;
 #pragma unroll
-            for (int nt = 0; nt < 8; ++nt) o[nt] *= es;
+            for (int nt = 0; nt < DL; ++nt) o[nt] *= es;
             for (int k = 0; k < npre; ++k) {
               const float2 mk = pm[k];
               if (mk.x == kNegInf) continue;
               const float e = __builtin_amdgcn_exp2f(mk.x - Mt);
               L = fmaf(e, mk.y, L);
-              const float4* src = reinterpret_cast<const float4*>(P.part_acc + (orow * P.max_parts + k) * HD + 8 * n);
-              const float4 a0 = src[0], a1 = src[1];
-              o[0] = fmaf(e, a0.x, o[0]); o[1] = fmaf(e, a0.y, o[1]); o[2] = fmaf(e, a0.z, o[2]); o[3] = fmaf(e, a0.w, o[3]);
-              o[4] = fmaf(e, a1.x, o[4]); o[5] = fmaf(e, a1.y, o[5]); o[6] = fmaf(e, a1.z, o[6]); o[7] = fmaf(e, a1.w, o[7]);
+              const float4* src = reinterpret_cast<const float4*>(P.part_acc + (orow * P.max_parts + k) * HD + DL * n);
+#pragma unroll
+              for (int q4 = 0; q4 < DL / 4; ++q4) {
+                const float4 a4 = src[q4];
+                o[4 * q4] = fmaf(e, a4.x, o[4 * q4]); o[4 * q4 + 1] = fmaf(e, a4.y, o[4 * q4 + 1]);
+                o[4 * q4 + 2] = fmaf(e, a4.z, o[4 * q4 + 2]); o[4 * q4 + 3] = fmaf(e, a4.w, o[4 * q4 + 3]);
+              }
             }
           }
           const float inv = L > 0.f ? 1.f / L : 0.f;  // a tree row that sees no token attends to nothing
-          if (8 * n < P.io_hd) {
-            float4* dst = reinterpret_cast<float4*>(P.out + orow * P.io_hd + 8 * n);
-            dst[0] = make_float4(o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
-            dst[1] = make_float4(o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv);
+          if (DL * n < P.io_hd) {
+            float4* dst = reinterpret_cast<float4*>(P.out + orow * P.io_hd + DL * n);
+#pragma unroll
+            for (int q4 = 0; q4 < DL / 4; ++q4)
+              dst[q4] = make_float4(o[4 * q4] * inv, o[4 * q4 + 1] * inv, o[4 * q4 + 2] * inv, o[4 * q4 + 3] * inv);
           }
         } else {
           const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
-          float4* dst = reinterpret_cast<float4*>(pacc + pr * HD + 8 * n);
-          dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-          dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+          float4* dst = reinterpret_cast<float4*>(pacc + pr * HD + DL * n);
+#pragma unroll
+          for (int q4 = 0; q4 < DL / 4; ++q4) dst[q4] = make_float4(o[4 * q4], o[4 * q4 + 1], o[4 * q4 + 2], o[4 * q4 + 3]);
           if (n == 0) reinterpret_cast<float2*>(pml)[pr] = make_float2(Mr, lr);
         }
       }
@@ -1313,19 +1338,21 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
 }
 
 // attn_piece for every KV type: fp32 pools take the fp32 matrix-core piece.
-template <int KV, int G, int RT, bool TREE, int QT>
+template <int KV, int G, int RT, bool TREE, int QT, int D = HD>
 DEV void attn_piece_kv(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                        int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
-  if constexpr (KV == KV_F32)
+  if constexpr (KV == KV_F32) {
+    static_assert(D == HD, "fp32 pools take the 128-dim piece");
     attn_piece_f32<G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml);
-  else
-    attn_piece<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
+  } else {
+    attn_piece<KV, G, RT, TREE, QT, D>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
+  }
 }
 
 // Split-K entry: unit = (row group, KV head, partition, sequence), kv head
 // fastest. Partitions that start past the context exit; an empty decode context
 // writes zero rows.
-template <int KV, int G, int RT, bool TREE, int QT = DT_F16>
+template <int KV, int G, int RT, bool TREE, int QT = DT_F16, int D = HD>
 DEV void attn_unit_mfma(const DecodeParams& P) {
   int unit = blockIdx.x;
   int rg = 0;
@@ -1360,7 +1387,7 @@ DEV void attn_unit_mfma(const DecodeParams& P) {
   // the rest of a context in one partition after a shared prefix writes the
   // output itself, folding in the prefix partials
   const bool fold = C0 > 0 && nparts == C0 + 1;
-  attn_piece_kv<KV, G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, nparts == 1 || fold, pbase, P.max_parts, P.part_acc,
+  attn_piece_kv<KV, G, RT, TREE, QT, D>(P, s, kvh, rg, start, end, ctx_c, nparts == 1 || fold, pbase, P.max_parts, P.part_acc,
                                   P.part_ml, fold ? C0 : 0);
 }
 
@@ -1404,7 +1431,7 @@ DEV int seq_units(const DecodeParams& P, int s) {
   return nb > 0 ? P.n_kv_heads * (nb + P.sk_penalty) : 0;
 }
 
-template <int KV, int G, int QT = DT_F16>
+template <int KV, int G, int QT = DT_F16, int D = HD>
 DEV void attn_streamk_mfma(const DecodeParams& P) {
   const int lane = lane_id();
   const int w = blockIdx.x;
@@ -1459,8 +1486,8 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     sk_piece(seg0, nb, pen, x, c1, &o0, &o1);
     if (o0 < o1) {
       const int slot = o0 > 0 ? 0 : 1;
-      attn_piece_kv<KV, G, 1, false, QT>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                         ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc, P.part_ml);
+      attn_piece_kv<KV, G, 1, false, QT, D>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
+                                            ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc, P.part_ml);
     }
     x = seg0 + su;
     if (kvh == Hkv - 1) {
@@ -1478,7 +1505,7 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
 //   out = sum_w 2^(M_w - M) acc_w / sum_w 2^(M_w - M) l_w,  M = max_w M_w,
 // so a uniform batch needs no partials in HBM and no merge launch.
 constexpr int kWgMaxWaves = 8;
-template <int KV, int G, int QT = DT_F16>
+template <int KV, int G, int QT = DT_F16, int D = HD>
 DEV void attn_wg_mfma(const DecodeParams& P) {
   constexpr int GM = lds_rows<G>();
   __shared__ float wacc[kWgMaxWaves][GM][HD];
@@ -1499,7 +1526,7 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   const int per = (nb + nw - 1) / nw;
   const int b0 = min(nb, w * per), b1 = min(nb, b0 + per);
   if (b0 < b1) {
-    attn_piece_kv<KV, G, 1, false, QT>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
+    attn_piece_kv<KV, G, 1, false, QT, D>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
                                        &wml[w][0][0]);
   } else if (lane < Gn) {
     wml[w][lane][0] = kNegInf;
@@ -2988,6 +3015,30 @@ VK_GX_DECODE(0) VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
     attn_wg_mfma<KV, 0, DT_F32>(P);                                                                            \
   }
 VK_GX_WG(0) VK_GX_WG(2) VK_GX_WG(3)
+// head_dim 64 (64-dim pieces, any group size up to 16): split-K, stream-K and,
+// for int8 pools, the workgroup split
+#define VK_D64_DECODE(KV)                                                                                       \
+  extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx_d64(const DecodeParams P) {       \
+    attn_unit_mfma<KV, 0, 1, false, DT_F16, HD / 2>(P);                                                        \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx_d64_q0(const DecodeParams P) {    \
+    attn_unit_mfma<KV, 0, 1, false, DT_F32, HD / 2>(P);                                                        \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64(const DecodeParams P) { \
+    attn_streamk_mfma<KV, 0, DT_F16, HD / 2>(P);                                                               \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64_q0(const DecodeParams P) { \
+    attn_streamk_mfma<KV, 0, DT_F32, HD / 2>(P);                                                               \
+  }
+VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
+#define VK_D64_WG(KV)                                                                                           \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_d64(const DecodeParams P) { \
+    attn_wg_mfma<KV, 0, DT_F16, HD / 2>(P);                                                                    \
+  }                                                                                                             \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_d64_q0(const DecodeParams P) { \
+    attn_wg_mfma<KV, 0, DT_F32, HD / 2>(P);                                                                    \
+  }
+VK_D64_WG(2) VK_D64_WG(3)
 #define VK_GX_TREE(KV, RT, QT, ATTR)                                                                            \
   extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_r##RT##_q##QT(const DecodeParams P) { \
     attn_unit_mfma<KV, 0, RT, true, QT>(P);                                                                    \
