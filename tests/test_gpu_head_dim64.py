@@ -253,19 +253,20 @@ def test_hd64_pieces_group_sizes_and_long_units(ctx, kv, G, sched):
     assert ok, f"max err {err:.3g}, {nbad} out of tolerance ({pl['kernel']})"
 
 
+@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
 @pytest.mark.parametrize("G", [3, 8])
-def test_hd64_workgroup_split_group_sizes(ctx, G):
-    """The 64-dim workgroup split over an int8 pool at runtime group sizes."""
-    print(f"hd64 workgroup split G={G}", flush=True)
+def test_hd64_workgroup_split_group_sizes(ctx, kv, G):
+    """The 64-dim workgroup split over fp16 and int8 pools at runtime group sizes."""
+    print(f"hd64 workgroup split kv={kv} G={G}", flush=True)
     lens = list(synth.rng(1470 + G).integers(2, 400, 64))
-    case = hd64_case(O.I8_BLK, lens, n_kv_heads=8, n_heads=8 * G, seed=1471 + G)
+    case = hd64_case(kv, lens, n_kv_heads=8, n_heads=8 * G, seed=1471 + G)
     pool = hd64_pool(ctx, case)
     q64 = np.ascontiguousarray(case.q[..., :D])
     out = ctx.alloc(case.S * case.n_heads * D * 4)
     ctx.set_decode_schedule(velokv.SCHED_SPLIT)
     try:
         pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1])
-        assert pl["kernel"] == "vk_decode_wg_kv3_gx_d64", pl
+        assert pl["kernel"] == f"vk_decode_wg_kv{kv}_gx_d64", pl
         ctx.paged_decode(pool, 0, ctx.upload(q64), velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
                          int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
                          bt_stride=case.block_tables.shape[1])

@@ -290,7 +290,7 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       if (kv != VK_KV_F32) {  // head_dim 64
         names.push_back(decode_mfma_name(kv, 3, qt, true));
         names.push_back(decode_sk_name(kv, 3, qt, true));
-        if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, 3, qt, true));
+        names.push_back(decode_wg_name(kv, 3, qt, true));
       }
     }
   }
@@ -789,7 +789,9 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     return VK_OK;
   }
   pl->wg_waves = 0;
-  if (mfma && P == 0 && G <= kMaxGroupTile && d.kv_type != VK_KV_F16) {
+  // (fp16 pools at 128 dims: the dot2 split-K, or the matrix-core split-K with an
+  // fp32 q, measured faster than a workgroup split; at 64 dims the split wins)
+  if (mfma && P == 0 && G <= kMaxGroupTile && (d.kv_type != VK_KV_F16 || d64)) {
     // Workgroup split: NW waves per (sequence, KV head), the smallest power of two
     // whose workgroups fill one round of resident waves, when each wave's share
     // fits its four block-id windows (256 blocks).

@@ -3015,8 +3015,8 @@ VK_GX_DECODE(0) VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
     attn_wg_mfma<KV, 0, DT_F32>(P);                                                                            \
   }
 VK_GX_WG(0) VK_GX_WG(2) VK_GX_WG(3)
-// head_dim 64 (64-dim pieces, any group size up to 16): split-K, stream-K and,
-// for int8 pools, the workgroup split
+// head_dim 64 (64-dim pieces, any group size up to 16): split-K, stream-K and
+// the workgroup split
 #define VK_D64_DECODE(KV)                                                                                       \
   extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx_d64(const DecodeParams P) {       \
     attn_unit_mfma<KV, 0, 1, false, DT_F16, HD / 2>(P);                                                        \
@@ -3038,7 +3038,7 @@ VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
   extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_d64_q0(const DecodeParams P) { \
     attn_wg_mfma<KV, 0, DT_F32, HD / 2>(P);                                                                    \
   }
-VK_D64_WG(2) VK_D64_WG(3)
+VK_D64_WG(1) VK_D64_WG(2) VK_D64_WG(3)
 #define VK_GX_TREE(KV, RT, QT, ATTR)                                                                            \
   extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_r##RT##_q##QT(const DecodeParams P) { \
     attn_unit_mfma<KV, 0, RT, true, QT>(P);                                                                    \
