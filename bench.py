@@ -9,7 +9,10 @@ head) fp16 scales) as the headline and fp16 KV beside it.
 One step = one decode token for all 64 sequences through 32 layers: per layer,
 append the new K/V token of every sequence at position 8191 (slot mapping into a
 randomly scattered 40k-block pool, on-the-fly INT8 quantization) and run paged
-decode attention over the full 8192-token context. Inputs (pool contents, new
+decode attention over the full 8192-token context. With INT8 KV and no RoPE
+the layer is one vk_append_decode call, whose workgroup-split decode appends
+the new token itself (ms_per_step_two_launches reports the same steps with the
+append as a launch of its own). Inputs (pool contents, new
 K/V, q) are synthetic (seeded SplitMix64 normals generated on the GPU) and are
 resident in HBM before timing starts.
 
@@ -226,9 +229,22 @@ def run_gpu(ctx, args, kv_name: str):
                          block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
                          stream=stream, sum_context_len=int(lens.sum()))
 
-    def step(i, app_evs=None):
+    # INT8 (I8_BLK) under the workgroup split, without RoPE: vk_append_decode,
+    # whose decode appends each sequence's new token itself (one launch per
+    # layer); otherwise the append and the decode are two launches
+    fused = kv == velokv.KV_I8_BLK and not rope and plan["wg_waves"] > 0
+
+    def append_decode(layer, r):
+        ctx.append_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, qs[r], qdt, out, d_lens, S, H, int(lens.max()),
+                          block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition, stream=stream,
+                          sum_context_len=int(lens.sum()))
+
+    def step(i, app_evs=None, one_launch=fused):
         r = i % R
         for layer in range(NL):
+            if one_launch and app_evs is None:
+                append_decode(layer, r)
+                continue
             if app_evs is not None:
                 app_evs[layer][0].record(stream)
             if rope:
@@ -253,8 +269,18 @@ def run_gpu(ctx, args, kv_name: str):
     stream.sync()
     ctx.sync()
     total_ms = start.elapsed_ms(end)
+    two_ms = None
+    if fused:  # the same steps with the append in a launch of its own (untimed for the value)
+        start.record(stream)
+        for i in range(args.steps):
+            step(args.warmup + i, one_launch=False)
+        end.record(stream)
+        stream.sync()
+        two_ms = start.elapsed_ms(end) / args.steps
     # decode calls alone: NL x steps back-to-back calls (layers and input sets rotating)
     dec_mean_ms, dec_ms = time_calls(ctx, stream, lambda i: decode(i % NL, (i // NL) % R), NL * args.steps)
+    fold_ms = (time_calls(ctx, stream, lambda i: append_decode(i % NL, (i // NL) % R), NL * args.steps)[0]
+               if fused else None)
     # append time per layer, from two more (untimed) steps with events around the appends only
     app_evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(2)]
     for i in range(2):
@@ -280,6 +306,9 @@ def run_gpu(ctx, args, kv_name: str):
         "append": {"kernel": "vk_append_kv%d" % kv, "call": "vk_append_rope" if rope else "vk_append",
                    "rope": args.rope, "ms_mean": round(float(np.mean(app_ms)), 5),
                    "q_rotated_heads": S * H if rope else 0},
+        "step_call": "vk_append_decode (append folded into the decode launch)" if fused else "append + decode",
+        "append_decode_ms_mean": round(fold_ms, 5) if fused else None,
+        "ms_per_step_two_launches": round(two_ms, 4) if fused else None,
         "plan": plan,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),

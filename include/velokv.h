@@ -115,7 +115,9 @@ int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
 #define VK_MISUSE_PAGE_OUT_OF_POOL 1u  /* an attention call read a block-table page id
                                           outside [0, n_blocks) (clamped into the pool) */
 #define VK_MISUSE_BLK_SPLIT_RUN    2u  /* an I8_BLK append had tokens of one block that
-                                          were not adjacent in the call               */
+                                          were not adjacent in the call (in
+                                          vk_append_decode: two sequences' new
+                                          tokens in one block)                        */
 /* Waits for all work of the context's device, then reports and clears the misuse
  * flags (*flags = the flags read; NULL to skip): VK_OK when none were set. */
 int vk_ctx_check(vk_ctx* ctx, uint32_t* flags);
@@ -330,10 +332,12 @@ int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* s
  * kernels.metal:637-640, 770-774); a sequence with context 0 appends nothing,
  * and a page id outside the pool stores nothing (the decode reports it,
  * VK_MISUSE_PAGE_OUT_OF_POOL). The result equals vk_append of those slots
- * followed by vk_paged_decode, bit for bit: the append is a launch of the append
- * kernel with the slots derived in the kernel, then the decode (an append fused
- * into the decode launch measured slower: its chain of dependent loads waits
- * behind the decode's streaming loads).
+ * followed by vk_paged_decode, bit for bit. Over VK_KV_I8_BLK pools under the
+ * workgroup-split schedule the decode launch appends the tokens itself (the
+ * wave that holds a sequence's last block applies the append rule to it before
+ * loading it; two sequences whose new tokens share a block are reported,
+ * VK_MISUSE_BLK_SPLIT_RUN); otherwise the append kernel runs first, with the
+ * slots derived in the kernel, then the decode.
  * The reference runs kv_update then the attention kernel per layer
  * (metal/model.rs:399-471). */
 int vk_append_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new, int32_t in_dtype,

@@ -131,3 +131,41 @@ def test_blk_append_split_run_is_reported(ctx):
     k = np.zeros((6, 8, HD), np.float16)
     ctx.append(pool, 0, ctx.upload(k), ctx.upload(k), velokv.DT_F16, ctx.upload(sl), 6)
     ctx.sync()
+
+
+def test_folded_append_shared_block_is_reported(ctx):
+    """vk_append_decode under the workgroup split, where each sequence's decode
+    appends its own new token: two sequences whose new tokens land in the same
+    block (the same last page in both table rows) would rewrite it at the same
+    time and are reported; the same call with distinct blocks, repeated (a new
+    claim epoch per call), reports nothing."""
+    print("misuse: folded append, two sequences on one block", flush=True)
+    S, H = 64, 32
+    lens = np.array([40 + 3 * i for i in range(S)], np.int32)
+    case = make_case(O.I8_BLK, lens, seed=705, outlier_scale=8.0)
+    pool = gpu_pool(ctx, case, with_last=False)
+    sl, kk, vv = case.last_slots()
+    out = ctx.alloc(S * H * HD * 4)
+
+    def call(bt, lens):
+        ctx.append_decode(pool, 0, ctx.upload(kk), ctx.upload(vv), velokv.DT_F16, ctx.upload(case.q), velokv.DT_F16,
+                          out, ctx.upload(lens), S, H, int(lens.max()), block_tables=ctx.upload(bt),
+                          bt_stride=bt.shape[1], sum_context_len=int(lens.sum()))
+
+    ctx.set_decode_schedule(velokv.SCHED_SPLIT)
+    try:
+        pl = ctx.decode_plan(pool, S, H, int(lens.max()), bt_stride=case.block_tables.shape[1],
+                             sum_context_len=int(lens.sum()))
+        assert pl["schedule"] == velokv.SCHED_WORKGROUP, pl
+        for _ in range(2):
+            call(case.block_tables, lens)
+            ctx.sync()
+        assert ctx.check_misuse() == 0
+        bt = case.block_tables.copy()
+        lens2 = lens.copy()
+        lens2[1] = lens2[0]
+        bt[1] = bt[0]
+        call(bt, lens2)
+        expect_misuse(ctx, velokv.MISUSE_BLK_SPLIT_RUN)
+    finally:
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)

@@ -663,6 +663,10 @@ constexpr int kPkMaxRounds = 16; // items per vk_decode_pk_* workgroup
 // Measured on configs 2 and 3 with 0, 4, 8, 12, 16, 24: 8 was fastest (config 3
 // 110.7 -> 109.2 us per call, config 2 208 -> 206 us).
 constexpr int kSkPenalty = 8;
+// Blocks' worth of time the append costs the wave that folds it into a
+// workgroup-split decode (vk_append_decode over I8_BLK pools): that wave's range
+// is this much shorter.
+constexpr int kFoldBlocks = 3;
 
 struct DecodePlan {
   const int32_t* bt;
@@ -915,7 +919,12 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
-  if (k_new && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
+  // I8_BLK pools under the workgroup split take the append inside the decode
+  // launch (the wave that holds a sequence's last block appends the token
+  // before loading it); every other plan appends in a launch of its own first
+  const bool fold = k_new && pool->desc.kv_type == VK_KV_I8_BLK && pl.wg_waves > 0 &&
+                    (pool->desc.head_dim == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
+  if (k_new && !fold && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
   uint8_t* ws = nullptr;
   if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes, &ws)))
     return rc;
@@ -961,6 +970,17 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   p.sk_penalty = (pl.stream_k || pl.packed) ? kSkPenalty : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.err = ctx->err_word;
+  if (fold) {
+    p.fold_k = k_new;
+    p.fold_v = v_new;
+    p.fold_dtype = in_dtype;
+    p.claim = pool->claim;
+    p.fold_epoch = pool->claim ? pool->next_epoch() : 0u;
+    // the folding wave's range is shortened by kFoldBlocks while every wave's
+    // share stays within its four block-id windows
+    const int64_t nb = ((int64_t)a->max_context_len + kBS - 1) / kBS;
+    p.fold_blocks = (nb + kFoldBlocks + pl.wg_waves - 1) / pl.wg_waves <= kMaxPartTokens / kBS ? kFoldBlocks : 0;
+  }
 
   MergeParams m{};
   m.io_hd = pool->geom.io_hd;

@@ -202,6 +202,7 @@ struct BlockIds {
   int b[kWin];
   float ks[kWin];
   float vs[kWin];
+  uint32_t oob;  // bit k: the page of this lane's block in window k was outside the pool
 };
 // A page id outside [0, n_blocks) is clamped into the pool (the read stays in
 // bounds) and reported as MISUSE_PAGE_OUT_OF_POOL. Tile u of a sequence (tokens
@@ -211,6 +212,7 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
   const int lane = lane_id();
   const int ps = P.page_shift;
   bool bad = false;
+  w.oob = 0u;
 #pragma unroll
   for (int k = 0; k < kWin; ++k) {
     w.b[k] = 0;
@@ -220,7 +222,9 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
     if (idx < nblk) {
       const int u = blk0 + idx;
       const int raw = bt[u >> ps];
-      bad |= raw < 0 || raw >= P.n_blocks;
+      const bool out = raw < 0 || raw >= P.n_blocks;
+      bad |= out;
+      w.oob |= out ? 1u << k : 0u;
       w.b[k] = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
       if constexpr (BLK) {
         w.ks[k] = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
@@ -753,6 +757,197 @@ DEV void mstage_load(MStage<KV, DK>& st, const DecodeParams& P, const BlockIds& 
   }
 }
 
+// ---- KV append helpers (shared by the append kernels and the folded append) ----
+DEV void load_x2(const void* src, int in_dtype, int64_t off, float& x0, float& x1) {
+  if (in_dtype == DT_F16) {
+    const uint32_t w = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(src) + off)[0];
+    x0 = half_lo(w); x1 = half_hi(w);
+  } else {
+    const float2 v = reinterpret_cast<const float2*>(reinterpret_cast<const float*>(src) + off)[0];
+    x0 = v.x; x1 = v.y;
+  }
+}
+
+// Byte offset inside a (block, head) tile of element (token, dim), D = head_dim
+// (64 or 128):
+//   V: [tok/2][D][2] (token pairs interleaved)
+//   K, fp16 / fp32: [tok][D]
+//   K, int8: [h][tok][D/32][16] with h = (d/16) % 2: the 32 codes of dims
+//     32c..32c+31 of token t are two 16-byte pieces at (t D/32 + c)*16 and
+//     8 D + (t D/32 + c)*16, so one 16-byte load per lane covers whole cache lines
+template <bool IS_V>
+DEV uint32_t tile_elem(int tok, int d, int esz, int D) {
+  if (IS_V) return (uint32_t)(((tok >> 1) * D + d) * 2 + (tok & 1)) * esz;
+  if (esz == 1) return (uint32_t)(((d >> 4) & 1) * 8 * D + (tok * (D >> 5) + (d >> 5)) * 16 + (d & 15));
+  return (uint32_t)(tok * D + d) * esz;
+}
+
+DEV int clamp127(float r) { return (int)fminf(fmaxf(r, -127.f), 127.f); }
+
+// The I8_BLK rule for one new token x (dims 2*lane, 2*lane + 1) at offset o of
+// a block whose scale is s_old:
+//   s_new = max(s_old, fp16(amax / 127))
+//   if s_new > s_old: c' = clamp(rne((c * s_old) / s_new)) for tokens before o
+//   c = s_new > 0 ? clamp(rne(x / s_new)) : 0
+// s_new of the row; s_bits becomes its fp16 bits when it grows.
+DEV float blk_scale(float s_old, uint16_t& s_bits, float x0, float x1) {
+  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+  const uint16_t cand = f2h(amax / 127.0f);
+  if (h2f(cand) > s_old) {
+    s_bits = cand;
+    return h2f(cand);
+  }
+  return s_old;
+}
+DEV int blk_requant(int c, float s_old, float s_new) { return clamp127(__builtin_rintf(((float)c * s_old) / s_new)); }
+DEV int blk_code(float x, float s_new) { return (s_new > 0.f) ? clamp127(__builtin_rintf(x / s_new)) : 0; }
+
+// The rule over a block whose codes are in registers (cd) and whose scale is
+// s_old (bits s_bits).
+DEV void blk_put(int (&cd)[BS][2], int o, float& s_old, uint16_t& s_bits, float x0, float x1) {
+  const float s_new = blk_scale(s_old, s_bits, x0, x1);
+  if (s_new > s_old && o > 0) {
+#pragma unroll
+    for (int u = 0; u < BS; ++u) {
+      if (u < o) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) cd[u][k] = blk_requant(cd[u][k], s_old, s_new);
+      }
+    }
+  }
+  const int c0 = blk_code(x0, s_new);
+  const int c1 = blk_code(x1, s_new);
+#pragma unroll
+  for (int u = 0; u < BS; ++u)
+    if (u == o) { cd[u][0] = c0; cd[u][1] = c1; }
+  s_old = s_new;
+}
+
+// ---- the append of vk_append_decode inside the decode launch (I8_BLK) --------
+// The piece that holds a sequence's last context token (position ctx - 1)
+// appends the sequence's new K and V rows there before it loads that block: the
+// rule of append_blk_run for a run of one token at offset o = (ctx - 1) % 16
+// (s_old = 0 when o = 0), lane l holding dims 2l, 2l+1, then attends over the
+// block as rewritten (its stores come before its own loads of the block in the
+// wave's program order). fold_issue issues the loads of the new rows and the
+// stored scales beside the piece's first loads; fold_finish applies the rule
+// and stores the new token's codes, and when the scale grows loads, requantizes
+// and stores the codes of the tokens before o. A page id outside the pool
+// appends nothing (the decode reports it), as the append kernel drops such a
+// slot.
+struct FoldIn {
+  float x[2][2];          // [K, V] new-token dims 2 lane, 2 lane + 1
+  uint16_t stored[2];     // [K, V] stored block scale
+  unsigned long long claim_old;
+  uint64_t tix;           // (tile, KV head) index of the block
+  int o;
+  bool on;
+};
+
+// Loads of the folded append of sequence s, KV head kvh, whose piece holds nblk
+// blocks (window bw), the last one holding position ctx - 1.
+template <int D>
+DEV void fold_issue(FoldIn& f, const DecodeParams& P, const BlockIds& bw, int nblk, int s, int kvh, int ctx) {
+  const int i = nblk - 1;
+  f.on = ((readlane_i((int)bw.oob, i & 63) >> (i >> 6)) & 1) == 0;
+  if (!f.on) return;
+  const int tile_id = window_at(bw.b, i);
+  f.tix = (uint64_t)tile_id * P.n_kv_heads + kvh;
+  f.o = (ctx - 1) & (BS - 1);
+  f.claim_old = 0;
+  if (P.claim && kvh == 0 && lane_id() == 0)
+    f.claim_old = __hip_atomic_exchange(&P.claim[tile_id], ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int d0 = 2 * lane_id();
+  const int64_t row = ((int64_t)s * P.n_kv_heads + kvh) * D + d0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    f.x[e][0] = f.x[e][1] = 0.f;
+    if (d0 < D) load_x2(e ? P.fold_v : P.fold_k, P.fold_dtype, row, f.x[e][0], f.x[e][1]);
+  }
+  f.stored[0] = reinterpret_cast<const uint16_t*>(P.ks)[f.tix];
+  f.stored[1] = reinterpret_cast<const uint16_t*>(P.vs)[f.tix];
+}
+
+DEV int byte_at(uint32_t w, int k) { return (int)(int8_t)(uint8_t)(w >> (8 * k)); }
+
+// The rule for K (IS_V false) or V; returns the block's new scale. Lanes past a
+// 64-dim row read the codes 64 dims below and store nothing. K codes of token u
+// at dims 2 lane, 2 lane + 1 are two adjacent bytes; V codes of the token pair
+// 2p, 2p + 1 are four (dim 2 lane: tokens 2p, 2p + 1; then dim 2 lane + 1).
+template <bool IS_V, int D>
+DEV float fold_finish_one(FoldIn& f, const DecodeParams& P) {
+  const int e = IS_V ? 1 : 0;
+  const int o = f.o;
+  const int d0 = 2 * lane_id(), da = d0 & (D - 1);
+  const bool st = d0 < D;
+  const float s_old = (o == 0) ? 0.f : h2f(f.stored[e]);
+  uint16_t s_bits = (o == 0) ? (uint16_t)0 : f.stored[e];
+  const float s_new = blk_scale(s_old, s_bits, f.x[e][0], f.x[e][1]);
+  uint8_t* tile = const_cast<uint8_t*>(IS_V ? P.vc : P.kc) + f.tix * P.tile_bytes;
+  if (s_new > s_old && o > 0) {  // requantize the tokens before o
+    if constexpr (!IS_V) {
+      uint32_t c[BS - 1];
+#pragma unroll
+      for (int u = 0; u < BS - 1; ++u)
+        c[u] = u < o ? *reinterpret_cast<const uint16_t*>(tile + tile_elem<false>(u, da, 1, D)) : 0u;
+#pragma unroll
+      for (int u = 0; u < BS - 1; ++u) {
+        if (u < o && st) {
+          const int a = blk_requant(byte_at(c[u], 0), s_old, s_new), b = blk_requant(byte_at(c[u], 1), s_old, s_new);
+          *reinterpret_cast<uint16_t*>(tile + tile_elem<false>(u, da, 1, D)) = (uint16_t)((a & 0xFF) | ((b & 0xFF) << 8));
+        }
+      }
+    } else {
+      uint32_t c[BS / 2];
+#pragma unroll
+      for (int p = 0; p < BS / 2; ++p)
+        c[p] = 2 * p < o ? *reinterpret_cast<const uint32_t*>(tile + tile_elem<true>(2 * p, da, 1, D)) : 0u;
+#pragma unroll
+      for (int t = 0; t < BS - 1; ++t) {
+        if (t < o && st) {
+          tile[tile_elem<true>(t, da, 1, D)] = (uint8_t)blk_requant(byte_at(c[t >> 1], t & 1), s_old, s_new);
+          tile[tile_elem<true>(t, da + 1, 1, D)] = (uint8_t)blk_requant(byte_at(c[t >> 1], 2 + (t & 1)), s_old, s_new);
+        }
+      }
+    }
+  }
+  const int c0 = blk_code(f.x[e][0], s_new), c1 = blk_code(f.x[e][1], s_new);
+  if (st) {
+    if constexpr (!IS_V) {
+      *reinterpret_cast<uint16_t*>(tile + tile_elem<false>(o, da, 1, D)) = (uint16_t)((c0 & 0xFF) | ((c1 & 0xFF) << 8));
+    } else {
+      tile[tile_elem<true>(o, da, 1, D)] = (uint8_t)c0;
+      tile[tile_elem<true>(o, da + 1, 1, D)] = (uint8_t)c1;
+    }
+  }
+  if (lane_id() == 0) reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(IS_V ? P.vs : P.ks))[f.tix] = s_bits;
+  return s_new;
+}
+
+// The rule, the stores, and the block's new scales in bw. One run per block and
+// call, as in append_blk: a second sequence whose new token lands in the same
+// block (claimed in this call) is reported.
+template <int D>
+DEV void fold_finish(FoldIn& f, const DecodeParams& P, BlockIds& bw, int nblk, int s) {
+  if (!f.on) return;
+  const int lane = lane_id();
+  if (P.claim && lane == 0 && f.tix % P.n_kv_heads == 0) {
+    const unsigned long long me = ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s;
+    if ((uint32_t)(f.claim_old >> 32) == P.fold_epoch && f.claim_old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
+  }
+  const float ks = fold_finish_one<false, D>(f, P);
+  const float vs = fold_finish_one<true, D>(f, P);
+  const int i = nblk - 1;
+#pragma unroll
+  for (int k = 0; k < kWin; ++k) {
+    if (k == (i >> 6) && lane == (i & 63)) {
+      bw.ks[k] = ks;
+      bw.vs[k] = vs;
+    }
+  }
+}
+
 // Tokens of a sequence with ctx committed tokens that a shared prefix of pb
 // pages covers: whole pages only, so that the rest of the context starts on a
 // page boundary.
@@ -775,7 +970,7 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 // normalised rows; otherwise it writes the unnormalised partial (acc, M, l) of
 // row R at index TREE ? out_row(R) * max_parts + pbase : pbase + R * pstride of
 // pacc ([.][HD] fp32) and pml ([.][2] fp32), in HBM or in LDS.
-template <int KV, int G, int RT, bool TREE, int QT, int D = HD>
+template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = false>
 DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                     int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   constexpr int ESZ = Esz<KV>::v;
@@ -808,6 +1003,23 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
 
   BlockIds bw;
   load_block_ids<BLK>(bw, P, bt, blk0, nblk, kvh);
+
+  // vk_append_decode with the append folded in: this piece holds the last token
+  // and appends it (after the first stage's loads and q, unless the block is in
+  // the first stage)
+  static_assert(!FOLD || (BLK && !TREE), "the folded append is the I8_BLK decode's");
+  // vk_append_decode with the append folded in: this piece holds the last token.
+  // Its block in the first stage: append before any tile load; otherwise issue
+  // the append's loads now and finish it after q, while the first stage is in
+  // flight
+  bool fold = false;
+  if constexpr (FOLD) fold = P.fold_k != nullptr && end == ctx_c && nblk > 0;
+  const bool fold_first = fold && nblk <= CH;
+  FoldIn fin;
+  if constexpr (FOLD) {
+    if (fold) fold_issue<D>(fin, P, bw, nblk, s, kvh, ctx_c);
+    if (fold_first) fold_finish<D>(fin, P, bw, nblk, s);
+  }
 
   MStage<KV, D> sa, sb;
   mstage_load<KV, D>(sa, P, bw, 0, nblk, kvh, n, g);
@@ -864,6 +1076,9 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     if constexpr (TREE) {
       if (R < nrows) mrow[rt] = P.tree_mask[(int64_t)s * N + R / Gn];
     }
+  }
+  if constexpr (FOLD) {
+    if (fold && !fold_first) fold_finish<D>(fin, P, bw, nblk, s);
   }
 
   float M[RT], lrun[RT], psum[RT];   // state of row n (each lane holds a quarter of the row's sums)
@@ -1338,14 +1553,14 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
 }
 
 // attn_piece for every KV type: fp32 pools take the fp32 matrix-core piece.
-template <int KV, int G, int RT, bool TREE, int QT, int D = HD>
+template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = false>
 DEV void attn_piece_kv(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                        int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   if constexpr (KV == KV_F32) {
     static_assert(D == HD, "fp32 pools take the 128-dim piece");
     attn_piece_f32<G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml);
   } else {
-    attn_piece<KV, G, RT, TREE, QT, D>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
+    attn_piece<KV, G, RT, TREE, QT, D, FOLD>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
   }
 }
 
@@ -1523,11 +1738,15 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
     return;
   }
   const int nb = (ctx + BS - 1) / BS;
-  const int per = (nb + nw - 1) / nw;
+  // under vk_append_decode (I8_BLK) the wave whose range ends at the context's
+  // last token appends the new token first (fold_issue, fold_finish): the split
+  // counts that append as fold_blocks more blocks of that wave's range
+  const int fw = (KV == KV_I8_BLK && P.fold_k != nullptr) ? P.fold_blocks : 0;
+  const int per = (nb + fw + nw - 1) / nw;
   const int b0 = min(nb, w * per), b1 = min(nb, b0 + per);
   if (b0 < b1) {
-    attn_piece_kv<KV, G, 1, false, QT, D>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1, &wacc[w][0][0],
-                                       &wml[w][0][0]);
+    attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1,
+                                                           &wacc[w][0][0], &wml[w][0][0]);
   } else if (lane < Gn) {
     wml[w][lane][0] = kNegInf;
     wml[w][lane][1] = 0.f;
@@ -2163,16 +2382,6 @@ __device__ void decode_merge_sk(const MergeParams& P) {
 // Workgroup (token n, KV head h) with two waves: wave 0 writes K, wave 1 writes V.
 // Lane l owns dims 2l and 2l+1.
 // =============================================================================
-DEV void load_x2(const void* src, int in_dtype, int64_t off, float& x0, float& x1) {
-  if (in_dtype == DT_F16) {
-    const uint32_t w = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(src) + off)[0];
-    x0 = half_lo(w); x1 = half_hi(w);
-  } else {
-    const float2 v = reinterpret_cast<const float2*>(reinterpret_cast<const float*>(src) + off)[0];
-    x0 = v.x; x1 = v.y;
-  }
-}
-
 // ---- RoPE (fused into the append) --------------------------------------------
 // Pair i of a head row at position p is rotated by the table's (cos, sin) of
 // angle p * base^(-2i/D), D the caller's head_dim: ROPE_INTERLEAVED pairs dims (2i, 2i+1)
@@ -2241,52 +2450,6 @@ DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h
   x0 = x1 = 0.f;
   if (2 * lane_id() < io) load_x2(src, P.in_dtype, ((int64_t)m * P.g.n_kv_heads + h) * io + 2 * lane_id(), x0, x1);
   if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, P.positions[m], io, x0, x1);
-}
-
-// Byte offset inside a (block, head) tile of element (token, dim), D = head_dim
-// (64 or 128):
-//   V: [tok/2][D][2] (token pairs interleaved)
-//   K, fp16 / fp32: [tok][D]
-//   K, int8: [h][tok][D/32][16] with h = (d/16) % 2: the 32 codes of dims
-//     32c..32c+31 of token t are two 16-byte pieces at (t D/32 + c)*16 and
-//     8 D + (t D/32 + c)*16, so one 16-byte load per lane covers whole cache lines
-template <bool IS_V>
-DEV uint32_t tile_elem(int tok, int d, int esz, int D) {
-  if (IS_V) return (uint32_t)(((tok >> 1) * D + d) * 2 + (tok & 1)) * esz;
-  if (esz == 1) return (uint32_t)(((d >> 4) & 1) * 8 * D + (tok * (D >> 5) + (d >> 5)) * 16 + (d & 15));
-  return (uint32_t)(tok * D + d) * esz;
-}
-
-DEV int clamp127(float r) { return (int)fminf(fmaxf(r, -127.f), 127.f); }
-
-// One token (dims 2*lane, 2*lane + 1 of x) into offset o of a block whose codes
-// are in registers (cd) and whose scale is s_old (bits s_bits); the I8_BLK rule:
-//   s_new = max(s_old, fp16(amax / 127))
-//   if s_new > s_old: c' = clamp(rne((c * s_old) / s_new)) for tokens before o
-//   c = s_new > 0 ? clamp(rne(x / s_new)) : 0
-DEV void blk_put(int (&cd)[BS][2], int o, float& s_old, uint16_t& s_bits, float x0, float x1) {
-  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const uint16_t cand = f2h(amax / 127.0f);
-  float s_new = s_old;
-  if (h2f(cand) > s_old) { s_new = h2f(cand); s_bits = cand; }
-  if (s_new > s_old && o > 0) {
-#pragma unroll
-    for (int u = 0; u < BS; ++u) {
-      if (u < o) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const float r = ((float)cd[u][k] * s_old) / s_new;
-          cd[u][k] = clamp127(__builtin_rintf(r));
-        }
-      }
-    }
-  }
-  const int c0 = (s_new > 0.f) ? clamp127(__builtin_rintf(x0 / s_new)) : 0;
-  const int c1 = (s_new > 0.f) ? clamp127(__builtin_rintf(x1 / s_new)) : 0;
-#pragma unroll
-  for (int u = 0; u < BS; ++u)
-    if (u == o) { cd[u][0] = c0; cd[u][1] = c1; }
-  s_old = s_new;
 }
 
 // VK_KV_I8_BLK: per-(block, head) fp16 scale, round-half-even codes clamped to +-127.

@@ -120,6 +120,15 @@ struct DecodeParams {
   // the prefix pass, the partitions of the rest of the context follow
   int32_t prefix_blocks, prefix_chunks;
   uint32_t* err;            // the context's misuse word (page ids outside the pool)
+  // vk_append_decode over an I8_BLK pool with the append folded into the decode
+  // (null otherwise): the new K and V rows [n_seqs][n_kv_heads][io_hd] of
+  // fold_dtype, the call's append epoch and the pool's per-tile claim words
+  const void* fold_k;
+  const void* fold_v;
+  int32_t fold_dtype;
+  uint32_t fold_epoch;
+  unsigned long long* claim;
+  int32_t fold_blocks;      // workgroup split: blocks' worth of time the append costs the wave that folds it
 };
 
 constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)
