@@ -47,6 +47,10 @@
  * the same layouts at D = 64: [16][64] K, [8][64][2] V, and int8 K as
  * [2][16][2][16] (dims 32c..32c+15 of token t at byte (2t + c)*16, dims
  * 32c+16..32c+31 at 512 + (2t + c)*16); callers pass 64-dim rows.
+ * Other head_dims (any multiple of 8 up to 128, kernels.metal:464) are stored in
+ * the tiles of the next width, 64 dims for head_dim <= 64, else 128, with the
+ * dims past head_dim held as zeros; callers pass head_dim-long rows (K, V, q,
+ * out) and the softmax scale defaults to 1/sqrt(head_dim).
  * Element size: F32 4, F16 2, I8_* 1 byte.
  */
 #ifndef VELOKV_H
@@ -169,7 +173,8 @@ typedef struct vk_pool_desc {
                              16, 32, 64, 128 or 256 tokens per page; other sizes >
                              0 are VK_ERR_UNSUPPORTED, 0 VK_ERR_INVALID_BLOCK_SIZE */
   int32_t n_kv_heads;     /* ModelMeta::n_head_kv                                  */
-  int32_t head_dim;       /* ModelMeta::head_dim: 128 or 64                        */
+  int32_t head_dim;       /* ModelMeta::head_dim: a multiple of 8 up to 128 (64- or
+                             128-dim tiles, zero-padded past head_dim)            */
   int32_t kv_type;        /* VK_KV_*  (MemoryRuntimeConfig::kv_type)               */
   int32_t max_slots;      /* MemoryRuntimeConfig::max_slots (runtime.rs:59)        */
   int32_t max_pages_per_slot; /* row length of the slot block table; 0 = n_blocks

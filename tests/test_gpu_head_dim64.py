@@ -208,7 +208,8 @@ def test_hd64_tree_commit(ctx, kv):
 
 
 def test_hd64_limits(ctx):
-    for bad in (32, 96, 256):
+    # head_dim takes multiples of 8 up to 128 (64- or 128-dim tiles)
+    for bad in (100, 36, 136, 256):
         with pytest.raises(velokv.VkError) as e:
             velokv.Pool(ctx, 1, 8, BS, 2, bad, O.F16)
         assert e.value.code == velokv.ERR_UNSUPPORTED, bad

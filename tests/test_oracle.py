@@ -501,3 +501,74 @@ def test_head_dim64_layer_equals_zero_padded_128(kv):
     got = O.paged_decode(L64, q64, case.block_tables, case.ctx_lens)
     ref = O.paged_decode(L128, qp, case.block_tables, case.ctx_lens, scale=1.0 / np.sqrt(D))
     assert np.array_equal(got, ref[..., :D])
+
+
+@pytest.mark.parametrize("hd", [96, 80, 40, 8])
+@pytest.mark.parametrize("kv", [O.F32, O.I8_REF])
+def test_other_head_dims_padded_layer_equals_reference_restatement(kv, hd):
+    """A head_dim that is not 64 or 128 is held in the tiles of the next width (64
+    or 128 dims) with zeros past head_dim. Pinned against the restatements of the
+    reference's own kernels at that head_dim (kv_update / kv_update_int8 and
+    paged_attention_flash[_int8], kernels.metal:440-501, 619-645, 672-732,
+    753-802, which take any head_dim up to 128): the padded layer holds the
+    reference's codes and scales (an int8 scale comes from the row's absmax,
+    which zero dims do not move) and zeros past head_dim, and attention over it
+    with the 1/sqrt(head_dim) scale gives the reference's output."""
+    T = 64 if hd <= 64 else HD
+    n_blocks, Hkv, H = 6, 2, 4
+    table = np.array([4, 1, 5], np.uint32)
+    row = 4 * hd if kv == O.F32 else hd + 4
+    kref = np.zeros(n_blocks * BS * Hkv * row, np.uint8)
+    vref = np.zeros_like(kref)
+    L = O.Layer(n_blocks, Hkv, BS, T, kv)
+    r = np.random.default_rng(31 + hd)
+    n_tok = 40
+    for pos in range(n_tok):
+        k = (r.standard_normal((Hkv, hd)) * r.uniform(0.5, 4)).astype(np.float32)
+        v = (r.standard_normal((Hkv, hd)) * r.uniform(0.5, 4)).astype(np.float32)
+        if kv == O.F32:
+            O.ref_kv_update(kref.view(np.float32), vref.view(np.float32), k, v, 0, table, 3, BS, Hkv, hd, pos)
+        else:
+            O.ref_kv_update_int8(kref.view(np.int8), vref.view(np.int8), k, v, 0, table, 3, BS, Hkv, hd, pos)
+        kp, vp = np.zeros((1, Hkv, T), np.float32), np.zeros((1, Hkv, T), np.float32)
+        kp[0, :, :hd], vp[0, :, :hd] = k, v
+        O.append(L, kp, vp, [int(table[pos // BS]) * BS + pos % BS])
+    for is_v, ref in ((0, kref), (1, vref)):
+        got = O.to_reference_layout(L, is_v).reshape(n_blocks * BS * Hkv, -1)
+        want = ref.reshape(n_blocks * BS * Hkv, row)
+        esz = 4 if kv == O.F32 else 1
+        assert np.array_equal(got[:, :hd * esz], want[:, :hd * esz])       # codes (or fp32 values)
+        assert not np.any(got[:, hd * esz:T * esz])                         # zeros past head_dim
+        if kv == O.I8_REF:
+            assert np.array_equal(got[:, T:], want[:, hd:])                  # the per-token fp32 scale
+    q = r.standard_normal((H, hd)).astype(np.float32)
+    qp = np.zeros((1, H, T), np.float32)
+    qp[0, :, :hd] = q
+    bt = table[None].astype(np.int32)
+    got = O.paged_decode(L, qp.astype(np.float32), bt, np.array([n_tok], np.int32), scale=1.0 / np.sqrt(hd))[0]
+    want = O.ref_paged_attention_flash(q, kref.view(np.float32 if kv == O.F32 else np.int8),
+                                       vref.view(np.float32 if kv == O.F32 else np.int8), kv == O.I8_REF, hd,
+                                       n_tok - 1, 0, table, 3, BS, Hkv, H)
+    assert not np.any(got[:, hd:])
+    assert np.max(np.abs(got[:, :hd] - want)) < 2e-5
+
+
+@pytest.mark.parametrize("hd", [96, 40])
+def test_other_head_dims_blk_closed_form(hd):
+    """I8_BLK over a padded head: one token per block, so each block's scale is
+    fp16_rne(amax / 127) over the head's own dims and its codes rne(x / s) clipped
+    to +-127 (numpy float16 and rint, no oracle step), zeros past head_dim."""
+    T = 64 if hd <= 64 else HD
+    r = np.random.default_rng(7 + hd)
+    L = O.Layer(8, 1, BS, T, O.I8_BLK)
+    for b in range(8):
+        x = (r.standard_normal(hd) * r.uniform(0.01, 30)).astype(np.float32)
+        xp = np.zeros((1, 1, T), np.float32)
+        xp[0, 0, :hd] = x
+        O.append(L, xp, xp, [b * BS])
+        s = (np.max(np.abs(x)) / np.float32(127)).astype(np.float16)
+        assert L.ks.view(np.float16)[b] == s
+        c = np.clip(np.rint(x.astype(np.float32) / np.float32(s)), -127, 127).astype(np.int8)
+        codes = L.tile_codes(0, b, 0)
+        assert np.array_equal(codes[0, :hd], c)
+        assert not np.any(codes[0, hd:])

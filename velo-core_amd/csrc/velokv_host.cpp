@@ -82,9 +82,12 @@ PoolGeom page_geom(const PoolGeom& t) {
   return g;
 }
 
-// The append kernel of a pool (the I8_BLK rule has its own build for head_dim 64).
+// Tile width of a pool: heads of up to 64 dims are stored in 64-dim tiles, wider
+// ones in 128-dim tiles; the dims past head_dim hold zeros.
+int tile_hd(int head_dim) { return head_dim <= kHD / 2 ? kHD / 2 : kHD; }
+// The append kernel of a pool (the I8_BLK rule has its own build for 64-dim tiles).
 std::string append_kernel_name(int kv_type, int head_dim) {
-  return "vk_append_kv" + std::to_string(kv_type) + (kv_type == VK_KV_I8_BLK && head_dim != kHD ? "_d64" : "");
+  return "vk_append_kv" + std::to_string(kv_type) + (kv_type == VK_KV_I8_BLK && tile_hd(head_dim) != kHD ? "_d64" : "");
 }
 
 std::string default_code_object_path() {
@@ -190,8 +193,11 @@ std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) 
   return "vk_decode_sk_kv" + std::to_string(kv) + (d64 ? std::string("_gx_d64") : gtag(g)) + q0_suffix(qt);
 }
 // The head_dim-64 kernels serve this pool and group size: int8 and fp16 pools
-// of 64-dim heads, one 16-row tile of query rows per (sequence, KV head).
-bool use_d64(const vk_pool_desc& d, int g) { return d.head_dim == kHD / 2 && d.kv_type != VK_KV_F32 && g <= kMaxGroupTile; }
+// of 64-dim tiles (heads of up to 64 dims), one 16-row tile of query rows per
+// (sequence, KV head).
+bool use_d64(const vk_pool_desc& d, int g) {
+  return tile_hd(d.head_dim) == kHD / 2 && d.kv_type != VK_KV_F32 && g <= kMaxGroupTile;
+}
 std::string decode_pk_name(int kv, int g, int qt = VK_DT_F16) {
   return "vk_decode_pk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
@@ -384,8 +390,8 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
       d->max_pages_per_slot < 0)
     return fail(VK_ERR_BAD_ARG, "pool sizes must be positive");
   if (kv_esz(d->kv_type) == 0) return fail(VK_ERR_BAD_ARG, "unknown kv_type %d", d->kv_type);
-  if (d->head_dim != kHD && d->head_dim != kHD / 2)
-    return fail(VK_ERR_UNSUPPORTED, "head_dim %d: the kernels take 64 or 128", d->head_dim);
+  if (d->head_dim > kHD || d->head_dim % 8 != 0)
+    return fail(VK_ERR_UNSUPPORTED, "head_dim %d: the kernels take multiples of 8 up to 128", d->head_dim);
   int ps = 0;  // pages of 16 << ps tokens: 16-token tiles, 2^ps per page
   while (ps < kMaxPageShift && (kBS << ps) < d->block_size) ++ps;
   if ((kBS << ps) != d->block_size)
@@ -398,14 +404,15 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
   if (p->desc.max_pages_per_slot == 0) p->desc.max_pages_per_slot = d->n_blocks;
   const int esz = kv_esz(d->kv_type);
   PoolGeom& g = p->geom;  // tile view: 16-token tiles, 2^ps per page
-  // a tile holds 16 tokens of one head, head_dim wide
-  g.tile_bytes = (uint32_t)(kBS * d->head_dim * esz);
+  // a tile holds 16 tokens of one head, 64 or 128 dims wide (zeros past head_dim)
+  const int tw = tile_hd(d->head_dim);
+  g.tile_bytes = (uint32_t)(kBS * tw * esz);
   g.stile_bytes = (uint32_t)kv_stile(d->kv_type, kBS);
   g.n_blocks = d->n_blocks << ps;
   g.page_shift = ps;
   g.n_kv_heads = d->n_kv_heads;
   g.block_size = kBS;
-  g.head_dim = d->head_dim;
+  g.head_dim = tw;
   g.io_hd = d->head_dim;
   g.kv_type = d->kv_type;
   g.n_layer = d->n_layer;
@@ -923,7 +930,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   // launch (the wave that holds a sequence's last block appends the token
   // before loading it); every other plan appends in a launch of its own first
   const bool fold = k_new && pool->desc.kv_type == VK_KV_I8_BLK && pl.wg_waves > 0 &&
-                    (pool->desc.head_dim == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
+                    (tile_hd(pool->desc.head_dim) == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
   if (k_new && !fold && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
   uint8_t* ws = nullptr;
   if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes, &ws)))
@@ -935,6 +942,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
 
   DecodeParams p{};
   p.io_hd = pool->geom.io_hd;
+  p.tile_hd = pool->geom.head_dim;
   p.kc = L + g.k_off;
   p.vc = L + g.v_off;
   p.ks = g.stile_bytes ? L + g.ks_off : nullptr;
@@ -1155,6 +1163,7 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
 
   DecodeParams p{};
   p.io_hd = pool->geom.io_hd;
+  p.tile_hd = pool->geom.head_dim;
   p.kc = L + g.k_off;
   p.vc = L + g.v_off;
   p.ks = g.stile_bytes ? L + g.ks_off : nullptr;

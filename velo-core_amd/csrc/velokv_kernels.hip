@@ -717,7 +717,7 @@ DEV void mstage_load(MStage<KV, DK>& st, const DecodeParams& P, const BlockIds& 
                      int g) {
   constexpr int ESZ = Esz<KV>::v;
   constexpr int CH = MStage<KV, DK>::CH;
-  const int D = DK == HD ? P.io_hd : DK;
+  const int D = DK == HD ? P.tile_hd : DK;
   const int gk = g & (D / 32 - 1), nv = n & (D / 8 - 1);
 #pragma unroll
   for (int u = 0; u < CH; ++u) {
@@ -858,12 +858,13 @@ DEV void fold_issue(FoldIn& f, const DecodeParams& P, const BlockIds& bw, int nb
   if (P.claim && kvh == 0 && lane_id() == 0)
     f.claim_old = __hip_atomic_exchange(&P.claim[tile_id], ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s,
                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the new rows are io_hd long; the tile's dims past it take zeros
   const int d0 = 2 * lane_id();
-  const int64_t row = ((int64_t)s * P.n_kv_heads + kvh) * D + d0;
+  const int64_t row = ((int64_t)s * P.n_kv_heads + kvh) * P.io_hd + d0;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     f.x[e][0] = f.x[e][1] = 0.f;
-    if (d0 < D) load_x2(e ? P.fold_v : P.fold_k, P.fold_dtype, row, f.x[e][0], f.x[e][1]);
+    if (d0 < P.io_hd) load_x2(e ? P.fold_v : P.fold_k, P.fold_dtype, row, f.x[e][0], f.x[e][1]);
   }
   f.stored[0] = reinterpret_cast<const uint16_t*>(P.ks)[f.tix];
   f.stored[1] = reinterpret_cast<const uint16_t*>(P.vs)[f.tix];
@@ -1039,13 +1040,12 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   for (int rt = 0; rt < RT; ++rt) {
     const int R = row0 + 16 * rt + n;
     float qsum = 0.f;
-    // q rows are io_hd long: dims 32g.. past it are zero
+    // q rows are io_hd long (a multiple of 8): the 8-dim chunks past it are zero
     const int64_t qoff = out_row(R) * P.io_hd + 8 * KC * g;
-    const bool qin = R < nrows && 8 * KC * g < P.io_hd;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
-      if (qin) {
+      if (R < nrows && 8 * (KC * g + kc) < P.io_hd) {
         if constexpr (QT == DT_F32) {
           const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff) + 2 * kc;
           const float4 x0 = q32[0], x1 = q32[1];
@@ -1365,7 +1365,7 @@ DEV void f32_stage_load(F32Stage& st, const DecodeParams& P, const BlockIds& bw,
   // up (j, t >= 4) read the bytes of the dims 64 below (they meet zero q dims and
   // their outputs are dropped). Two base offsets each, so that j and t stay
   // immediates; the pair r goes in the scalar offset.
-  const int D = P.io_hd;
+  const int D = P.tile_hd;
   const int k0 = n * 4 * D + 16 * g, k1 = k0 - (D < HD ? 256 : 0);
   const int v0 = 16 * g * D + 8 * n, v1 = v0 - (D < HD ? 512 : 0);
 #pragma unroll
@@ -1410,7 +1410,7 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (R < nrows && 16 * j < P.io_hd) {
+      if (R < nrows && 16 * j + 4 * g < P.io_hd) {
         if constexpr (QT == DT_F32) {
           x = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 16 * j);
         } else {
@@ -1540,7 +1540,7 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
           const float inv = lr > 0.f ? 1.f / lr : 0.f;
 #pragma unroll
           for (int t = 0; t < 8; ++t)
-            if (16 * t < P.io_hd) P.out[orow * P.io_hd + 16 * t + n] = acc[rt][t][r] * inv;
+            if (16 * t + n < P.io_hd) P.out[orow * P.io_hd + 16 * t + n] = acc[rt][t][r] * inv;
         } else {
           const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
 #pragma unroll
@@ -2006,7 +2006,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (valid && 32 * kc < P.io_hd) {
+      if (valid && 32 * kc + 8 * g < P.io_hd) {
         if constexpr (QT == DT_F32) {
           const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 32 * kc);
           const float4 x0 = q32[0], x1 = q32[1];
@@ -2051,7 +2051,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   const int vd = tid & (HD - 1), vq = tid >> 7;
   // A head_dim-64 tile is 64 dims wide: dims 64 and up are read from the dims 64
   // below (they meet zero q dims, and those output dims are dropped).
-  const int D = P.io_hd;
+  const int D = P.tile_hd;
   const int kdt = kd & (D - 1), vdt = vd & (D - 1);
   // byte offset of K dims kd..kd+3 of token kt: int8 tiles hold dims 32c + 16h + j
   // of token t at byte 8 D h + (t D/32 + c) 16 + j
@@ -2389,7 +2389,9 @@ __device__ void decode_merge_sk(const MergeParams& P) {
 // (llama_cpu.rs:113-131). y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32 with
 // every product and sum rounded separately (no fused multiply-add), the
 // reference's expression order. Lane l holds dims 2l, 2l+1 of the row.
-// D = 64 or 128: lanes 2l >= D hold zeros and stay zero.
+// D = any multiple of 4 up to 128 (the half-split partners of the lane's dims,
+// d + D/2 or d - D/2, then sit together in lane l + D/4 or l - D/4): lanes
+// 2l >= D hold zeros and stay zero.
 DEV void rope_rotate(int style, const float* cos_sin, int pos, int D, float& x0, float& x1) {
 #pragma clang fp contract(off)
   const int lane = lane_id();
@@ -2404,9 +2406,11 @@ DEV void rope_rotate(int style, const float* cos_sin, int pos, int D, float& x0,
       x1 = y1;
     }
   } else {
-    const float p0 = __shfl_xor(x0, hl, WAVE), p1 = __shfl_xor(x1, hl, WAVE);  // dims d ^ D/2
+    const int lh = lane < hl ? lane : lane - hl;                             // the lane's place in its half
+    const float p0 = __shfl(x0, lane < hl ? lane + hl : lh, WAVE);          // dims d -+ D/2
+    const float p1 = __shfl(x1, lane < hl ? lane + hl : lh, WAVE);
     if (2 * lane >= D) return;
-    const float4 cs = reinterpret_cast<const float4*>(row)[lane & (hl - 1)];  // pairs 2(l%hl), 2(l%hl)+1
+    const float4 cs = reinterpret_cast<const float4*>(row)[lh];  // pairs 2 lh, 2 lh + 1
     if (lane < hl) {  // first half: y = x c - partner s
       const float y0 = x0 * cs.x - p0 * cs.y;
       const float y1 = x1 * cs.z - p1 * cs.w;
@@ -2649,7 +2653,7 @@ DEV void append_plain(const AppendParams& P, const void* src, uint8_t* codes, in
   const int d0 = 2 * lane;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
   const int D = P.g.head_dim;
-  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE) && D == HD) {
+  if (ESZ == 2 && P.in_dtype == DT_F16 && (IS_V || P.rope == ROPE_NONE) && D == HD && P.g.io_hd == HD) {
     const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src) + ((int64_t)n * Hkv + h) * HD + d0;
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0, 2, HD)) = s16[0];
     *reinterpret_cast<uint16_t*>(tile + tile_elem<IS_V>(o, d0 + 1, 2, HD)) = s16[1];

@@ -27,12 +27,13 @@ struct PoolGeom {
   uint64_t layer_stride;   // bytes between layers
   uint64_t k_off, v_off;   // byte offsets of K / V codes inside a layer
   uint64_t ks_off, vs_off; // byte offsets of K / V scales inside a layer
-  uint32_t tile_bytes;     // codes of one (block, head): block_size * head_dim * esz
+  uint32_t tile_bytes;     // codes of one (block, head): block_size * head_dim * esz (head_dim = tile width)
   uint32_t stile_bytes;    // scales of one (block, head): 2 (I8_BLK, per 16 tokens), 4 per token (I8_REF), 0
   int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
   int32_t page_shift;      // tile view: log2(page tokens / 16)
-  int32_t io_hd;           // head_dim of the caller's K/V/q/out rows (64 or 128), the
-                           // same as head_dim
+  int32_t io_hd;           // head_dim of the caller's K/V/q/out rows: any multiple of 8 up to
+                           // 128; head_dim above is the tile width, 64 (io_hd <= 64) or 128,
+                           // the dims past io_hd held as zeros
 };
 
 enum RopeStyle : int32_t { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
@@ -105,7 +106,8 @@ struct DecodeParams {
   int32_t n_seqs, n_heads, n_kv_heads;
   int32_t n_blocks;         // pages in the pool (block-table entries range)
   int32_t page_shift;       // log2(page tokens / 16): table entry p holds tiles p << page_shift ..
-  int32_t io_hd;            // head_dim: q / out row length and tile width (64 or 128)
+  int32_t io_hd;            // head_dim: q / out row length (a multiple of 8 up to 128)
+  int32_t tile_hd;          // tile width, 64 or 128 (>= io_hd; the dims past io_hd hold zeros)
   int32_t max_parts;        // partitions per sequence in the grid
   int32_t part_tokens;      // tokens per partition (multiple of the block size)
   int32_t cap_tokens;       // tokens a table row can address: min(max_parts*part_tokens, bt_stride*bs)
@@ -208,7 +210,7 @@ struct MergeParams {
   int32_t n_workers, n_kv_heads, n_seqs;
   int32_t sk_penalty;                    // stream-K cost units per segment (DecodeParams)
   int32_t prefix_blocks, prefix_chunks;  // tree verify with a shared prefix (DecodeParams)
-  int32_t io_hd;                         // out row length (64 or 128)
+  int32_t io_hd;                         // out row length (a multiple of 8 up to 128)
 };
 
 // Stream-K split of W cost units over nw workers of one wave each: worker w
