@@ -10,8 +10,8 @@ One step = one decode token for all 64 sequences through 32 layers: per layer,
 append the new K/V token of every sequence at position 8191 (slot mapping into a
 randomly scattered 40k-block pool, on-the-fly INT8 quantization) and run paged
 decode attention over the full 8192-token context. With INT8 KV and no RoPE
-the layer is one vk_append_decode call, whose workgroup-split decode appends
-the new token itself (ms_per_step_two_launches reports the same steps with the
+the layer is one vk_append_decode call, whose decode (workgroup split, or
+stream-K for ragged batches) appends the new token itself (ms_per_step_two_launches reports the same steps with the
 append as a launch of its own). Inputs (pool contents, new
 K/V, q) are synthetic (seeded SplitMix64 normals generated on the GPU) and are
 resident in HBM before timing starts.
@@ -229,10 +229,10 @@ def run_gpu(ctx, args, kv_name: str):
                          block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
                          stream=stream, sum_context_len=int(lens.sum()))
 
-    # INT8 (I8_BLK) under the workgroup split, without RoPE: vk_append_decode,
-    # whose decode appends each sequence's new token itself (one launch per
-    # layer); otherwise the append and the decode are two launches
-    fused = kv == velokv.KV_I8_BLK and not rope and plan["wg_waves"] > 0
+    # INT8 (I8_BLK) under the workgroup split or stream-K, without RoPE:
+    # vk_append_decode, whose decode appends each sequence's new token itself
+    # (one launch per layer); otherwise the append and the decode are two launches
+    fused = kv == velokv.KV_I8_BLK and not rope and (plan["wg_waves"] > 0 or plan["schedule"] == velokv.SCHED_STREAM)
 
     def append_decode(layer, r):
         ctx.append_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, qs[r], qdt, out, d_lens, S, H, int(lens.max()),

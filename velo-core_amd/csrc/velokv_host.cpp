@@ -926,10 +926,10 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
-  // I8_BLK pools under the workgroup split take the append inside the decode
-  // launch (the wave that holds a sequence's last block appends the token
-  // before loading it); every other plan appends in a launch of its own first
-  const bool fold = k_new && pool->desc.kv_type == VK_KV_I8_BLK && pl.wg_waves > 0 &&
+  // I8_BLK pools under the workgroup split or stream-K take the append inside
+  // the decode launch (the wave that holds a sequence's last block appends the
+  // token before loading it); every other plan appends in a launch of its own first
+  const bool fold = k_new && pool->desc.kv_type == VK_KV_I8_BLK && (pl.wg_waves > 0 || pl.stream_k) &&
                     (tile_hd(pool->desc.head_dim) == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
   if (k_new && !fold && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
   uint8_t* ws = nullptr;
@@ -984,10 +984,12 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
     p.fold_dtype = in_dtype;
     p.claim = pool->claim;
     p.fold_epoch = pool->claim ? pool->next_epoch() : 0u;
-    // the folding wave's range is shortened by kFoldBlocks while every wave's
-    // share stays within its four block-id windows
+    // workgroup split: the folding wave's range is shortened by kFoldBlocks
+    // while every wave's share stays within its four block-id windows (stream-K
+    // ranges are not shortened)
     const int64_t nb = ((int64_t)a->max_context_len + kBS - 1) / kBS;
-    p.fold_blocks = (nb + kFoldBlocks + pl.wg_waves - 1) / pl.wg_waves <= kMaxPartTokens / kBS ? kFoldBlocks : 0;
+    p.fold_blocks = pl.wg_waves > 0 && (nb + kFoldBlocks + pl.wg_waves - 1) / pl.wg_waves <= kMaxPartTokens / kBS
+                        ? kFoldBlocks : 0;
   }
 
   MergeParams m{};

@@ -1700,9 +1700,14 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     int o0, o1;
     sk_piece(seg0, nb, pen, x, c1, &o0, &o1);
     if (o0 < o1) {
+      // under vk_append_decode (I8_BLK) the piece that ends at the context's last
+      // token appends the new token first (fold_issue, fold_finish): no other
+      // piece of the launch reads that block
       const int slot = o0 > 0 ? 0 : 1;
-      attn_piece_kv<KV, G, 1, false, QT, D>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s, o0 == 0 && o1 == nb,
-                                            ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc, P.part_ml);
+      attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s,
+                                                            o0 == 0 && o1 == nb,
+                                                            ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc,
+                                                            P.part_ml);
     }
     x = seg0 + su;
     if (kvh == Hkv - 1) {
