@@ -10,7 +10,8 @@ layer with the 1/sqrt(hd) scale (within the north-star tolerance). That padded
 oracle is pinned on the CPU against the reference-kernel restatements at hd
 itself and a numpy closed form of the int8 block rule (tests/test_oracle.py).
 hd = 80 and 40 leave a lane group's last 8-dim chunks of q past the row (the
-per-chunk q masks); hd = 40 runs the 64-dim pieces."""
+per-chunk q masks); hd = 40 and 8 run the 64-dim pieces; hd = 72 is the
+narrowest head on 128-dim tiles."""
 import numpy as np
 import pytest
 
@@ -24,6 +25,7 @@ pytestmark = pytest.mark.gpu
 
 KV_ALL = [O.F32, O.F16, O.I8_REF, O.I8_BLK]
 HDS = [96, 80, 40]
+HDS_EDGE = [72, 8]  # the narrowest head on 128-dim tiles, the narrowest head overall
 
 
 def tile_w(hd):
@@ -72,7 +74,7 @@ def oracle_decode(layer, q, hd, bt, lens):
     return ref[..., :hd]
 
 
-@pytest.mark.parametrize("hd", HDS)
+@pytest.mark.parametrize("hd", HDS + HDS_EDGE)
 @pytest.mark.parametrize("kv", KV_ALL)
 def test_append_bit_exact(ctx, kv, hd):
     print(f"hd{hd} append kv={kv}", flush=True)
@@ -90,7 +92,7 @@ SCHEDS = {"split": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 0), "split-p64": (ve
 
 @pytest.mark.parametrize("qd", [np.float16, np.float32])
 @pytest.mark.parametrize("sched", list(SCHEDS))
-@pytest.mark.parametrize("hd", HDS)
+@pytest.mark.parametrize("hd", HDS + HDS_EDGE)
 @pytest.mark.parametrize("kv", KV_ALL)
 def test_decode(ctx, kv, hd, sched, qd):
     print(f"hd{hd} decode kv={kv} sched={sched} q={np.dtype(qd).name}", flush=True)
@@ -182,7 +184,7 @@ def test_tree_verify(ctx, kv, hd, shared):
 
 
 @pytest.mark.parametrize("style", [O.ROPE_INTERLEAVED, O.ROPE_HALF])
-@pytest.mark.parametrize("hd", [96, 40])
+@pytest.mark.parametrize("hd", [96, 40, 8])
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
 def test_append_rope_bit_exact(ctx, kv, hd, style):
     """RoPE over hd-dim rows (pairs (2i, 2i+1) or (i, i + hd/2), the angles of an
