@@ -11,7 +11,8 @@ append the new K/V token of every sequence at position 8191 (slot mapping into a
 randomly scattered 40k-block pool, on-the-fly INT8 quantization) and run paged
 decode attention over the full 8192-token context. With INT8 KV and no RoPE
 the layer is one vk_append_decode call, whose decode (workgroup split, or
-stream-K for ragged batches) appends the new token itself (ms_per_step_two_launches reports the same steps with the
+stream-K for ragged batches, where fp16 KV folds the append too) appends the
+new token itself (ms_per_step_two_launches reports the same steps with the
 append as a launch of its own). Inputs (pool contents, new
 K/V, q) are synthetic (seeded SplitMix64 normals generated on the GPU) and are
 resident in HBM before timing starts.
@@ -229,10 +230,11 @@ def run_gpu(ctx, args, kv_name: str):
                          block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
                          stream=stream, sum_context_len=int(lens.sum()))
 
-    # INT8 (I8_BLK) under the workgroup split or stream-K, without RoPE:
-    # vk_append_decode, whose decode appends each sequence's new token itself
+    # INT8 (I8_BLK) under the workgroup split or stream-K, fp16 under stream-K,
+    # without RoPE: vk_append_decode, whose decode appends each sequence's new token itself
     # (one launch per layer); otherwise the append and the decode are two launches
-    fused = kv == velokv.KV_I8_BLK and not rope and (plan["wg_waves"] > 0 or plan["schedule"] == velokv.SCHED_STREAM)
+    fused = not rope and ((kv == velokv.KV_I8_BLK and plan["wg_waves"] > 0) or
+                          (kv in (velokv.KV_I8_BLK, velokv.KV_F16) and plan["schedule"] == velokv.SCHED_STREAM))
 
     def append_decode(layer, r):
         ctx.append_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, qs[r], qdt, out, d_lens, S, H, int(lens.max()),

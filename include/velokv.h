@@ -338,7 +338,8 @@ int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* s
  * and a page id outside the pool stores nothing (the decode reports it,
  * VK_MISUSE_PAGE_OUT_OF_POOL). The result equals vk_append of those slots
  * followed by vk_paged_decode, bit for bit. Over VK_KV_I8_BLK pools under the
- * workgroup-split or stream-K schedule the decode launch appends the tokens itself (the
+ * workgroup-split or stream-K schedule, and over VK_KV_F16 pools under
+ * stream-K, the decode launch appends the tokens itself (the
  * wave that holds a sequence's last block applies the append rule to it before
  * loading it; two sequences whose new tokens share a block are reported,
  * VK_MISUSE_BLK_SPLIT_RUN); otherwise the append kernel runs first, with the

@@ -113,17 +113,19 @@ def test_int8_workgroup_split(ctx, qd, in_dt):
 
 @pytest.mark.parametrize("qd", [np.float16, np.float32])
 @pytest.mark.parametrize("G", [4, 3])
-def test_int8_stream_k_folds_the_append(ctx, G, qd):
-    """A ragged batch under stream-K: the piece that ends at a context's last
-    token appends the new token in the decode launch. New tokens at every block
-    offset, first tokens of a context (L = 1), and (even sequences) new rows 3x
-    larger, so that the block scale grows and the earlier codes are requantized."""
-    print(f"append_decode stream-K G={G} q={np.dtype(qd).name}", flush=True)
+@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16])
+def test_stream_k_folds_the_append(ctx, kv, G, qd):
+    """A ragged batch under stream-K over int8 block and fp16 pools: the piece
+    that ends at a context's last token appends the new token in the decode
+    launch. New tokens at every block offset, first tokens of a context (L = 1),
+    and (even sequences) new rows 3x larger, so that an int8 block scale grows
+    and the earlier codes are requantized."""
+    print(f"append_decode stream-K kv={kv} G={G} q={np.dtype(qd).name}", flush=True)
     r = synth.rng(960 + G)
     lens = r.integers(1, 3000, 64)
     lens[:6] = [1, 16, 17, 32, 33, 48]
     lens[6:22] = 1200 + np.arange(16)  # every offset of a block
-    case = make_case(O.I8_BLK, lens, n_kv_heads=8, n_heads=8 * G, seed=961 + G, outlier_scale=8.0)
+    case = make_case(kv, lens, n_kv_heads=8, n_heads=8 * G, seed=961 + G, outlier_scale=8.0)
     for s_ in range(0, case.S, 2):
         case.k[s_][-1] = (case.k[s_][-1].astype(np.float32) * 3).astype(np.float16)
         case.v[s_][-1] = (case.v[s_][-1].astype(np.float32) * 3).astype(np.float16)

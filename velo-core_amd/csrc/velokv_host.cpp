@@ -926,10 +926,13 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   if (a->n_seqs == 0) return VK_OK;
   if (!a->q || !a->out || !a->context_lens) return fail(VK_ERR_BAD_ARG, "null device pointer");
   if ((rc = set_device(ctx))) return rc;
-  // I8_BLK pools under the workgroup split or stream-K take the append inside
-  // the decode launch (the wave that holds a sequence's last block appends the
-  // token before loading it); every other plan appends in a launch of its own first
-  const bool fold = k_new && pool->desc.kv_type == VK_KV_I8_BLK && (pl.wg_waves > 0 || pl.stream_k) &&
+  // I8_BLK pools under the workgroup split or stream-K, and fp16 pools under
+  // stream-K, take the append inside the decode launch (the wave that holds a
+  // sequence's last block appends the token before loading it); every other
+  // plan appends in a launch of its own first
+  const int kvt = pool->desc.kv_type;
+  const bool fold = k_new &&
+                    ((kvt == VK_KV_I8_BLK && (pl.wg_waves > 0 || pl.stream_k)) || (kvt == VK_KV_F16 && pl.stream_k)) &&
                     (tile_hd(pool->desc.head_dim) == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
   if (k_new && !fold && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
   uint8_t* ws = nullptr;

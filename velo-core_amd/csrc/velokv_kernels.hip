@@ -845,8 +845,9 @@ struct FoldIn {
 };
 
 // Loads of the folded append of sequence s, KV head kvh, whose piece holds nblk
-// blocks (window bw), the last one holding position ctx - 1.
-template <int D>
+// blocks (window bw), the last one holding position ctx - 1 (I8_BLK: also the
+// block's stored scales; fp16 pools store the new rows as they are).
+template <int KV, int D>
 DEV void fold_issue(FoldIn& f, const DecodeParams& P, const BlockIds& bw, int nblk, int s, int kvh, int ctx) {
   const int i = nblk - 1;
   f.on = ((readlane_i((int)bw.oob, i & 63) >> (i >> 6)) & 1) == 0;
@@ -866,8 +867,10 @@ DEV void fold_issue(FoldIn& f, const DecodeParams& P, const BlockIds& bw, int nb
     f.x[e][0] = f.x[e][1] = 0.f;
     if (d0 < P.io_hd) load_x2(e ? P.fold_v : P.fold_k, P.fold_dtype, row, f.x[e][0], f.x[e][1]);
   }
-  f.stored[0] = reinterpret_cast<const uint16_t*>(P.ks)[f.tix];
-  f.stored[1] = reinterpret_cast<const uint16_t*>(P.vs)[f.tix];
+  if constexpr (KV == KV_I8_BLK) {
+    f.stored[0] = reinterpret_cast<const uint16_t*>(P.ks)[f.tix];
+    f.stored[1] = reinterpret_cast<const uint16_t*>(P.vs)[f.tix];
+  }
 }
 
 DEV int byte_at(uint32_t w, int k) { return (int)(int8_t)(uint8_t)(w >> (8 * k)); }
@@ -929,10 +932,22 @@ DEV float fold_finish_one(FoldIn& f, const DecodeParams& P) {
 // The rule, the stores, and the block's new scales in bw. One run per block and
 // call, as in append_blk: a second sequence whose new token lands in the same
 // block (claimed in this call) is reported.
-template <int D>
+template <int KV, int D>
 DEV void fold_finish(FoldIn& f, const DecodeParams& P, BlockIds& bw, int nblk, int s) {
   if (!f.on) return;
   const int lane = lane_id();
+  if constexpr (KV == KV_F16) {  // the new rows rounded to fp16 (RNE), as vk_append_kv1 stores them
+    const int d0 = 2 * lane;
+    if (d0 < D) {
+      uint8_t* kt = const_cast<uint8_t*>(P.kc) + f.tix * P.tile_bytes;
+      uint8_t* vt = const_cast<uint8_t*>(P.vc) + f.tix * P.tile_bytes;
+      *reinterpret_cast<uint16_t*>(kt + tile_elem<false>(f.o, d0, 2, D)) = f2h(f.x[0][0]);
+      *reinterpret_cast<uint16_t*>(kt + tile_elem<false>(f.o, d0 + 1, 2, D)) = f2h(f.x[0][1]);
+      *reinterpret_cast<uint16_t*>(vt + tile_elem<true>(f.o, d0, 2, D)) = f2h(f.x[1][0]);
+      *reinterpret_cast<uint16_t*>(vt + tile_elem<true>(f.o, d0 + 1, 2, D)) = f2h(f.x[1][1]);
+    }
+    return;
+  }
   if (P.claim && lane == 0 && f.tix % P.n_kv_heads == 0) {
     const unsigned long long me = ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s;
     if ((uint32_t)(f.claim_old >> 32) == P.fold_epoch && f.claim_old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
@@ -1008,7 +1023,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   // vk_append_decode with the append folded in: this piece holds the last token
   // and appends it (after the first stage's loads and q, unless the block is in
   // the first stage)
-  static_assert(!FOLD || (BLK && !TREE), "the folded append is the I8_BLK decode's");
+  static_assert(!FOLD || ((BLK || KV == KV_F16) && !TREE), "the folded append is the I8_BLK and fp16 decode's");
   // vk_append_decode with the append folded in: this piece holds the last token.
   // Its block in the first stage: append before any tile load; otherwise issue
   // the append's loads now and finish it after q, while the first stage is in
@@ -1018,8 +1033,8 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   const bool fold_first = fold && nblk <= CH;
   FoldIn fin;
   if constexpr (FOLD) {
-    if (fold) fold_issue<D>(fin, P, bw, nblk, s, kvh, ctx_c);
-    if (fold_first) fold_finish<D>(fin, P, bw, nblk, s);
+    if (fold) fold_issue<KV, D>(fin, P, bw, nblk, s, kvh, ctx_c);
+    if (fold_first) fold_finish<KV, D>(fin, P, bw, nblk, s);
   }
 
   MStage<KV, D> sa, sb;
@@ -1078,7 +1093,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     }
   }
   if constexpr (FOLD) {
-    if (fold && !fold_first) fold_finish<D>(fin, P, bw, nblk, s);
+    if (fold && !fold_first) fold_finish<KV, D>(fin, P, bw, nblk, s);
   }
 
   float M[RT], lrun[RT], psum[RT];   // state of row n (each lane holds a quarter of the row's sums)
@@ -1700,11 +1715,11 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
     int o0, o1;
     sk_piece(seg0, nb, pen, x, c1, &o0, &o1);
     if (o0 < o1) {
-      // under vk_append_decode (I8_BLK) the piece that ends at the context's last
-      // token appends the new token first (fold_issue, fold_finish): no other
-      // piece of the launch reads that block
+      // under vk_append_decode (I8_BLK and fp16 pools) the piece that ends at the
+      // context's last token appends the new token first (fold_issue,
+      // fold_finish): no other piece of the launch reads that block
       const int slot = o0 > 0 ? 0 : 1;
-      attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s,
+      attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK || KV == KV_F16>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s,
                                                             o0 == 0 && o1 == nb,
                                                             ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc,
                                                             P.part_ml);
