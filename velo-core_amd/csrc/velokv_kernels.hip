@@ -823,7 +823,8 @@ DEV void blk_put(int (&cd)[BS][2], int o, float& s_old, uint16_t& s_bits, float 
   s_old = s_new;
 }
 
-// ---- the append of vk_append_decode inside the decode launch (I8_BLK) --------
+// ---- the append of vk_append_decode inside the decode launch (I8_BLK; fp16
+// pools under stream-K store the new rows as they are, fold_finish) ----------
 // The piece that holds a sequence's last context token (position ctx - 1)
 // appends the sequence's new K and V rows there before it loads that block: the
 // rule of append_blk_run for a run of one token at offset o = (ctx - 1) % 16
