@@ -132,10 +132,9 @@ def append_bytes(kv: int, S: int, Hkv: int, hd: int = HD) -> int:
 
 def measured_traffic(kernel: str, S: int, L: int, H: int, Hkv: int, ragged: bool):
     """HBM bytes per launch of `kernel` on this workload from the committed PMC
-    summary (profiles/*.md lines 'traffic <kernel> S=..,L=..,H=..,Hkv=.. <bytes>'), or None."""
-    if ragged:
-        return None
-    key = f"S={S},L={L},H={H},Hkv={Hkv}"
+    summary (profiles/*.md lines 'traffic <kernel> S=..,L=..,H=..,Hkv=.. <bytes>'), or None.
+    Ragged workloads (L = U[1024, ctx], lengths from seed 2024) have keys of their own."""
+    key = f"S={S},L={'U[1024,%d]' % L if ragged else L},H={H},Hkv={Hkv}"
     pdir = os.path.join(ROOT, "profiles")
     for fn in sorted(os.listdir(pdir)) if os.path.isdir(pdir) else []:
         if not fn.endswith(".md"):
