@@ -40,9 +40,11 @@
  *              token t at byte (4t + c)*16 of the tile, dims 32c+16..32c+31 at
  *              1024 + (4t + c)*16)
  *    V codes   [n_tiles][n_kv_heads][8][128][2]   (token pairs interleaved)
- *    K scales  I8_BLK: fp16 [n_tiles][n_kv_heads] (one scale per 16 tokens and
- *              head); I8_REF: fp32 [n_tiles][n_kv_heads][16]
- *    V scales  same as K scales
+ *    scales    I8_BLK: fp16 pairs [n_tiles][n_kv_heads][2] (one K and one V
+ *              scale per 16 tokens and head, K first: a (tile, head)'s two
+ *              scales are one 4-byte word);
+ *              I8_REF: fp32 [n_tiles][n_kv_heads][16] for K, then the same
+ *              array for V
  * n_tiles = n_blocks * block_size / 16. A head_dim-64 pool has 64-dim tiles in
  * the same layouts at D = 64: [16][64] K, [8][64][2] V, and int8 K as
  * [2][16][2][16] (dims 32c..32c+15 of token t at byte (2t + c)*16, dims
@@ -108,6 +110,23 @@ int vk_ctx_create(int device, const char* code_object_path, vk_ctx** out);
 int vk_ctx_destroy(vk_ctx* ctx);
 /* Name of the GPU architecture the context runs on (e.g. "gfx950"). */
 int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap);
+
+/* No reference counterpart (the Metal encoder reports a bad threadgroup size
+ * itself). Checks a workgroup of `threads` threads against what `kernel` was
+ * compiled for (its __launch_bounds__, read once per kernel at vk_ctx_create)
+ * without launching anything: VK_OK, VK_ERR_BAD_ARG naming the kernel and its
+ * limit, or VK_ERR_NOT_WIRED for an unknown kernel. *max_threads (optional)
+ * receives the limit (0 if unknown). Every launch of the library runs this
+ * check first, so a wrong workgroup size is an error, not a device fault. */
+int vk_kernel_launch_check(const vk_ctx* ctx, const char* kernel, int32_t threads, int32_t* max_threads);
+
+/* No reference counterpart. Size in bytes the context's own split-K workspace
+ * grows to when it holds `cur` bytes and a call needs `need` (callers that pass
+ * no workspace): max(need, 2 * cur), 256-byte aligned; `cur` when need <= cur.
+ * Outgrown buffers are kept until vk_ctx_destroy (a call on another host thread
+ * may still have work queued on one), and doubling keeps their sum below the
+ * live buffer's size. */
+uint64_t vk_workspace_grow_bytes(uint64_t cur, uint64_t need);
 
 /* Misuse the kernels detect without trapping. The work still completes on the
  * clamped input, a flag is or-ed into the context's device error word, and the
@@ -183,12 +202,17 @@ typedef struct vk_pool_desc {
 } vk_pool_desc;
 
 /* Device addresses of one layer, for callers that read or write the pool
- * directly (tests, KV migration). */
+ * directly (tests, KV migration). Scales are read in 16-bit units: unit e of
+ * the K (V) scales is at k_scales (v_scales) + e * scale_step. VK_KV_I8_REF:
+ * scale_step 2, each kind contiguous. VK_KV_I8_BLK: scale_step 4, the K and V
+ * scale of one (block, head) share a 4-byte word (K low, V high: v_scales =
+ * k_scales + 2), so a decode fetches both with one load. */
 typedef struct vk_layer_view {
   void* k_codes;  void* v_codes;
   void* k_scales; void* v_scales;   /* NULL for F32 / F16 */
   uint64_t codes_bytes;             /* bytes of each of k_codes / v_codes  */
-  uint64_t scales_bytes;            /* bytes of each of k_scales / v_scales */
+  uint64_t scales_bytes;            /* bytes of each kind's scales (units x 2) */
+  uint32_t scale_step;              /* bytes between a kind's 16-bit scale units: 2, 4 (I8_BLK), 0 */
 } vk_layer_view;
 
 /* Allocate and zero the K and V pools of all layers plus the slot block table

@@ -161,3 +161,31 @@ def test_decode_workspace_query_needs_no_gpu_for_validation():
     lib = _capi.lib()
     n = C.c_uint64()
     assert lib.vk_paged_decode_workspace(None, None, C.byref(n)) == velokv.ERR_BAD_ARG
+
+
+def test_workspace_growth_keeps_retired_buffers_below_the_live_one():
+    """The context's own split-K workspace grows at least geometrically, so the
+    outgrown buffers it keeps until vk_ctx_destroy sum to less than the live
+    one. Needs as stream-K plans them when max_context_len grows 16 tokens at a
+    time past the point where the workers outnumber the resident waves
+    (S=64, Hkv=8, G=4: ceil(units / 256) workers, 2 partial rows of G per worker)."""
+    grow = _capi.lib().vk_workspace_grow_bytes
+    assert grow(0, 1000) == 1024
+    assert grow(4096, 100) == 4096
+    assert grow(4096, 5000) == 8192
+    assert grow(4096, 9000) == 9216
+    S, Hkv, G, pen = 64, 8, 4, 8
+    cur, retired, allocs = 0, 0, 0
+    for L in range(16384, 32769, 16):
+        units = S * Hkv * (L // 16 + pen)
+        nw = max(2048, -(-units // 256))
+        prow = nw * 2 * G
+        need = -(-prow * 128 * 4 // 256) * 256 + -(-prow * 2 * 4 // 256) * 256 + -(-(S + 1) * 4 // 256) * 256
+        nxt = grow(cur, need)
+        assert nxt >= need
+        if nxt != cur:
+            retired += cur
+            cur = nxt
+            allocs += 1
+    assert retired < cur
+    assert allocs <= 4  # 1025 growing calls, a handful of allocations

@@ -119,6 +119,10 @@ struct vk_ctx {
   std::string arch;
   hipModule_t module = nullptr;
   std::unordered_map<std::string, hipFunction_t> fns;
+  // threads per workgroup each kernel was compiled for (__launch_bounds__), read
+  // once at vk_ctx_create: a launch with more faults the device, so launch()
+  // refuses it
+  std::unordered_map<std::string, int> max_threads;
   std::mutex ws_mu;
   void* ws = nullptr;
   uint64_t ws_bytes = 0;
@@ -213,10 +217,23 @@ int set_device(const vk_ctx* ctx) {
   return VK_OK;
 }
 
+// A workgroup shape the kernel was compiled for: at least one thread and at most
+// its __launch_bounds__ (HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK).
+int check_launch_shape(const vk_ctx* ctx, const char* name, uint64_t threads) {
+  auto it = ctx->max_threads.find(name);
+  if (it == ctx->max_threads.end()) return fail(VK_ERR_NOT_WIRED, "kernel %s is not in the code object", name);
+  if (threads == 0 || threads > (uint64_t)it->second)
+    return fail(VK_ERR_BAD_ARG, "kernel %s launched with %llu threads per workgroup; it was compiled for at most %d",
+                name, (unsigned long long)threads, it->second);
+  return VK_OK;
+}
+
 template <typename P>
 int launch(const vk_ctx* ctx, const char* name, dim3 grid, dim3 block, const P& params, void* stream) {
   hipFunction_t f = ctx->fn(name);
   if (!f) return fail(VK_ERR_NOT_WIRED, "kernel %s is not in the code object", name);
+  int rc = check_launch_shape(ctx, name, (uint64_t)block.x * block.y * block.z);
+  if (rc) return rc;
   void* args[] = {const_cast<P*>(&params)};
   HIP_TRY(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0,
                                 reinterpret_cast<hipStream_t>(stream), args, nullptr));
@@ -322,7 +339,15 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       delete ctx;
       return fail(VK_ERR_NOT_WIRED, "kernel %s missing from %s: %s", nm.c_str(), path.c_str(), hipGetErrorString(e));
     }
+    int max_threads = 0;
+    e = hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, f);
+    if (e != hipSuccess || max_threads <= 0) {
+      hipModuleUnload(ctx->module);
+      delete ctx;
+      return fail(VK_ERR_NOT_WIRED, "workgroup limit of kernel %s unreadable: %s", nm.c_str(), hipGetErrorString(e));
+    }
     ctx->fns[nm] = f;
+    ctx->max_threads[nm] = max_threads;
   }
   e = hipMalloc(reinterpret_cast<void**>(&ctx->err_word), 256);
   if (e == hipSuccess) e = hipMemset(ctx->err_word, 0, 256);
@@ -378,6 +403,13 @@ extern "C" int vk_ctx_arch(const vk_ctx* ctx, char* buf, size_t cap) {
   return VK_OK;
 }
 
+extern "C" int vk_kernel_launch_check(const vk_ctx* ctx, const char* kernel, int32_t threads, int32_t* max_threads) {
+  if (!ctx || !kernel) return fail(VK_ERR_BAD_ARG, "null argument");
+  auto it = ctx->max_threads.find(kernel);
+  if (max_threads) *max_threads = it == ctx->max_threads.end() ? 0 : it->second;
+  return check_launch_shape(ctx, kernel, threads < 0 ? 0 : (uint64_t)threads);
+}
+
 // ============================================================================
 // pools
 // ============================================================================
@@ -421,8 +453,16 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
   g.k_off = 0;
   g.v_off = align_up(codes, 256);
   g.ks_off = g.v_off + align_up(codes, 256);
-  g.vs_off = g.ks_off + align_up(scales, 256);
-  g.layer_stride = g.vs_off + align_up(scales, 256);
+  if (d->kv_type == VK_KV_I8_BLK) {
+    // one array of (K, V) scale words: V is the high half of each word
+    g.s_step = kBlkScaleStep;
+    g.vs_off = g.ks_off + 2;
+    g.layer_stride = g.ks_off + align_up(2 * scales, 256);
+  } else {
+    g.s_step = scales ? 2 : 0;
+    g.vs_off = g.ks_off + align_up(scales, 256);
+    g.layer_stride = g.vs_off + align_up(scales, 256);
+  }
   p->bytes = g.layer_stride * (uint64_t)d->n_layer;
   int rc = set_device(ctx);
   if (rc) { delete p; return rc; }
@@ -481,6 +521,7 @@ extern "C" int vk_pool_layer_view(const vk_pool* pool, int32_t layer, vk_layer_v
   out->scales_bytes = (uint64_t)g.n_blocks * g.n_kv_heads * g.stile_bytes;
   out->k_scales = g.stile_bytes ? L + g.ks_off : nullptr;
   out->v_scales = g.stile_bytes ? L + g.vs_off : nullptr;
+  out->scale_step = g.s_step;
   return VK_OK;
 }
 
@@ -636,6 +677,16 @@ extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q
                 stream);
 }
 
+// Size the context's own split-K workspace grows to when it holds `cur` bytes
+// and a call needs `need`: at least twice `cur`, so that the buffers it retires
+// (kept until vk_ctx_destroy) always sum to less than the live one, however
+// slowly the calls' needs grow.
+extern "C" uint64_t vk_workspace_grow_bytes(uint64_t cur, uint64_t need) {
+  if (need <= cur) return cur;
+  const uint64_t twice = cur > UINT64_MAX / 2 ? UINT64_MAX : 2 * cur;
+  return align_up(std::max(need, twice), 256);
+}
+
 namespace {
 
 // Split-K workspace: the caller's buffer when given (and large enough), else the
@@ -651,11 +702,12 @@ int split_workspace(vk_ctx* ctx, void* given, uint64_t given_bytes, uint64_t nee
   std::lock_guard<std::mutex> lk(ctx->ws_mu);
   if (ctx->ws_bytes < need) {
     // never freed here: work queued by another thread may still use the old one
+    const uint64_t bytes = vk_workspace_grow_bytes(ctx->ws_bytes, need);
     void* grown = nullptr;
-    HIP_TRY(hipMalloc(&grown, need));
+    HIP_TRY(hipMalloc(&grown, bytes));
     if (ctx->ws) ctx->ws_retired.push_back(ctx->ws);
     ctx->ws = grown;
-    ctx->ws_bytes = need;
+    ctx->ws_bytes = bytes;
   }
   *out = reinterpret_cast<uint8_t*>(ctx->ws);
   return VK_OK;

@@ -226,9 +226,11 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
       bad |= out;
       w.oob |= out ? 1u << k : 0u;
       w.b[k] = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
-      if constexpr (BLK) {
-        w.ks[k] = h2f(reinterpret_cast<const uint16_t*>(P.ks)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
-        w.vs[k] = h2f(reinterpret_cast<const uint16_t*>(P.vs)[(int64_t)w.b[k] * P.n_kv_heads + kvh]);
+      if constexpr (BLK) {  // the (K, V) scale word of the (block, head): one load
+        const uint32_t sw =
+            *reinterpret_cast<const uint32_t*>(P.ks + ((int64_t)w.b[k] * P.n_kv_heads + kvh) * kBlkScaleStep);
+        w.ks[k] = h2f((uint16_t)(sw & 0xFFFFu));
+        w.vs[k] = h2f((uint16_t)(sw >> 16));
       }
     }
   }
@@ -272,6 +274,15 @@ DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   void* u = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
   return __builtin_amdgcn_make_buffer_rsrc(u, 0, (int)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
 }
+// A stage past the end of a piece (the pipeline issues one or two) or a block
+// past the piece in a partly used stage takes a descriptor of zero bytes: its
+// loads are issued as usual (the same instructions and wait counts on every
+// path, so the pipeline keeps its loads in flight; a branch around them made the
+// compiler wait for every outstanding load at the join) but are out of range,
+// return zeros and move no bytes. Clamping them to the last block instead
+// re-read up to four tiles per piece, 1.8 % of a ragged call's HBM traffic.
+DEV uint32_t stage_bytes(int i, int nblk, uint32_t bytes) { return i < nblk ? bytes : 0u; }
+
 // Cache policy of tile loads: V is streamed non-temporally. K rows are split
 // over several load instructions (each covers a half (int8) or a quarter (fp16)
 // of every 128-byte line of the tile), so K stays in the normal L2 policy unless
@@ -297,8 +308,8 @@ DEV DW<N> buf_load(rsrc_t r, uint32_t off) {
   return out;
 }
 
-// Issue the loads of batch `b` (blocks b*CH .. b*CH+CH-1 of the unit, clamped to
-// the last block so the tail needs no branch).
+// Issue the loads of batch `b` (blocks b*CH .. b*CH+CH-1 of the unit; blocks past
+// the unit load zeros through zero-size descriptors, so the tail needs no branch).
 template <int KV>
 DEV void stage_load(Stage<KV>& st, const DecodeParams& P, const BlockIds& bw, int b, int nblk, int kvh, int t) {
   constexpr int ESZ = Esz<KV>::v;
@@ -309,8 +320,9 @@ DEV void stage_load(Stage<KV>& st, const DecodeParams& P, const BlockIds& bw, in
     const int i = min(b * CH + u, nblk - 1);
     const int blk = window_at(bw.b, i);
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
-    const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
-    const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+    const uint32_t tb = stage_bytes(b * CH + u, nblk, P.tile_bytes);
+    const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, tb);
+    const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, tb);
     if constexpr (ESZ == 1) {  // lane 4t + c: pieces at 16 lane and 1024 + 16 lane (int8 K layout)
       const DW<4> lo = buf_load<4, k_aux<ESZ>()>(kr, lane * 16);
       const DW<4> hi = buf_load<4, k_aux<ESZ>()>(kr, 1024 + lane * 16);
@@ -322,8 +334,9 @@ DEV void stage_load(Stage<KV>& st, const DecodeParams& P, const BlockIds& bw, in
 #pragma unroll
     for (int j = 0; j < 8; ++j) st.v[u][j] = buf_load<ESZ>(vr, j * (HD * 2 * ESZ) + lane * (4 * ESZ));
     if constexpr (KV == KV_I8_REF) {
-      const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
-      const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
+      const uint32_t sb = stage_bytes(b * CH + u, nblk, P.stile_bytes);
+      const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, sb);
+      const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, sb);
       st.ks[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(sr, t * 4, 0, 0));
       st.vs[u] = bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(svr, t * 4, 0, 0));
     }
@@ -724,8 +737,9 @@ DEV void mstage_load(MStage<KV, DK>& st, const DecodeParams& P, const BlockIds& 
     const int i = min(b * CH + u, nblk - 1);
     const int blk = window_at(bw.b, i);
     const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
-    const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
-    const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+    const uint32_t tb = stage_bytes(b * CH + u, nblk, P.tile_bytes);
+    const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, tb);
+    const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, tb);
     if constexpr (DK == 64) {
       // K dims 16g..16g+15 of token n: int8 half g & 1 of 32-dim chunk g >> 1
       // (byte 8 D h + (n D/32 + c) 16), fp16 32 contiguous bytes; V dims
@@ -749,8 +763,9 @@ DEV void mstage_load(MStage<KV, DK>& st, const DecodeParams& P, const BlockIds& 
       for (int r = 0; r < 2; ++r) st.v[u][r] = buf_load<4 * ESZ>(vr, ((2 * g + r) * D * 2 + 16 * nv) * ESZ);
     }
     if constexpr (KV == KV_I8_REF) {
-      const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, P.stile_bytes);
-      const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, P.stile_bytes);
+      const uint32_t sb = stage_bytes(b * CH + u, nblk, P.stile_bytes);
+      const rsrc_t sr = make_rsrc(P.ks + tix * P.stile_bytes, sb);
+      const rsrc_t svr = make_rsrc(P.vs + tix * P.stile_bytes, sb);
       st.ks[u] = bitcast<float4>(__builtin_amdgcn_raw_buffer_load_b128(sr, g * 16, 0, 0));
       st.vs[u] = bitcast<float4>(__builtin_amdgcn_raw_buffer_load_b128(svr, g * 16, 0, 0));
     }
@@ -869,8 +884,9 @@ DEV void fold_issue(FoldIn& f, const DecodeParams& P, const BlockIds& bw, int nb
     if (d0 < P.io_hd) load_x2(e ? P.fold_v : P.fold_k, P.fold_dtype, row, f.x[e][0], f.x[e][1]);
   }
   if constexpr (KV == KV_I8_BLK) {
-    f.stored[0] = reinterpret_cast<const uint16_t*>(P.ks)[f.tix];
-    f.stored[1] = reinterpret_cast<const uint16_t*>(P.vs)[f.tix];
+    const uint32_t sw = *reinterpret_cast<const uint32_t*>(P.ks + f.tix * kBlkScaleStep);
+    f.stored[0] = (uint16_t)(sw & 0xFFFFu);
+    f.stored[1] = (uint16_t)(sw >> 16);
   }
 }
 
@@ -926,7 +942,8 @@ DEV float fold_finish_one(FoldIn& f, const DecodeParams& P) {
       tile[tile_elem<true>(o, da + 1, 1, D)] = (uint8_t)c1;
     }
   }
-  if (lane_id() == 0) reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(IS_V ? P.vs : P.ks))[f.tix] = s_bits;
+  if (lane_id() == 0)
+    *reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(IS_V ? P.vs : P.ks) + f.tix * kBlkScaleStep) = s_bits;
   return s_new;
 }
 
@@ -1374,8 +1391,9 @@ DEV void f32_stage_load(F32Stage& st, const DecodeParams& P, const BlockIds& bw,
                         int g) {
   const int blk = window_at(bw.b, min(i, nblk - 1));
   const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
-  const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, P.tile_bytes);
-  const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, P.tile_bytes);
+  const uint32_t tb = stage_bytes(i, nblk, P.tile_bytes);
+  const rsrc_t kr = make_rsrc(P.kc + tix * P.tile_bytes, tb);
+  const rsrc_t vr = make_rsrc(P.vc + tix * P.tile_bytes, tb);
   // K dims 16 j + 4 g .. + 3 of token n at 4 (n D + 16 j + 4 g); V dim 16 t + n of
   // token pair 2 g + r at 8 ((2 g + r) D + 16 t + n). A 64-dim tile: dims 64 and
   // up (j, t >= 4) read the bytes of the dims 64 below (they meet zero q dims and
@@ -2005,9 +2023,10 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       const int b = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
       const uint32_t tix = (uint32_t)b * (uint32_t)P.n_kv_heads + (uint32_t)kvh;
       pid[i] = tix;
-      if constexpr (I8) {
-        pks[i] = P.scale_log2 * h2f(reinterpret_cast<const uint16_t*>(P.ks)[tix]);
-        pvs[i] = reinterpret_cast<const uint16_t*>(P.vs)[tix];
+      if constexpr (I8) {  // the (K, V) scale word of the (page, head)
+        const uint32_t sw = *reinterpret_cast<const uint32_t*>(P.ks + (uint64_t)tix * kBlkScaleStep);
+        pks[i] = P.scale_log2 * h2f((uint16_t)(sw & 0xFFFFu));
+        pvs[i] = (uint16_t)(sw >> 16);
       }
     }
     if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) flag_misuse(P.err, MISUSE_PAGE_OUT_OF_POOL);
@@ -2512,7 +2531,7 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
   if (b >= P.g.n_blocks) return;
   const int Hkv = P.g.n_kv_heads;
   uint8_t* tile = codes + ((uint64_t)b * Hkv + h) * P.g.tile_bytes;
-  uint16_t* sp = scales + (uint64_t)b * Hkv + h;
+  uint16_t* sp = scales + ((uint64_t)b * Hkv + h) * (kBlkScaleStep / 2);
   const int d0 = 2 * lane;
   // lanes past the row (2 lane >= D) read the codes of the dims D below and never
   // write them back; their new-token values are zero, so the absmax is the row's
@@ -2766,16 +2785,17 @@ __device__ void copy_blocks_kernel(const CopyParams& P) {
   const int src = P.pairs[2 * pi], dst = P.pairs[2 * pi + 1];
   uint8_t* L = P.base + (uint64_t)layer * P.g.layer_stride;
   const uint64_t cb = (uint64_t)P.g.n_kv_heads * P.g.tile_bytes;   // codes per block
-  const uint64_t sb = (uint64_t)P.g.n_kv_heads * P.g.stile_bytes;  // scale bytes per block
+  const uint64_t sb = (uint64_t)P.g.n_kv_heads * P.g.stile_bytes;  // scale bytes per block, K or V
   const uint8_t* cs = L + (is_v ? P.g.v_off : P.g.k_off) + (uint64_t)src * cb;
   uint8_t* cdst = L + (is_v ? P.g.v_off : P.g.k_off) + (uint64_t)dst * cb;
   for (uint64_t i = threadIdx.x; i < cb / 16; i += blockDim.x)
     reinterpret_cast<uint4*>(cdst)[i] = reinterpret_cast<const uint4*>(cs)[i];
-  if (sb) {
-    const uint8_t* ss = L + (is_v ? P.g.vs_off : P.g.ks_off) + (uint64_t)src * sb;
-    uint8_t* sd = L + (is_v ? P.g.vs_off : P.g.ks_off) + (uint64_t)dst * sb;
-    for (uint64_t i = threadIdx.x; i < sb / 2; i += blockDim.x)
-      reinterpret_cast<uint16_t*>(sd)[i] = reinterpret_cast<const uint16_t*>(ss)[i];
+  if (sb) {  // the block's sb / 2 16-bit scale units of this kind, s_step bytes apart
+    const uint64_t ne = sb / 2, st = P.g.s_step;
+    const uint8_t* ss = L + (is_v ? P.g.vs_off : P.g.ks_off) + (uint64_t)src * ne * st;
+    uint8_t* sd = L + (is_v ? P.g.vs_off : P.g.ks_off) + (uint64_t)dst * ne * st;
+    for (uint64_t i = threadIdx.x; i < ne; i += blockDim.x)
+      *reinterpret_cast<uint16_t*>(sd + i * st) = *reinterpret_cast<const uint16_t*>(ss + i * st);
   }
 }
 
@@ -2856,13 +2876,13 @@ __device__ void nixl_copy_kernel(const NixlParams& P) {
     u32x4* dst = reinterpret_cast<u32x4*>(P.unpack ? pt : wt);
     __builtin_nontemporal_store(__builtin_nontemporal_load(src), dst);
   }
-  if (sb && slice == 0) {
+  if (sb && slice == 0) {  // the record holds K's units, then V's, each kind contiguous
     uint16_t* ws = reinterpret_cast<uint16_t*>(payload + (uint64_t)I.n_pages * P.n_layers * 2 * cb + (uint64_t)r * 2 * sb);
-    uint16_t* sk = reinterpret_cast<uint16_t*>(L + P.g.ks_off + (uint64_t)page * sb);
-    uint16_t* sv = reinterpret_cast<uint16_t*>(L + P.g.vs_off + (uint64_t)page * sb);
-    const uint32_t ne = (uint32_t)(sb / 2);
+    const uint32_t ne = (uint32_t)(sb / 2), st = P.g.s_step;  // units of one kind, bytes between them
+    uint8_t* sk = L + P.g.ks_off + (uint64_t)page * ne * st;
+    uint8_t* sv = L + P.g.vs_off + (uint64_t)page * ne * st;
     for (uint32_t e = threadIdx.x; e < 2 * ne; e += blockDim.x) {
-      uint16_t* pe = e < ne ? sk + e : sv + (e - ne);
+      uint16_t* pe = reinterpret_cast<uint16_t*>(e < ne ? sk + (uint64_t)e * st : sv + (uint64_t)(e - ne) * st);
       if (P.unpack) *pe = ws[e]; else ws[e] = *pe;
     }
   }
@@ -2928,7 +2948,8 @@ DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE 
           e[k][1] = t[off1];
         }
         sv[k] = 0.f;
-        if constexpr (KV == KV_I8_BLK) sv[k] = h2f(reinterpret_cast<const uint16_t*>(scales)[(uint64_t)blk * Hkv + h]);
+        if constexpr (KV == KV_I8_BLK)
+          sv[k] = h2f(*reinterpret_cast<const uint16_t*>(scales + ((uint64_t)blk * Hkv + h) * kBlkScaleStep));
         if constexpr (KV == KV_I8_REF) sv[k] = reinterpret_cast<const float*>(scales)[((uint64_t)blk * Hkv + h) * BS + q % BS];
       }
 #pragma unroll
@@ -2975,7 +2996,7 @@ DEV void commit_wave(const CommitParams& P, uint8_t (&raw)[kMaxCommit][2 * WAVE 
         uint8_t* t = codes + ((uint64_t)blk * Hkv + h) * P.g.tile_bytes;
         uint8_t* const lp0 = t + off0;
         uint8_t* const lp1 = t + off1;
-        uint16_t* sp = reinterpret_cast<uint16_t*>(scales) + (uint64_t)blk * Hkv + h;
+        uint16_t* sp = reinterpret_cast<uint16_t*>(scales + ((uint64_t)blk * Hkv + h) * kBlkScaleStep);
         int cd[BS][2];
 #pragma unroll
         for (int u = 0; u < BS; ++u) {

@@ -23,12 +23,20 @@ enum DType : int32_t { DT_F32 = 0, DT_F16 = 1 };
 // commit) has n_blocks = tiles and block_size = 16; the page view (COW copy,
 // NIXL) has n_blocks = pages, block_size = page tokens, page_shift = 0 and the
 // tile sizes of a whole page.
+// I8_BLK scales: the K and V scale (fp16) of one (block, head) share one 4-byte
+// word, K in the low half: entry (block b, head h) of a layer's scale array is
+// the word b * n_kv_heads + h, so that a decode wave fetches both with one load
+// (one 32-byte sector per (block, head) instead of two).
+constexpr uint32_t kBlkScaleStep = 4;
+
 struct PoolGeom {
   uint64_t layer_stride;   // bytes between layers
   uint64_t k_off, v_off;   // byte offsets of K / V codes inside a layer
   uint64_t ks_off, vs_off; // byte offsets of K / V scales inside a layer
   uint32_t tile_bytes;     // codes of one (block, head): block_size * head_dim * esz (head_dim = tile width)
   uint32_t stile_bytes;    // scales of one (block, head): 2 (I8_BLK, per 16 tokens), 4 per token (I8_REF), 0
+  uint32_t s_step;         // bytes from one 16-bit unit of a kind's (K or V) scales to its next: 2 for
+                           // I8_REF (contiguous), kBlkScaleStep for I8_BLK, 0 without scales
   int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
   int32_t page_shift;      // tile view: log2(page tokens / 16)
   int32_t io_hd;           // head_dim of the caller's K/V/q/out rows: any multiple of 8 up to

@@ -69,7 +69,8 @@ class PoolDesc(C.Structure):
 
 class LayerView(C.Structure):
     _fields_ = [("k_codes", C.c_void_p), ("v_codes", C.c_void_p), ("k_scales", C.c_void_p),
-                ("v_scales", C.c_void_p), ("codes_bytes", C.c_uint64), ("scales_bytes", C.c_uint64)]
+                ("v_scales", C.c_void_p), ("codes_bytes", C.c_uint64), ("scales_bytes", C.c_uint64),
+                ("scale_step", C.c_uint32)]
 
 
 class DecodeArgs(C.Structure):
@@ -114,6 +115,8 @@ PROTOTYPES = {
     "vk_ctx_create": [C.c_int, C.c_char_p, PP],
     "vk_ctx_destroy": [P],
     "vk_ctx_arch": [P, C.c_char_p, C.c_size_t],
+    "vk_kernel_launch_check": [P, C.c_char_p, I32, PI32],
+    "vk_workspace_grow_bytes": [U64, U64],
     "vk_ctx_set_decode_kernel": [P, C.c_int],
     "vk_ctx_set_decode_schedule": [P, C.c_int],
     "vk_pool_create": [P, C.POINTER(PoolDesc), PP],
@@ -177,6 +180,8 @@ PROTOTYPES = {
     "vk_event_elapsed_ms": [P, P, P, C.POINTER(C.c_float)],
     "vk_fill_normal_f16": [P, P, U64, U64, I32, C.c_float, P],
 }
+# entries that return something other than an int32 status
+RESTYPES = {"vk_workspace_grow_bytes": C.c_uint64}
 
 _lib = None
 
@@ -191,7 +196,7 @@ def lib():
         for name, argtypes in PROTOTYPES.items():
             fn = getattr(L, name)
             fn.argtypes = argtypes
-            fn.restype = C.c_int
+            fn.restype = RESTYPES.get(name, C.c_int)
         L.vk_last_error.argtypes = []
         L.vk_last_error.restype = C.c_char_p
         _lib = L

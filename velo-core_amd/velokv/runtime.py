@@ -172,6 +172,13 @@ class Context:
                 "n_workers": p.n_workers, "max_blocks_per_wave": p.max_blocks_per_wave,
                 "workspace_bytes": p.workspace_bytes, "merge_launch": bool(p.merge_launch)}
 
+    def launch_check(self, kernel: str, threads: int) -> int:
+        """vk_kernel_launch_check: the kernel's workgroup limit; raises VkError when
+        `threads` exceeds it (nothing is launched)."""
+        mx = C.c_int32()
+        check(lib().vk_kernel_launch_check(self.h, kernel.encode(), threads, C.byref(mx)))
+        return mx.value
+
     def decode_workspace_bytes(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0,
                                partition_tokens=0, q_dtype=DT_F16, sum_context_len=0) -> int:
         a = _capi.DecodeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None,
@@ -415,21 +422,45 @@ class Pool:
         check(lib().vk_bind_slot(self.h, slot, arr.ctypes.data_as(C.POINTER(C.c_uint32)), len(arr)))
 
     def download_layer(self, layer: int) -> dict:
-        """Raw bytes of one layer: k, v codes and ks, vs scales (None if absent)."""
+        """Raw bytes of one layer: k, v codes and ks, vs scales (None if absent),
+        each kind's scales as one contiguous array (I8_BLK pools interleave the K
+        and V scale of a (block, head) in one word; they are split here)."""
         v = self.layer_view(layer)
         def dl(ptr, n):
             if not ptr or n == 0:
                 return None
             b = DeviceBuffer(self.ctx, n, ptr=ptr, owned=False)
             return b.download((n,), np.uint8)
-        return {"k": dl(v.k_codes, v.codes_bytes), "v": dl(v.v_codes, v.codes_bytes),
-                "ks": dl(v.k_scales, v.scales_bytes), "vs": dl(v.v_scales, v.scales_bytes)}
+        out = {"k": dl(v.k_codes, v.codes_bytes), "v": dl(v.v_codes, v.codes_bytes)}
+        if v.k_scales and v.scale_step == 4:
+            w = dl(v.k_scales, 2 * v.scales_bytes).view(np.uint16).reshape(-1, 2)
+            out["ks"] = np.ascontiguousarray(w[:, 0]).view(np.uint8)
+            out["vs"] = np.ascontiguousarray(w[:, 1]).view(np.uint8)
+        else:
+            out["ks"], out["vs"] = dl(v.k_scales, v.scales_bytes), dl(v.v_scales, v.scales_bytes)
+        return out
 
     def upload_layer(self, layer: int, parts: dict):
+        """Write parts of one layer given as download_layer returns them."""
         v = self.layer_view(layer)
-        for key, ptr, n in (("k", v.k_codes, v.codes_bytes), ("v", v.v_codes, v.codes_bytes),
-                            ("ks", v.k_scales, v.scales_bytes), ("vs", v.v_scales, v.scales_bytes)):
+        for key, ptr, n in (("k", v.k_codes, v.codes_bytes), ("v", v.v_codes, v.codes_bytes)):
             if parts.get(key) is not None and ptr:
+                a = np.ascontiguousarray(parts[key]).view(np.uint8).reshape(-1)
+                assert a.nbytes == n, (key, a.nbytes, n)
+                DeviceBuffer(self.ctx, n, ptr=ptr, owned=False).upload(a)
+        if not v.k_scales or (parts.get("ks") is None and parts.get("vs") is None):
+            return
+        n = v.scales_bytes
+        if v.scale_step == 4:  # interleaved (K, V) words: keep the half not given
+            cur = self.download_layer(layer)
+            ks = np.ascontiguousarray(parts["ks"] if parts.get("ks") is not None else cur["ks"]).view(np.uint8)
+            vs = np.ascontiguousarray(parts["vs"] if parts.get("vs") is not None else cur["vs"]).view(np.uint8)
+            assert ks.nbytes == n and vs.nbytes == n, (ks.nbytes, vs.nbytes, n)
+            w = np.stack([ks.reshape(-1).view(np.uint16), vs.reshape(-1).view(np.uint16)], 1)
+            DeviceBuffer(self.ctx, 2 * n, ptr=v.k_scales, owned=False).upload(np.ascontiguousarray(w).view(np.uint8))
+            return
+        for key, ptr in (("ks", v.k_scales), ("vs", v.v_scales)):
+            if parts.get(key) is not None:
                 a = np.ascontiguousarray(parts[key]).view(np.uint8).reshape(-1)
                 assert a.nbytes == n, (key, a.nbytes, n)
                 DeviceBuffer(self.ctx, n, ptr=ptr, owned=False).upload(a)
