@@ -108,19 +108,21 @@ def parse():
 
 
 def decode_bytes(kv: int, S: int, H: int, Hkv: int, lens: np.ndarray, bt_stride: int, q_esz: int = 2,
-                 hd: int = HD) -> int:
+                 hd: int = HD, page: int = BS) -> int:
     """Algorithmic HBM bytes of one decode call: each K/V element of every context
-    token read once, its scales, q, the output and the block-table entries used
-    (hd = the pool's head_dim)."""
+    token read once, its scales (one per 16-token tile and head for INT8 BLK), q,
+    the output and the block-table entries used (one per page of `page` tokens;
+    hd = the pool's head_dim)."""
     tok = int(lens.sum())
     blocks = int(sum(-(-int(L) // BS) for L in lens))
+    pages = int(sum(-(-int(L) // page) for L in lens))
     esz = {velokv.KV_F16: 2, velokv.KV_I8_BLK: 1, velokv.KV_I8_REF: 1, velokv.KV_F32: 4}[kv]
     kvb = 2 * tok * Hkv * hd * esz
     if kv == velokv.KV_I8_BLK:
         kvb += 2 * blocks * Hkv * 2
     elif kv == velokv.KV_I8_REF:
         kvb += 2 * tok * Hkv * 4
-    return kvb + S * H * hd * q_esz + S * H * hd * 4 + blocks * 4 + S * 4
+    return kvb + S * H * hd * q_esz + S * H * hd * 4 + pages * 4 + S * 4
 
 
 def append_bytes(kv: int, S: int, Hkv: int, hd: int = HD) -> int:
@@ -179,13 +181,15 @@ def run_gpu(ctx, args, kv_name: str):
     bt = synth.scatter_block_tables(n_pages, pages, seed=11, stride=-(-L // PG))
     pool = velokv.Pool(ctx, NL, n_pages, PG, Hkv, D, kv)
 
-    # ---- fill the pool: prefill tokens 0 .. L-2 of every sequence, per layer ----
-    n_pre = int((lens - 1).sum())
-    rows = np.repeat(np.arange(S), lens - 1)
-    pos = np.concatenate([np.arange(int(x) - 1) for x in lens])
+    # ---- fill the pool: tokens 0 .. base-1 of every sequence, per layer, base the
+    # first position of the sequence's last 16-token block ----
+    base = (BS * ((lens.astype(np.int64) - 1) // BS)).astype(np.int32)
+    n_pre = int(base.sum())
+    rows = np.repeat(np.arange(S), base)
+    pos = np.concatenate([np.arange(int(x)) for x in base])
     pre_slots = ctx.upload(synth.slots_for_positions(bt, pos, PG, rows))
-    kbuf = ctx.alloc(n_pre * Hkv * D * 2)
-    vbuf = ctx.alloc(n_pre * Hkv * D * 2)
+    kbuf = ctx.alloc(max(1, n_pre) * Hkv * D * 2)
+    vbuf = ctx.alloc(max(1, n_pre) * Hkv * D * 2)
     outlier = 8.0 if kv in (velokv.KV_I8_BLK, velokv.KV_I8_REF) else 1.0
     for layer in range(NL):
         ctx.fill_normal_f16(kbuf, n_pre * Hkv * D, 1000 + 2 * layer, Hkv * D, outlier)
@@ -195,8 +199,18 @@ def run_gpu(ctx, args, kv_name: str):
     kbuf.free()
     vbuf.free()
 
-    # ---- per-step inputs, rotated over R sets so consecutive steps differ ----
+    # ---- per-step inputs ----
+    # Step i appends every sequence's new token at offset o = i % 16 of its last
+    # block (position base + o, context base + o + 1), so consecutive steps walk
+    # the block as a real decode does: the int8 block scale restarts at offset 0
+    # and grows (requantizing the earlier codes) whenever a new row's absmax needs
+    # it. New rows, q and K/V come from R input sets rotated per step.
     R = 4
+    W = BS
+    walk_lens = [base + o + 1 for o in range(W)]
+    d_walk = [ctx.upload(x.astype(np.int32)) for x in walk_lens]
+    walk_slots = [ctx.upload(synth.slots_for_positions(bt, (base + o).astype(np.int64), PG)) for o in range(W)]
+    walk_max = int((base + W).max())
     new_slots = ctx.upload(synth.slots_for_positions(bt, lens.astype(np.int64) - 1, PG))
     qs, ks, vs = [], [], []
     qdt = velokv.DT_F32 if args.q_dtype == "fp32" else velokv.DT_F16
@@ -217,17 +231,19 @@ def run_gpu(ctx, args, kv_name: str):
     stream = velokv.Stream(ctx)
     rope = {"none": 0, "interleaved": velokv.ROPE_INTERLEAVED, "half": velokv.ROPE_HALF}[args.rope]
     if rope:
-        n_pos = int(lens.max())
+        n_pos = max(int(lens.max()), walk_max)
         d_table = ctx.upload(velokv.rope_table(n_pos, D, 500000.0))
         d_pos = ctx.upload(lens.astype(np.int32) - 1)
+        d_walk_pos = [ctx.upload((base + o).astype(np.int32)) for o in range(W)]
 
     plan = ctx.decode_plan(pool, S, H, int(lens.max()), bt_stride=bt.shape[1], partition_tokens=args.partition,
                            q_dtype=qdt, sum_context_len=int(lens.sum()))
 
-    def decode(layer, r):
-        ctx.paged_decode(pool, layer, qs[r], qdt, out, d_lens, S, H, int(lens.max()),
+    def decode(layer, r, cl=None, cmax=None, csum=None):
+        ctx.paged_decode(pool, layer, qs[r], qdt, out, d_lens if cl is None else cl, S, H,
+                         int(lens.max()) if cmax is None else cmax,
                          block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
-                         stream=stream, sum_context_len=int(lens.sum()))
+                         stream=stream, sum_context_len=int(lens.sum()) if csum is None else csum)
 
     # INT8 (I8_BLK) under the workgroup split or stream-K, fp16 under stream-K,
     # without RoPE: vk_append_decode, whose decode appends each sequence's new token itself
@@ -235,29 +251,41 @@ def run_gpu(ctx, args, kv_name: str):
     fused = not rope and ((kv == velokv.KV_I8_BLK and plan["wg_waves"] > 0) or
                           (kv in (velokv.KV_I8_BLK, velokv.KV_F16) and plan["schedule"] == velokv.SCHED_STREAM))
 
-    def append_decode(layer, r):
-        ctx.append_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, qs[r], qdt, out, d_lens, S, H, int(lens.max()),
+    def append_decode(layer, r, o=None):
+        cl, cmax, csum = ((d_lens, int(lens.max()), int(lens.sum())) if o is None else
+                          (d_walk[o], walk_max, int(walk_lens[o].sum())))
+        ctx.append_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, qs[r], qdt, out, cl, S, H, cmax,
                           block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition, stream=stream,
-                          sum_context_len=int(lens.sum()))
+                          sum_context_len=csum)
 
-    def step(i, app_evs=None, one_launch=fused):
+    def step(i, app_evs=None, one_launch=fused, walk=True):
+        """One decode step over all layers; walk: the new token at offset i % 16
+        of the last block (else at position L - 1, the same every step)."""
         r = i % R
+        o = i % W if walk else None
         for layer in range(NL):
             if one_launch and app_evs is None:
-                append_decode(layer, r)
+                append_decode(layer, r, o)
                 continue
             if app_evs is not None:
                 app_evs[layer][0].record(stream)
+            sl = new_slots if o is None else walk_slots[o]
             if rope:
-                ctx.append_rope(pool, layer, ks[r], vs[r], velokv.DT_F16, d_pos, new_slots, S, d_table, n_pos, rope,
-                                q=qs[r], q_dtype=qdt, n_heads=H, stream=stream)
+                ctx.append_rope(pool, layer, ks[r], vs[r], velokv.DT_F16, d_pos if o is None else d_walk_pos[o], sl,
+                                S, d_table, n_pos, rope, q=qs[r], q_dtype=qdt, n_heads=H, stream=stream)
             else:
-                ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, new_slots, S, stream=stream)
+                ctx.append(pool, layer, ks[r], vs[r], velokv.DT_F16, sl, S, stream=stream)
             if app_evs is not None:
                 app_evs[layer][1].record(stream)
-            decode(layer, r)
+            if o is None:
+                decode(layer, r)
+            else:
+                decode(layer, r, d_walk[o], walk_max, int(walk_lens[o].sum()))
 
-    for i in range(args.warmup):
+    # warm-up walks the whole last block once (every position holds a token
+    # before any step is timed), then W more steps
+    n_warm = max(args.warmup, 0) + W
+    for i in range(n_warm):
         step(i)
     stream.sync()
     ctx.sync()
@@ -265,23 +293,33 @@ def run_gpu(ctx, args, kv_name: str):
     start, end = velokv.Event(ctx), velokv.Event(ctx)
     start.record(stream)
     for i in range(args.steps):
-        step(args.warmup + i)
+        step(n_warm + i)
     end.record(stream)
     stream.sync()
     ctx.sync()
     total_ms = start.elapsed_ms(end)
+    timed_offsets = [(n_warm + i) % W for i in range(args.steps)]
     two_ms = None
     if fused:  # the same steps with the append in a launch of its own (untimed for the value)
         start.record(stream)
         for i in range(args.steps):
-            step(args.warmup + i, one_launch=False)
+            step(n_warm + i, one_launch=False)
         end.record(stream)
         stream.sync()
         two_ms = start.elapsed_ms(end) / args.steps
-    # decode calls alone: NL x steps back-to-back calls (layers and input sets rotating)
+    # the same number of steps with every new token at position L - 1 (after the
+    # first pass the block scales stop growing: the append never requantizes)
+    start.record(stream)
+    for i in range(args.steps):
+        step(i, walk=False)
+    end.record(stream)
+    stream.sync()
+    rep_ms = start.elapsed_ms(end) / args.steps
+    # decode calls alone at the full context lengths: NL x steps back-to-back
+    # calls (layers and input sets rotating)
     dec_mean_ms, dec_ms = time_calls(ctx, stream, lambda i: decode(i % NL, (i // NL) % R), NL * args.steps)
-    fold_ms = (time_calls(ctx, stream, lambda i: append_decode(i % NL, (i // NL) % R), NL * args.steps)[0]
-               if fused else None)
+    fold_ms = (time_calls(ctx, stream, lambda i: append_decode(i % NL, (i // NL) % R, ((i // NL) % W)),
+                          NL * args.steps)[0] if fused else None)
     # append time per layer, from two more (untimed) steps with events around the appends only
     app_evs = [[[velokv.Event(ctx), velokv.Event(ctx)] for _ in range(NL)] for _ in range(2)]
     for i in range(2):
@@ -290,11 +328,14 @@ def run_gpu(ctx, args, kv_name: str):
     app_ms = [app_evs[i][l][0].elapsed_ms(app_evs[i][l][1]) for i in range(2) for l in range(NL)]
 
     ms_step = total_ms / args.steps
-    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1], 4 if qdt == velokv.DT_F32 else 2, D)
+    q_esz = 4 if qdt == velokv.DT_F32 else 2
+    dbytes = decode_bytes(kv, S, H, Hkv, lens, bt.shape[1], q_esz, D, PG)  # one call at the full lengths
+    walk_dbytes = float(np.mean([decode_bytes(kv, S, H, Hkv, walk_lens[o], bt.shape[1], q_esz, D, PG)
+                                 for o in timed_offsets]))
     abytes = append_bytes(kv, S, Hkv, D)
     if rope:  # q read and written (fp16), positions, one table row (D/2 cos, sin pairs) per token
         abytes += 2 * S * H * D * (4 if qdt == velokv.DT_F32 else 2) + S * 4 + S * D * 4
-    step_bytes = NL * (dbytes + abytes)
+    step_bytes = NL * (walk_dbytes + abytes)
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
     kname = plan["kernel"]
     res = {
@@ -308,8 +349,12 @@ def run_gpu(ctx, args, kv_name: str):
                    "rope": args.rope, "ms_mean": round(float(np.mean(app_ms)), 5),
                    "q_rotated_heads": S * H if rope else 0},
         "step_call": "vk_append_decode (append folded into the decode launch)" if fused else "append + decode",
+        "step_positions": "new token at offset i % 16 of each sequence's last block (context base + o + 1); "
+                          "the block scale restarts at offset 0 and grows as the rows require",
+        "step_bytes": int(step_bytes),
         "append_decode_ms_mean": round(fold_ms, 5) if fused else None,
         "ms_per_step_two_launches": round(two_ms, 4) if fused else None,
+        "ms_per_step_repeated_position": round(rep_ms, 4),
         "plan": plan,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -747,7 +792,16 @@ def main():
         f32.q_dtype, f32.steps, f32.warmup = "fp32", min(args.steps, 10), min(args.warmup, 2)
         configs["headline_int8_fp32q"] = run_gpu(ctx, f32, "int8")
         # the reference's default cache type (fp32 K/V, fp32 q) at the headline shape
-        configs["config1_fp32_kv"] = run_gpu(ctx, f32, "fp32")
+        configs["headline_fp32_kv"] = run_gpu(ctx, f32, "fp32")
+        # radix-shared 4096-token prefix, 256 sequences, 8-node tree verify + commit
+        c4 = copy.copy(args)
+        c4.seqs, c4.steps, c4.warmup = 256, min(args.steps, 10), min(args.warmup, 2)
+        configs["config4_tree"] = run_tree(ctx, c4)
+        # BASELINE config 5, one GPU's share: 32 x 32768, 64 / 8 heads, INT8, 80 layers, 65,536-block pool
+        c5 = copy.copy(args)
+        c5.seqs, c5.ctx, c5.heads, c5.layers, c5.pool_blocks = 32, 32768, 64, 80, 65536
+        c5.steps, c5.warmup = min(args.steps, 10), min(args.warmup, 2)
+        configs["config5_s32_ctx32k"] = run_gpu(ctx, c5, "int8")
     cpu = None if args.no_cpu else cpu_baseline(args)
     workload = ("S=%d, L=%s, H=%d/Hkv=%d, D=%d, bs=%d, %s KV, %d layers, %sappend+decode per layer, pool %d blocks" %
                 (args.seqs, "U[1024,%d]" % args.ctx if args.ragged else str(args.ctx), args.heads, args.kv_heads,

@@ -360,8 +360,10 @@ int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* s
  * (slot = table[row][pos / bs] * bs + pos % bs, as kv_update derives it,
  * kernels.metal:637-640, 770-774); a sequence with context 0 appends nothing,
  * and a page id outside the pool stores nothing (the decode reports it,
- * VK_MISUSE_PAGE_OUT_OF_POOL). The result equals vk_append of those slots
- * followed by vk_paged_decode, bit for bit. Over VK_KV_I8_BLK pools under the
+ * VK_MISUSE_PAGE_OUT_OF_POOL). The pool afterwards equals vk_append of those
+ * slots followed by vk_paged_decode, bit for bit, and so do the outputs except
+ * under the workgroup split, whose folding wave takes a few blocks fewer (the
+ * outputs then agree to fp32 rounding of a different split). Over VK_KV_I8_BLK pools under the
  * workgroup-split or stream-K schedule, and over VK_KV_F16 pools under
  * stream-K, the decode launch appends the tokens itself (the
  * wave that holds a sequence's last block applies the append rule to it before
@@ -419,6 +421,22 @@ typedef struct vk_tree_args {
 /* Bytes of split-K workspace vk_tree_verify needs for these arguments (0 when
  * one partition covers every sequence). */
 int vk_tree_verify_workspace(const vk_pool* pool, const vk_tree_args* a, uint64_t* bytes);
+
+/* What vk_tree_verify would launch for these arguments, launching nothing. No
+ * reference counterpart (the reference's tree kernel has no caller). */
+typedef struct vk_tree_plan {
+  char kernel[64];             /* rest-of-context (or whole-context) tree kernel     */
+  char prefix_kernel[64];      /* shared-prefix pass, "" when there is none          */
+  int32_t prefix_chunks;       /* chunks the shared prefix is cut into (0 = no pass) */
+  int32_t prefix_row_tiles;    /* prefix pass: 256-row tiles of query rows per KV head */
+  int32_t row_tiles;           /* tree kernel: 16-row tiles per (sequence, KV head)   */
+  int32_t rows_per_tile;       /* 16 or 32 (the kernel's row tiles per wave x 16)     */
+  int32_t partition_tokens;    /* rest of the context: tokens per partition          */
+  int32_t max_partitions;      /* partial slots per row, prefix chunks included      */
+  uint64_t workspace_bytes;    /* split-K scratch the call needs                     */
+  int32_t merge_launch;        /* 1 when vk_decode_merge follows                     */
+} vk_tree_plan;
+int vk_tree_verify_plan(const vk_pool* pool, const vk_tree_args* a, vk_tree_plan* out);
 
 /* Multi-query tree-verify attention over fp32, fp16 or int8 pools: query row (node i,
  * head h) attends to the committed context (positions 0..context_len-1) and to

@@ -3,8 +3,12 @@ position context_len - 1, then decode; metal/model.rs:399-471 runs kv_update the
 the attention kernel per layer): the append kernel with the slots derived from
 the block table in the kernel, then the decode, over every schedule.
 Each case is checked three ways: pool bytes bit for bit against the oracle's
-append of the same tokens and against vk_append + vk_paged_decode on a second
-pool, and outputs within the north-star tolerance of the oracle's decode."""
+append of the same tokens and against vk_append + vk_paged_decode (same
+schedule) on a second pool, and outputs within the north-star tolerance of the
+oracle's decode. Under stream-K the two calls cut the contexts into the same
+pieces, so their outputs are also compared bit for bit; under the workgroup
+split the folding wave's range is kFoldBlocks shorter, so outputs agree to fp32
+rounding of a different split (checked within the tolerance)."""
 import numpy as np
 import pytest
 
@@ -47,13 +51,13 @@ def _one_call_step(ctx, pool, case, qd, in_dt, block_tables, seq_rows, bt_stride
     return pl, out.download((S, H, HD), np.float32)
 
 
-def two_call_step(ctx, case, qd=np.float16, in_dt=np.float16):
+def two_call_step(ctx, case, qd=np.float16, in_dt=np.float16, sched=velokv.SCHED_SPLIT):
     pool = gpu_pool(ctx, case, with_last=False, in_dtype=in_dt)
     sl, kk, vv = case.last_slots()
     ctx.append(pool, 0, ctx.upload(kk.astype(in_dt)), ctx.upload(vv.astype(in_dt)),
                velokv.DT_F32 if in_dt == np.float32 else velokv.DT_F16, ctx.upload(sl), len(sl))
     out = ctx.alloc(case.S * case.n_heads * HD * 4)
-    ctx.set_decode_schedule(velokv.SCHED_SPLIT)
+    ctx.set_decode_schedule(sched)
     try:
         ctx.paged_decode(pool, 0, ctx.upload(case.q.astype(qd)), velokv.DT_F32 if qd == np.float32 else velokv.DT_F16,
                          out, ctx.upload(case.ctx_lens), case.S, case.n_heads, int(case.ctx_lens.max()),
@@ -65,13 +69,15 @@ def two_call_step(ctx, case, qd=np.float16, in_dt=np.float16):
     return pool, out.download((case.S, case.n_heads, HD), np.float32)
 
 
-def check_all(ctx, case, pool, got, qd, in_dt=np.float16):
+def check_all(ctx, case, pool, got, qd, in_dt=np.float16, sched=velokv.SCHED_SPLIT, same_pieces=False):
     ref_layer = oracle_layer_in(case, in_dt)
     assert_layer_equal(pool, 0, ref_layer)
-    pool2, got2 = two_call_step(ctx, case, qd, in_dt)
+    pool2, got2 = two_call_step(ctx, case, qd, in_dt, sched)
     a, b = pool.download_layer(0), pool2.download_layer(0)
     for key in ("k", "v", "ks", "vs"):
         assert (a[key] is None and b[key] is None) or np.array_equal(a[key], b[key]), key
+    if same_pieces:
+        assert np.array_equal(got, got2), "folded call and append + decode differ"
     ref = O.paged_decode(ref_layer, case.q.astype(qd), case.block_tables, case.ctx_lens)
     for g, what in ((got, "append_decode"), (got2, "append + decode")):
         ok, err, nbad = tol_check(g, ref)
@@ -136,7 +142,7 @@ def test_stream_k_folds_the_append(ctx, kv, G, qd):
     finally:
         ctx.set_decode_schedule(velokv.SCHED_AUTO)
     assert pl["schedule"] == velokv.SCHED_STREAM and "_sk_" in pl["kernel"], pl
-    check_all(ctx, case, pool, got, qd)
+    check_all(ctx, case, pool, got, qd, sched=velokv.SCHED_STREAM, same_pieces=True)
 
 
 @pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
@@ -196,15 +202,22 @@ def test_slot_table_rows_empty_context_and_bad_page(ctx):
     assert "0x1" in str(e.value)
 
 
-def test_headline_shape_sampled(ctx):
-    """64 x 8192 (the metric's shape), INT8: the call against the oracle
-    on four sampled sequences (pool bytes of their blocks and outputs)."""
-    print("append_decode headline", flush=True)
+@pytest.mark.parametrize("shape", ["headline", "config5"])
+def test_full_shape_fold_sampled(ctx, shape):
+    """The folded call at the shapes the bench times, INT8, against the oracle on
+    four sampled sequences (pool bytes of their blocks and outputs): 64 x 8192
+    (the metric's shape, GQA 4, 4-wave workgroups of 128 blocks) and config 5's
+    one-GPU share, 32 x 32768 with GQA 8 in a 65,536-block pool (8-wave
+    workgroups of 256 blocks: the folding wave takes its last block from
+    block-id window 3)."""
+    print(f"append_decode full shape {shape}", flush=True)
     from test_gpu_fullshape import build_pool, oracle_sample, check_pool_bytes
-    S, L, Hkv, H = 64, 8192, 8, 32
-    sample = [0, 21, 42, 63]
+    S, L, Hkv, H, n_blocks, kernel, waves = {
+        "headline": (64, 8192, 8, 32, 40000, "vk_decode_wg_kv3_g4", 4),
+        "config5": (32, 32768, 8, 64, 65536, "vk_decode_wg_kv3_g8", 8)}[shape]
+    sample = [0, S // 3, 2 * S // 3, S - 1]
     lens_pre = np.full(S, L - 1, np.int32)
-    pool, bt, inputs = build_pool(ctx, O.I8_BLK, lens_pre, Hkv, 40000, seed=58, sample=sample, outlier_scale=8.0)
+    pool, bt, inputs = build_pool(ctx, O.I8_BLK, lens_pre, Hkv, n_blocks, seed=58, sample=sample, outlier_scale=8.0)
     try:
         row = Hkv * HD
         kn = synth.normals_f16(S * row, 5801, row, 8.0).reshape(S, Hkv, HD)
@@ -215,7 +228,8 @@ def test_headline_shape_sampled(ctx):
         q = synth.normals_f16(S * H * HD, 5803).reshape(S, H, HD)
         out = ctx.alloc(S * H * HD * 4)
         pl = ctx.decode_plan(pool, S, H, L, bt_stride=bt_full.shape[1], sum_context_len=S * L)
-        assert pl["kernel"] == "vk_decode_wg_kv3_g4", pl
+        assert pl["kernel"] == kernel and pl["wg_waves"] == waves, pl
+        assert pl["max_blocks_per_wave"] == L // BS // waves, pl
         ctx.append_decode(pool, 0, ctx.upload(kn), ctx.upload(vn), velokv.DT_F16, ctx.upload(q), velokv.DT_F16, out,
                           ctx.upload(lens), S, H, L, block_tables=ctx.upload(bt_full), bt_stride=bt_full.shape[1],
                           sum_context_len=S * L)

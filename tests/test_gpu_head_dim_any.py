@@ -234,3 +234,53 @@ def test_tree_commit(ctx, kv, hd):
     for s, a in enumerate(accepts):
         O.tree_commit(ref, case.block_tables[s], int(ctxs[s]), a)
     assert_layer_equal(pool, 0, ref)
+
+
+@pytest.mark.parametrize("in_dt", [np.float16, np.float32])
+@pytest.mark.parametrize("hd", [64, 96, 40])
+@pytest.mark.parametrize("kv", [O.I8_BLK, O.F16])
+def test_stream_k_folds_the_append(ctx, kv, hd, in_dt):
+    """vk_append_decode under stream-K over int8 block and fp16 pools of head_dim
+    64 (the 64-dim stream-K pieces, lanes 32-63 storing nothing), 96 and 40 (new
+    rows shorter than the tile): the piece that ends at a context's last token
+    appends the hd-long new rows in the decode launch. fp32 new rows (scaled so
+    they are not fp16 values) are rounded by the fold as the append kernels
+    round them; half the rows are 3x larger, so int8 block scales grow and the
+    earlier codes are requantized. Pool bytes bit for bit, outputs within the
+    tolerance."""
+    print(f"hd{hd} stream-K fold kv={kv} in={np.dtype(in_dt).name}", flush=True)
+    lens = synth.rng(1530 + hd).integers(1, 1500, 40)
+    lens[:6] = [1, 16, 17, 32, 33, 48]
+    case = hd_case(kv, lens, hd, n_kv_heads=8, n_heads=32, seed=1531 + hd)
+    pool = gpu_pool(ctx, case, hd, with_last=False)
+    sl, kk, vv = case.last_slots()
+    kk, vv = kk.astype(np.float32), vv.astype(np.float32)
+    kk[::2] *= 3
+    vv[::2] *= 3
+    if in_dt == np.float32:
+        kk, vv = kk * np.float32(1.37), vv * np.float32(0.61)
+    else:
+        kk, vv = kk.astype(np.float16), vv.astype(np.float16)
+    out = ctx.alloc(case.S * case.n_heads * hd * 4)
+    ctx.set_decode_kernel(velokv.DECODE_MFMA)
+    ctx.set_decode_schedule(velokv.SCHED_STREAM)
+    try:
+        pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1])
+        assert pl["schedule"] == velokv.SCHED_STREAM and "_sk_" in pl["kernel"], pl
+        assert ("_d64" in pl["kernel"]) == (hd <= 64), pl
+        ctx.append_decode(pool, 0, ctx.upload(kk), ctx.upload(vv),
+                          velokv.DT_F32 if in_dt == np.float32 else velokv.DT_F16, ctx.upload(case.q),
+                          velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
+                          int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
+                          bt_stride=case.block_tables.shape[1])
+        ctx.sync()
+    finally:
+        ctx.set_decode_kernel(velokv.DECODE_AUTO)
+        ctx.set_decode_schedule(velokv.SCHED_AUTO)
+    T = tile_w(hd)
+    ref_layer = oracle_padded(case, hd, with_last=False)
+    O.append(ref_layer, pad(kk.astype(np.float32), T), pad(vv.astype(np.float32), T), sl)
+    assert_layer_equal(pool, 0, ref_layer)
+    got = out.download((case.S, case.n_heads, hd), np.float32)
+    ok, err, nbad = tol_check(got, oracle_decode(ref_layer, case.q, hd, case.block_tables, case.ctx_lens))
+    assert ok, (err, nbad)

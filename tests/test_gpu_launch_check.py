@@ -57,3 +57,17 @@ def test_planned_shapes_fit_the_kernels(ctx, kv, S, H, L, sched, sum_l):
     app = "vk_append_kv%d" % kv
     assert ctx.launch_check(app, 128) == 128
     del pool
+
+
+def test_tree_plan_shapes_fit_the_kernels(ctx):
+    """vk_tree_verify_plan at configuration 4's shape (256 sequences, 8 nodes,
+    GQA 4, a 256-page shared prefix): the prefix pass (16 waves per workgroup)
+    and the tree kernel (one wave) fit their kernels' limits."""
+    print("launch check: tree plan, config 4 shape", flush=True)
+    pool = velokv.Pool(ctx, 1, 64, 16, 8, 128, velokv.KV_I8_BLK)
+    pl = ctx.tree_plan(pool, 256, 8, 32, 4608, bt_stride=300, shared_blocks=256)
+    assert pl["prefix_chunks"] == 1 and pl["prefix_row_tiles"] == 32 and pl["row_tiles"] == 1, pl
+    assert pl["rows_per_tile"] == 32 and not pl["merge_launch"], pl
+    assert ctx.launch_check(pl["prefix_kernel"], 1024) == 1024
+    assert ctx.launch_check(pl["kernel"], 64) >= 64
+    del pool

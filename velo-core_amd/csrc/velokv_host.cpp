@@ -1201,6 +1201,25 @@ extern "C" int vk_tree_verify_workspace(const vk_pool* pool, const vk_tree_args*
   return VK_OK;
 }
 
+extern "C" int vk_tree_verify_plan(const vk_pool* pool, const vk_tree_args* a, vk_tree_plan* out) {
+  if (!pool || !a || !out) return fail(VK_ERR_BAD_ARG, "null argument");
+  TreePlan pl;
+  int rc = plan_tree(pool->ctx, pool, a, &pl);
+  if (rc) return rc;
+  memset(out, 0, sizeof *out);
+  snprintf(out->kernel, sizeof out->kernel, "%s", pl.kernel.c_str());
+  snprintf(out->prefix_kernel, sizeof out->prefix_kernel, "%s", pl.prefix_chunks > 0 ? pl.pfx_kernel.c_str() : "");
+  out->prefix_chunks = pl.prefix_chunks;
+  out->prefix_row_tiles = pl.pfx_row_tiles;
+  out->row_tiles = pl.n_rgroups;
+  out->rows_per_tile = 16 * pl.rt;
+  out->partition_tokens = pl.part_tokens;
+  out->max_partitions = pl.max_parts;
+  out->workspace_bytes = pl.max_parts > 1 ? pl.acc_bytes + pl.ml_bytes : 0;
+  out->merge_launch = pl.max_parts == pl.prefix_chunks + 1 ? 0 : 1;
+  return VK_OK;
+}
+
 extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a, void* stream) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;

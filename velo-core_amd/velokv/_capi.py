@@ -87,6 +87,13 @@ class DecodePlan(C.Structure):
                 ("max_blocks_per_wave", C.c_int32), ("workspace_bytes", C.c_uint64), ("merge_launch", C.c_int32)]
 
 
+class TreePlan(C.Structure):
+    _fields_ = [("kernel", C.c_char * 64), ("prefix_kernel", C.c_char * 64), ("prefix_chunks", C.c_int32),
+                ("prefix_row_tiles", C.c_int32), ("row_tiles", C.c_int32), ("rows_per_tile", C.c_int32),
+                ("partition_tokens", C.c_int32), ("max_partitions", C.c_int32), ("workspace_bytes", C.c_uint64),
+                ("merge_launch", C.c_int32)]
+
+
 class TreeArgs(C.Structure):
     _fields_ = [("layer", C.c_int32), ("q", C.c_void_p), ("q_dtype", C.c_int32), ("out", C.c_void_p),
                 ("block_tables", C.c_void_p), ("bt_stride", C.c_int32), ("seq_rows", C.c_void_p),
@@ -137,6 +144,7 @@ PROTOTYPES = {
     "vk_paged_decode_noalloc": [P, P, C.POINTER(DecodeArgs), P],
     "vk_append_decode": [P, P, P, P, I32, C.POINTER(DecodeArgs), P],
     "vk_tree_verify_workspace": [P, C.POINTER(TreeArgs), C.POINTER(U64)],
+    "vk_tree_verify_plan": [P, C.POINTER(TreeArgs), C.POINTER(TreePlan)],
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],
     "vk_tree_mask": [PI32, I32, PU32],
     "vk_copy_blocks": [P, P, PI32, I32, P],

@@ -214,6 +214,19 @@ class Context:
         check(lib().vk_tree_verify_workspace(pool.h, C.byref(a), C.byref(n)))
         return n.value
 
+    def tree_plan(self, pool: "Pool", n_seqs, n_nodes, n_heads, max_context_len, bt_stride=0, partition_tokens=0,
+                  q_dtype=DT_F16, shared_blocks: int = 0) -> dict:
+        """vk_tree_verify_plan as a dict (kernels, prefix chunks and row tiles, partitions, workspace)."""
+        a = _capi.TreeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None, None,
+                           n_seqs, n_nodes, n_heads, max_context_len, 0.0, partition_tokens, None, 0, shared_blocks)
+        p = _capi.TreePlan()
+        check(lib().vk_tree_verify_plan(pool.h, C.byref(a), C.byref(p)))
+        return {"kernel": p.kernel.decode(), "prefix_kernel": p.prefix_kernel.decode(),
+                "prefix_chunks": p.prefix_chunks, "prefix_row_tiles": p.prefix_row_tiles, "row_tiles": p.row_tiles,
+                "rows_per_tile": p.rows_per_tile, "partition_tokens": p.partition_tokens,
+                "max_partitions": p.max_partitions, "workspace_bytes": p.workspace_bytes,
+                "merge_launch": bool(p.merge_launch)}
+
     def copy_blocks(self, pool: "Pool", pairs, stream=None):
         p = np.ascontiguousarray(np.asarray(pairs, dtype=np.int32).reshape(-1))
         check(lib().vk_copy_blocks(self.h, pool.h, p.ctypes.data_as(C.POINTER(C.c_int32)), len(p) // 2,
