@@ -87,8 +87,9 @@ def parse():
     ap.add_argument("--sched", choices=["auto", "split", "stream", "packed"], default="auto",
                     help="decode work schedule (vk_ctx_set_decode_schedule)")
     ap.add_argument("--rope", choices=["none", "interleaved", "half"], default="none",
-                    help="decode step: fused RoPE + append (vk_append_rope: K rotated before quantization, "
-                         "q rotated in place in the same launch) instead of the plain append")
+                    help="decode step with RoPE at each new token's position: vk_append_rope_decode (K and q "
+                         "rotated inside the decode launch) where the plan folds the append, else vk_append_rope "
+                         "(K rotated before quantization, q rotated in place) then the decode")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workload", choices=["decode", "tree", "nixl"], default="decode",
@@ -245,15 +246,21 @@ def run_gpu(ctx, args, kv_name: str):
                          block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition,
                          stream=stream, sum_context_len=int(lens.sum()) if csum is None else csum)
 
-    # INT8 (I8_BLK) under the workgroup split or stream-K, fp16 under stream-K,
-    # without RoPE: vk_append_decode, whose decode appends each sequence's new token itself
-    # (one launch per layer); otherwise the append and the decode are two launches
-    fused = not rope and ((kv == velokv.KV_I8_BLK and plan["wg_waves"] > 0) or
-                          (kv in (velokv.KV_I8_BLK, velokv.KV_F16) and plan["schedule"] == velokv.SCHED_STREAM))
+    # INT8 (I8_BLK) under the workgroup split or stream-K, fp16 under stream-K:
+    # vk_append_decode, whose decode appends each sequence's new token itself (one
+    # launch per layer), with RoPE vk_append_rope_decode, whose decode also rotates
+    # the new K row and q; otherwise the append and the decode are two launches
+    fused = ((kv == velokv.KV_I8_BLK and plan["wg_waves"] > 0) or
+             (kv in (velokv.KV_I8_BLK, velokv.KV_F16) and plan["schedule"] == velokv.SCHED_STREAM))
 
     def append_decode(layer, r, o=None):
         cl, cmax, csum = ((d_lens, int(lens.max()), int(lens.sum())) if o is None else
                           (d_walk[o], walk_max, int(walk_lens[o].sum())))
+        if rope:
+            ctx.append_rope_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, d_table, n_pos, rope, qs[r], qdt, out,
+                                   cl, S, H, cmax, block_tables=d_bt, bt_stride=bt.shape[1],
+                                   partition_tokens=args.partition, stream=stream, sum_context_len=csum)
+            return
         ctx.append_decode(pool, layer, ks[r], vs[r], velokv.DT_F16, qs[r], qdt, out, cl, S, H, cmax,
                           block_tables=d_bt, bt_stride=bt.shape[1], partition_tokens=args.partition, stream=stream,
                           sum_context_len=csum)
@@ -333,7 +340,9 @@ def run_gpu(ctx, args, kv_name: str):
     walk_dbytes = float(np.mean([decode_bytes(kv, S, H, Hkv, walk_lens[o], bt.shape[1], q_esz, D, PG)
                                  for o in timed_offsets]))
     abytes = append_bytes(kv, S, Hkv, D)
-    if rope:  # q read and written (fp16), positions, one table row (D/2 cos, sin pairs) per token
+    if rope and fused:  # one table row (D/2 cos, sin pairs) per token; q is rotated in registers
+        abytes += S * D * 4
+    elif rope:  # q read and written, positions, one table row per token
         abytes += 2 * S * H * D * (4 if qdt == velokv.DT_F32 else 2) + S * 4 + S * D * 4
     step_bytes = NL * (walk_dbytes + abytes)
     achieved = dbytes / (dec_mean_ms * 1e-3) / 1e9
@@ -348,7 +357,9 @@ def run_gpu(ctx, args, kv_name: str):
         "append": {"kernel": "vk_append_kv%d" % kv, "call": "vk_append_rope" if rope else "vk_append",
                    "rope": args.rope, "ms_mean": round(float(np.mean(app_ms)), 5),
                    "q_rotated_heads": S * H if rope else 0},
-        "step_call": "vk_append_decode (append folded into the decode launch)" if fused else "append + decode",
+        "step_call": ("vk_append_rope_decode (RoPE and append folded into the decode launch)" if fused and rope else
+                      "vk_append_decode (append folded into the decode launch)" if fused else
+                      "RoPE append + decode" if rope else "append + decode"),
         "step_positions": "new token at offset i % 16 of each sequence's last block (context base + o + 1); "
                           "the block scale restarts at offset 0 and grows as the rows require",
         "step_bytes": int(step_bytes),

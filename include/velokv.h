@@ -284,7 +284,8 @@ int vk_rope_table(float* out, int32_t n_pos, int32_t head_dim, float freq_base);
  * (and quantized for the I8 types); V is stored as is. When q is not NULL the
  * same launch rotates q in place (dev [n_tok][n_heads][head_dim] of q_dtype;
  * fp16 q is rounded to fp16 after the fp32 rotation). cos_sin is the dev table
- * of vk_rope_table with n_pos positions; a token whose position is outside
+ * of vk_rope_table with n_pos positions, 16-byte aligned (the kernels read it
+ * in 16-byte chunks; VK_ERR_BAD_ARG otherwise); a token whose position is outside
  * [0, n_pos) is skipped like a negative slot (not appended, q not rotated).
  * Rotation: y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32, every product and sum
  * rounded separately, the reference's expression order (llama_cpu.rs:128-129).
@@ -374,6 +375,25 @@ int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* s
  * (metal/model.rs:399-471). */
 int vk_append_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new, int32_t in_dtype,
                      const vk_decode_args* a, void* stream);
+
+/* One decode step of a layer with rotary position embedding: the reference's
+ * rope -> kv_update -> attention (metal/model.rs:380-471). As vk_append_decode,
+ * with the new K rows and every q row rotated at the new token's position
+ * (context_len - 1) by the vk_rope_table rows cos_sin (16-byte aligned; style
+ * VK_ROPE_INTERLEAVED or VK_ROPE_HALF), exactly as vk_append_rope rotates them;
+ * a position outside [0, n_pos) rotates nothing and appends nothing. The
+ * attention uses the rotated q; the caller's q buffer is left unchanged. Where
+ * vk_append_decode folds the append into the decode launch and head_dim is 64
+ * or 128, the rotation folds too (one launch per layer: the folding wave
+ * rotates the new K row, every wave its q rows in registers); otherwise the
+ * RoPE append runs first and writes the rotated q rows into the workspace,
+ * whose size vk_append_rope_decode_workspace gives. The pool afterwards equals
+ * vk_append_rope (positions context_len - 1) followed by vk_paged_decode on the
+ * rotated q, bit for bit. No separate reference counterpart. */
+int vk_append_rope_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new, int32_t in_dtype,
+                          const float* cos_sin, int32_t n_pos, int32_t rope_style, const vk_decode_args* a,
+                          void* stream);
+int vk_append_rope_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes);
 
 /* vk_paged_decode that allocates nothing. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph capture,

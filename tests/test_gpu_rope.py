@@ -96,3 +96,6 @@ def test_append_rope_rejects_bad_arguments(ctx):
         with pytest.raises(velokv.VkError) as e:
             ctx.append_rope(pool, 0, buf, buf, velokv.DT_F16, buf, buf, 1, buf, n_pos, style)
         assert e.value.code == velokv.ERR_BAD_ARG
+    with pytest.raises(velokv.VkError) as e:  # the table is read in 16-byte chunks
+        ctx.append_rope(pool, 0, buf, buf, velokv.DT_F16, buf, buf, 1, buf.ptr + 8, 16, O.ROPE_INTERLEAVED)
+    assert e.value.code == velokv.ERR_BAD_ARG and "aligned" in str(e.value)

@@ -202,6 +202,8 @@ std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) 
 bool use_d64(const vk_pool_desc& d, int g) {
   return tile_hd(d.head_dim) == kHD / 2 && d.kv_type != VK_KV_F32 && g <= kMaxGroupTile;
 }
+// The folding kernels' variants that also rotate the new K row and q (RoPE)
+const char* const kRopeSuffix = "_rope";
 std::string decode_pk_name(int kv, int g, int qt = VK_DT_F16) {
   return "vk_decode_pk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
@@ -317,6 +319,15 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       }
     }
   }
+  // vk_append_rope_decode's kernels: every kernel that folds the append, suffix _rope
+  for (int kv : {VK_KV_F16, VK_KV_I8_BLK})
+    for (int g : {1, 2, 4, 8, 3})
+      for (int qt : {VK_DT_F16, VK_DT_F32})
+        for (bool d64 : {false, true}) {
+          if (d64 && g != 3) continue;
+          names.push_back(decode_sk_name(kv, g, qt, d64) + kRopeSuffix);
+          if (kv == VK_KV_I8_BLK) names.push_back(decode_wg_name(kv, g, qt, d64) + kRopeSuffix);
+        }
   for (int kv = 0; kv < 4; ++kv)
     for (int g : {1, 2, 4, 8}) {
       for (int qt = 0; qt < 2; ++qt) names.push_back(decode_name(kv, g, qt));
@@ -650,6 +661,7 @@ extern "C" int vk_append_rope(vk_ctx* ctx, vk_pool* pool, int32_t layer, void* q
     return fail(VK_ERR_BAD_ARG, "q needs n_heads > 0 and q_dtype VK_DT_F32 / VK_DT_F16");
   if (n_tok == 0) return VK_OK;
   if (!k || !v || !slot_mapping || !positions || !cos_sin) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  if (reinterpret_cast<uintptr_t>(cos_sin) % 16) return fail(VK_ERR_BAD_ARG, "cos_sin must be 16-byte aligned");
   AppendParams p{};
   p.base = pool->base;
   p.g = pool->geom;
@@ -941,8 +953,34 @@ namespace {
 // The new token of every sequence (k_new / v_new rows [S][Hkv][D] of in_dtype)
 // appended at position context_len - 1 of its table row by the append kernel,
 // slots derived in the kernel (the unfused half of vk_append_decode).
+// Whether the decode launch of this plan appends the new tokens itself
+// (vk_append_decode): I8_BLK pools under the workgroup split or stream-K, fp16
+// pools under stream-K, over tiles the folded kernels are built for.
+bool plan_folds_append(const vk_pool* pool, const vk_decode_args* a, const DecodePlan& pl) {
+  const int kvt = pool->desc.kv_type;
+  return ((kvt == VK_KV_I8_BLK && (pl.wg_waves > 0 || pl.stream_k)) || (kvt == VK_KV_F16 && pl.stream_k)) &&
+         (tile_hd(pool->desc.head_dim) == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
+}
+
+// vk_append_rope_decode rotates the new K row and q inside the folding decode
+// kernel (its _rope variant) when the plan folds the append and q's half-split
+// partner chunk sits in lane ^ 32 (head_dim equal to the tile width); otherwise
+// the RoPE append writes the rotated q rows into the workspace and the decode
+// reads them there.
+bool plan_folds_rope(const vk_pool* pool, const vk_decode_args* a, const DecodePlan& pl) {
+  return plan_folds_append(pool, a, pl) && pool->geom.io_hd == pool->geom.head_dim;
+}
+
+// RoPE of vk_append_rope_decode (style ROPE_NONE: none).
+struct RopeArgs {
+  int32_t style = ROPE_NONE;
+  const float* cos_sin = nullptr;
+  int32_t n_pos = 0;
+};
+
 int append_new_tokens(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, const DecodePlan& pl, const void* k_new,
-                      const void* v_new, int in_dtype, void* stream) {
+                      const void* v_new, int in_dtype, void* stream, const RopeArgs& rope = RopeArgs(),
+                      void* q_out = nullptr) {
   AppendParams p{};
   p.base = pool->base;
   p.g = pool->geom;
@@ -962,15 +1000,27 @@ int append_new_tokens(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, const
   p.err = ctx->err_word;
   p.claim = pool->claim;
   p.epoch = pool->claim ? pool->next_epoch() : 0u;
+  unsigned rows = (unsigned)pool->desc.n_kv_heads;
+  if (rope.style != ROPE_NONE) {  // positions derived (context_len - 1); q rotated into q_out
+    p.rope = rope.style;
+    p.positions = nullptr;
+    p.cos_sin = rope.cos_sin;
+    p.n_pos = rope.n_pos;
+    p.n_heads = a->n_heads;
+    p.q = const_cast<void*>(a->q);
+    p.q_out = q_out;
+    p.q_dtype = a->q_dtype;
+    rows += (unsigned)((a->n_heads + 1) / 2);
+  }
   const std::string name = append_kernel_name(pool->desc.kv_type, pool->desc.head_dim);
-  return launch(ctx, name.c_str(), dim3((unsigned)((a->n_seqs + p.tok_per_wg - 1) / p.tok_per_wg),
-                                        (unsigned)pool->desc.n_kv_heads), dim3(128), p, stream);
+  return launch(ctx, name.c_str(), dim3((unsigned)((a->n_seqs + p.tok_per_wg - 1) / p.tok_per_wg), rows), dim3(128),
+                p, stream);
 }
 
 // vk_paged_decode, and with k_new the append of vk_append_decode as a launch
 // before it.
 int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream, const void* k_new,
-               const void* v_new, int in_dtype) {
+               const void* v_new, int in_dtype, const RopeArgs& rope = RopeArgs()) {
   int rc = check_pool(ctx, pool);
   if (rc) return rc;
   DecodePlan pl;
@@ -983,12 +1033,19 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   // sequence's last block appends the token before loading it); every other
   // plan appends in a launch of its own first
   const int kvt = pool->desc.kv_type;
-  const bool fold = k_new &&
-                    ((kvt == VK_KV_I8_BLK && (pl.wg_waves > 0 || pl.stream_k)) || (kvt == VK_KV_F16 && pl.stream_k)) &&
-                    (tile_hd(pool->desc.head_dim) == kHD || use_d64(pool->desc, a->n_heads / pool->desc.n_kv_heads));
-  if (k_new && !fold && (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream))) return rc;
+  const bool fold = k_new && plan_folds_append(pool, a, pl);
+  const bool rope_fold = fold && rope.style != ROPE_NONE && plan_folds_rope(pool, a, pl);
+  const std::string kernel = rope_fold ? pl.kernel + kRopeSuffix : pl.kernel;
+  const bool rope_copy = rope.style != ROPE_NONE && !rope_fold;
+  const uint64_t q_bytes = rope_copy ? align_up((uint64_t)a->n_seqs * a->n_heads * pool->geom.io_hd *
+                                                (a->q_dtype == VK_DT_F32 ? 4 : 2), 256) : 0;
   uint8_t* ws = nullptr;
-  if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes, pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes, &ws)))
+  if ((rc = split_workspace(ctx, a->workspace, a->workspace_bytes,
+                            pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes + q_bytes, &ws)))
+    return rc;
+  void* q_rot = rope_copy ? ws + pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes : nullptr;
+  if (k_new && (!fold || rope_copy) &&
+      (rc = append_new_tokens(ctx, pool, a, pl, k_new, v_new, in_dtype, stream, rope, q_rot)))
     return rc;
   const vk_pool_desc& d = pool->desc;
   const PoolGeom& g = pool->geom;
@@ -1002,7 +1059,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   p.vc = L + g.v_off;
   p.ks = g.stile_bytes ? L + g.ks_off : nullptr;
   p.vs = g.stile_bytes ? L + g.vs_off : nullptr;
-  p.q = a->q;
+  p.q = rope_copy ? q_rot : a->q;
   p.out = a->out;
   p.part_acc = reinterpret_cast<float*>(ws);
   p.part_ml = reinterpret_cast<float*>(ws + pl.acc_bytes);
@@ -1033,7 +1090,12 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   p.sk_penalty = (pl.stream_k || pl.packed) ? kSkPenalty : 0;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.err = ctx->err_word;
-  if (fold) {
+  if (fold && !rope_copy) {
+    if (rope_fold) {
+      p.rope = rope.style;
+      p.cos_sin = rope.cos_sin;
+      p.rope_n_pos = rope.n_pos;
+    }
     p.fold_k = k_new;
     p.fold_v = v_new;
     p.fold_dtype = in_dtype;
@@ -1066,17 +1128,17 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   m.n_seqs = a->n_seqs;
   const dim3 merge_grid((unsigned)((m.n_rows + 3) / 4));
   if (pl.stream_k) {
-    if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64), p, stream))) return rc;
+    if ((rc = launch(ctx, kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64), p, stream))) return rc;
     return launch(ctx, "vk_decode_merge_sk", merge_grid, dim3(256), m, stream);
   }
   if (pl.packed)
-    return launch(ctx, pl.kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64 * kWgMaxWaves), p, stream);
+    return launch(ctx, kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64 * kWgMaxWaves), p, stream);
   if (pl.wg_waves)
-    return launch(ctx, pl.kernel.c_str(), dim3((unsigned)(a->n_seqs * d.n_kv_heads)), dim3(64 * (unsigned)pl.wg_waves),
+    return launch(ctx, kernel.c_str(), dim3((unsigned)(a->n_seqs * d.n_kv_heads)), dim3(64 * (unsigned)pl.wg_waves),
                   p, stream);
   const uint64_t units = (uint64_t)a->n_seqs * pl.max_parts * d.n_kv_heads;
   if (units > 0x7FFFFFFFull) return fail(VK_ERR_UNSUPPORTED, "grid too large");
-  if ((rc = launch(ctx, pl.kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
+  if ((rc = launch(ctx, kernel.c_str(), dim3((unsigned)units), dim3(64), p, stream))) return rc;
   if (pl.max_parts == 1) return VK_OK;  // every sequence was finished by the decode kernel
   return launch(ctx, "vk_decode_merge", merge_grid, dim3(256), m, stream);
 }
@@ -1085,6 +1147,34 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
 
 extern "C" int vk_paged_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream) {
   return run_decode(ctx, pool, a, stream, nullptr, nullptr, VK_DT_F16);
+}
+
+extern "C" int vk_append_rope_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new,
+                                     int32_t in_dtype, const float* cos_sin, int32_t n_pos, int32_t rope_style,
+                                     const vk_decode_args* a, void* stream) {
+  if (in_dtype != VK_DT_F32 && in_dtype != VK_DT_F16) return fail(VK_ERR_BAD_ARG, "in_dtype %d", in_dtype);
+  if (rope_style != VK_ROPE_INTERLEAVED && rope_style != VK_ROPE_HALF)
+    return fail(VK_ERR_BAD_ARG, "rope_style %d (VK_ROPE_INTERLEAVED or VK_ROPE_HALF)", rope_style);
+  if (!a) return fail(VK_ERR_BAD_ARG, "args is null");
+  if (n_pos <= 0) return fail(VK_ERR_BAD_ARG, "n_pos must be positive");
+  if (a->n_seqs > 0 && (!k_new || !v_new || !cos_sin)) return fail(VK_ERR_BAD_ARG, "null device pointer");
+  if (reinterpret_cast<uintptr_t>(cos_sin) % 16) return fail(VK_ERR_BAD_ARG, "cos_sin must be 16-byte aligned");
+  RopeArgs r;
+  r.style = rope_style;
+  r.cos_sin = cos_sin;
+  r.n_pos = n_pos;
+  return run_decode(ctx, pool, a, stream, k_new, v_new, in_dtype, r);
+}
+
+extern "C" int vk_append_rope_decode_workspace(const vk_pool* pool, const vk_decode_args* a, uint64_t* bytes) {
+  if (!pool || !a || !bytes) return fail(VK_ERR_BAD_ARG, "null argument");
+  DecodePlan pl;
+  int rc = plan_decode(pool->ctx, pool, a, &pl);
+  if (rc) return rc;
+  *bytes = pl.acc_bytes + pl.ml_bytes + pl.prefix_bytes;
+  if (!plan_folds_rope(pool, a, pl))
+    *bytes += align_up((uint64_t)a->n_seqs * a->n_heads * pool->geom.io_hd * (a->q_dtype == VK_DT_F32 ? 4 : 2), 256);
+  return VK_OK;
 }
 
 extern "C" int vk_append_decode(vk_ctx* ctx, vk_pool* pool, const void* k_new, const void* v_new, int32_t in_dtype,

@@ -46,6 +46,14 @@ constexpr int DPP_ROW_HALF_MIRROR = 0x141;
 constexpr int DPP_ROW_MIRROR = 0x140;
 
 DEV float shfl_xor(float x, int m) { return __shfl_xor(x, m, WAVE); }
+// x of lane l ^ 32: v_permlane32_swap exchanges lanes 32..63 of its first
+// operand with lanes 0..31 of its second (a VALU exchange, no LDS round trip);
+// with both operands x, the second result holds x[l + 32] in lanes 0..31 and the
+// first holds x[l - 32] in lanes 32..63.
+DEV float xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(lane_id() < 32 ? r[1] : r[0]);
+}
 
 DEV float wave_max(float x) {
   x = fmaxf(x, dpp<DPP_QUAD_XOR1>(x));
@@ -200,39 +208,38 @@ constexpr float kRescaleThreshold = 4.0f;  // log2 units
 constexpr int kWin = 4;
 struct BlockIds {
   int b[kWin];
-  float ks[kWin];
-  float vs[kWin];
-  uint32_t oob;  // bit k: the page of this lane's block in window k was outside the pool
+  uint32_t sw[kWin];  // I8_BLK: the (K, V) scale word of the lane's (block, head), K low, V high (fp16)
+  uint32_t oob;       // bit k: the page of this lane's block in window k was outside the pool
 };
 // A page id outside [0, n_blocks) is clamped into the pool (the read stays in
 // bounds) and reported as MISUSE_PAGE_OUT_OF_POOL. Tile u of a sequence (tokens
-// 16u .. 16u + 15) is tile u % 2^page_shift of page bt[u >> page_shift].
+// 16u .. 16u + 15) is tile u % 2^page_shift of page bt[u >> page_shift]. Lanes
+// past the piece's nblk blocks hold its last block. Every load is issued
+// outside any branch (lanes past nblk read the last block's entries) and the
+// scale words are kept as loaded: a load in a branch, or a use here, would wait
+// for it, and the windows' table and scale loads would complete one after
+// another before the piece's first tile loads go out.
 template <bool BLK>
 DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, int blk0, int nblk, int kvh) {
   const int lane = lane_id();
   const int ps = P.page_shift;
+  const int last = max(nblk - 1, 0);
+  int raw[kWin];
+#pragma unroll
+  for (int k = 0; k < kWin; ++k) raw[k] = bt[(blk0 + min(64 * k + lane, last)) >> ps];
   bool bad = false;
   w.oob = 0u;
 #pragma unroll
   for (int k = 0; k < kWin; ++k) {
-    w.b[k] = 0;
-    w.ks[k] = 1.f;
-    w.vs[k] = 1.f;
     const int idx = 64 * k + lane;
-    if (idx < nblk) {
-      const int u = blk0 + idx;
-      const int raw = bt[u >> ps];
-      const bool out = raw < 0 || raw >= P.n_blocks;
-      bad |= out;
-      w.oob |= out ? 1u << k : 0u;
-      w.b[k] = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
-      if constexpr (BLK) {  // the (K, V) scale word of the (block, head): one load
-        const uint32_t sw =
-            *reinterpret_cast<const uint32_t*>(P.ks + ((int64_t)w.b[k] * P.n_kv_heads + kvh) * kBlkScaleStep);
-        w.ks[k] = h2f((uint16_t)(sw & 0xFFFFu));
-        w.vs[k] = h2f((uint16_t)(sw >> 16));
-      }
-    }
+    const int u = blk0 + min(idx, last);
+    const bool out = idx < nblk && (raw[k] < 0 || raw[k] >= P.n_blocks);
+    bad |= out;
+    w.oob |= out ? 1u << k : 0u;
+    w.b[k] = (min(max(raw[k], 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
+    w.sw[k] = 0u;
+    if constexpr (BLK)  // the (K, V) scale word of the (block, head): one load
+      w.sw[k] = *reinterpret_cast<const uint32_t*>(P.ks + ((int64_t)w.b[k] * P.n_kv_heads + kvh) * kBlkScaleStep);
   }
   if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) flag_misuse(P.err, MISUSE_PAGE_OUT_OF_POOL);
 }
@@ -251,6 +258,9 @@ DEV T window_at(const T (&a)[kWin], int i) {
   }
   return bitcast<T>(v);
 }
+// I8_BLK block scales of block i (wave-uniform) of a piece.
+DEV float blk_kscale(const BlockIds& w, int i) { return half_lo(window_at(w.sw, i)); }
+DEV float blk_vscale(const BlockIds& w, int i) { return half_hi(window_at(w.sw, i)); }
 
 template <int KV>
 struct Stage {
@@ -490,7 +500,7 @@ DEV void decode_unit(const DecodeParams& P) {
         a[g] += dpp<DPP_QUAD_XOR2>(a[g]);
       }
       float kscale = P.scale_log2;
-      if constexpr (BLK) kscale *= window_at(bw.ks, min(i, nblk - 1));
+      if constexpr (BLK) kscale *= blk_kscale(bw, min(i, nblk - 1));
       if constexpr (REF) kscale *= st.ks[u];
       const bool valid = (i < nblk) && (start + i * BS + t < end);
 #pragma unroll
@@ -558,7 +568,7 @@ DEV void decode_unit(const DecodeParams& P) {
       const int i = b * CH + u;
       if (i < nblk) {
         float vscale = 1.f;
-        if constexpr (BLK) vscale = window_at(bw.vs, i);
+        if constexpr (BLK) vscale = blk_vscale(bw, i);
         if constexpr (REF) vscale = st.vs[u];
 #pragma unroll
         for (int k = 0; k < SPL; ++k) {
@@ -772,6 +782,171 @@ DEV void mstage_load(MStage<KV, DK>& st, const DecodeParams& P, const BlockIds& 
   }
 }
 
+// ---- RoPE (fused into the append) --------------------------------------------
+// Pair i of a head row at position p is rotated by the table's (cos, sin) of
+// angle p * base^(-2i/D), D the caller's head_dim: ROPE_INTERLEAVED pairs dims (2i, 2i+1)
+// (kernels.metal:103-131), ROPE_HALF pairs dims (i, i + D/2)
+// (llama_cpu.rs:113-131). y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32 with
+// every product and sum rounded separately (no fused multiply-add), the
+// reference's expression order. Lane l holds dims 2l, 2l+1 of the row.
+// D = any multiple of 4 up to 128 (the half-split partners of the lane's dims,
+// d + D/2 or d - D/2, then sit together in lane l + D/4 or l - D/4): lanes
+// 2l >= D hold zeros and stay zero.
+// rope_rotate in two steps: rope_cs loads the 16-byte table chunk that holds
+// the lane's (cos, sin) values, with no branch and no use (so that it can be
+// issued with other loads and wait for nothing), and rope_apply takes the
+// values from it and rotates. Interleaved: pair `lane` of the row (D/2 pairs of
+// (cos, sin)) is in chunk lane / 2, .xy for even lanes, .zw for odd ones;
+// half-split: pairs 2 lh, 2 lh + 1 of the lane's place lh in its half are chunk
+// lh. Lanes past the row read chunk 0.
+DEV float4 rope_cs(int style, const float* cos_sin, int pos, int D) {
+  const int lane = lane_id();
+  const int hl = D / 4;  // lanes of one half of the row
+  const int lh = lane < hl ? lane : lane - hl;
+  int c = style == ROPE_HALF ? lh : lane >> 1;
+  c = 2 * lane < D ? c : 0;
+  return reinterpret_cast<const float4*>(cos_sin + (int64_t)pos * D)[c];
+}
+
+DEV void rope_apply(int style, const float4 t, int D, float& x0, float& x1) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const int hl = D / 4;
+  if (style == ROPE_INTERLEAVED) {
+    if (2 * lane < D) {
+      const float2 cs = (lane & 1) ? make_float2(t.z, t.w) : make_float2(t.x, t.y);
+      const float y0 = x0 * cs.x - x1 * cs.y;
+      const float y1 = x0 * cs.y + x1 * cs.x;
+      x0 = y0;
+      x1 = y1;
+    }
+  } else {
+    const int lh = lane < hl ? lane : lane - hl;                             // the lane's place in its half
+    const float p0 = __shfl(x0, lane < hl ? lane + hl : lh, WAVE);          // dims d -+ D/2
+    const float p1 = __shfl(x1, lane < hl ? lane + hl : lh, WAVE);
+    if (2 * lane >= D) return;
+    if (lane < hl) {  // first half: y = x c - partner s
+      const float y0 = x0 * t.x - p0 * t.y;
+      const float y1 = x1 * t.z - p1 * t.w;
+      x0 = y0;
+      x1 = y1;
+    } else {          // second half: y = partner s + x c
+      const float y0 = p0 * t.y + x0 * t.x;
+      const float y1 = p1 * t.w + x1 * t.z;
+      x0 = y0;
+      x1 = y1;
+    }
+  }
+}
+
+DEV void rope_rotate(int style, const float* cos_sin, int pos, int D, float& x0, float& x1) {
+  rope_apply(style, rope_cs(style, cos_sin, pos, D), D, x0, x1);
+}
+
+// RoPE of a lane's q chunks in the matrix-core pieces (vk_append_rope_decode):
+// chunk kc holds dims d0 = 8 (KC g + kc) .. d0 + 7 of row R (zeros when R is
+// past the tile's rows). The rotation of rope_rotate at the table row of the new
+// token's position (D = head_dim), in its expression order, every product and
+// sum rounded separately: ROPE_INTERLEAVED pairs (2i, 2i + 1) within the chunk;
+// ROPE_HALF pairs d with d + D/2, whose chunk is the same chunk of lane l ^ 32
+// (lane group g ^ 2 holds the dims D/2 further on, at D = 64 and 128), fetched
+// with one lane exchange per value. A position outside the table leaves q as it is.
+// rope_q_issue issues every load of q and of the table, none in a branch,
+// before the piece's first tile loads; rope_q_finish rotates while those are
+// in flight (its waits count only the loads issued before them), both styles
+// in one branch-free form (selects, not a branch on the style, so that no load
+// is sunk into a branch and waited for behind the tile loads):
+//   y_j = x_j c - p s   (interleaved, j even; half-split, first half)
+//   y_j = p s + x_j c   (interleaved, j odd;  half-split, second half)
+// with p the partner value (x_{j^1}, or lane l ^ 32's x_j).
+template <int QT, int KC>
+struct RopeQ {
+  uint4 raw[KC][QT == DT_F32 ? 2 : 1];  // q chunks as loaded
+  float4 t[KC][4];  // pairs 2h', 2h' + 1 of the chunk: interleaved h' = h / 2 (d0/2 + ..), half h' = h (df + ..)
+  bool row_ok, rot;
+};
+
+// qoff: the lane's chunks of row R; qoff_ok: a row of q that exists, read by
+// lanes past the rows (they then take zeros); pos: the new token's position.
+template <int QT, int KC>
+DEV void rope_q_issue(RopeQ<QT, KC>& r, const DecodeParams& P, int64_t qoff, int64_t qoff_ok, bool row_ok, int pos,
+                      int g) {
+  const int D = P.io_hd;
+  const bool half = P.rope == ROPE_HALF;
+  r.row_ok = row_ok;
+  r.rot = pos >= 0 && pos < P.rope_n_pos;
+  const float* csr = P.cos_sin + (int64_t)(r.rot ? pos : 0) * D;
+  const int64_t qo = row_ok ? qoff : qoff_ok;
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    if constexpr (QT == DT_F32) {
+      const uint4* q32 = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(P.q) + qo) + 2 * kc;
+      r.raw[kc][0] = q32[0];
+      r.raw[kc][1] = q32[1];
+    } else {
+      r.raw[kc][0] = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qo)[kc];
+    }
+  }
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    const int d0 = 8 * (KC * g + kc);
+    const int df = d0 < D / 2 ? d0 : d0 - D / 2;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      r.t[kc][h] = *reinterpret_cast<const float4*>(half ? csr + 2 * df + 4 * h : csr + d0 + 4 * (h >> 1));
+  }
+}
+
+template <int QT, int KC, bool QSPLIT>
+DEV void rope_q_finish(const RopeQ<QT, KC>& r, const DecodeParams& P, int g, half8 (&qa)[KC], half8 (&qlo)[KC]) {
+#pragma clang fp contract(off)
+  const int D = P.io_hd;
+  const bool half = P.rope == ROPE_HALF;
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    float x[8];
+    if constexpr (QT == DT_F32) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        x[4 * u + 0] = __uint_as_float(r.raw[kc][u].x);
+        x[4 * u + 1] = __uint_as_float(r.raw[kc][u].y);
+        x[4 * u + 2] = __uint_as_float(r.raw[kc][u].z);
+        x[4 * u + 3] = __uint_as_float(r.raw[kc][u].w);
+      }
+    } else {
+      const half8 h = bitcast<half8>(r.raw[kc][0]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = (float)h[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = r.row_ok ? x[j] : 0.f;
+    const bool first = 8 * (KC * g + kc) < D / 2;
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float ph = xor32(x[j]);
+      const float p = half ? ph : x[j ^ 1];
+      const float4 tt = r.t[kc][j >> 1];
+      const bool zw = half ? (j & 1) != 0 : ((j >> 1) & 1) != 0;  // pair 2h' + 1 of t
+      const float c = zw ? tt.z : tt.x, sn = zw ? tt.w : tt.y;
+      const bool form1 = half ? first : (j & 1) == 0;
+      y[j] = form1 ? x[j] * c - p * sn : p * sn + x[j] * c;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = r.rot ? y[j] : x[j];
+    const uint4 v = make_uint4(pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7]));
+    qa[kc] = bitcast<half8>(v);
+    qlo[kc] = bitcast<half8>(make_uint4(0, 0, 0, 0));
+    if constexpr (QSPLIT) {
+      const half8 h = qa[kc];
+      qlo[kc] = bitcast<half8>(make_uint4(pack_h2(x[0] - (float)h[0], x[1] - (float)h[1]),
+                                          pack_h2(x[2] - (float)h[2], x[3] - (float)h[3]),
+                                          pack_h2(x[4] - (float)h[4], x[5] - (float)h[5]),
+                                          pack_h2(x[6] - (float)h[6], x[7] - (float)h[7])));
+    }
+  }
+}
+
 // ---- KV append helpers (shared by the append kernels and the folded append) ----
 DEV void load_x2(const void* src, int in_dtype, int64_t off, float& x0, float& x1) {
   if (in_dtype == DT_F16) {
@@ -850,10 +1025,20 @@ DEV void blk_put(int (&cd)[BS][2], int o, float& s_old, uint16_t& s_bits, float 
 // and stores the new token's codes, and when the scale grows loads, requantizes
 // and stores the codes of the tokens before o. A page id outside the pool
 // appends nothing (the decode reports it), as the append kernel drops such a
-// slot.
+// slot. For I8_BLK the block's codes come with the first loads too (whole
+// 16-byte pieces, and the V token pair of o), so that a requantization waits
+// for no load: K pieces hold one token each and are rewritten whole when that
+// token is before o; V pieces hold a token pair and are rewritten whole when
+// both are before o; the pair holding o is stored by the lanes of the rule
+// (dims 2 lane, 2 lane + 1) as one word with token o's codes, so no two stores
+// of the call overlap.
 struct FoldIn {
-  float x[2][2];          // [K, V] new-token dims 2 lane, 2 lane + 1
-  uint16_t stored[2];     // [K, V] stored block scale
+  uint32_t w[2][2];       // [K, V] new-token dims 2 lane, 2 lane + 1 as loaded (fp16: both in w[e][0])
+  float x[2][2];          // the same as fp32 (fold_finish)
+  float4 cs;              // RoPE: the lane's table chunk at ctx - 1 (rope_cs)
+  uint32_t sw;            // I8_BLK: the block's scale word as loaded (K low, V high)
+  uint4 kq[2], vq[2];     // I8_BLK: 16-byte pieces lane + 64 j of the K and V tiles (j < D / 64)
+  uint32_t vpair;         // I8_BLK: V codes of tokens 2P, 2P + 1 (P = o / 2) at dims 2 lane, 2 lane + 1
   unsigned long long claim_old;
   uint64_t tix;           // (tile, KV head) index of the block
   int o;
@@ -862,98 +1047,156 @@ struct FoldIn {
 
 // Loads of the folded append of sequence s, KV head kvh, whose piece holds nblk
 // blocks (window bw), the last one holding position ctx - 1 (I8_BLK: also the
-// block's stored scales; fp16 pools store the new rows as they are).
-template <int KV, int D>
+// block's stored scales; fp16 pools store the new rows as they are). Every load
+// is issued whether or not the append happens (f.on), from an address that
+// exists, and none is used here: a use here, or a load in a branch, would wait
+// for them (and, vector loads completing in order, for nothing more) before the
+// piece's first tile loads go out, on the folding wave's critical path.
+template <int KV, int D, bool ROPE = false>
 DEV void fold_issue(FoldIn& f, const DecodeParams& P, const BlockIds& bw, int nblk, int s, int kvh, int ctx) {
   const int i = nblk - 1;
   f.on = ((readlane_i((int)bw.oob, i & 63) >> (i >> 6)) & 1) == 0;
-  if (!f.on) return;
-  const int tile_id = window_at(bw.b, i);
+  // with RoPE, a position outside the table appends nothing (as the RoPE append skips it)
+  if constexpr (ROPE) {
+    if (ctx - 1 < 0 || ctx - 1 >= P.rope_n_pos) f.on = false;
+  }
+  const int tile_id = f.on ? window_at(bw.b, i) : 0;
   f.tix = (uint64_t)tile_id * P.n_kv_heads + kvh;
   f.o = (ctx - 1) & (BS - 1);
+  // the claim of the block (one run per block and call), checked after the piece
   f.claim_old = 0;
-  if (P.claim && kvh == 0 && lane_id() == 0)
+  if (P.claim && f.on && kvh == 0 && lane_id() == 0)
     f.claim_old = __hip_atomic_exchange(&P.claim[tile_id], ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s,
                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // the new rows are io_hd long; the tile's dims past it take zeros
+  // the new rows are io_hd long; lanes past it read dim 0 and take zeros (fold_finish)
   const int d0 = 2 * lane_id();
-  const int64_t row = ((int64_t)s * P.n_kv_heads + kvh) * P.io_hd + d0;
+  const int64_t row = ((int64_t)s * P.n_kv_heads + kvh) * P.io_hd + (d0 < P.io_hd ? d0 : 0);
+  const bool f16 = P.fold_dtype == DT_F16;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    f.x[e][0] = f.x[e][1] = 0.f;
-    if (d0 < P.io_hd) load_x2(e ? P.fold_v : P.fold_k, P.fold_dtype, row, f.x[e][0], f.x[e][1]);
+    const uint32_t* src = f16 ? reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(e ? P.fold_v : P.fold_k) + row)
+                              : reinterpret_cast<const uint32_t*>(reinterpret_cast<const float*>(e ? P.fold_v : P.fold_k) + row);
+    f.w[e][0] = src[0];
+    f.w[e][1] = src[f16 ? 0 : 1];
   }
+  // RoPE of the new K row: the table chunk now, the rotation in fold_finish
+  if constexpr (ROPE) f.cs = rope_cs(P.rope, P.cos_sin, f.on ? ctx - 1 : 0, P.io_hd);
   if constexpr (KV == KV_I8_BLK) {
-    const uint32_t sw = *reinterpret_cast<const uint32_t*>(P.ks + f.tix * kBlkScaleStep);
-    f.stored[0] = (uint16_t)(sw & 0xFFFFu);
-    f.stored[1] = (uint16_t)(sw >> 16);
+    f.sw = *reinterpret_cast<const uint32_t*>(P.ks + f.tix * kBlkScaleStep);
+    const uint4* kt = reinterpret_cast<const uint4*>(P.kc + f.tix * P.tile_bytes);
+    const uint4* vt = reinterpret_cast<const uint4*>(P.vc + f.tix * P.tile_bytes);
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+      f.kq[j] = kt[lane_id() + 64 * j];
+      f.vq[j] = vt[lane_id() + 64 * j];
+    }
+    f.vpair = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(vt) +
+                                                 tile_elem<true>(f.o & ~1, d0 & (D - 1), 1, D));
   }
 }
 
 DEV int byte_at(uint32_t w, int k) { return (int)(int8_t)(uint8_t)(w >> (8 * k)); }
 
-// The rule for K (IS_V false) or V; returns the block's new scale. Lanes past a
+// The rule for K (IS_V false) or V; returns the block's new scale (fp16 bits). Lanes past a
 // 64-dim row read the codes 64 dims below and store nothing. K codes of token u
 // at dims 2 lane, 2 lane + 1 are two adjacent bytes; V codes of the token pair
 // 2p, 2p + 1 are four (dim 2 lane: tokens 2p, 2p + 1; then dim 2 lane + 1).
-template <bool IS_V, int D>
-DEV float fold_finish_one(FoldIn& f, const DecodeParams& P) {
-  const int e = IS_V ? 1 : 0;
-  const int o = f.o;
-  const int d0 = 2 * lane_id(), da = d0 & (D - 1);
-  const bool st = d0 < D;
-  const float s_old = (o == 0) ? 0.f : h2f(f.stored[e]);
-  uint16_t s_bits = (o == 0) ? (uint16_t)0 : f.stored[e];
-  const float s_new = blk_scale(s_old, s_bits, f.x[e][0], f.x[e][1]);
-  uint8_t* tile = const_cast<uint8_t*>(IS_V ? P.vc : P.kc) + f.tix * P.tile_bytes;
-  if (s_new > s_old && o > 0) {  // requantize the tokens before o
-    if constexpr (!IS_V) {
-      uint32_t c[BS - 1];
+DEV uint32_t blk_requant4(uint32_t w, float s_old, float s_new) {
+  uint32_t r = 0;
 #pragma unroll
-      for (int u = 0; u < BS - 1; ++u)
-        c[u] = u < o ? *reinterpret_cast<const uint16_t*>(tile + tile_elem<false>(u, da, 1, D)) : 0u;
-#pragma unroll
-      for (int u = 0; u < BS - 1; ++u) {
-        if (u < o && st) {
-          const int a = blk_requant(byte_at(c[u], 0), s_old, s_new), b = blk_requant(byte_at(c[u], 1), s_old, s_new);
-          *reinterpret_cast<uint16_t*>(tile + tile_elem<false>(u, da, 1, D)) = (uint16_t)((a & 0xFF) | ((b & 0xFF) << 8));
-        }
-      }
-    } else {
-      uint32_t c[BS / 2];
-#pragma unroll
-      for (int p = 0; p < BS / 2; ++p)
-        c[p] = 2 * p < o ? *reinterpret_cast<const uint32_t*>(tile + tile_elem<true>(2 * p, da, 1, D)) : 0u;
-#pragma unroll
-      for (int t = 0; t < BS - 1; ++t) {
-        if (t < o && st) {
-          tile[tile_elem<true>(t, da, 1, D)] = (uint8_t)blk_requant(byte_at(c[t >> 1], t & 1), s_old, s_new);
-          tile[tile_elem<true>(t, da + 1, 1, D)] = (uint8_t)blk_requant(byte_at(c[t >> 1], 2 + (t & 1)), s_old, s_new);
-        }
-      }
-    }
-  }
-  const int c0 = blk_code(f.x[e][0], s_new), c1 = blk_code(f.x[e][1], s_new);
-  if (st) {
-    if constexpr (!IS_V) {
-      *reinterpret_cast<uint16_t*>(tile + tile_elem<false>(o, da, 1, D)) = (uint16_t)((c0 & 0xFF) | ((c1 & 0xFF) << 8));
-    } else {
-      tile[tile_elem<true>(o, da, 1, D)] = (uint8_t)c0;
-      tile[tile_elem<true>(o, da + 1, 1, D)] = (uint8_t)c1;
-    }
-  }
-  if (lane_id() == 0)
-    *reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(IS_V ? P.vs : P.ks) + f.tix * kBlkScaleStep) = s_bits;
-  return s_new;
+  for (int k = 0; k < 4; ++k) r |= (uint32_t)(blk_requant(byte_at(w, k), s_old, s_new) & 0xFF) << (8 * k);
+  return r;
+}
+DEV uint4 blk_requant16(uint4 v, float s_old, float s_new) {
+  return make_uint4(blk_requant4(v.x, s_old, s_new), blk_requant4(v.y, s_old, s_new), blk_requant4(v.z, s_old, s_new),
+                    blk_requant4(v.w, s_old, s_new));
 }
 
-// The rule, the stores, and the block's new scales in bw. One run per block and
-// call, as in append_blk: a second sequence whose new token lands in the same
-// block (claimed in this call) is reported.
-template <int KV, int D>
+template <bool IS_V, int D>
+DEV uint32_t fold_finish_one(FoldIn& f, const DecodeParams& P) {
+  const int e = IS_V ? 1 : 0;
+  const int o = f.o;
+  const int lane = lane_id();
+  const int d0 = 2 * lane, da = d0 & (D - 1);
+  const bool st = d0 < D;
+  const uint16_t stored = (uint16_t)(e ? f.sw >> 16 : f.sw & 0xFFFFu);
+  const float s_old = (o == 0) ? 0.f : h2f(stored);
+  uint16_t s_bits = (o == 0) ? (uint16_t)0 : stored;
+  const float s_new = blk_scale(s_old, s_bits, f.x[e][0], f.x[e][1]);
+  const bool grew = s_new > s_old && o > 0;  // requantize the tokens before o
+  uint8_t* tile = const_cast<uint8_t*>(IS_V ? P.vc : P.kc) + f.tix * P.tile_bytes;
+  const int c0 = blk_code(f.x[e][0], s_new), c1 = blk_code(f.x[e][1], s_new);
+  if constexpr (!IS_V) {
+    if (grew) {
+#pragma unroll
+      for (int j = 0; j < D / 64; ++j) {
+        const int q = lane + 64 * j;
+        if ((q % (D / 2)) / (D / 32) < o)  // the piece's token
+          reinterpret_cast<uint4*>(tile)[q] = blk_requant16(f.kq[j], s_old, s_new);
+      }
+    }
+    if (st)
+      *reinterpret_cast<uint16_t*>(tile + tile_elem<false>(o, da, 1, D)) = (uint16_t)((c0 & 0xFF) | ((c1 & 0xFF) << 8));
+  } else {
+    if (grew) {
+#pragma unroll
+      for (int j = 0; j < D / 64; ++j) {
+        const int q = lane + 64 * j;
+        if (q / (D / 8) < (o >> 1))  // the piece's token pair
+          reinterpret_cast<uint4*>(tile)[q] = blk_requant16(f.vq[j], s_old, s_new);
+      }
+    }
+    if (st) {  // bytes: (2P, d0), (2P + 1, d0), (2P, d0 + 1), (2P + 1, d0 + 1)
+      uint32_t w = f.vpair;
+      if (o & 1) {  // token o - 1 (requantized when the scale grew), then token o
+        int a0 = byte_at(w, 0), a1 = byte_at(w, 2);
+        if (grew) {
+          a0 = blk_requant(a0, s_old, s_new);
+          a1 = blk_requant(a1, s_old, s_new);
+        }
+        w = (uint32_t)(a0 & 0xFF) | ((uint32_t)(c0 & 0xFF) << 8) | ((uint32_t)(a1 & 0xFF) << 16) |
+            ((uint32_t)(c1 & 0xFF) << 24);
+      } else {      // token o, then token o + 1 as it was (not yet written)
+        w = (uint32_t)(c0 & 0xFF) | (w & 0xFF00u) | ((uint32_t)(c1 & 0xFF) << 16) | (w & 0xFF000000u);
+      }
+      *reinterpret_cast<uint32_t*>(tile + tile_elem<true>(o & ~1, da, 1, D)) = w;
+    }
+  }
+  if (lane == 0)
+    *reinterpret_cast<uint16_t*>(const_cast<uint8_t*>(IS_V ? P.vs : P.ks) + f.tix * kBlkScaleStep) = s_bits;
+  return s_bits;  // h2f(s_bits) == s_new
+}
+
+// One run per block and call, as in append_blk: a second sequence whose new
+// token lands in the same block (claimed in this call) is reported. Checked
+// after the piece, when the claim's old value has long arrived.
+DEV void fold_claim_check(const FoldIn& f, const DecodeParams& P, int s) {
+  if (f.on && P.claim && lane_id() == 0 && f.tix % P.n_kv_heads == 0) {
+    const unsigned long long me = ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s;
+    if ((uint32_t)(f.claim_old >> 32) == P.fold_epoch && f.claim_old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
+  }
+}
+
+// The rule, the stores, and the block's new scales in bw.
+template <int KV, int D, bool ROPE = false>
 DEV void fold_finish(FoldIn& f, const DecodeParams& P, BlockIds& bw, int nblk, int s) {
   if (!f.on) return;
   const int lane = lane_id();
+  const bool in_row = 2 * lane < P.io_hd;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    if (P.fold_dtype == DT_F16) {
+      f.x[e][0] = half_lo(f.w[e][0]);
+      f.x[e][1] = half_hi(f.w[e][0]);
+    } else {
+      f.x[e][0] = __uint_as_float(f.w[e][0]);
+      f.x[e][1] = __uint_as_float(f.w[e][1]);
+    }
+    f.x[e][0] = in_row ? f.x[e][0] : 0.f;
+    f.x[e][1] = in_row ? f.x[e][1] : 0.f;
+  }
+  // RoPE of the new K row before the append rule, as the RoPE append rotates it
+  if constexpr (ROPE) rope_apply(P.rope, f.cs, P.io_hd, f.x[0][0], f.x[0][1]);
   if constexpr (KV == KV_F16) {  // the new rows rounded to fp16 (RNE), as vk_append_kv1 stores them
     const int d0 = 2 * lane;
     if (d0 < D) {
@@ -966,19 +1209,12 @@ DEV void fold_finish(FoldIn& f, const DecodeParams& P, BlockIds& bw, int nblk, i
     }
     return;
   }
-  if (P.claim && lane == 0 && f.tix % P.n_kv_heads == 0) {
-    const unsigned long long me = ((unsigned long long)P.fold_epoch << 32) | (uint32_t)s;
-    if ((uint32_t)(f.claim_old >> 32) == P.fold_epoch && f.claim_old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
-  }
-  const float ks = fold_finish_one<false, D>(f, P);
-  const float vs = fold_finish_one<true, D>(f, P);
+  const uint32_t ks = fold_finish_one<false, D>(f, P);
+  const uint32_t vs = fold_finish_one<true, D>(f, P);
   const int i = nblk - 1;
 #pragma unroll
   for (int k = 0; k < kWin; ++k) {
-    if (k == (i >> 6) && lane == (i & 63)) {
-      bw.ks[k] = ks;
-      bw.vs[k] = vs;
-    }
+    if (k == (i >> 6) && lane == (i & 63)) bw.sw[k] = ks | (vs << 16);
   }
 }
 
@@ -1004,7 +1240,7 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 // normalised rows; otherwise it writes the unnormalised partial (acc, M, l) of
 // row R at index TREE ? out_row(R) * max_parts + pbase : pbase + R * pstride of
 // pacc ([.][HD] fp32) and pml ([.][2] fp32), in HBM or in LDS.
-template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = false>
+template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = false, bool ROPE = false>
 DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                     int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   constexpr int ESZ = Esz<KV>::v;
@@ -1042,6 +1278,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   // and appends it (after the first stage's loads and q, unless the block is in
   // the first stage)
   static_assert(!FOLD || ((BLK || KV == KV_F16) && !TREE), "the folded append is the I8_BLK and fp16 decode's");
+  static_assert(!ROPE || FOLD, "RoPE folds with the folded append");
   // vk_append_decode with the append folded in: this piece holds the last token.
   // Its block in the first stage: append before any tile load; otherwise issue
   // the append's loads now and finish it after q, while the first stage is in
@@ -1051,9 +1288,19 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   const bool fold_first = fold && nblk <= CH;
   FoldIn fin;
   if constexpr (FOLD) {
-    if (fold) fold_issue<KV, D>(fin, P, bw, nblk, s, kvh, ctx_c);
-    if (fold_first) fold_finish<KV, D>(fin, P, bw, nblk, s);
+    if (fold) fold_issue<KV, D, ROPE>(fin, P, bw, nblk, s, kvh, ctx_c);
+    if (fold_first) fold_finish<KV, D, ROPE>(fin, P, bw, nblk, s);
   }
+
+  // vk_append_rope_decode: q rotated in registers at the new token's position
+  // (ctx_c - 1), as the RoPE append would have rotated it in memory; its loads
+  // go out before the first stage's
+  static_assert(!ROPE || RT == 1, "the RoPE decode has one tile of rows");
+  constexpr bool QSPLIT = (QT == DT_F32) && !TREE;
+  RopeQ<QT, KC> rq;
+  if constexpr (ROPE)
+    rope_q_issue<QT, KC>(rq, P, out_row(row0 + n) * P.io_hd + 8 * KC * g, out_row(0) * P.io_hd + 8 * KC * g,
+                         row0 + n < nrows, ctx_c - 1, g);
 
   MStage<KV, D> sa, sb;
   mstage_load<KV, D>(sa, P, bw, 0, nblk, kvh, n, g);
@@ -1064,7 +1311,6 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   // score takes two products (hi, then lo, into the same accumulator), so the
   // scores see q to about 2^-22 instead of fp16's 2^-11; the tree kernels
   // round an fp32 q to fp16.
-  constexpr bool QSPLIT = (QT == DT_F32) && !TREE;
   half8 qa[RT][KC];
   half8 qlo[RT][KC];
   float qb[RT];        // int8 KV: 1152 * sum_d q[row n][d] (of hi + lo when split)
@@ -1075,29 +1321,35 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     float qsum = 0.f;
     // q rows are io_hd long (a multiple of 8): the 8-dim chunks past it are zero
     const int64_t qoff = out_row(R) * P.io_hd + 8 * KC * g;
+    if constexpr (ROPE) {
+      rope_q_finish<QT, KC, QSPLIT>(rq, P, g, qa[rt], qlo[rt]);
+    } else {
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
-      if (R < nrows && 8 * (KC * g + kc) < P.io_hd) {
-        if constexpr (QT == DT_F32) {
-          const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff) + 2 * kc;
-          const float4 x0 = q32[0], x1 = q32[1];
-          v = make_uint4(pack_h2(x0.x, x0.y), pack_h2(x0.z, x0.w), pack_h2(x1.x, x1.y), pack_h2(x1.z, x1.w));
-          if constexpr (QSPLIT) {
-            const half8 h = bitcast<half8>(v);
-            vlo = make_uint4(pack_h2(x0.x - (float)h[0], x0.y - (float)h[1]), pack_h2(x0.z - (float)h[2], x0.w - (float)h[3]),
-                             pack_h2(x1.x - (float)h[4], x1.y - (float)h[5]), pack_h2(x1.z - (float)h[6], x1.w - (float)h[7]));
+      for (int kc = 0; kc < KC; ++kc) {
+        uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
+        if (R < nrows && 8 * (KC * g + kc) < P.io_hd) {
+          if constexpr (QT == DT_F32) {
+            const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff) + 2 * kc;
+            const float4 x0 = q32[0], x1 = q32[1];
+            v = make_uint4(pack_h2(x0.x, x0.y), pack_h2(x0.z, x0.w), pack_h2(x1.x, x1.y), pack_h2(x1.z, x1.w));
+            if constexpr (QSPLIT) {
+              const half8 h = bitcast<half8>(v);
+              vlo = make_uint4(pack_h2(x0.x - (float)h[0], x0.y - (float)h[1]), pack_h2(x0.z - (float)h[2], x0.w - (float)h[3]),
+                               pack_h2(x1.x - (float)h[4], x1.y - (float)h[5]), pack_h2(x1.z - (float)h[6], x1.w - (float)h[7]));
+            }
+          } else {
+            v = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qoff)[kc];
           }
-        } else {
-          v = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qoff)[kc];
         }
+        qa[rt][kc] = bitcast<half8>(v);
+        qlo[rt][kc] = bitcast<half8>(vlo);
       }
-      qa[rt][kc] = bitcast<half8>(v);
-      qlo[rt][kc] = bitcast<half8>(vlo);
-      if constexpr (I8) {
+    }
+    if constexpr (I8) {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int j = 0; j < 8; ++j) qsum += QSPLIT ? (float)qa[rt][kc][j] + (float)qlo[rt][kc][j] : (float)qa[rt][kc][j];
-      }
     }
     qb[rt] = 0.f;
     if constexpr (I8) {
@@ -1111,7 +1363,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     }
   }
   if constexpr (FOLD) {
-    if (fold && !fold_first) fold_finish<KV, D>(fin, P, bw, nblk, s);
+    if (fold && !fold_first) fold_finish<KV, D, ROPE>(fin, P, bw, nblk, s);
   }
 
   float M[RT], lrun[RT], psum[RT];   // state of row n (each lane holds a quarter of the row's sums)
@@ -1163,7 +1415,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
       // wave-uniform: every token of the block is committed context inside the partition
       const bool plain = (i < nblk) && (start + (i + 1) * BS <= plain_end);
       float kscale = P.scale_log2;
-      if constexpr (BLK) kscale *= window_at(bw.ks, min(i, nblk - 1));
+      if constexpr (BLK) kscale *= blk_kscale(bw, min(i, nblk - 1));
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -1218,7 +1470,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
       for (int u = 0; u < CH; ++u) {
         const int i = b * CH + u;
         float vscale = 1.f;
-        if constexpr (BLK) vscale = window_at(bw.vs, min(i, nblk - 1));
+        if constexpr (BLK) vscale = blk_vscale(bw, min(i, nblk - 1));
         float ph[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -1362,6 +1614,9 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
         }
       }
     }
+  }
+  if constexpr (FOLD) {
+    if (fold) fold_claim_check(fin, P, s);
   }
 }
 
@@ -1587,14 +1842,14 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
 }
 
 // attn_piece for every KV type: fp32 pools take the fp32 matrix-core piece.
-template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = false>
+template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = false, bool ROPE = false>
 DEV void attn_piece_kv(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                        int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   if constexpr (KV == KV_F32) {
     static_assert(D == HD, "fp32 pools take the 128-dim piece");
     attn_piece_f32<G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml);
   } else {
-    attn_piece<KV, G, RT, TREE, QT, D, FOLD>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
+    attn_piece<KV, G, RT, TREE, QT, D, FOLD, ROPE>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
   }
 }
 
@@ -1680,7 +1935,7 @@ DEV int seq_units(const DecodeParams& P, int s) {
   return nb > 0 ? P.n_kv_heads * (nb + P.sk_penalty) : 0;
 }
 
-template <int KV, int G, int QT = DT_F16, int D = HD>
+template <int KV, int G, int QT = DT_F16, int D = HD, bool ROPE = false>
 DEV void attn_streamk_mfma(const DecodeParams& P) {
   const int lane = lane_id();
   const int w = blockIdx.x;
@@ -1738,7 +1993,7 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
       // context's last token appends the new token first (fold_issue,
       // fold_finish): no other piece of the launch reads that block
       const int slot = o0 > 0 ? 0 : 1;
-      attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK || KV == KV_F16>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s,
+      attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK || KV == KV_F16, ROPE>(P, s, kvh, 0, o0 * BS, min(o1 * BS, ctx_s), ctx_s,
                                                             o0 == 0 && o1 == nb,
                                                             ((int64_t)w * 2 + slot) * group_size<G>(P), 1, P.part_acc,
                                                             P.part_ml);
@@ -1759,7 +2014,7 @@ DEV void attn_streamk_mfma(const DecodeParams& P) {
 //   out = sum_w 2^(M_w - M) acc_w / sum_w 2^(M_w - M) l_w,  M = max_w M_w,
 // so a uniform batch needs no partials in HBM and no merge launch.
 constexpr int kWgMaxWaves = 8;
-template <int KV, int G, int QT = DT_F16, int D = HD>
+template <int KV, int G, int QT = DT_F16, int D = HD, bool ROPE = false>
 DEV void attn_wg_mfma(const DecodeParams& P) {
   constexpr int GM = lds_rows<G>();
   __shared__ float wacc[kWgMaxWaves][GM][HD];
@@ -1784,7 +2039,7 @@ DEV void attn_wg_mfma(const DecodeParams& P) {
   const int per = (nb + fw + nw - 1) / nw;
   const int b0 = min(nb, w * per), b1 = min(nb, b0 + per);
   if (b0 < b1) {
-    attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1,
+    attn_piece_kv<KV, G, 1, false, QT, D, KV == KV_I8_BLK, ROPE>(P, s, kvh, 0, b0 * BS, min(b1 * BS, ctx), ctx, false, 0, 1,
                                                            &wacc[w][0][0], &wml[w][0][0]);
   } else if (lane < Gn) {
     wml[w][lane][0] = kNegInf;
@@ -2422,47 +2677,10 @@ __device__ void decode_merge_sk(const MergeParams& P) {
 // Workgroup (token n, KV head h) with two waves: wave 0 writes K, wave 1 writes V.
 // Lane l owns dims 2l and 2l+1.
 // =============================================================================
-// ---- RoPE (fused into the append) --------------------------------------------
-// Pair i of a head row at position p is rotated by the table's (cos, sin) of
-// angle p * base^(-2i/D), D the caller's head_dim: ROPE_INTERLEAVED pairs dims (2i, 2i+1)
-// (kernels.metal:103-131), ROPE_HALF pairs dims (i, i + D/2)
-// (llama_cpu.rs:113-131). y0 = x0 c - x1 s, y1 = x0 s + x1 c in fp32 with
-// every product and sum rounded separately (no fused multiply-add), the
-// reference's expression order. Lane l holds dims 2l, 2l+1 of the row.
-// D = any multiple of 4 up to 128 (the half-split partners of the lane's dims,
-// d + D/2 or d - D/2, then sit together in lane l + D/4 or l - D/4): lanes
-// 2l >= D hold zeros and stay zero.
-DEV void rope_rotate(int style, const float* cos_sin, int pos, int D, float& x0, float& x1) {
-#pragma clang fp contract(off)
-  const int lane = lane_id();
-  const float* row = cos_sin + (int64_t)pos * D;  // D/2 pairs of (cos, sin)
-  const int hl = D / 4;                             // lanes of one half of the row
-  if (style == ROPE_INTERLEAVED) {
-    if (2 * lane < D) {
-      const float2 cs = reinterpret_cast<const float2*>(row)[lane];
-      const float y0 = x0 * cs.x - x1 * cs.y;
-      const float y1 = x0 * cs.y + x1 * cs.x;
-      x0 = y0;
-      x1 = y1;
-    }
-  } else {
-    const int lh = lane < hl ? lane : lane - hl;                             // the lane's place in its half
-    const float p0 = __shfl(x0, lane < hl ? lane + hl : lh, WAVE);          // dims d -+ D/2
-    const float p1 = __shfl(x1, lane < hl ? lane + hl : lh, WAVE);
-    if (2 * lane >= D) return;
-    const float4 cs = reinterpret_cast<const float4*>(row)[lh];  // pairs 2 lh, 2 lh + 1
-    if (lane < hl) {  // first half: y = x c - partner s
-      const float y0 = x0 * cs.x - p0 * cs.y;
-      const float y1 = x1 * cs.z - p1 * cs.w;
-      x0 = y0;
-      x1 = y1;
-    } else {          // second half: y = partner s + x c
-      const float y0 = p0 * cs.y + x0 * cs.x;
-      const float y1 = p1 * cs.w + x1 * cs.z;
-      x0 = y0;
-      x1 = y1;
-    }
-  }
+// RoPE position of token m: the caller's, or without a position array the new
+// token's (context_len - 1, as its slot is derived).
+DEV int rope_pos(const AppendParams& P, int m) {
+  return P.positions ? P.positions[m] : min(P.context_lens[m], P.cap_tokens) - 1;
 }
 
 // Flat slot of token m, or -1 when it is padding (a negative slot, or one at or
@@ -2481,7 +2699,7 @@ DEV int64_t token_slot(const AppendParams& P, int m) {
   }
   if (slot < 0 || slot >= (int64_t)P.g.n_blocks * BS) return -1;
   if (P.rope != ROPE_NONE) {
-    const int pos = P.positions[m];
+    const int pos = rope_pos(P, m);
     if (pos < 0 || pos >= P.n_pos) return -1;
   }
   return slot;
@@ -2493,7 +2711,7 @@ DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h
   const int io = P.g.io_hd;
   x0 = x1 = 0.f;
   if (2 * lane_id() < io) load_x2(src, P.in_dtype, ((int64_t)m * P.g.n_kv_heads + h) * io + 2 * lane_id(), x0, x1);
-  if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, P.positions[m], io, x0, x1);
+  if (P.rope != ROPE_NONE && !is_v) rope_rotate(P.rope, P.cos_sin, rope_pos(P, m), io, x0, x1);
 }
 
 // VK_KV_I8_BLK: per-(block, head) fp16 scale, round-half-even codes clamped to +-127.
@@ -2721,20 +2939,21 @@ DEV void append_kernel(const AppendParams& P) {
   if ((int)blockIdx.y >= P.g.n_kv_heads) {  // RoPE of two query heads of the window's tokens
     const int head = 2 * ((int)blockIdx.y - P.g.n_kv_heads) + (int)(threadIdx.x / WAVE);
     if (head >= P.n_heads) return;
+    void* qd = P.q_out ? P.q_out : P.q;
     for (int n = w0; n < w1; ++n) {
-      const int pos = P.positions[n];
-      if (pos < 0 || pos >= P.n_pos) continue;
+      const int pos = rope_pos(P, n);
       const int64_t off = ((int64_t)n * P.n_heads + head) * P.g.io_hd + 2 * lane_id();
       float x0 = 0.f, x1 = 0.f;
       const bool in = 2 * lane_id() < P.g.io_hd;
       if (in) load_x2(P.q, P.q_dtype, off, x0, x1);
-      rope_rotate(P.rope, P.cos_sin, pos, P.g.io_hd, x0, x1);
-      if (!in) continue;
+      const bool rot = pos >= 0 && pos < P.n_pos;  // (wave-uniform)
+      if (rot) rope_rotate(P.rope, P.cos_sin, pos, P.g.io_hd, x0, x1);
+      if (!in || (!rot && !P.q_out)) continue;  // unrotated rows stay as they are (copied when q_out is given)
       if (P.q_dtype == DT_F16) {
-        reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(P.q) + off)[0] =
+        reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(qd) + off)[0] =
             (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
       } else {
-        reinterpret_cast<float2*>(reinterpret_cast<float*>(P.q) + off)[0] = make_float2(x0, x1);
+        reinterpret_cast<float2*>(reinterpret_cast<float*>(qd) + off)[0] = make_float2(x0, x1);
       }
     }
     return;
@@ -3248,6 +3467,37 @@ VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
     attn_wg_mfma<KV, 0, DT_F32, HD / 2>(P);                                                                    \
   }
 VK_D64_WG(1) VK_D64_WG(2) VK_D64_WG(3)
+// vk_append_rope_decode: the kernels that fold the append (stream-K over fp16
+// and I8_BLK pools, the workgroup split over I8_BLK pools), with the new K row
+// and q rotated in registers; suffix _rope
+#define VK_ROPE_SK(KV, TAG, QT, D)                                                  \
+  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
+      vk_decode_sk_kv##KV##TAG##_rope(const DecodeParams P) {                       \
+    attn_streamk_mfma<KV, GTAG_##TAG, QT, D, true>(P);                              \
+  }
+#define VK_ROPE_WG(KV, TAG, QT, D)                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves)                    \
+      vk_decode_wg_kv##KV##TAG##_rope(const DecodeParams P) {                       \
+    attn_wg_mfma<KV, GTAG_##TAG, QT, D, true>(P);                                   \
+  }
+#define GTAG__g1 1
+#define GTAG__g2 2
+#define GTAG__g4 4
+#define GTAG__g8 8
+#define GTAG__gx 0
+#define GTAG__gx_d64 0
+#define GTAG__g1_q0 1
+#define GTAG__g2_q0 2
+#define GTAG__g4_q0 4
+#define GTAG__g8_q0 8
+#define GTAG__gx_q0 0
+#define GTAG__gx_d64_q0 0
+#define VK_ROPE_ALL(M, KV)                                                                       \
+  M(KV, _g1, DT_F16, HD) M(KV, _g2, DT_F16, HD) M(KV, _g4, DT_F16, HD) M(KV, _g8, DT_F16, HD)    \
+  M(KV, _gx, DT_F16, HD) M(KV, _gx_d64, DT_F16, HD / 2)                                          \
+  M(KV, _g1_q0, DT_F32, HD) M(KV, _g2_q0, DT_F32, HD) M(KV, _g4_q0, DT_F32, HD)                  \
+  M(KV, _g8_q0, DT_F32, HD) M(KV, _gx_q0, DT_F32, HD) M(KV, _gx_d64_q0, DT_F32, HD / 2)
+VK_ROPE_ALL(VK_ROPE_SK, 1) VK_ROPE_ALL(VK_ROPE_SK, 3) VK_ROPE_ALL(VK_ROPE_WG, 3)
 #define VK_GX_TREE(KV, RT, QT, ATTR)                                                                            \
   extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_r##RT##_q##QT(const DecodeParams P) { \
     attn_unit_mfma<KV, 0, RT, true, QT>(P);                                                                    \

@@ -64,11 +64,12 @@ struct AppendParams {
   const int64_t* slot_mapping;
   int32_t n_tok;
   int32_t rope;             // RopeStyle; ROPE_NONE = plain append
-  const int32_t* positions; // [n_tok] RoPE positions (rope only)
+  const int32_t* positions; // [n_tok] RoPE positions (rope only); null: the new token's, context_len - 1
   const float* cos_sin;     // [n_pos][D/2][2] cos, sin of pair i at each position
   int32_t n_pos;
-  int32_t n_heads;          // query heads rotated in place (0 = none)
-  void* q;                  // [n_tok][n_heads][D] of q_dtype
+  int32_t n_heads;          // query heads rotated (0 = none)
+  void* q;                  // [n_tok][n_heads][D] of q_dtype, rotated in place unless q_out is given
+  void* q_out;              // or the rotated rows go here (same shape and type), q left unchanged
   int32_t q_dtype;
   int32_t tok_per_wg;       // tokens per workgroup (1..64)
   uint32_t* err;            // the context's misuse word
@@ -139,6 +140,14 @@ struct DecodeParams {
   uint32_t fold_epoch;
   unsigned long long* claim;
   int32_t fold_blocks;      // workgroup split: blocks' worth of time the append costs the wave that folds it
+  // vk_append_rope_decode with the append folded in: RoPE of the new K rows (the
+  // folding wave) and of every q row (each wave, in registers) at position
+  // context_len - 1; positions outside [0, rope_n_pos) rotate nothing and append
+  // nothing. Only with io_hd equal to the tile width (the half-split partner of
+  // a q chunk sits in lane ^ 32).
+  int32_t rope;             // RopeStyle
+  const float* cos_sin;     // [rope_n_pos][io_hd / 2][2]
+  int32_t rope_n_pos;
 };
 
 constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)

@@ -143,6 +143,8 @@ PROTOTYPES = {
     "vk_paged_decode_plan": [P, C.POINTER(DecodeArgs), C.POINTER(DecodePlan)],
     "vk_paged_decode_noalloc": [P, P, C.POINTER(DecodeArgs), P],
     "vk_append_decode": [P, P, P, P, I32, C.POINTER(DecodeArgs), P],
+    "vk_append_rope_decode": [P, P, P, P, I32, P, I32, I32, C.POINTER(DecodeArgs), P],
+    "vk_append_rope_decode_workspace": [P, C.POINTER(DecodeArgs), C.POINTER(U64)],
     "vk_tree_verify_workspace": [P, C.POINTER(TreeArgs), C.POINTER(U64)],
     "vk_tree_verify_plan": [P, C.POINTER(TreeArgs), C.POINTER(TreePlan)],
     "vk_tree_verify": [P, P, C.POINTER(TreeArgs), P],

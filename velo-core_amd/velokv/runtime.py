@@ -149,6 +149,19 @@ class Context:
         check(lib().vk_append_decode(self.h, pool.h, _bptr(k_new), _bptr(v_new), in_dtype, C.byref(a),
                                      _sptr(stream)))
 
+    def append_rope_decode(self, pool: "Pool", layer: int, k_new, v_new, in_dtype: int, cos_sin, n_pos: int,
+                           rope_style: int, q, q_dtype: int, out, context_lens, n_seqs: int, n_heads: int,
+                           max_context_len: int, block_tables=None, bt_stride: int = 0, seq_rows=None,
+                           scale: float = 0.0, partition_tokens: int = 0, workspace=None, workspace_bytes: int = 0,
+                           stream=None, sum_context_len: int = 0):
+        """vk_append_rope_decode: RoPE at context_len - 1 of the new K rows and of q (q left unchanged), the
+        append, then decode over the rotated q."""
+        a = _capi.DecodeArgs(layer, _bptr(q), q_dtype, _bptr(out), _bptr(block_tables), bt_stride, _bptr(seq_rows),
+                             _bptr(context_lens), n_seqs, n_heads, max_context_len, scale, partition_tokens,
+                             _bptr(workspace), workspace_bytes, sum_context_len)
+        check(lib().vk_append_rope_decode(self.h, pool.h, _bptr(k_new), _bptr(v_new), in_dtype, _bptr(cos_sin),
+                                          n_pos, rope_style, C.byref(a), _sptr(stream)))
+
     def paged_decode_noalloc(self, pool: "Pool", layer: int, q, q_dtype: int, out, context_lens, n_seqs: int,
                              n_heads: int, max_context_len: int, block_tables=None, bt_stride: int = 0,
                              seq_rows=None, scale: float = 0.0, partition_tokens: int = 0, stream=None,
@@ -185,6 +198,16 @@ class Context:
                              n_seqs, n_heads, max_context_len, 0.0, partition_tokens, None, 0, sum_context_len)
         n = C.c_uint64()
         check(lib().vk_paged_decode_workspace(pool.h, C.byref(a), C.byref(n)))
+        return n.value
+
+    def append_rope_decode_workspace_bytes(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0,
+                                           partition_tokens=0, q_dtype=DT_F16, sum_context_len=0) -> int:
+        """vk_append_rope_decode_workspace: the decode's workspace, plus the rotated
+        q rows when the RoPE is not folded into the decode kernel."""
+        a = _capi.DecodeArgs(0, None, q_dtype, None, C.c_void_p(1) if bt_stride else None, bt_stride, None, None,
+                             n_seqs, n_heads, max_context_len, 0.0, partition_tokens, None, 0, sum_context_len)
+        n = C.c_uint64()
+        check(lib().vk_append_rope_decode_workspace(pool.h, C.byref(a), C.byref(n)))
         return n.value
 
     def decode_kernel_name(self, pool: "Pool", n_seqs, n_heads, max_context_len, bt_stride=0, partition_tokens=0,
