@@ -411,9 +411,10 @@ int vk_paged_decode_noalloc(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a,
 typedef struct vk_tree_args {
   int32_t layer;
   const void* q;              /* dev [S][n_nodes][n_heads][head_dim] of q_dtype */
-  int32_t q_dtype;            /* VK_DT_F16, or VK_DT_F32 (rounded to fp16 for the
-                                 fp16 / int8 matrix-core kernels, kept in fp32
-                                 over fp32 KV) */
+  int32_t q_dtype;            /* VK_DT_F16, or VK_DT_F32 (split into fp16 hi +
+                                 lo for the fp16 / int8 matrix-core kernels, each
+                                 score taking both products, so q keeps about 22
+                                 bits; kept in fp32 over fp32 KV) */
   float* out;                 /* dev fp32 [S][n_nodes][n_heads][head_dim]       */
   const int32_t* block_tables;/* dev [rows][bt_stride]; NULL = slot table        */
   int32_t bt_stride;

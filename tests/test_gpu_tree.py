@@ -310,3 +310,40 @@ def test_tree_shared_prefix_bad_arguments(ctx):
             ctx.tree_verify(pool, 0, q, velokv.DT_F16, out, cl, mk, case.S, 4, case.n_heads, 80, block_tables=bt,
                             bt_stride=case.block_tables.shape[1], shared_blocks=shared)
         assert e.value.code == velokv.ERR_BAD_ARG
+
+
+# The bound of the fp32-q test, 4-5x tighter than the north-star tolerance
+# (2e-3 + 1e-2 |ref|); q rounded to fp16 misses it on the test's inputs
+TIGHT = {O.F16: dict(atol=5e-4, rtol=2e-3), O.I8_BLK: dict(atol=5e-4, rtol=2e-3)}
+
+
+@pytest.mark.parametrize("shared", [False, True])
+@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
+def test_tree_fp32_q_keeps_its_precision(ctx, kv, shared):
+    """An fp32 q with x20 outlier channels (values fp16 does not hold): the tree
+    kernels and the shared-prefix pass split q into fp16 hi + lo and take both
+    products per score, as the reference's tree kernel computes q.k in fp32
+    (kernels.metal:512-599). Outputs match the oracle's fp32-q tree verify within
+    the bound TIGHT, which the same q rounded to fp16 misses (checked on the
+    oracle itself). K and V have no outlier channels here: the value product's
+    fp16 p * v_scale, a rounding apart from q's, grows with |v|."""
+    print(f"tree fp32 q precision kv={kv} shared={shared}", flush=True)
+    from test_gpu_decode import outlier_q
+    N, P = 8, 24
+    committed = np.array([P * BS + 300, 1, 15, 16, 100, P * BS + 5, 700, P * BS], np.int32)
+    case = tree_case(kv, committed, N, seed=341)
+    bt = case.block_tables.copy()
+    if shared:  # every row reads row 0's first P pages (row 0 holds the longest context, so they are written)
+        bt[:, :P] = bt[0, :P]
+    ref_layer = oracle_layer(case)
+    pool = gpu_pool(ctx, case)
+    q = outlier_q((case.S, N, case.n_heads, HD), 342, 20.0)
+    mask = np.tile(mask_222(N), (case.S, 1))
+    got = run_tree(ctx, pool, case, q, committed, mask, q_dtype=np.float32, block_tables=bt,
+                   shared_blocks=P if shared else 0)
+    ref = O.tree_verify(ref_layer, q, bt, committed, mask)
+    ok, err, nbad = tol_check(got, ref, **TIGHT[kv])
+    print(f"  max abs err {err:.3g}", flush=True)
+    assert ok, f"fp32 q: max err {err:.3g}, {nbad} elements out of the tight bound"
+    r16 = O.tree_verify(ref_layer, q.astype(np.float16), bt, committed, mask)
+    assert not tol_check(r16, ref, **TIGHT[kv])[0], "the bound does not separate fp16-rounded q"

@@ -1234,7 +1234,7 @@ DEV float f4_at(const float4& v, int r) { return r == 0 ? v.x : r == 1 ? v.y : r
 
 // Rows of a unit: RT tiles of 16 query rows. Row R of the (sequence, KV head)
 // pair is (node R / G, head kvh*G + R % G); decode has one node.
-// An fp32 q (QT == DT_F32) is rounded to fp16 for the matrix cores.
+// An fp32 q (QT == DT_F32) is split into fp16 hi + lo parts for the matrix cores.
 // One piece of work: tokens [start, end) of (sequence s, KV head kvh), row group
 // rg, committed context ctx_c. direct: the piece is the whole context and writes
 // normalised rows; otherwise it writes the unnormalised partial (acc, M, l) of
@@ -1296,7 +1296,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   // (ctx_c - 1), as the RoPE append would have rotated it in memory; its loads
   // go out before the first stage's
   static_assert(!ROPE || RT == 1, "the RoPE decode has one tile of rows");
-  constexpr bool QSPLIT = (QT == DT_F32) && !TREE;
+  constexpr bool QSPLIT = (QT == DT_F32);
   RopeQ<QT, KC> rq;
   if constexpr (ROPE)
     rope_q_issue<QT, KC>(rq, P, out_row(row0 + n) * P.io_hd + 8 * KC * g, out_row(0) * P.io_hd + 8 * KC * g,
@@ -1306,14 +1306,20 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
   mstage_load<KV, D>(sa, P, bw, 0, nblk, kvh, n, g);
 
   // q^T as the B operand: row n of each tile (rows >= nrows are zero and their
-  // results are dropped), dims 32g..32g+31 in 4 chunks (D = 64: 16g..16g+15 in 2). An fp32 q of the decode
-  // kernels is split as q = hi + lo, hi = fp16(q), lo = fp16(q - hi), and each
-  // score takes two products (hi, then lo, into the same accumulator), so the
-  // scores see q to about 2^-22 instead of fp16's 2^-11; the tree kernels
-  // round an fp32 q to fp16.
+  // results are dropped), dims 32g..32g+31 in 4 chunks (D = 64: 16g..16g+15 in 2). An fp32 q
+  // is split as q = hi + lo, hi = fp16(q), lo = fp16(q - hi), and each score
+  // takes two products (hi, then lo, into the same accumulator), so the scores
+  // see q to about 2^-22 instead of fp16's 2^-11.
   half8 qa[RT][KC];
   half8 qlo[RT][KC];
-  float qb[RT];        // int8 KV: 1152 * sum_d q[row n][d] (of hi + lo when split)
+  // int8 K enters the score products as fp16 1152 + c (two v_perm per four
+  // codes) and the decode subtracts qb = 1152 * sum_d q[row n][d] (of hi + lo
+  // when split) from each score; its fp32 sums then carry 1152 sum q, rounded in
+  // proportion to sum |q| (within the north-star tolerance for queries with x30
+  // outlier channels). Tree verify subtracts 1152 from the codes in fp16 first
+  // (exact) and needs no qb: its fp32 queries keep their precision.
+  constexpr bool KBIAS = I8 && !TREE;
+  float qb[RT];
   uint32_t mrow[RT];   // tree: mask row of row n's node
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -1345,14 +1351,14 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
         qlo[rt][kc] = bitcast<half8>(vlo);
       }
     }
-    if constexpr (I8) {
+    if constexpr (KBIAS) {
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
         for (int j = 0; j < 8; ++j) qsum += QSPLIT ? (float)qa[rt][kc][j] + (float)qlo[rt][kc][j] : (float)qa[rt][kc][j];
     }
     qb[rt] = 0.f;
-    if constexpr (I8) {
+    if constexpr (KBIAS) {
       qsum += shfl_xor(qsum, 16);
       qsum += shfl_xor(qsum, 32);   // full sum of row n
       qb[rt] = kBias * qsum;
@@ -1390,6 +1396,11 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
         if constexpr (I8) {
           i8x4_to_h2x2_biased(st.k[u].d[2 * kc], kb[0], kb[1]);
           i8x4_to_h2x2_biased(st.k[u].d[2 * kc + 1], kb[2], kb[3]);
+          if constexpr (!KBIAS) {  // (1152 + c) - 1152 = c exactly
+            const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) kb[w] = bitcast<uint32_t>(bitcast<half2v>(kb[w]) - bias);
+          }
         } else {
 #pragma unroll
           for (int w = 0; w < 4; ++w) kb[w] = st.k[u].d[4 * kc + w];
@@ -1422,7 +1433,7 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
         for (int r = 0; r < 4; ++r) {
           float ksr = kscale;
           if constexpr (REF) ksr *= f4_at(st.ks[u], r);
-          float x = I8 ? (sc[rt][u][r] - qb[rt]) * ksr : sc[rt][u][r] * ksr;
+          float x = KBIAS ? (sc[rt][u][r] - qb[rt]) * ksr : sc[rt][u][r] * ksr;
           if (!plain) {
             const int tpos = tpos0 + r;
             bool ok = (i < nblk) && tpos < end;
@@ -2188,7 +2199,11 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
 // loaded by the first 8 waves, converted to fp16 (int8 codes become 1152 + c
 // exactly, as in attn_piece) and written to LDS; every wave then runs its score
 // and value products on the matrix cores against the staged tiles, two blocks
-// at a time, with the lazy running max of attn_piece. Row r of sequence s sees
+// at a time, with the lazy running max of attn_piece. int8 K is staged as the
+// codes c themselves ((1152 + c) - 1152 in fp16, exact), so a score needs no
+// bias term: with the biased codes of attn_piece the fp32 sums carry
+// 1152 sum q, whose rounding grows with sum |q| (queries with outlier channels
+// lost 0.1 and more of a score). Row r of sequence s sees
 // prefix positions below prefix_tokens_of(ctx_s, pb). The chunk's unnormalised
 // partial (acc, M, l) goes to partial slot `chunk` of the row; the tree kernel
 // writes the rest of the context to the slots that follow and vk_decode_merge
@@ -2200,8 +2215,8 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
 //           B = staged V (dim 16 nt + n); lane (n, g) accumulates rows 4g..4g+3,
 //           dims 16 nt + n. int8 V is staged as fp16 c * v_scale (one rounding),
 //           so the product needs no scale and no bias term.
-//   softmax y = S a + c with a = scale_log2 * k_scale and c = -(1152 sum q) a - M
-//           folded per block, p = 2^y; l sums the fp16 p pairs with v_dot2.
+//   softmax y = S a - M with a = scale_log2 * k_scale folded per block,
+//           p = 2^y; l sums the fp16 p pairs with v_dot2.
 // LDS: two stage buffers, one barrier per stage; a loader thread holds the
 // next stage's raw bytes in registers while the current one is consumed. The
 // chunk's page ids and block scales are staged in LDS once at the start, so the
@@ -2234,7 +2249,6 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   constexpr int RT = kPfxRT;
   constexpr bool I8 = (KV == KV_I8_BLK);
   constexpr int ESZ = Esz<KV>::v;
-  constexpr float kBias = 1152.0f;
   __shared__ __attribute__((aligned(16))) _Float16 kl[2][kPfxCH][BS * kPfxKPitch];
   __shared__ __attribute__((aligned(16))) _Float16 vl[2][kPfxCH / 2][HD * kPfxVPitch];
   // the chunk's tiles (page id * n_kv_heads + kvh) and (int8) block scales: K
@@ -2288,39 +2302,35 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   }
   __syncthreads();
 
-  // ---- q^T operands of rows wrow0 + 16 rt + n, and the prefix each row sees ----
+  // ---- q^T operands of rows wrow0 + 16 rt + n, and the prefix each row sees.
+  // An fp32 q is split as q = hi + lo (fp16 each) and each score takes both
+  // products, as in attn_piece ----
+  constexpr bool QSPLIT = (QT == DT_F32);
   half8 qa[RT][4];
-  float qb[RT];
+  half8 qlo[RT][QSPLIT ? 4 : 1];
   int lim[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int r = wrow0 + 16 * rt + n;
     const bool valid = r < R;
     const int64_t qoff = (valid ? out_row(r) : 0) * P.io_hd + 8 * g;
-    float qsum = 0.f;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
-      uint4 v = make_uint4(0, 0, 0, 0);
+      uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
       if (valid && 32 * kc + 8 * g < P.io_hd) {
         if constexpr (QT == DT_F32) {
           const float4* q32 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(P.q) + qoff + 32 * kc);
           const float4 x0 = q32[0], x1 = q32[1];
           v = make_uint4(pack_h2(x0.x, x0.y), pack_h2(x0.z, x0.w), pack_h2(x1.x, x1.y), pack_h2(x1.z, x1.w));
+          const half8 h = bitcast<half8>(v);
+          vlo = make_uint4(pack_h2(x0.x - (float)h[0], x0.y - (float)h[1]), pack_h2(x0.z - (float)h[2], x0.w - (float)h[3]),
+                           pack_h2(x1.x - (float)h[4], x1.y - (float)h[5]), pack_h2(x1.z - (float)h[6], x1.w - (float)h[7]));
         } else {
           v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(P.q) + qoff + 32 * kc);
         }
       }
       qa[rt][kc] = bitcast<half8>(v);
-      if constexpr (I8) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) qsum += (float)qa[rt][kc][j];
-      }
-    }
-    qb[rt] = 0.f;
-    if constexpr (I8) {
-      qsum += shfl_xor(qsum, 16);
-      qsum += shfl_xor(qsum, 32);
-      qb[rt] = kBias * qsum;
+      if constexpr (QSPLIT) qlo[rt][kc] = bitcast<half8>(vlo);
     }
     // rows past the end see the whole chunk (their results are dropped)
     lim[rt] = valid ? prefix_tokens_of(max(0, min(P.context_lens[r / RS], P.cap_tokens)), PB) : PB * BS;
@@ -2394,11 +2404,14 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       if constexpr (ESZ == 1) {
         i8x4_to_h2x2_biased(rw.k[u][0], kw0, kw1);
         i8x4_to_h2x2_biased(rw.v[u][0] | (rw.v[u][1] << 16), vw0, vw1);
-        // (1152 + c) - 1152 = c exactly, then one rounding of c * v_scale
+        // (1152 + c) - 1152 = c exactly (K), then one rounding of c * v_scale (V)
+        const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        kw0 = bitcast<uint32_t>(bitcast<half2v>(kw0) - bias);
+        kw1 = bitcast<uint32_t>(bitcast<half2v>(kw1) - bias);
         const int b = cb0 + st * kPfxCH + u;
         const int bi = (st < nst && b < cb1) ? b - cb0 : 0;
         const _Float16 vsh = bitcast<_Float16>(pvs[bi]);
-        const half2v vs2 = {vsh, vsh}, bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const half2v vs2 = {vsh, vsh};
         vw0 = bitcast<uint32_t>((bitcast<half2v>(vw0) - bias) * vs2);
         vw1 = bitcast<uint32_t>((bitcast<half2v>(vw1) - bias) * vs2);
       } else {
@@ -2428,7 +2441,10 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       for (int rt = 0; rt < RT; ++rt) {
         float4v sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kc], qa[rt][kc], sc, 0, 0, 0);
+        for (int kc = 0; kc < 4; ++kc) {
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kc], qa[rt][kc], sc, 0, 0, 0);
+          if constexpr (QSPLIT) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kc], qlo[rt][kc], sc, 0, 0, 0);
+        }
         scv[rt][j] = sc;
       }
     }
@@ -2453,7 +2469,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float c = (I8 ? fmaf(-qb[rt], a[j], -Ms) : -Ms) + hide[rt][j];
+        const float c = -Ms + hide[rt][j];
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[rt][j][r] = fmaf(scv[rt][j][r], a[j], c);
       }
@@ -3397,8 +3413,9 @@ VK_DECODE_SK_G(0) VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
 VK_DECODE_SK_Q0_G(0) VK_DECODE_SK_Q0_G(1) VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G(3)
 
 // Tree verify: RT tiles of 16 (node, head) rows per wave. Over int8 pools the
-// kernels are held to 256 registers (two waves per SIMD) without spills; the fp16
-// ones would spill, so they keep one wave per SIMD.
+// kernels are held to 256 registers (two waves per SIMD); the fp16 ones would
+// spill, so they keep one wave per SIMD, and so do the int8 two-tile kernels of
+// an fp32 q, whose lo parts (32 registers more) would spill at two waves.
 #define VK_TREE(KV, G, RT, QT, ATTR)                                                \
   extern "C" __global__ void __launch_bounds__(64) ATTR                             \
       vk_tree_kv##KV##_g##G##_r##RT##_q##QT(const DecodeParams P) {                 \
@@ -3406,12 +3423,12 @@ VK_DECODE_SK_Q0_G(0) VK_DECODE_SK_Q0_G(1) VK_DECODE_SK_Q0_G(2) VK_DECODE_SK_Q0_G
   }
 #define VK_TREE_G(KV, RT, QT, ATTR) \
   VK_TREE(KV, 1, RT, QT, ATTR) VK_TREE(KV, 2, RT, QT, ATTR) VK_TREE(KV, 4, RT, QT, ATTR) VK_TREE(KV, 8, RT, QT, ATTR)
-#define VK_TREE_KV(KV, ATTR) \
-  VK_TREE_G(KV, 1, 0, ATTR) VK_TREE_G(KV, 1, 1, ATTR) VK_TREE_G(KV, 2, 0, ATTR) VK_TREE_G(KV, 2, 1, ATTR)
-VK_TREE_KV(0, )
-VK_TREE_KV(1, )
-VK_TREE_KV(2, VK_TWO_WAVES)
-VK_TREE_KV(3, VK_TWO_WAVES)
+#define VK_TREE_KV(KV, ATTR, ATTR_R2Q0) \
+  VK_TREE_G(KV, 1, 0, ATTR) VK_TREE_G(KV, 1, 1, ATTR) VK_TREE_G(KV, 2, 0, ATTR_R2Q0) VK_TREE_G(KV, 2, 1, ATTR)
+VK_TREE_KV(0, , )
+VK_TREE_KV(1, , )
+VK_TREE_KV(2, VK_TWO_WAVES, )
+VK_TREE_KV(3, VK_TWO_WAVES, )
 
 // Any other GQA group size ("_gx"): the group size is n_heads / n_kv_heads at run
 // time, at most 16 rows per tile (decode), two tiles ("_gx2", split-K) up to 32.
@@ -3502,9 +3519,9 @@ VK_ROPE_ALL(VK_ROPE_SK, 1) VK_ROPE_ALL(VK_ROPE_SK, 3) VK_ROPE_ALL(VK_ROPE_WG, 3)
   extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_r##RT##_q##QT(const DecodeParams P) { \
     attn_unit_mfma<KV, 0, RT, true, QT>(P);                                                                    \
   }
-#define VK_GX_TREE_KV(KV, ATTR) \
-  VK_GX_TREE(KV, 1, 0, ATTR) VK_GX_TREE(KV, 1, 1, ATTR) VK_GX_TREE(KV, 2, 0, ATTR) VK_GX_TREE(KV, 2, 1, ATTR)
-VK_GX_TREE_KV(0, ) VK_GX_TREE_KV(1, ) VK_GX_TREE_KV(2, VK_TWO_WAVES) VK_GX_TREE_KV(3, VK_TWO_WAVES)
+#define VK_GX_TREE_KV(KV, ATTR, ATTR_R2Q0) \
+  VK_GX_TREE(KV, 1, 0, ATTR) VK_GX_TREE(KV, 1, 1, ATTR) VK_GX_TREE(KV, 2, 0, ATTR_R2Q0) VK_GX_TREE(KV, 2, 1, ATTR)
+VK_GX_TREE_KV(0, , ) VK_GX_TREE_KV(1, , ) VK_GX_TREE_KV(2, VK_TWO_WAVES, ) VK_GX_TREE_KV(3, VK_TWO_WAVES, )
 
 // Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
 #define VK_TREE_PFX(KV, G, QT)                                                      \
