@@ -76,7 +76,7 @@ def parse():
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--kv-heads", type=int, default=8)
     ap.add_argument("--pool-blocks", type=int, default=40000, help="pool capacity in 16-token blocks")
-    ap.add_argument("--page", type=int, default=16, help="decode workload: tokens per page (16, 32, 64, 128, 256)")
+    ap.add_argument("--page", type=int, default=16, help="decode workload: tokens per page (16 k, k = 1..16)")
     ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128], help="decode workload: head_dim")
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = auto)")
     ap.add_argument("--q-dtype", choices=["fp16", "fp32"], default="fp16",

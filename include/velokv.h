@@ -32,8 +32,8 @@
  *
  * Layout of one layer of a pool in HBM ("build layout"; the reference layout
  * is [blk][tok][head][D(+4)], kernels.metal:474,700). The unit is a tile of 16
- * tokens and 128 dims per KV head; a page of block_size = 16 << s tokens is the
- * 2^s tiles n_tiles = page << s .. (page + 1 << s) - 1, so a flat slot
+ * tokens and 128 dims per KV head; a page of block_size = 16 k tokens is the
+ * k tiles page * k .. (page + 1) * k - 1, so a flat slot
  * page * block_size + offset is also tile * 16 + offset % 16:
  *    K codes   [n_tiles][n_kv_heads][16][128] for F32 / F16;
  *              I8_*: [n_tiles][n_kv_heads][2][16][4][16] (dims 32c..32c+15 of
@@ -189,8 +189,9 @@ typedef struct vk_pool_desc {
   int32_t n_layer;        /* MemoryRuntimeConfig::n_layer (runtime.rs:55)          */
   int32_t n_blocks;       /* MemoryRuntimeConfig::paged_total_pages (runtime.rs:53) */
   int32_t block_size;     /* MemoryRuntimeConfig::paged_block_size (runtime.rs:51):
-                             16, 32, 64, 128 or 256 tokens per page; other sizes >
-                             0 are VK_ERR_UNSUPPORTED, 0 VK_ERR_INVALID_BLOCK_SIZE */
+                             16 k tokens per page, k = 1..16 (16, 32, 48 .. 256);
+                             other sizes > 0 are VK_ERR_UNSUPPORTED, 0
+                             VK_ERR_INVALID_BLOCK_SIZE */
   int32_t n_kv_heads;     /* ModelMeta::n_head_kv                                  */
   int32_t head_dim;       /* ModelMeta::head_dim: a multiple of 8 up to 128 (64- or
                              128-dim tiles, zero-padded past head_dim)            */

@@ -1,9 +1,9 @@
-"""GPU parity for pages of 32, 64 and 256 tokens (the reference takes any
+"""GPU parity for pages of 32, 48, 64 and 256 tokens (the reference takes any
 paged_block_size > 0, paged_attention.rs:103-106, metal/runtime.rs:152-155,
 and indexes the cache with it at kernels.metal:472, 637-640, 770-774).
 
-The kernels work on 16-token tiles; a page of 16 << s tokens is 2^s tiles back
-to back, so a flat slot page * page_tokens + offset is also tile * 16 + offset
+The kernels work on 16-token tiles; a page of 16 k tokens is k tiles back
+to back (48 tokens: 3 tiles, the page and the tile in it found by division), so a flat slot page * page_tokens + offset is also tile * 16 + offset
 % 16 and the pool bytes equal those of a 16-token pool whose tables list the
 pages' tiles. The checks therefore compare against the oracle on the expanded
 16-token tables (bit-exact pool bytes, decode and tree verify within the
@@ -66,7 +66,7 @@ def page_oracle(case, pt, page, n_pages):
 
 
 @pytest.mark.parametrize("kv", KV_ALL)
-@pytest.mark.parametrize("page", [32, 64, 256])
+@pytest.mark.parametrize("page", [32, 48, 64, 256])
 def test_page_append_bit_exact(ctx, kv, page):
     print(f"page append kv={kv} page={page}", flush=True)
     case, pt, n_pages = page_case(kv, [1, 15, 16, 17, 31, 33, 100, 257, 600], page, seed=1300 + page)
@@ -81,7 +81,7 @@ SCHEDS = {"split": (velokv.DECODE_MFMA, velokv.SCHED_SPLIT, 0), "split-p48": (ve
 
 
 @pytest.mark.parametrize("kv", KV_ALL)
-@pytest.mark.parametrize("page", [32, 64, 256])
+@pytest.mark.parametrize("page", [32, 48, 64, 256])
 @pytest.mark.parametrize("sched", list(SCHEDS))
 def test_page_decode(ctx, kv, page, sched):
     print(f"page decode kv={kv} page={page} sched={sched}", flush=True)
@@ -139,7 +139,7 @@ def test_page_workgroup_split_and_append_decode(ctx, kv):
 
 
 @pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_BLK])
-@pytest.mark.parametrize("page,shared", [(32, 0), (32, 3), (64, 2)])
+@pytest.mark.parametrize("page,shared", [(32, 0), (32, 3), (48, 0), (48, 3), (64, 2)])
 def test_page_tree_verify(ctx, kv, page, shared):
     """Tree verify over page tables, with the shared-prefix pass over the first
     `shared` pages of every row (fp16 / I8_BLK) or without."""
@@ -218,12 +218,13 @@ def test_page_copy_blocks_moves_whole_pages(ctx, kv):
     assert_layer_equal(pool, 0, ref)
 
 
+@pytest.mark.parametrize("page", [32, 48])
 @pytest.mark.parametrize("kv", [O.F32, O.I8_BLK])
-def test_page_tree_commit(ctx, kv):
-    """Accepted-path commit over 32-token pages equals the oracle's commit on the
-    expanded tile tables."""
-    print(f"page commit kv={kv}", flush=True)
-    page, N = 32, 8
+def test_page_tree_commit(ctx, kv, page):
+    """Accepted-path commit over 32- and 48-token pages equals the oracle's
+    commit on the expanded tile tables."""
+    print(f"page commit kv={kv} page={page}", flush=True)
+    N = 8
     ctxs = np.array([0, 14, 30, 31, 32, 60, 100], np.int32)
     case, pt, n_pages = page_case(kv, ctxs + N, page, seed=1360)
     pool = page_pool(ctx, case, page, n_pages)
@@ -245,13 +246,14 @@ def test_page_tree_commit(ctx, kv):
     assert_layer_equal(pool, 0, ref)
 
 
+@pytest.mark.parametrize("page", [32, 48])
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
-def test_page_nixl_round_trip(ctx, kv):
-    """NIXL records over 32-token pages: the payload of a (page, layer) unit is
-    the page's K codes (its tiles back to back), V codes, then the scales; pack
-    then unpack into other pages restores the bytes exactly."""
-    print(f"page nixl kv={kv}", flush=True)
-    page, k, n_layer = 32, 2, 2
+def test_page_nixl_round_trip(ctx, kv, page):
+    """NIXL records over 32- and 48-token pages: the payload of a (page, layer)
+    unit is the page's K codes (its tiles back to back), V codes, then the
+    scales; pack then unpack into other pages restores the bytes exactly."""
+    print(f"page nixl kv={kv} page={page}", flush=True)
+    k, n_layer = page // BS, 2
     case, pt, n_pages = page_case(kv, [70, 33], page, seed=1370)
     pool = velokv.Pool(ctx, n_layer, n_pages, page, case.n_kv_heads, HD, kv)
     sl, kk, vv = case.prefill_slots()
@@ -265,7 +267,7 @@ def test_page_nixl_round_trip(ctx, kv):
         items.append((500 + s, tl, len(pages), off))
         pages += pt[s, :np_].tolist()
         off = (off + 16 + pool.nixl_payload_bytes(tl) + 15) // 16 * 16
-    assert pool.nixl_payload_bytes(69) == 3 * pool.nixl_payload_bytes(32)  # whole pages
+    assert pool.nixl_payload_bytes(69) == -(-69 // page) * pool.nixl_payload_bytes(32)  # whole pages
     wire = ctx.upload(np.zeros(off, np.uint8))
     status = ctx.upload(np.full(2, -7, np.int32))
     ctx.nixl_pack(pool, items, ctx.upload(np.asarray(pages, np.int32)), len(pages), wire, off, status)
@@ -299,7 +301,7 @@ def test_page_nixl_round_trip(ctx, kv):
 
 
 def test_page_size_limits(ctx):
-    for bad in (8, 48, 512):
+    for bad in (8, 24, 40, 272, 512):
         with pytest.raises(velokv.VkError) as e:
             velokv.Pool(ctx, 1, 8, bad, 2, HD, O.F16)
         assert e.value.code == velokv.ERR_UNSUPPORTED, bad

@@ -48,7 +48,7 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr int kBS = 16;   // tokens per tile, the kernels' block
-constexpr int kMaxPageShift = 4;  // pages of up to 16 << 4 = 256 tokens
+constexpr int kMaxPageTiles = 16;  // pages of 16 * k tokens, k <= 16 (up to 256 tokens)
 constexpr int kHD = 128;  // head_dim the kernels are built for
 constexpr int kMaxPartTokens = 4096;  // 256 blocks: four block-id windows of one wave
 constexpr int kMaxTreeNodes = 32;     // one 32-bit mask row per node
@@ -71,14 +71,14 @@ int kv_stile(int kv, int bs) {
 }
 
 // Page view of a pool's geometry (COW copy, NIXL): one block = one page of
-// 16 << page_shift tokens, its tiles back to back.
+// 16 * page_tiles tokens, its tiles back to back.
 PoolGeom page_geom(const PoolGeom& t) {
   PoolGeom g = t;
-  g.tile_bytes = t.tile_bytes << t.page_shift;
-  g.stile_bytes = t.stile_bytes << t.page_shift;
-  g.n_blocks = t.n_blocks >> t.page_shift;
-  g.block_size = t.block_size << t.page_shift;
-  g.page_shift = 0;
+  g.tile_bytes = t.tile_bytes * (uint32_t)t.page_tiles;
+  g.stile_bytes = t.stile_bytes * (uint32_t)t.page_tiles;
+  g.n_blocks = t.n_blocks / t.page_tiles;
+  g.block_size = t.block_size * t.page_tiles;
+  g.page_tiles = 1;
   return g;
 }
 
@@ -435,24 +435,24 @@ extern "C" int vk_pool_create(vk_ctx* ctx, const vk_pool_desc* d, vk_pool** out)
   if (kv_esz(d->kv_type) == 0) return fail(VK_ERR_BAD_ARG, "unknown kv_type %d", d->kv_type);
   if (d->head_dim > kHD || d->head_dim % 8 != 0)
     return fail(VK_ERR_UNSUPPORTED, "head_dim %d: the kernels take multiples of 8 up to 128", d->head_dim);
-  int ps = 0;  // pages of 16 << ps tokens: 16-token tiles, 2^ps per page
-  while (ps < kMaxPageShift && (kBS << ps) < d->block_size) ++ps;
-  if ((kBS << ps) != d->block_size)
-    return fail(VK_ERR_UNSUPPORTED, "block_size %d: the kernels take pages of 16, 32, 64, 128 or 256 tokens",
-                d->block_size);
-  if (((int64_t)d->n_blocks << ps) > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "pool too large");
+  // pages of 16 * pt tokens: 16-token tiles, pt per page
+  const int pt = d->block_size / kBS;
+  if (d->block_size % kBS != 0 || pt > kMaxPageTiles)
+    return fail(VK_ERR_UNSUPPORTED, "block_size %d: the kernels take pages of 16 * k tokens, k = 1..%d", d->block_size,
+                kMaxPageTiles);
+  if ((int64_t)d->n_blocks * pt > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "pool too large");
   auto* p = new vk_pool();
   p->ctx = ctx;
   p->desc = *d;
   if (p->desc.max_pages_per_slot == 0) p->desc.max_pages_per_slot = d->n_blocks;
   const int esz = kv_esz(d->kv_type);
-  PoolGeom& g = p->geom;  // tile view: 16-token tiles, 2^ps per page
+  PoolGeom& g = p->geom;  // tile view: 16-token tiles, pt per page
   // a tile holds 16 tokens of one head, 64 or 128 dims wide (zeros past head_dim)
   const int tw = tile_hd(d->head_dim);
   g.tile_bytes = (uint32_t)(kBS * tw * esz);
   g.stile_bytes = (uint32_t)kv_stile(d->kv_type, kBS);
-  g.n_blocks = d->n_blocks << ps;
-  g.page_shift = ps;
+  g.n_blocks = d->n_blocks * pt;
+  g.page_tiles = pt;
   g.n_kv_heads = d->n_kv_heads;
   g.block_size = kBS;
   g.head_dim = tw;
@@ -1075,7 +1075,7 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   p.n_heads = a->n_heads;
   p.n_kv_heads = d.n_kv_heads;
   p.n_blocks = d.n_blocks;
-  p.page_shift = g.page_shift;
+  p.page_tiles = g.page_tiles;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
   // stream-K: contexts are clamped to max_context_len, which bounds every worker's
@@ -1241,7 +1241,7 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
     pl->pfx_row_tiles = (int32_t)((qrows + kPfxRowsPerGroup - 1) / kPfxRowsPerGroup);
     const int64_t groups = std::max<int64_t>(1, (int64_t)pl->pfx_row_tiles * d.n_kv_heads);
     const int64_t n_cu = ctx ? ctx->n_cu : 256;
-    const int32_t tiles = a->shared_blocks << pool->geom.page_shift;  // the prefix in 16-token tiles
+    const int32_t tiles = a->shared_blocks * pool->geom.page_tiles;  // the prefix in 16-token tiles
     const int64_t max_chunks = std::max(1, tiles / 16);
     const int64_t min_chunks = (tiles + kPfxMaxChunkBlocks - 1) / kPfxMaxChunkBlocks;
     pl->prefix_chunks = (int32_t)std::max(
@@ -1350,7 +1350,7 @@ extern "C" int vk_tree_verify(vk_ctx* ctx, vk_pool* pool, const vk_tree_args* a,
   p.n_heads = a->n_heads;
   p.n_kv_heads = d.n_kv_heads;
   p.n_blocks = d.n_blocks;
-  p.page_shift = pool->geom.page_shift;
+  p.page_tiles = pool->geom.page_tiles;
   p.max_parts = pl.max_parts;
   p.part_tokens = pl.part_tokens;
   p.cap_tokens = (int32_t)std::min<int64_t>((int64_t)pl.prefix_blocks * kBS +

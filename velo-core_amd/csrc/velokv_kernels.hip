@@ -4,7 +4,7 @@
 // that the host library loads with hipModuleLoad and launches with
 // hipModuleLaunchKernel. Every kernel takes one argument struct (velokv_params.h).
 //
-// The kernels work on 16-token tiles (a page of 16 << s tokens is 2^s tiles back
+// The kernels work on 16-token tiles (a page of 16 k tokens is k tiles back
 // to back) and 128-dim rows in registers; a head_dim-64 pool stores 64-dim tiles,
 // which the loaders read into the lower half of those rows (the upper half takes
 // a copy of the lower one and meets zero q dims; outputs keep the lower half).
@@ -213,7 +213,7 @@ struct BlockIds {
 };
 // A page id outside [0, n_blocks) is clamped into the pool (the read stays in
 // bounds) and reported as MISUSE_PAGE_OUT_OF_POOL. Tile u of a sequence (tokens
-// 16u .. 16u + 15) is tile u % 2^page_shift of page bt[u >> page_shift]. Lanes
+// 16u .. 16u + 15) is tile u % page_tiles of page bt[u / page_tiles]. Lanes
 // past the piece's nblk blocks hold its last block. Every load is issued
 // outside any branch (lanes past nblk read the last block's entries) and the
 // scale words are kept as loaded: a load in a branch, or a use here, would wait
@@ -222,11 +222,11 @@ struct BlockIds {
 template <bool BLK>
 DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, int blk0, int nblk, int kvh) {
   const int lane = lane_id();
-  const int ps = P.page_shift;
+  const uint32_t pt = (uint32_t)P.page_tiles;
   const int last = max(nblk - 1, 0);
   int raw[kWin];
 #pragma unroll
-  for (int k = 0; k < kWin; ++k) raw[k] = bt[(blk0 + min(64 * k + lane, last)) >> ps];
+  for (int k = 0; k < kWin; ++k) raw[k] = bt[(uint32_t)(blk0 + min(64 * k + lane, last)) / pt];
   bool bad = false;
   w.oob = 0u;
 #pragma unroll
@@ -236,7 +236,7 @@ DEV void load_block_ids(BlockIds& w, const DecodeParams& P, const int32_t* bt, i
     const bool out = idx < nblk && (raw[k] < 0 || raw[k] >= P.n_blocks);
     bad |= out;
     w.oob |= out ? 1u << k : 0u;
-    w.b[k] = (min(max(raw[k], 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
+    w.b[k] = min(max(raw[k], 0), P.n_blocks - 1) * (int)pt + (int)((uint32_t)u % pt);
     w.sw[k] = 0u;
     if constexpr (BLK)  // the (K, V) scale word of the (block, head): one load
       w.sw[k] = *reinterpret_cast<const uint32_t*>(P.ks + ((int64_t)w.b[k] * P.n_kv_heads + kvh) * kBlkScaleStep);
@@ -2286,10 +2286,11 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   {
     bool bad = false;
     for (int i = tid; i < cb1 - cb0; i += (int)blockDim.x) {
-      const int u = cb0 + i, ps = P.page_shift;
-      const int raw = bt[u >> ps];
+      const int u = cb0 + i;
+      const uint32_t pt = (uint32_t)P.page_tiles;
+      const int raw = bt[(uint32_t)u / pt];
       bad |= raw < 0 || raw >= P.n_blocks;
-      const int b = (min(max(raw, 0), P.n_blocks - 1) << ps) | (u & ((1 << ps) - 1));
+      const int b = min(max(raw, 0), P.n_blocks - 1) * (int)pt + (int)((uint32_t)u % pt);
       const uint32_t tix = (uint32_t)b * (uint32_t)P.n_kv_heads + (uint32_t)kvh;
       pid[i] = tix;
       if constexpr (I8) {  // the (K, V) scale word of the (page, head)
@@ -2707,11 +2708,11 @@ DEV int64_t token_slot(const AppendParams& P, int m) {
     slot = P.slot_mapping[m];
   } else {  // the new token of sequence m, at its last context position (kernels.metal:770-774)
     const int pos = min(P.context_lens[m], P.cap_tokens) - 1;
-    const int ps = 4 + P.g.page_shift;  // log2 of the page's tokens
-    if (pos < 0 || (pos >> ps) >= P.bt_stride) return -1;
+    const int ptok = BS * P.g.page_tiles;  // the page's tokens
+    if (pos < 0 || pos / ptok >= P.bt_stride) return -1;
     int row = P.seq_rows ? P.seq_rows[m] : m;
     if (P.bt_rows > 0) row = min(max(row, 0), P.bt_rows - 1);
-    slot = ((int64_t)P.block_tables[(int64_t)row * P.bt_stride + (pos >> ps)] << ps) + (pos & ((1 << ps) - 1));
+    slot = (int64_t)P.block_tables[(int64_t)row * P.bt_stride + pos / ptok] * ptok + pos % ptok;
   }
   if (slot < 0 || slot >= (int64_t)P.g.n_blocks * BS) return -1;
   if (P.rope != ROPE_NONE) {
@@ -3292,17 +3293,17 @@ DEV void tree_commit(const CommitParams& P) {
   if (moved == 0) { report(COMMIT_OK); return; }  // every accepted node is already in place
   const int d0 = __builtin_ctzll(moved);
   const int last = ctx + readlane_i(a, na - 1);
-  const int ps = P.g.page_shift;
-  if ((int64_t)last >= ((int64_t)P.bt_stride << (4 + ps))) { report(COMMIT_PAST_TABLE); return; }
+  const int pt = P.g.page_tiles;
+  if ((int64_t)last >= (int64_t)P.bt_stride * BS * pt) { report(COMMIT_PAST_TABLE); return; }
   const int32_t* bt = P.block_tables + (int64_t)s * P.bt_stride;
   const int b_first = (ctx + d0) / BS, nb = last / BS - b_first + 1;  // at most 3 tiles
-  // tile b_first + lane: page bt[tile >> ps], tile (tile % 2^ps) of that page
-  const int pg = lane < nb ? bt[(b_first + lane) >> ps] : 0;
-  if (__builtin_amdgcn_ballot_w64(lane < nb && (pg < 0 || pg >= (P.g.n_blocks >> ps))) != 0) {
+  // tile b_first + lane: page bt[tile / page_tiles], tile (tile % page_tiles) of that page
+  const int pg = lane < nb ? bt[(b_first + lane) / pt] : 0;
+  if (__builtin_amdgcn_ballot_w64(lane < nb && (pg < 0 || pg >= P.g.n_blocks / pt)) != 0) {
     report(COMMIT_BAD_PAGE);
     return;
   }
-  const int blk_l = (pg << ps) | ((b_first + lane) & ((1 << ps) - 1));
+  const int blk_l = pg * pt + (b_first + lane) % pt;
   report(COMMIT_OK);
   // D as a constant, so that tile offsets fold into the instructions
   if (P.g.head_dim == HD) {

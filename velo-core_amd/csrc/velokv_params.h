@@ -17,11 +17,11 @@ enum DType : int32_t { DT_F32 = 0, DT_F16 = 1 };
 
 // Geometry of one layer of a pool (see include/velokv.h for the layout). The
 // kernels work on blocks of 16 tokens ("tiles"); a pool whose pages hold
-// 16 << page_shift tokens stores page p as tiles p << page_shift ..
-// (p + 1 << page_shift) - 1, back to back, so a flat slot page * page_tokens +
+// 16 * page_tiles tokens stores page p as tiles p * page_tiles ..
+// (p + 1) * page_tiles - 1, back to back, so a flat slot page * page_tokens +
 // offset is also tile * 16 + offset % 16. The tile view (append, decode,
 // commit) has n_blocks = tiles and block_size = 16; the page view (COW copy,
-// NIXL) has n_blocks = pages, block_size = page tokens, page_shift = 0 and the
+// NIXL) has n_blocks = pages, block_size = page tokens, page_tiles = 1 and the
 // tile sizes of a whole page.
 // I8_BLK scales: the K and V scale (fp16) of one (block, head) share one 4-byte
 // word, K in the low half: entry (block b, head h) of a layer's scale array is
@@ -38,7 +38,7 @@ struct PoolGeom {
   uint32_t s_step;         // bytes from one 16-bit unit of a kind's (K or V) scales to its next: 2 for
                            // I8_REF (contiguous), kBlkScaleStep for I8_BLK, 0 without scales
   int32_t n_blocks, n_kv_heads, block_size, head_dim, kv_type, n_layer;
-  int32_t page_shift;      // tile view: log2(page tokens / 16)
+  int32_t page_tiles;      // tile view: page tokens / 16
   int32_t io_hd;           // head_dim of the caller's K/V/q/out rows: any multiple of 8 up to
                            // 128; head_dim above is the tile width, 64 (io_hd <= 64) or 128,
                            // the dims past io_hd held as zeros
@@ -114,7 +114,7 @@ struct DecodeParams {
   int32_t bt_rows;          // rows of the block table when known (pool slot table), else 0
   int32_t n_seqs, n_heads, n_kv_heads;
   int32_t n_blocks;         // pages in the pool (block-table entries range)
-  int32_t page_shift;       // log2(page tokens / 16): table entry p holds tiles p << page_shift ..
+  int32_t page_tiles;       // page tokens / 16: table entry p holds tiles p * page_tiles .. (p + 1) * page_tiles - 1
   int32_t io_hd;            // head_dim: q / out row length (a multiple of 8 up to 128)
   int32_t tile_hd;          // tile width, 64 or 128 (>= io_hd; the dims past io_hd hold zeros)
   int32_t max_parts;        // partitions per sequence in the grid
