@@ -250,7 +250,7 @@ def run_gpu(ctx, args, kv_name: str):
     # vk_append_decode, whose decode appends each sequence's new token itself (one
     # launch per layer), with RoPE vk_append_rope_decode, whose decode also rotates
     # the new K row and q; otherwise the append and the decode are two launches
-    fused = ((kv == velokv.KV_I8_BLK and plan["wg_waves"] > 0) or
+    fused = ((kv == velokv.KV_I8_BLK and plan["schedule"] == velokv.SCHED_WORKGROUP) or
              (kv in (velokv.KV_I8_BLK, velokv.KV_F16) and plan["schedule"] == velokv.SCHED_STREAM))
 
     def append_decode(layer, r, o=None):

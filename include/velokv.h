@@ -337,10 +337,12 @@ int vk_paged_decode_kernel(const vk_pool* pool, const vk_decode_args* a, char* b
 typedef struct vk_decode_plan {
   char kernel[64];             /* attention kernel name                                */
   int32_t schedule;            /* VK_SCHED_SPLIT, _STREAM, _WORKGROUP or _PACKED       */
-  int32_t wg_waves;            /* workgroup / packed split: waves per workgroup        */
+  int32_t wg_waves;            /* waves per workgroup of the attention launch
+                                  (workgroup split, packed split, stream-K)          */
   int32_t partition_tokens;    /* fixed partitions: tokens per partition               */
   int32_t max_partitions;      /* fixed partitions: partitions of the longest context  */
-  int32_t n_workers;           /* stream-K: workers (one wave each); packed: workgroups */
+  int32_t n_workers;           /* stream-K: workers (one wave each, wg_waves of them
+                                  per workgroup); packed: workgroups                 */
   int32_t max_blocks_per_wave; /* the most blocks one wave can walk (<= 256)           */
   uint64_t workspace_bytes;    /* split-K scratch the call needs                       */
   int32_t merge_launch;        /* 1 when a merge launch follows the attention kernel   */

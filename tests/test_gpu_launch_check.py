@@ -49,7 +49,9 @@ def test_planned_shapes_fit_the_kernels(ctx, kv, S, H, L, sched, sum_l):
         pl = ctx.decode_plan(pool, S, H, L, bt_stride=L // 16, sum_context_len=sum_l)
     finally:
         ctx.set_decode_schedule(velokv.SCHED_AUTO)
-    threads = 64 * pl["wg_waves"] if pl["schedule"] in (velokv.SCHED_WORKGROUP, velokv.SCHED_PACKED) else 64
+    threads = 64 * pl["wg_waves"] if pl["wg_waves"] > 0 else 64  # split-K: one wave per workgroup
+    if pl["schedule"] == velokv.SCHED_STREAM:
+        assert pl["wg_waves"] == 4, pl  # four stream-K workers per workgroup
     assert ctx.launch_check(pl["kernel"], threads) >= threads
     if pl["merge_launch"]:
         merge = "vk_decode_merge_sk" if pl["schedule"] == velokv.SCHED_STREAM else "vk_decode_merge"

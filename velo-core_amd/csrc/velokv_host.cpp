@@ -850,7 +850,7 @@ int plan_decode(vk_ctx* ctx, const vk_pool* pool, const vk_decode_args* a, Decod
     // worker: a worker's blocks are at most its units, ceil(units / nw)
     const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads *
                               ((a->max_context_len + kBS - 1) / kBS + kSkPenalty);
-    const int64_t waves = ctx ? resident_waves(ctx, pl->kernel) : 2048;
+    const int64_t waves = ctx ? resident_waves(ctx, pl->kernel, 64 * kSkWaves) : 2048;
     const int64_t nw = std::max<int64_t>(1, std::max(waves, (units_max + 255) / 256));
     if (units_max > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "batch too large for the stream-K schedule");
     if (nw > 0x7FFFFFFF) return fail(VK_ERR_UNSUPPORTED, "grid too large");
@@ -931,6 +931,7 @@ extern "C" int vk_paged_decode_plan(const vk_pool* pool, const vk_decode_args* a
   } else if (pl.stream_k) {
     const int64_t units_max = (int64_t)a->n_seqs * d.n_kv_heads * (nb + kSkPenalty);
     out->schedule = VK_SCHED_STREAM;
+    out->wg_waves = kSkWaves;
     out->n_workers = pl.n_workers;
     out->max_blocks_per_wave = (int32_t)std::min<int64_t>(nb, (units_max + pl.n_workers - 1) / pl.n_workers);
     out->merge_launch = 1;
@@ -1128,7 +1129,10 @@ int run_decode(vk_ctx* ctx, vk_pool* pool, const vk_decode_args* a, void* stream
   m.n_seqs = a->n_seqs;
   const dim3 merge_grid((unsigned)((m.n_rows + 3) / 4));
   if (pl.stream_k) {
-    if ((rc = launch(ctx, kernel.c_str(), dim3((unsigned)pl.n_workers), dim3(64), p, stream))) return rc;
+    // kSkWaves workers per workgroup; the waves past n_workers return at once
+    if ((rc = launch(ctx, kernel.c_str(), dim3((unsigned)((pl.n_workers + kSkWaves - 1) / kSkWaves)),
+                     dim3(64 * kSkWaves), p, stream)))
+      return rc;
     return launch(ctx, "vk_decode_merge_sk", merge_grid, dim3(256), m, stream);
   }
   if (pl.packed)

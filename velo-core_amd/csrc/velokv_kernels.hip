@@ -1949,7 +1949,7 @@ DEV int seq_units(const DecodeParams& P, int s) {
 template <int KV, int G, int QT = DT_F16, int D = HD, bool ROPE = false>
 DEV void attn_streamk_mfma(const DecodeParams& P) {
   const int lane = lane_id();
-  const int w = blockIdx.x;
+  const int w = (int)blockIdx.x * ((int)blockDim.x / WAVE) + (int)threadIdx.x / WAVE;
   const int nw = P.n_workers;
   const int S = P.n_seqs, Hkv = P.n_kv_heads, pen = P.sk_penalty;
   int W = 0;
@@ -3399,14 +3399,14 @@ VK_DECODE_PK_G(1, DT_F32, _q0) VK_DECODE_PK_G(2, DT_F32, _q0) VK_DECODE_PK_G(3, 
 // Two waves per SIMD (at most 256 registers).
 #define VK_TWO_WAVES __attribute__((amdgpu_waves_per_eu(2)))
 #define VK_DECODE_SK(KV, G)                                                         \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES          \
       vk_decode_sk_kv##KV##_g##G(const DecodeParams P) {                            \
     attn_streamk_mfma<KV, G>(P);                                                    \
   }
 #define VK_DECODE_SK_G(KV) VK_DECODE_SK(KV, 1) VK_DECODE_SK(KV, 2) VK_DECODE_SK(KV, 4) VK_DECODE_SK(KV, 8)
 VK_DECODE_SK_G(0) VK_DECODE_SK_G(1) VK_DECODE_SK_G(2) VK_DECODE_SK_G(3)
 #define VK_DECODE_SK_Q0(KV, G)                                                      \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES          \
       vk_decode_sk_kv##KV##_g##G##_q0(const DecodeParams P) {                       \
     attn_streamk_mfma<KV, G, DT_F32>(P);                                            \
   }
@@ -3446,10 +3446,10 @@ VK_TREE_KV(3, VK_TWO_WAVES, )
   extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx2_q0(const DecodeParams P) {       \
     attn_unit_mfma<KV, 0, 2, false, DT_F32>(P);                                                                \
   }                                                                                                             \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx(const DecodeParams P) { \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx(const DecodeParams P) { \
     attn_streamk_mfma<KV, 0>(P);                                                                               \
   }                                                                                                             \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_q0(const DecodeParams P) { \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_q0(const DecodeParams P) { \
     attn_streamk_mfma<KV, 0, DT_F32>(P);                                                                       \
   }
 VK_GX_DECODE(0) VK_GX_DECODE(1) VK_GX_DECODE(2) VK_GX_DECODE(3)
@@ -3470,10 +3470,10 @@ VK_GX_WG(0) VK_GX_WG(2) VK_GX_WG(3)
   extern "C" __global__ void __launch_bounds__(64) vk_decode_mfma_kv##KV##_gx_d64_q0(const DecodeParams P) {    \
     attn_unit_mfma<KV, 0, 1, false, DT_F32, HD / 2>(P);                                                        \
   }                                                                                                             \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64(const DecodeParams P) { \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64(const DecodeParams P) { \
     attn_streamk_mfma<KV, 0, DT_F16, HD / 2>(P);                                                               \
   }                                                                                                             \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64_q0(const DecodeParams P) { \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64_q0(const DecodeParams P) { \
     attn_streamk_mfma<KV, 0, DT_F32, HD / 2>(P);                                                               \
   }
 VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
@@ -3489,7 +3489,7 @@ VK_D64_WG(1) VK_D64_WG(2) VK_D64_WG(3)
 // and I8_BLK pools, the workgroup split over I8_BLK pools), with the new K row
 // and q rotated in registers; suffix _rope
 #define VK_ROPE_SK(KV, TAG, QT, D)                                                  \
-  extern "C" __global__ void __launch_bounds__(64) VK_TWO_WAVES                     \
+  extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES          \
       vk_decode_sk_kv##KV##TAG##_rope(const DecodeParams P) {                       \
     attn_streamk_mfma<KV, GTAG_##TAG, QT, D, true>(P);                              \
   }

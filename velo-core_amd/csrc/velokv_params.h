@@ -150,6 +150,10 @@ struct DecodeParams {
   int32_t rope_n_pos;
 };
 
+// Stream-K decode: waves per workgroup (each wave one worker, workers
+// blockIdx.x * kSkWaves .. + kSkWaves - 1); fewer, larger workgroups than one
+// wave each reach the device sooner.
+constexpr int kSkWaves = 4;
 constexpr int kMaxCopyPairs = 224;  // pairs per copy launch (kernarg limit)
 // Shared-prefix pass of tree verify: pages per prefix chunk, whose page ids and
 // block scales one workgroup stages in LDS (the host cuts longer prefixes into
