@@ -2342,10 +2342,12 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   const int minlim = __builtin_amdgcn_readfirstlane((int)(-wave_max(-(float)lmin)));
 
   float M[RT], lrun[RT];
+  float nMs[RT], thr[RT];  // -M (0 while M = -inf) and the rescale threshold (-inf while M = -inf)
   float4v acc[RT][8];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     M[rt] = kNegInf; lrun[rt] = 0.f;
+    nMs[rt] = 0.f; thr[rt] = kNegInf;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
@@ -2449,53 +2451,37 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         scv[rt][j] = sc;
       }
     }
-    int vis[RT][2];
-    float hide[RT][2] = {};
-    bool partial = false;
-    if (!plain) {
+    // scores relative to the running max: y = S a - M (log2 units; nMs = -M,
+    // 0 before the first score)
+    float y[RT][2][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[rt][j][r] = fmaf(scv[rt][j][r], a[j], nMs[rt]);
+    if (!plain) {  // tokens at or past a row's limit (or of a missing second block)
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          vis[rt][j] = (j == 0 || has1) ? lim[rt] - (b0 + j) * BS - 4 * g : 0;
-          hide[rt][j] = vis[rt][j] > 0 ? 0.f : kNegInf;
-          partial |= vis[rt][j] > 0 && vis[rt][j] < 4;
+          const int vis = (j == 0 || has1) ? lim[rt] - (b0 + j) * BS - 4 * g : 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[rt][j][r] = (r < vis) ? y[rt][j][r] : kNegInf;
         }
     }
-    // scores relative to the running max: y = S a + c - M (log2 units)
-    float y[RT][2][4];
     bool need = false;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const float c = -Ms + hide[rt][j];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) y[rt][j][r] = fmaf(scv[rt][j][r], a[j], c);
-      }
-    }
-    if (__builtin_amdgcn_ballot_w64(partial) != 0) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) y[rt][j][r] = (r < vis[rt][j]) ? y[rt][j][r] : kNegInf;
-    }
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const float thr = (M[rt] == kNegInf) ? kNegInf : kRescaleThreshold;
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) need |= y[rt][j][r] > thr;
-    }
+        for (int r = 0; r < 4; ++r) need |= y[rt][j][r] > thr[rt];
     // lazy running max of row n (rare after the first blocks)
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        const float Ms = (M[rt] == kNegInf) ? 0.f : M[rt];
+        const float Ms = -nMs[rt];
         float m = y[rt][0][0];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -2507,6 +2493,8 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         const float alpha = (Mn == kNegInf) ? 1.f : __builtin_amdgcn_exp2f(M[rt] - Mn);
         const float shift = (Mn == kNegInf) ? 0.f : Mn - Ms;
         M[rt] = Mn;
+        nMs[rt] = (Mn == kNegInf) ? 0.f : -Mn;
+        thr[rt] = (Mn == kNegInf) ? kNegInf : kRescaleThreshold;
         lrun[rt] *= alpha;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
