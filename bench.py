@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the KV-cache hot path on one MI355X.
 
-Metric (BASELINE.json): paged decode-attention achieved HBM GB/s (% of peak) and
+Metric: paged decode-attention achieved HBM GB/s (% of peak) and
 tokens/s at B=64 sequences x 8192 context, Llama-3-8B decode-layer shapes
 (32 query heads, 8 KV heads, head_dim 128, block size 16), INT8 KV (per-(block,
 head) fp16 scales) as the headline and fp16 KV beside it.
@@ -792,7 +792,7 @@ def main():
     configs = {}
     if (not args.no_configs and not args.ragged and args.kv == "int8" and args.q_dtype == "fp16"
             and (args.page, args.head_dim) == (BS, HD)):
-        # BASELINE configs 2 (fp16) and 3 (INT8 with outliers): the same shapes with
+        # benchmark configurations 2 (fp16) and 3 (INT8 with outliers): the same shapes with
         # L ~ U[1024, ctx]; and the headline with the reference kernels' fp32 q
         import copy
         rag = copy.copy(args)
@@ -804,11 +804,11 @@ def main():
         configs["headline_int8_fp32q"] = run_gpu(ctx, f32, "int8")
         # the reference's default cache type (fp32 K/V, fp32 q) at the headline shape
         configs["headline_fp32_kv"] = run_gpu(ctx, f32, "fp32")
-        # radix-shared 4096-token prefix, 256 sequences, 8-node tree verify + commit
+        # benchmark configuration 4: radix-shared 4096-token prefix, 256 sequences, 8-node tree verify + commit
         c4 = copy.copy(args)
         c4.seqs, c4.steps, c4.warmup = 256, min(args.steps, 10), min(args.warmup, 2)
         configs["config4_tree"] = run_tree(ctx, c4)
-        # BASELINE config 5, one GPU's share: 32 x 32768, 64 / 8 heads, INT8, 80 layers, 65,536-block pool
+        # benchmark configuration 5, one GPU's share: 32 x 32768, 64 / 8 heads, INT8, 80 layers, 65,536-block pool
         c5 = copy.copy(args)
         c5.seqs, c5.ctx, c5.heads, c5.layers, c5.pool_blocks = 32, 32768, 64, 80, 65536
         c5.steps, c5.warmup = min(args.steps, 10), min(args.warmup, 2)

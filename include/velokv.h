@@ -83,11 +83,11 @@ extern "C" {
  * KvCacheType (paged_attention.rs:27-35) has Fp32 / Int8 / Fp8; Fp8 is routed
  * to the Int8 kernels (metal/model.rs:404,442), so it maps to VK_KV_I8_REF.  */
 #define VK_KV_F32     0  /* KvCacheType::Fp32, kernels.metal:619-645 / 440-501 */
-#define VK_KV_F16     1  /* fp16 KV (BASELINE configs 2 and 5)                 */
+#define VK_KV_F16     1  /* fp16 KV (benchmark configurations 2 and 5)         */
 #define VK_KV_I8_REF  2  /* KvCacheType::Int8: per-(token, head) fp32 scale,
                             truncating codes, kernels.metal:753-802           */
 #define VK_KV_I8_BLK  3  /* per-(block, head) fp16 scale, round-half-even codes
-                            clamped to +-127             */
+                            clamped to +-127 (benchmark configuration 3)     */
 
 /* element types of caller tensors (q, new K/V) */
 #define VK_DT_F32 0

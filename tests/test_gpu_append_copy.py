@@ -43,7 +43,7 @@ def assert_layer_equal(pool, layer_idx, ref: O.Layer):
 @pytest.mark.parametrize("kv", KV_ALL)
 def test_append_bit_exact_config1(ctx, kv):
     print(f"append config1 kv={kv}", flush=True)
-    # 32 blocks permuted within a 64-block pool, context 512
+    # benchmark configuration 1: 32 blocks permuted within a 64-block pool, context 512
     case = make_case(kv, [512], n_blocks=64, seed=101)
     ref = oracle_layer(case)
     pool = gpu_pool(ctx, case)

@@ -1,4 +1,4 @@
-"""GPU parity at the full shapes the measured kernels run (3,
+"""GPU parity at the full shapes the measured kernels run (benchmark configurations 2, 3,
 5 and the B=64 x 8k headline), on one layer of a full-size pool.
 
 K/V are generated on the GPU (vk_fill_normal_f16), one sequence at a time, and

@@ -179,7 +179,7 @@ def test_ref_layout_build_layout_agree_for_f32():
     assert np.array_equal(O.to_reference_layout(L, 1).view(np.float32), vref)
 
 
-# ------------------------------------------------ BASELINE INT8 (BLK) -------
+# ------------------------------------------- per-block INT8 (BLK) ---------
 
 def _blk_block(tokens):
     """Append `tokens` ([n][D] fp32, one head) at offsets 0..n-1 of block 0."""
