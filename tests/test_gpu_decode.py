@@ -287,30 +287,31 @@ def outlier_q(shape, seed, scale):
     return q
 
 
-@pytest.mark.parametrize("scale", [10.0, 30.0])
-@pytest.mark.parametrize("qd", [np.float16, np.float32])
 @pytest.mark.parametrize("kv", [O.I8_BLK, O.I8_REF, O.F16])
 @pytest.mark.parametrize("sched", [velokv.SCHED_SPLIT, velokv.SCHED_STREAM])
-def test_decode_outlier_queries(ctx, sched, kv, qd, scale):
-    """q with x10 and x30 outlier channels (|q| up to about 100): the int8
-    kernels' biased products, sum_d q (1152 + c) - 1152 sum_d q, lose bits in
-    proportion to sum_d |q|, and an fp32 q takes the hi + lo split. Outputs stay
-    within the north-star tolerance of the oracle over the same q, on the
-    workgroup split (int8) or split-K (fp16) and on stream-K."""
-    print(f"decode outlier q sched={sched} kv={kv} q={np.dtype(qd).name} x{scale}", flush=True)
+def test_decode_outlier_queries(ctx, sched, kv):
+    """q with x10 and x30 outlier channels (|q| up to about 100), as fp16 and as
+    fp32: the int8 kernels' biased products, sum_d q (1152 + c) - 1152 sum_d q,
+    lose bits in proportion to sum_d |q|, and an fp32 q takes the hi + lo split.
+    Outputs stay within the north-star tolerance of the oracle over the same q,
+    on the workgroup split (int8) or split-K (fp16) and on stream-K. One pool
+    and one oracle layer serve the four queries."""
     lens = synth.rng(451).integers(1, 3000, 64)
     lens[:4] = [1, 16, 17, 2999]
     case = make_case(kv, lens, n_kv_heads=8, n_heads=32, seed=452, outlier_scale=8.0 if kv != O.F16 else 1.0)
     ref_layer = oracle_layer(case)
     pool = gpu_pool(ctx, case)
-    q = outlier_q(case.q.shape, 453, scale).astype(qd)
-    ctx.set_decode_kernel(velokv.DECODE_MFMA)
-    ctx.set_decode_schedule(sched)
-    try:
-        got = run_decode(ctx, pool, case, q=q, q_dtype=qd)
-    finally:
-        ctx.set_decode_kernel(velokv.DECODE_AUTO)
-        ctx.set_decode_schedule(velokv.SCHED_AUTO)
-    ref = O.paged_decode(ref_layer, q, case.block_tables, case.ctx_lens)
-    err = check(got, ref, f"outlier q x{scale}")
-    print(f"  max abs err {err:.3g}", flush=True)
+    for qd in (np.float16, np.float32):
+        for scale in (10.0, 30.0):
+            print(f"decode outlier q sched={sched} kv={kv} q={np.dtype(qd).name} x{scale}", flush=True)
+            q = outlier_q(case.q.shape, 453, scale).astype(qd)
+            ctx.set_decode_kernel(velokv.DECODE_MFMA)
+            ctx.set_decode_schedule(sched)
+            try:
+                got = run_decode(ctx, pool, case, q=q, q_dtype=qd)
+            finally:
+                ctx.set_decode_kernel(velokv.DECODE_AUTO)
+                ctx.set_decode_schedule(velokv.SCHED_AUTO)
+            ref = O.paged_decode(ref_layer, q, case.block_tables, case.ctx_lens)
+            err = check(got, ref, f"outlier q x{scale}")
+            print(f"  max abs err {err:.3g}", flush=True)
