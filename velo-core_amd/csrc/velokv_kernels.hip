@@ -1561,6 +1561,27 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
     }
   }
 
+  // ---- one shared-prefix chunk (the common fold): its partials of every row
+  // this lane writes are loaded at once, before the first output store, so the
+  // fold waits for one round trip (loads issued row by row each waited for the
+  // previous row's loads and stores: vector memory counts both) ----
+  const bool fold1 = direct && npre == 1;  // wave-uniform
+  float2 pm1[RT][4];
+  float4 pa1[RT][4][DL / 4];
+  if (fold1) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int R = min(row0 + 16 * rt + 4 * g + r, nrows - 1);  // rows past the last are not stored
+        const int64_t pr = out_row(R) * P.max_parts;
+        pm1[rt][r] = reinterpret_cast<const float2*>(P.part_ml)[pr];
+        const float4* src = reinterpret_cast<const float4*>(P.part_acc + pr * HD + DL * n);
+#pragma unroll
+        for (int q4 = 0; q4 < DL / 4; ++q4) pa1[rt][r][q4] = src[q4];
+      }
+  }
+
   // ---- partials: acc rows 16 rt + 4g + r, dims DL n .. DL n + DL - 1 ----
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -1585,7 +1606,20 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
         for (int nt = 0; nt < NT; ++nt) o[nt] = I8 ? fmaf(-kBias, psr, acc[rt][nt][r]) : acc[rt][nt][r];
         if (direct) {
           float L = lr;
-          if (npre > 0) {
+          if (fold1) {
+            //   out = (2^(Mr-M) o + 2^(M_0-M) acc_0) / (2^(Mr-M) lr + 2^(M_0-M) l_0)
+            const float2 mk = pm1[rt][r];
+            const float Mt = fmaxf(Mr, mk.x);
+            const float es = (Mr == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(Mr - Mt);
+            const float e = (mk.x == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(mk.x - Mt);
+            L = fmaf(e, mk.y, lr * es);
+#pragma unroll
+            for (int q4 = 0; q4 < DL / 4; ++q4) {
+              const float4 a4 = pa1[rt][r][q4];
+              o[4 * q4] = fmaf(e, a4.x, o[4 * q4] * es); o[4 * q4 + 1] = fmaf(e, a4.y, o[4 * q4 + 1] * es);
+              o[4 * q4 + 2] = fmaf(e, a4.z, o[4 * q4 + 2] * es); o[4 * q4 + 3] = fmaf(e, a4.w, o[4 * q4 + 3] * es);
+            }
+          } else if (npre > 0) {
             // fold in the shared-prefix partials of the row (slots 0..npre-1):
             //   out = (2^(Mr-M) o + sum_k 2^(M_k-M) acc_k) / (2^(Mr-M) lr + sum_k 2^(M_k-M) l_k)
             const float2* pm = reinterpret_cast<const float2*>(P.part_ml) + orow * P.max_parts;
