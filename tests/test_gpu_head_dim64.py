@@ -129,11 +129,15 @@ def test_hd64_workgroup_split_and_append_decode(ctx, kv):
     assert ok, (err, nbad)
 
 
+@pytest.mark.parametrize("G,qd", [(4, np.float16), (1, np.float16), (4, np.float32), (5, np.float16)])
 @pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_REF, O.I8_BLK])
 @pytest.mark.parametrize("shared", [0, 8])
-def test_hd64_tree_verify(ctx, kv, shared):
-    print(f"hd64 tree kv={kv} shared={shared}", flush=True)
-    N, G, Hkv = 8, 4, 2
+def test_hd64_tree_verify(ctx, kv, shared, G, qd):
+    """Tree verify over 64-dim tiles: fp16 and int8 pools take the 64-dim tree
+    kernels (one or two row tiles, fp16 or fp32 q, any group size), fp32 pools
+    the 128-dim ones."""
+    print(f"hd64 tree kv={kv} shared={shared} G={G} q={np.dtype(qd).name}", flush=True)
+    N, Hkv = 8, 2
     committed = np.array([shared * BS + 3, shared * BS + 60, shared * BS + 200, shared * BS], np.int32)
     case = hd64_case(kv, committed + N, n_kv_heads=Hkv, n_heads=Hkv * G, seed=1430 + kv)
     if shared:
@@ -144,10 +148,14 @@ def test_hd64_tree_verify(ctx, kv, shared):
     bt = case.block_tables.copy()
     if shared:
         bt[1:, :shared] = bt[0, :shared]
-    q64 = synth.normals_f16(case.S * N * case.n_heads * D, 1431).reshape(case.S, N, case.n_heads, D)
+    q64 = synth.normals_f16(case.S * N * case.n_heads * D, 1431).reshape(case.S, N, case.n_heads, D).astype(qd)
+    qdt = velokv.DT_F32 if qd == np.float32 else velokv.DT_F16
     mask = np.tile(velokv.branching_tree([2, 2, 2], N).ancestor_mask(), (case.S, 1)).astype(np.uint32)
+    pl = ctx.tree_plan(pool, case.S, N, case.n_heads, int(committed.max()), bt_stride=bt.shape[1],
+                       q_dtype=qdt, shared_blocks=shared)
+    assert ("_gx_d64_" in pl["kernel"]) == (kv != O.F32), pl
     out = ctx.alloc(q64.size * 4)
-    ctx.tree_verify(pool, 0, ctx.upload(q64), velokv.DT_F16, out, ctx.upload(committed), ctx.upload(mask), case.S, N,
+    ctx.tree_verify(pool, 0, ctx.upload(q64), qdt, out, ctx.upload(committed), ctx.upload(mask), case.S, N,
                     case.n_heads, int(committed.max()), block_tables=ctx.upload(bt), bt_stride=bt.shape[1],
                     shared_blocks=shared)
     ctx.sync()

@@ -210,8 +210,10 @@ std::string decode_pk_name(int kv, int g, int qt = VK_DT_F16) {
 std::string tree_pfx_name(int kv, int g, int qt) {
   return "vk_tree_pfx_kv" + std::to_string(kv) + gtag(g) + "_q" + std::to_string(qt);
 }
-std::string tree_name(int kv, int g, int rt, int qt) {
-  return "vk_tree_kv" + std::to_string(kv) + gtag(g) + "_r" + std::to_string(rt) + "_q" + std::to_string(qt);
+// d64: the head_dim-64 tree kernels (64-dim pieces, runtime group size)
+std::string tree_name(int kv, int g, int rt, int qt, bool d64 = false) {
+  return "vk_tree_kv" + std::to_string(kv) + (d64 ? std::string("_gx_d64") : gtag(g)) + "_r" + std::to_string(rt) +
+         "_q" + std::to_string(qt);
 }
 
 int set_device(const vk_ctx* ctx) {
@@ -316,6 +318,7 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
         names.push_back(decode_mfma_name(kv, 3, qt, true));
         names.push_back(decode_sk_name(kv, 3, qt, true));
         names.push_back(decode_wg_name(kv, 3, qt, true));
+        for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt, true));
       }
     }
   }
@@ -1230,7 +1233,8 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
   const int rows = a->n_nodes * G;
   pl->rt = rows > 16 ? 2 : 1;
   pl->n_rgroups = (rows + 16 * pl->rt - 1) / (16 * pl->rt);
-  pl->kernel = tree_name(d.kv_type, G, pl->rt, a->q_dtype);
+  // pools of 64-dim tiles (fp16, int8) take the 64-dim tree kernels
+  pl->kernel = tree_name(d.kv_type, G, pl->rt, a->q_dtype, tile_hd(d.head_dim) == kHD / 2 && d.kv_type != VK_KV_F32);
   if (a->shared_blocks < 0 || a->shared_blocks > pl->bt_stride ||
       (int64_t)a->shared_blocks * d.block_size > a->max_context_len)
     return fail(VK_ERR_BAD_ARG, "shared_blocks %d: must be within the table row (%d pages) and max_context_len %d",
