@@ -165,6 +165,36 @@ def test_hd64_tree_verify(ctx, kv, shared, G, qd):
     assert ok, f"max err {err:.3g}, {nbad} out of tolerance"
 
 
+@pytest.mark.parametrize("G,N", [(1, 1), (3, 5), (16, 2), (40, 32), (2, 24)])
+@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+def test_hd64_tree_row_tiles_and_random_masks(ctx, kv, G, N):
+    """The 64-dim tree kernels over row tiles of 1 to 1280 rows (one or two
+    16-row tiles per wave, several row groups) with random per-sequence masks,
+    rows that see no tree node and, at context 0, nothing at all."""
+    print(f"hd64 tree tiles kv={kv} G={G} N={N}", flush=True)
+    Hkv = 2
+    committed = np.array([0, 3, 33, 250], np.int32)
+    case = hd64_case(kv, committed + N, n_kv_heads=Hkv, n_heads=Hkv * G, seed=1440 + 7 * G + N)
+    pool = hd64_pool(ctx, case)
+    q64 = synth.normals_f16(case.S * N * case.n_heads * D, 1441 + N).reshape(case.S, N, case.n_heads, D)
+    rng = np.random.default_rng(G * 100 + N)
+    full = (1 << N) - 1 if N < 32 else 0xFFFFFFFF
+    mask = rng.integers(0, 1 << 32, size=(case.S, N), dtype=np.uint64).astype(np.uint32) & np.uint32(full)
+    mask[0, 0] = 0  # context 0 and no visible node: output zeros
+    bt = case.block_tables
+    pl = ctx.tree_plan(pool, case.S, N, case.n_heads, int(committed.max()), bt_stride=bt.shape[1])
+    assert "_gx_d64_" in pl["kernel"], pl
+    out = ctx.alloc(q64.size * 4)
+    ctx.tree_verify(pool, 0, ctx.upload(q64), velokv.DT_F16, out, ctx.upload(committed), ctx.upload(mask), case.S, N,
+                    case.n_heads, int(committed.max()), block_tables=ctx.upload(bt), bt_stride=bt.shape[1])
+    ctx.sync()
+    got = out.download(q64.shape, np.float32)
+    ref = O.tree_verify(oracle64(case), q64, bt, committed, mask)
+    ok, err, nbad = tol_check(got, ref)
+    assert ok, f"max err {err:.3g}, {nbad} out of tolerance"
+    assert np.all(got[0, 0] == 0.0)
+
+
 @pytest.mark.parametrize("style", [O.ROPE_INTERLEAVED, O.ROPE_HALF])
 @pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
 def test_hd64_append_rope_bit_exact(ctx, kv, style):
