@@ -207,8 +207,8 @@ const char* const kRopeSuffix = "_rope";
 std::string decode_pk_name(int kv, int g, int qt = VK_DT_F16) {
   return "vk_decode_pk_kv" + std::to_string(kv) + "_g" + std::to_string(g) + q0_suffix(qt);
 }
-std::string tree_pfx_name(int kv, int g, int qt) {
-  return "vk_tree_pfx_kv" + std::to_string(kv) + gtag(g) + "_q" + std::to_string(qt);
+std::string tree_pfx_name(int kv, int g, int qt, bool d64 = false) {
+  return "vk_tree_pfx_kv" + std::to_string(kv) + (d64 ? std::string("_gx_d64") : gtag(g)) + "_q" + std::to_string(qt);
 }
 // d64: the head_dim-64 tree kernels (64-dim pieces, runtime group size)
 std::string tree_name(int kv, int g, int rt, int qt, bool d64 = false) {
@@ -319,6 +319,7 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
         names.push_back(decode_sk_name(kv, 3, qt, true));
         names.push_back(decode_wg_name(kv, 3, qt, true));
         for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt, true));
+        if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt, true));
       }
     }
   }
@@ -1255,7 +1256,7 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
     pl->prefix_chunks = (int32_t)std::max(
         min_chunks, std::min(max_chunks, std::max<int64_t>(1, (n_cu + groups - 1) / groups)));
     pl->prefix_blocks = tiles;
-    pl->pfx_kernel = tree_pfx_name(d.kv_type, G, a->q_dtype);
+    pl->pfx_kernel = tree_pfx_name(d.kv_type, G, a->q_dtype, tile_hd(d.head_dim) == kHD / 2);
     // the rest of a context: past the prefix, or the last partial page of a
     // context shorter than the prefix, then the tree nodes
     tokens = std::max<int64_t>((int64_t)a->max_context_len - (int64_t)a->shared_blocks * d.block_size,

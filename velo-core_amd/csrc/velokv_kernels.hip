@@ -2261,30 +2261,38 @@ DEV void attn_pk_mfma(const DecodeParams& P) {
 // reading row n at word 4g, rows must start 8 (mod 16) words apart for the
 // 16 lanes to cover the 64 banks once (measured: 72-word rows 0 conflict
 // cycles, 68- or 20-word rows 4 per read).
-//   K [tok][D + 16] fp16 (72-word rows); the loader writes 8 bytes per lane
-//     along a token row.
+//   K [tok][D + 16] fp16 (72-word rows at 128 dims, 40 at 64); the loader
+//     writes 8 bytes per lane along a token row.
 //   V per block pair [D][2 x 16 + 16] fp16 (24-word rows): a dim row holds, for
 //     g = 0..3, tokens 4g..4g+3 of u0 then of u1, so that a lane's 8 token slots
 //     are one 16-byte read. The loader writes 8 bytes (one dim, four tokens of
 //     one block) per lane, gathered from two token-pair rows of the pool tile.
 constexpr int kPfxLoadThreads = 512;      // the first 8 waves load the stages
 constexpr int kPfxCH = 4;                 // blocks per stage (two pairs)
-constexpr int kPfxKPitch = HD + 16;       // fp16 per staged K row (72 words)
 constexpr int kPfxVPitch = 2 * BS + 16;   // fp16 per staged V dim row of a block pair (24 words)
 
-template <int KV>
-struct PfxRaw {  // this thread's share of one stage
-  uint32_t k[kPfxCH][Esz<KV>::v];  // 4 dims of one K token row (int8: 4 bytes, fp16: 8 bytes)
-  uint32_t v[kPfxCH][2];           // tokens 4t..4t+1 and 4t+2..4t+3 of one V dim (int8: 2 bytes each, fp16: 4)
+template <int KV, int QPT>
+struct PfxRaw {  // this thread's share of one stage: QPT (block, quad) slots
+  uint32_t k[QPT][Esz<KV>::v];  // 4 dims of one K token row (int8: 4 bytes, fp16: 8 bytes)
+  uint32_t v[QPT][2];           // tokens 4t..4t+1 and 4t+2..4t+3 of one V dim (int8: 2 bytes each, fp16: 4)
 };
 
-template <int KV, int G, int QT>
+// DP: the tile width the pass is built for, 128 or 64 dims (pools of 64-dim
+// tiles: half the staged bytes, score products and value products per block).
+template <int KV, int G, int QT, int DP = HD>
 DEV void tree_prefix_mfma(const DecodeParams& P) {
   constexpr int RT = kPfxRT;
   constexpr bool I8 = (KV == KV_I8_BLK);
   constexpr int ESZ = Esz<KV>::v;
-  __shared__ __attribute__((aligned(16))) _Float16 kl[2][kPfxCH][BS * kPfxKPitch];
-  __shared__ __attribute__((aligned(16))) _Float16 vl[2][kPfxCH / 2][HD * kPfxVPitch];
+  constexpr int KC = DP / 32;    // 32-dim chunks of a score product
+  constexpr int NT = DP / 16;    // 16-dim tiles of the value product
+  constexpr int KP = DP + 16;    // fp16 per staged K row (8 mod 16 words: conflict-free reads)
+  // (block, quad) slots per loader thread and stage: a block's K and V are 4 DP
+  // quads each, spread over the kPfxLoadThreads loaders
+  constexpr int QPT = kPfxCH * 4 * DP / kPfxLoadThreads;
+  static_assert(QPT == kPfxCH || QPT * 2 == kPfxCH, "a loader thread takes every block or every other one");
+  __shared__ __attribute__((aligned(16))) _Float16 kl[2][kPfxCH][BS * KP];
+  __shared__ __attribute__((aligned(16))) _Float16 vl[2][kPfxCH / 2][DP * kPfxVPitch];
   // the chunk's tiles (page id * n_kv_heads + kvh) and (int8) block scales: K
   // scale times the softmax scale as fp32, V scale as fp16 bits
   __shared__ uint32_t pid[kPfxMaxChunkBlocks];
@@ -2341,8 +2349,8 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // An fp32 q is split as q = hi + lo (fp16 each) and each score takes both
   // products, as in attn_piece ----
   constexpr bool QSPLIT = (QT == DT_F32);
-  half8 qa[RT][4];
-  half8 qlo[RT][QSPLIT ? 4 : 1];
+  half8 qa[RT][KC];
+  half8 qlo[RT][QSPLIT ? KC : 1];
   int lim[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -2350,7 +2358,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     const bool valid = r < R;
     const int64_t qoff = (valid ? out_row(r) : 0) * P.io_hd + 8 * g;
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+    for (int kc = 0; kc < KC; ++kc) {
       uint4 v = make_uint4(0, 0, 0, 0), vlo = make_uint4(0, 0, 0, 0);
       if (valid && 32 * kc + 8 * g < P.io_hd) {
         if constexpr (QT == DT_F32) {
@@ -2377,20 +2385,23 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
 
   float M[RT], lrun[RT];
   float nMs[RT], thr[RT];  // -M (0 while M = -inf) and the rescale threshold (-inf while M = -inf)
-  float4v acc[RT][8];
+  float4v acc[RT][NT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     M[rt] = kNegInf; lrun[rt] = 0.f;
     nMs[rt] = 0.f; thr[rt] = kNegInf;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
   // ---- stage loader (threads 0..511): a thread reads 4 dims of K token kt and
   // 4 tokens of V dim vd (token group vq) of each block; int8 V is staged as
   // fp16 c * v_scale (the value product then needs no scale and no bias) ----
-  const int kt = tid >> 5, kd = (tid & 31) * 4;
-  const int vd = tid & (HD - 1), vq = tid >> 7;
+  // the thread's quad inside a block, and the blocks of its QPT slots
+  const int qi = (QPT == kPfxCH) ? tid : (tid & (kPfxLoadThreads / 2 - 1));
+  const int kt = qi / (DP / 4), kd = (qi % (DP / 4)) * 4;
+  const int vd = qi % DP, vq = qi / DP;
+  auto slot_block = [&](int i) { return (QPT == kPfxCH) ? i : 2 * i + (tid >> 8); };  // wave-uniform
   // A head_dim-64 tile is 64 dims wide: dims 64 and up are read from the dims 64
   // below (they meet zero q dims, and those output dims are dropped).
   const int D = P.tile_hd;
@@ -2407,9 +2418,10 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // compute then skips or masks. (A zero fill on a branch let the compiler hoist
   // the first step of the int8 conversion right behind each load, which turned
   // the two-stage prefetch into waits.)
-  auto gload = [&](PfxRaw<KV>& rw, int st) {
+  auto gload = [&](PfxRaw<KV, QPT>& rw, int st) {
 #pragma unroll
-    for (int u = 0; u < kPfxCH; ++u) {
+    for (int i = 0; i < QPT; ++i) {
+      const int u = slot_block(i);
       const int b = cb0 + st * kPfxCH + u;
       const int bi = (st < nst && b < cb1) ? b - cb0 : 0;
       // wave-uniform tile address (SALU): tile index from LDS, tile bytes fixed;
@@ -2417,30 +2429,31 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
       const uint32_t tix = (uint32_t)__builtin_amdgcn_readfirstlane((int)pid[bi]);
       // range: a 128-dim tile (a constant, so the descriptor stays in SGPRs); the
       // lane offsets stay inside the pool's own tile, 64 dims wide or 128
-      constexpr uint32_t kTileMax = (uint32_t)BS * HD * ESZ;
+      constexpr uint32_t kTileMax = (uint32_t)BS * DP * ESZ;
       const rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.kc + (uint64_t)tix * tile_b), 0,
                                                           (int)kTileMax, 0x00020000);
       const rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(P.vc + (uint64_t)tix * tile_b), 0,
                                                           (int)kTileMax, 0x00020000);
       if constexpr (ESZ == 1) {
-        rw.k[u][0] = __builtin_amdgcn_raw_buffer_load_b32(kr, (int)koff, 0, 0);
-        rw.v[u][0] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff0, 0, 0);
-        rw.v[u][1] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff1, 0, 0);
+        rw.k[i][0] = __builtin_amdgcn_raw_buffer_load_b32(kr, (int)koff, 0, 0);
+        rw.v[i][0] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff0, 0, 0);
+        rw.v[i][1] = __builtin_amdgcn_raw_buffer_load_b16(vr, (int)voff1, 0, 0);
       } else {
         const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(kr, (int)koff, 0, 0);
-        rw.k[u][0] = x.x; rw.k[u][1] = x.y;
-        rw.v[u][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)voff0, 0, 0);
-        rw.v[u][1] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)voff1, 0, 0);
+        rw.k[i][0] = x.x; rw.k[i][1] = x.y;
+        rw.v[i][0] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)voff0, 0, 0);
+        rw.v[i][1] = __builtin_amdgcn_raw_buffer_load_b32(vr, (int)voff1, 0, 0);
       }
     }
   };
-  auto lwrite = [&](int buf, int st, const PfxRaw<KV>& rw) {
+  auto lwrite = [&](int buf, int st, const PfxRaw<KV, QPT>& rw) {
 #pragma unroll
-    for (int u = 0; u < kPfxCH; ++u) {
+    for (int i = 0; i < QPT; ++i) {
+      const int u = slot_block(i);
       uint32_t kw0, kw1, vw0, vw1;
       if constexpr (ESZ == 1) {
-        i8x4_to_h2x2_biased(rw.k[u][0], kw0, kw1);
-        i8x4_to_h2x2_biased(rw.v[u][0] | (rw.v[u][1] << 16), vw0, vw1);
+        i8x4_to_h2x2_biased(rw.k[i][0], kw0, kw1);
+        i8x4_to_h2x2_biased(rw.v[i][0] | (rw.v[i][1] << 16), vw0, vw1);
         // (1152 + c) - 1152 = c exactly (K), then one rounding of c * v_scale (V)
         const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};
         kw0 = bitcast<uint32_t>(bitcast<half2v>(kw0) - bias);
@@ -2452,10 +2465,10 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         vw0 = bitcast<uint32_t>((bitcast<half2v>(vw0) - bias) * vs2);
         vw1 = bitcast<uint32_t>((bitcast<half2v>(vw1) - bias) * vs2);
       } else {
-        kw0 = rw.k[u][0]; kw1 = rw.k[u][1];
-        vw0 = rw.v[u][0]; vw1 = rw.v[u][1];
+        kw0 = rw.k[i][0]; kw1 = rw.k[i][1];
+        vw0 = rw.v[i][0]; vw1 = rw.v[i][1];
       }
-      *reinterpret_cast<u32x2*>(&kl[buf][u][kt * kPfxKPitch + kd]) = u32x2{kw0, kw1};
+      *reinterpret_cast<u32x2*>(&kl[buf][u][kt * KP + kd]) = u32x2{kw0, kw1};
       *reinterpret_cast<u32x2*>(&vl[buf][u >> 1][vd * kPfxVPitch + 8 * vq + 4 * (u & 1)]) = u32x2{vw0, vw1};
     }
   };
@@ -2469,16 +2482,16 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     float4v scv[RT][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const _Float16* kb = &kl[buf][up + j][n * kPfxKPitch + 8 * g];
-      half8 kop[4];
+      const _Float16* kb = &kl[buf][up + j][n * KP + 8 * g];
+      half8 kop[KC];
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) kop[kc] = *reinterpret_cast<const half8*>(kb + 32 * kc);
+      for (int kc = 0; kc < KC; ++kc) kop[kc] = *reinterpret_cast<const half8*>(kb + 32 * kc);
       a[j] = I8 ? pks[min(b0 + j, cb1 - 1) - cb0] : P.scale_log2;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         float4v sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
+        for (int kc = 0; kc < KC; ++kc) {
           sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kc], qa[rt][kc], sc, 0, 0, 0);
           if constexpr (QSPLIT) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[kc], qlo[rt][kc], sc, 0, 0, 0);
         }
@@ -2538,7 +2551,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         for (int r = 0; r < 4; ++r) {
           const float ar = __shfl(alpha, 4 * g + r, WAVE);
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt) acc[rt][nt][r] *= ar;
+          for (int nt = 0; nt < NT; ++nt) acc[rt][nt][r] *= ar;
         }
       }
     }
@@ -2559,7 +2572,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
     // values: B = V of dim 16 nt + n, tokens 4g..4g+3 of u0 then of u1
     const _Float16* vb = &vl[buf][up >> 1][n * kPfxVPitch + 8 * g];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
       const half8 vop = *reinterpret_cast<const half8*>(vb + 16 * nt * kPfxVPitch);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
@@ -2581,7 +2594,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
   // after the one being computed (an empty chunk, nst = 0 for the whole
   // workgroup, writes empty partials) ----
   if (nst > 0) {
-    PfxRaw<KV> ra;
+    PfxRaw<KV, QPT> ra;
     const bool ld = tid < kPfxLoadThreads;
     if (ld) { gload(ra, 0); lwrite(0, 0, ra); gload(ra, 1); }
     __syncthreads();
@@ -2612,7 +2625,7 @@ DEV void tree_prefix_mfma(const DecodeParams& P) {
         const int64_t pr = out_row(row) * P.max_parts + chunk;
         float* dst = P.part_acc + pr * HD + n;
 #pragma unroll
-        for (int nt = 0; nt < 8; ++nt) dst[16 * nt] = acc[rt][nt][r];
+        for (int nt = 0; nt < NT; ++nt) dst[16 * nt] = acc[rt][nt][r];
         if (n == 0) reinterpret_cast<float2*>(P.part_ml)[pr] = make_float2(Mr, lr);
       }
     }
@@ -3571,6 +3584,13 @@ VK_TREE_PFX_G(1, 0) VK_TREE_PFX_G(1, 1) VK_TREE_PFX_G(3, 0) VK_TREE_PFX_G(3, 1)
     tree_prefix_mfma<KV, 0, QT>(P);                                                 \
   }
 VK_GX_TREE_PFX(1, 0) VK_GX_TREE_PFX(1, 1) VK_GX_TREE_PFX(3, 0) VK_GX_TREE_PFX(3, 1)
+// pools of 64-dim tiles: the pass built for 64 dims, any group size
+#define VK_GX_TREE_PFX_D64(KV, QT)                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * kPfxWaves)                      \
+      __attribute__((amdgpu_waves_per_eu(kPfxWaves / 4))) vk_tree_pfx_kv##KV##_gx_d64_q##QT(const DecodeParams P) { \
+    tree_prefix_mfma<KV, 0, QT, HD / 2>(P);                                         \
+  }
+VK_GX_TREE_PFX_D64(1, 0) VK_GX_TREE_PFX_D64(1, 1) VK_GX_TREE_PFX_D64(3, 0) VK_GX_TREE_PFX_D64(3, 1)
 
 
 #define VK_APPEND(KV) \
