@@ -154,6 +154,8 @@ def test_hd64_tree_verify(ctx, kv, shared, G, qd):
     pl = ctx.tree_plan(pool, case.S, N, case.n_heads, int(committed.max()), bt_stride=bt.shape[1],
                        q_dtype=qdt, shared_blocks=shared)
     assert ("_gx_d64_" in pl["kernel"]) == (kv != O.F32), pl
+    if shared and kv in (O.F16, O.I8_BLK):  # the shared-prefix pass, built for 64 dims
+        assert "_gx_d64_" in pl["prefix_kernel"], pl
     out = ctx.alloc(q64.size * 4)
     ctx.tree_verify(pool, 0, ctx.upload(q64), qdt, out, ctx.upload(committed), ctx.upload(mask), case.S, N,
                     case.n_heads, int(committed.max()), block_tables=ctx.upload(bt), bt_stride=bt.shape[1],
