@@ -148,7 +148,7 @@ int vk_ctx_check(vk_ctx* ctx, uint32_t* flags);
 /* Kernel family of vk_paged_decode: VK_DECODE_MFMA (QK and PV on
  * v_mfma_f32_16x16x{32,16}_f16 over fp16 / int8 KV, where an fp32 q is split
  * into fp16 hi + lo parts; on v_mfma_f32_16x16x4_f32 in fp32 throughout over
- * fp32 KV; over 64-dim heads in int8 or fp16 pools at group sizes up to 16,
+ * fp32 KV; over 64-dim heads in every pool type at group sizes up to 16,
  * kernels built for 64 dims), VK_DECODE_VALU (v_dot2_f32_f16, or fp32
  * arithmetic for an fp32 q or fp32 KV, on the vector ALUs; GQA group sizes
  * 1, 2, 4, 8 and head_dim 128, else the matrix cores run) or VK_DECODE_AUTO

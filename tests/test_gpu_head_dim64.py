@@ -84,8 +84,8 @@ def test_hd64_decode(ctx, kv, sched, qd):
         pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()),
                              bt_stride=case.block_tables.shape[1], partition_tokens=P, q_dtype=qdt)
         assert "mfma" in pl["kernel"] or "_sk_" in pl["kernel"] or "_wg_" in pl["kernel"], pl  # no VALU at 64
-        # int8 and fp16 pools run the 64-dim pieces (2 score and 4 value products per block)
-        assert pl["kernel"].endswith("_d64" + ("_q0" if qd == np.float32 else "")) == (kv != O.F32), pl
+        # every pool type runs the 64-dim pieces (half the products per block of a 128-dim piece)
+        assert pl["kernel"].endswith("_d64" + ("_q0" if qd == np.float32 else "")), pl
         out = ctx.alloc(case.S * case.n_heads * D * 4)
         ctx.paged_decode(pool, 0, ctx.upload(q64), qdt, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
                          int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
@@ -112,7 +112,7 @@ def test_hd64_workgroup_split_and_append_decode(ctx, kv):
     ctx.set_decode_schedule(velokv.SCHED_SPLIT)
     try:
         pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()), bt_stride=case.block_tables.shape[1])
-        assert pl["kernel"] == (f"vk_decode_wg_kv{kv}_g4" if kv == O.F32 else f"vk_decode_wg_kv{kv}_gx_d64"), pl
+        assert pl["kernel"] == f"vk_decode_wg_kv{kv}_gx_d64", pl
         ctx.append_decode(pool, 0, ctx.upload(np.ascontiguousarray(kk[..., :D])),
                           ctx.upload(np.ascontiguousarray(vv[..., :D])), velokv.DT_F16, ctx.upload(q64),
                           velokv.DT_F16, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
@@ -255,7 +255,7 @@ def test_hd64_limits(ctx):
         assert e.value.code == velokv.ERR_UNSUPPORTED, bad
 
 
-@pytest.mark.parametrize("kv", [O.F16, O.I8_REF, O.I8_BLK])
+@pytest.mark.parametrize("kv", KV_ALL)
 @pytest.mark.parametrize("G", [3, 8, 16])
 @pytest.mark.parametrize("sched", ["split", "stream", "auto"])
 def test_hd64_pieces_group_sizes_and_long_units(ctx, kv, G, sched):
@@ -294,10 +294,10 @@ def test_hd64_pieces_group_sizes_and_long_units(ctx, kv, G, sched):
     assert ok, f"max err {err:.3g}, {nbad} out of tolerance ({pl['kernel']})"
 
 
-@pytest.mark.parametrize("kv", [O.F16, O.I8_BLK])
+@pytest.mark.parametrize("kv", [O.F32, O.F16, O.I8_BLK])
 @pytest.mark.parametrize("G", [3, 8])
 def test_hd64_workgroup_split_group_sizes(ctx, kv, G):
-    """The 64-dim workgroup split over fp16 and int8 pools at runtime group sizes."""
+    """The 64-dim workgroup split over fp32, fp16 and int8 pools at runtime group sizes."""
     print(f"hd64 workgroup split kv={kv} G={G}", flush=True)
     lens = list(synth.rng(1470 + G).integers(2, 400, 64))
     case = hd64_case(kv, lens, n_kv_heads=8, n_heads=8 * G, seed=1471 + G)

@@ -196,11 +196,11 @@ std::string decode_wg_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) 
 std::string decode_sk_name(int kv, int g, int qt = VK_DT_F16, bool d64 = false) {
   return "vk_decode_sk_kv" + std::to_string(kv) + (d64 ? std::string("_gx_d64") : gtag(g)) + q0_suffix(qt);
 }
-// The head_dim-64 kernels serve this pool and group size: int8 and fp16 pools
-// of 64-dim tiles (heads of up to 64 dims), one 16-row tile of query rows per
+// The head_dim-64 decode kernels serve this pool and group size: pools of
+// 64-dim tiles (heads of up to 64 dims), one 16-row tile of query rows per
 // (sequence, KV head).
 bool use_d64(const vk_pool_desc& d, int g) {
-  return tile_hd(d.head_dim) == kHD / 2 && d.kv_type != VK_KV_F32 && g <= kMaxGroupTile;
+  return tile_hd(d.head_dim) == kHD / 2 && g <= kMaxGroupTile;
 }
 // The folding kernels' variants that also rotate the new K row and q (RoPE)
 const char* const kRopeSuffix = "_rope";
@@ -314,10 +314,10 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       if (kv != VK_KV_F16) names.push_back(decode_wg_name(kv, 3, qt));
       if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt));
       for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt));
-      if (kv != VK_KV_F32) {  // head_dim 64
-        names.push_back(decode_mfma_name(kv, 3, qt, true));
-        names.push_back(decode_sk_name(kv, 3, qt, true));
-        names.push_back(decode_wg_name(kv, 3, qt, true));
+      names.push_back(decode_mfma_name(kv, 3, qt, true));  // head_dim 64
+      names.push_back(decode_sk_name(kv, 3, qt, true));
+      names.push_back(decode_wg_name(kv, 3, qt, true));
+      if (kv != VK_KV_F32) {  // tree verify at head_dim 64 (fp32 pools: the 128-dim kernels)
         for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt, true));
         if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt, true));
       }

@@ -1682,12 +1682,16 @@ DEV void attn_piece(const DecodeParams& P, int s, int kvh, int rg, int start, in
 //           contiguous bytes per 16 lanes); lane (n, g) accumulates rows 4g..4g+3,
 //           dim 16 tile + n.
 // =============================================================================
+// DF: the tile width the piece is built for (128, or 64 for pools of 64-dim
+// tiles: half the loads and products per block)
+template <int DF = HD>
 struct F32Stage {
-  u32x4 k[8];      // token n, dims 16 j + 4 g .. + 3
-  u32x2 v[8][2];   // tile t, token pair 2 g + r: dim 16 t + n of its two tokens
+  u32x4 k[DF / 16];      // token n, dims 16 j + 4 g .. + 3
+  u32x2 v[DF / 16][2];   // tile t, token pair 2 g + r: dim 16 t + n of its two tokens
 };
 
-DEV void f32_stage_load(F32Stage& st, const DecodeParams& P, const BlockIds& bw, int i, int nblk, int kvh, int n,
+template <int DF = HD>
+DEV void f32_stage_load(F32Stage<DF>& st, const DecodeParams& P, const BlockIds& bw, int i, int nblk, int kvh, int n,
                         int g) {
   const int blk = window_at(bw.b, min(i, nblk - 1));
   const uint64_t tix = (uint64_t)blk * P.n_kv_heads + kvh;
@@ -1703,17 +1707,18 @@ DEV void f32_stage_load(F32Stage& st, const DecodeParams& P, const BlockIds& bw,
   const int k0 = n * 4 * D + 16 * g, k1 = k0 - (D < HD ? 256 : 0);
   const int v0 = 16 * g * D + 8 * n, v1 = v0 - (D < HD ? 512 : 0);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, (j < 4 ? k0 : k1) + 64 * j, 0, 0);
+  for (int j = 0; j < DF / 16; ++j) st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kr, (j < 4 ? k0 : k1) + 64 * j, 0, 0);
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int t = 0; t < DF / 16; ++t)
 #pragma unroll
     for (int r = 0; r < 2; ++r)
       st.v[t][r] = __builtin_amdgcn_raw_buffer_load_b64(vr, (t < 4 ? v0 : v1) + 128 * t, r * 8 * D, kAuxNT);
 }
 
-template <int G, int RT, bool TREE, int QT>
+template <int G, int RT, bool TREE, int QT, int DF = HD>
 DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                         int64_t pbase, int pstride, float* pacc, float* pml) {
+  constexpr int NJ = DF / 16;  // 16-dim groups: score chunks of 4 instructions, value tiles
   const int lane = lane_id();
   const int n = lane & 15, g = lane >> 4;
   const int N = TREE ? P.n_nodes : 1;
@@ -1731,18 +1736,18 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
 
   BlockIds bw;
   load_block_ids<false>(bw, P, bt, blk0, nblk, kvh);
-  F32Stage sa, sb;
-  f32_stage_load(sa, P, bw, 0, nblk, kvh, n, g);
+  F32Stage<DF> sa, sb;
+  f32_stage_load<DF>(sa, P, bw, 0, nblk, kvh, n, g);
 
   // q of row n of each tile at the lane's dims 16 j + 4 g + e (rows past the end are 0)
-  float qf[RT][32];
+  float qf[RT][4 * NJ];
   uint32_t mrow[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int R = row0 + 16 * rt + n;
     const int64_t qoff = (R < nrows ? out_row(R) : 0) * P.io_hd + 4 * g;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
       if (R < nrows && 16 * j + 4 * g < P.io_hd) {
         if constexpr (QT == DT_F32) {
@@ -1761,21 +1766,21 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
   }
 
   float M[RT], lrun[RT];
-  float4v acc[RT][8];
+  float4v acc[RT][NJ];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     M[rt] = kNegInf; lrun[rt] = 0.f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[rt][t] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NJ; ++t) acc[rt][t] = float4v{0.f, 0.f, 0.f, 0.f};
   }
   const int last_valid = (end - start) - (nblk - 1) * BS;
 
-  auto compute = [&](const F32Stage& st, int i) {
+  auto compute = [&](const F32Stage<DF>& st, int i) {
     float4v sc[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) sc[rt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -1815,7 +1820,7 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
         for (int r = 0; r < 4; ++r) {
           const float ar = __shfl(alpha, 4 * g + r, WAVE);
 #pragma unroll
-          for (int t = 0; t < 8; ++t) acc[rt][t][r] *= ar;
+          for (int t = 0; t < NJ; ++t) acc[rt][t][r] *= ar;
         }
       }
     }
@@ -1832,7 +1837,7 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
     if (i < nblk) {
       const bool partial = (i == nblk - 1) && (last_valid < BS);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < NJ; ++t) {
         float vv[4] = {bitcast<float>(st.v[t][0].x), bitcast<float>(st.v[t][0].y), bitcast<float>(st.v[t][1].x),
                        bitcast<float>(st.v[t][1].y)};
         if (partial) {  // bytes past the context may be anything, NaN included
@@ -1849,10 +1854,10 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
   };
 
   for (int b = 0; b < nblk; b += 2) {
-    f32_stage_load(sb, P, bw, b + 1, nblk, kvh, n, g);
+    f32_stage_load<DF>(sb, P, bw, b + 1, nblk, kvh, n, g);
     compute(sa, b);
     if (b + 1 >= nblk) break;
-    f32_stage_load(sa, P, bw, b + 2, nblk, kvh, n, g);
+    f32_stage_load<DF>(sa, P, bw, b + 2, nblk, kvh, n, g);
     compute(sb, b + 1);
   }
 
@@ -1873,12 +1878,12 @@ DEV void attn_piece_f32(const DecodeParams& P, int s, int kvh, int rg, int start
         if (direct) {
           const float inv = lr > 0.f ? 1.f / lr : 0.f;
 #pragma unroll
-          for (int t = 0; t < 8; ++t)
+          for (int t = 0; t < NJ; ++t)
             if (16 * t + n < P.io_hd) P.out[orow * P.io_hd + 16 * t + n] = acc[rt][t][r] * inv;
         } else {
           const int64_t pr = TREE ? orow * P.max_parts + pbase : pbase + (int64_t)R * pstride;
 #pragma unroll
-          for (int t = 0; t < 8; ++t) pacc[pr * HD + 16 * t + n] = acc[rt][t][r];
+          for (int t = 0; t < NJ; ++t) pacc[pr * HD + 16 * t + n] = acc[rt][t][r];
           if (n == 0) reinterpret_cast<float2*>(pml)[pr] = make_float2(Mr, lr);
         }
       }
@@ -1891,8 +1896,7 @@ template <int KV, int G, int RT, bool TREE, int QT, int D = HD, bool FOLD = fals
 DEV void attn_piece_kv(const DecodeParams& P, int s, int kvh, int rg, int start, int end, int ctx_c, bool direct,
                        int64_t pbase, int pstride, float* pacc, float* pml, int npre = 0) {
   if constexpr (KV == KV_F32) {
-    static_assert(D == HD, "fp32 pools take the 128-dim piece");
-    attn_piece_f32<G, RT, TREE, QT>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml);
+    attn_piece_f32<G, RT, TREE, QT, D>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml);
   } else {
     attn_piece<KV, G, RT, TREE, QT, D, FOLD, ROPE>(P, s, kvh, rg, start, end, ctx_c, direct, pbase, pstride, pacc, pml, npre);
   }
@@ -3511,7 +3515,7 @@ VK_GX_WG(0) VK_GX_WG(2) VK_GX_WG(3)
   extern "C" __global__ void __launch_bounds__(64 * kSkWaves) VK_TWO_WAVES vk_decode_sk_kv##KV##_gx_d64_q0(const DecodeParams P) { \
     attn_streamk_mfma<KV, 0, DT_F32, HD / 2>(P);                                                               \
   }
-VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
+VK_D64_DECODE(0) VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
 #define VK_D64_WG(KV)                                                                                           \
   extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_d64(const DecodeParams P) { \
     attn_wg_mfma<KV, 0, DT_F16, HD / 2>(P);                                                                    \
@@ -3519,7 +3523,7 @@ VK_D64_DECODE(1) VK_D64_DECODE(2) VK_D64_DECODE(3)
   extern "C" __global__ void __launch_bounds__(64 * kWgMaxWaves) vk_decode_wg_kv##KV##_gx_d64_q0(const DecodeParams P) { \
     attn_wg_mfma<KV, 0, DT_F32, HD / 2>(P);                                                                    \
   }
-VK_D64_WG(1) VK_D64_WG(2) VK_D64_WG(3)
+VK_D64_WG(0) VK_D64_WG(1) VK_D64_WG(2) VK_D64_WG(3)
 // vk_append_rope_decode: the kernels that fold the append (stream-K over fp16
 // and I8_BLK pools, the workgroup split over I8_BLK pools), with the new K row
 // and q rotated in registers; suffix _rope
