@@ -317,10 +317,8 @@ extern "C" int vk_ctx_create(int device, const char* code_object_path, vk_ctx** 
       names.push_back(decode_mfma_name(kv, 3, qt, true));  // head_dim 64
       names.push_back(decode_sk_name(kv, 3, qt, true));
       names.push_back(decode_wg_name(kv, 3, qt, true));
-      if (kv != VK_KV_F32) {  // tree verify at head_dim 64 (fp32 pools: the 128-dim kernels)
-        for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt, true));
-        if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt, true));
-      }
+      for (int rt : {1, 2}) names.push_back(tree_name(kv, 3, rt, qt, true));  // tree verify at head_dim 64
+      if (kv == VK_KV_F16 || kv == VK_KV_I8_BLK) names.push_back(tree_pfx_name(kv, 3, qt, true));
     }
   }
   // vk_append_rope_decode's kernels: every kernel that folds the append, suffix _rope
@@ -1234,8 +1232,8 @@ int plan_tree(vk_ctx* ctx, const vk_pool* pool, const vk_tree_args* a, TreePlan*
   const int rows = a->n_nodes * G;
   pl->rt = rows > 16 ? 2 : 1;
   pl->n_rgroups = (rows + 16 * pl->rt - 1) / (16 * pl->rt);
-  // pools of 64-dim tiles (fp16, int8) take the 64-dim tree kernels
-  pl->kernel = tree_name(d.kv_type, G, pl->rt, a->q_dtype, tile_hd(d.head_dim) == kHD / 2 && d.kv_type != VK_KV_F32);
+  // pools of 64-dim tiles take the 64-dim tree kernels
+  pl->kernel = tree_name(d.kv_type, G, pl->rt, a->q_dtype, tile_hd(d.head_dim) == kHD / 2);
   if (a->shared_blocks < 0 || a->shared_blocks > pl->bt_stride ||
       (int64_t)a->shared_blocks * d.block_size > a->max_context_len)
     return fail(VK_ERR_BAD_ARG, "shared_blocks %d: must be within the table row (%d pages) and max_context_len %d",

@@ -3562,16 +3562,16 @@ VK_ROPE_ALL(VK_ROPE_SK, 1) VK_ROPE_ALL(VK_ROPE_SK, 3) VK_ROPE_ALL(VK_ROPE_WG, 3)
 #define VK_GX_TREE_KV(KV, ATTR, ATTR_R2Q0) \
   VK_GX_TREE(KV, 1, 0, ATTR) VK_GX_TREE(KV, 1, 1, ATTR) VK_GX_TREE(KV, 2, 0, ATTR_R2Q0) VK_GX_TREE(KV, 2, 1, ATTR)
 VK_GX_TREE_KV(0, , ) VK_GX_TREE_KV(1, , ) VK_GX_TREE_KV(2, VK_TWO_WAVES, ) VK_GX_TREE_KV(3, VK_TWO_WAVES, )
-// head_dim 64 (fp16 and int8 pools of 64-dim tiles): the tree kernels on 64-dim
-// pieces, any group size
+// head_dim 64 (pools of 64-dim tiles): the tree kernels on 64-dim pieces, any
+// group size
 #define VK_GX_TREE_D64(KV, RT, QT, ATTR)                                                                        \
   extern "C" __global__ void __launch_bounds__(64) ATTR vk_tree_kv##KV##_gx_d64_r##RT##_q##QT(const DecodeParams P) { \
     attn_unit_mfma<KV, 0, RT, true, QT, HD / 2>(P);                                                            \
   }
 #define VK_GX_TREE_D64_KV(KV, ATTR, ATTR_R2Q0) \
   VK_GX_TREE_D64(KV, 1, 0, ATTR) VK_GX_TREE_D64(KV, 1, 1, ATTR) VK_GX_TREE_D64(KV, 2, 0, ATTR_R2Q0) VK_GX_TREE_D64(KV, 2, 1, ATTR)
-VK_GX_TREE_D64_KV(1, VK_TWO_WAVES, VK_TWO_WAVES) VK_GX_TREE_D64_KV(2, VK_TWO_WAVES, VK_TWO_WAVES)
-VK_GX_TREE_D64_KV(3, VK_TWO_WAVES, VK_TWO_WAVES)
+VK_GX_TREE_D64_KV(0, , ) VK_GX_TREE_D64_KV(1, VK_TWO_WAVES, VK_TWO_WAVES)
+VK_GX_TREE_D64_KV(2, VK_TWO_WAVES, VK_TWO_WAVES) VK_GX_TREE_D64_KV(3, VK_TWO_WAVES, VK_TWO_WAVES)
 
 // Shared-prefix pass of tree verify: 8 waves (two per SIMD) per workgroup.
 #define VK_TREE_PFX(KV, G, QT)                                                      \
