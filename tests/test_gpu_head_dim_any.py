@@ -106,8 +106,8 @@ def test_decode(ctx, kv, hd, sched, qd):
     try:
         pl = ctx.decode_plan(pool, case.S, case.n_heads, int(case.ctx_lens.max()),
                              bt_stride=case.block_tables.shape[1], partition_tokens=P, q_dtype=qdt)
-        # 64-dim tiles of int8 / fp16 pools run the 64-dim pieces
-        assert ("_d64" in pl["kernel"]) == (tile_w(hd) == 64 and kv != O.F32), pl
+        # 64-dim tiles of every pool run the 64-dim pieces
+        assert ("_d64" in pl["kernel"]) == (tile_w(hd) == 64), pl
         out = ctx.alloc(case.S * case.n_heads * hd * 4)
         ctx.paged_decode(pool, 0, ctx.upload(q), qdt, out, ctx.upload(case.ctx_lens), case.S, case.n_heads,
                          int(case.ctx_lens.max()), block_tables=ctx.upload(case.block_tables),
