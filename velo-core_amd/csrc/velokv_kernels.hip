@@ -2779,7 +2779,7 @@ DEV void load_kv(const AppendParams& P, const void* src, bool is_v, int m, int h
 //   if s_new > s_old: c' = clamp(rne((c * s_old) / s_new)) for tokens before offset
 //   c = s_new > 0 ? clamp(rne(x / s_new)) : 0
 // Slots are read 64 tokens at a time (lane j: token base + j) and runs are found
-// with ballots; the K/V rows of up to 16 members are loaded together before the
+// with ballots; the K/V rows of up to 8 members are loaded together before the
 // rule runs over them.
 
 // Block of the nearest non-padding token before token n of the call, or -1.
@@ -2812,15 +2812,29 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
   const bool din = d0 < D;
   const int da = d0 & (D - 1);
   // element (u, d) sits at tile_elem(u, 0) + tile_elem(0, d) in both layouts:
-  // two lane pointers and constant offsets per token
+  // one lane pointer and constant offsets per token
   uint8_t* const lp0 = tile + tile_elem<IS_V>(0, da, 1, D);
-  uint8_t* const lp1 = tile + tile_elem<IS_V>(0, da + 1, 1, D);
 
+  // the lane's codes as whole words: K dims da, da + 1 of a token are adjacent
+  // bytes (one 16-bit word per token); V dims da, da + 1 of a token pair are 4
+  // adjacent bytes (tokens 2p, 2p + 1 of dim da, then of dim da + 1)
   int cd[BS][2];
+  if constexpr (IS_V) {
 #pragma unroll
-  for (int u = 0; u < BS; ++u) {
-    cd[u][0] = (int8_t)lp0[tile_elem<IS_V>(u, 0, 1, D)];
-    cd[u][1] = (int8_t)lp1[tile_elem<IS_V>(u, 0, 1, D)];
+    for (int p = 0; p < BS / 2; ++p) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(lp0 + tile_elem<true>(2 * p, 0, 1, D));
+      cd[2 * p][0] = (int8_t)(uint8_t)w;
+      cd[2 * p + 1][0] = (int8_t)(uint8_t)(w >> 8);
+      cd[2 * p][1] = (int8_t)(uint8_t)(w >> 16);
+      cd[2 * p + 1][1] = (int8_t)(uint8_t)(w >> 24);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < BS; ++u) {
+      const uint32_t w = *reinterpret_cast<const uint16_t*>(lp0 + tile_elem<false>(u, 0, 1, D));
+      cd[u][0] = (int8_t)(uint8_t)w;
+      cd[u][1] = (int8_t)(uint8_t)(w >> 8);
+    }
   }
   const uint16_t stored = *sp;
   float s_old = 0.f;
@@ -2837,56 +2851,104 @@ DEV void append_blk_run(const AppendParams& P, const void* src, uint8_t* codes, 
     uint64_t mem = __builtin_amdgcn_ballot_w64(ms >= 0 && lane < stop);
     const int moff = (int)(ms >= 0 ? ms % BS : 0);
     while (mem != 0) {
-      // up to 16 members: their rows loaded together, then the rule in order
-      // (a rolled loop over xs[0], the rows shifted down one per member, so
-      // that the rule is instantiated once and the kernel stays near 128
-      // registers: four waves per SIMD)
-      constexpr int kBatch = 16;
+      // up to 8 members: their rows loaded together, then the rule. What does
+      // not depend on the member before (the absmax and candidate scale, and
+      // once the running scales are known the new codes) is computed for all
+      // members at once; only the running scale and the placement, with its
+      // requantization when the scale grew, follow the members' order.
+      constexpr int kBatch = 8;
       float xs[kBatch][2];
-      uint64_t batch = 0;
+      int ok[kBatch];  // member offsets in the block (wave-uniform)
+      int nb = 0;
       {
         uint64_t rest = mem;
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
+          ok[k] = 0;
           if (rest != 0) {
             const int j = __builtin_ctzll(rest);
             rest &= rest - 1;
-            batch |= 1ull << j;
+            ok[k] = readlane_i(moff, j);
+            nb = k + 1;
             load_kv(P, src, IS_V, base + j, h, xs[k][0], xs[k][1]);
           }
         }
         mem = rest;
       }
-#pragma unroll 1
-      while (batch != 0) {
-        const int j = __builtin_ctzll(batch);
-        batch &= batch - 1;
-        const int o = readlane_i(moff, j);
-        if (first) {
-          s_old = (o == 0) ? 0.f : h2f(stored);
-          s_bits = (o == 0) ? (uint16_t)0 : stored;
-          first = false;
-        } else if (o == 0) {
-          s_old = 0.f;
-          s_bits = 0;
-        }
-        blk_put(cd, o, s_old, s_bits, xs[0][0], xs[0][1]);
-        hi_written = max(hi_written, o);
+      uint16_t cand[kBatch];  // fp16(amax / 127) of each member (wave-uniform)
 #pragma unroll
-        for (int k = 0; k + 1 < kBatch; ++k) {
-          xs[k][0] = xs[k + 1][0];
-          xs[k][1] = xs[k + 1][1];
+      for (int k = 0; k < kBatch; ++k) {
+        cand[k] = 0;
+        if (k < nb) {
+          const float amax = wave_max(fmaxf(fabsf(xs[k][0]), fabsf(xs[k][1])));
+          cand[k] = (uint16_t)__builtin_amdgcn_readfirstlane((int)f2h(amax / 127.0f));
+        }
+      }
+      // the scale before (so) and after (sn) each member
+      float so[kBatch], sn[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        so[k] = sn[k] = 0.f;
+        if (k < nb) {
+          const int o = ok[k];
+          if (first) {
+            s_old = (o == 0) ? 0.f : h2f(stored);
+            s_bits = (o == 0) ? (uint16_t)0 : stored;
+            first = false;
+          } else if (o == 0) {
+            s_old = 0.f;
+            s_bits = 0;
+          }
+          so[k] = s_old;
+          if (h2f(cand[k]) > s_old) {
+            s_bits = cand[k];
+            s_old = h2f(cand[k]);
+          }
+          sn[k] = s_old;
+        }
+      }
+      int cc[kBatch][2];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        cc[k][0] = k < nb ? blk_code(xs[k][0], sn[k]) : 0;
+        cc[k][1] = k < nb ? blk_code(xs[k][1], sn[k]) : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        if (k < nb) {
+          const int o = ok[k];
+          if (sn[k] > so[k] && o > 0) {
+#pragma unroll
+            for (int u = 0; u < BS; ++u) {
+              if (u < o) {
+                cd[u][0] = blk_requant(cd[u][0], so[k], sn[k]);
+                cd[u][1] = blk_requant(cd[u][1], so[k], sn[k]);
+              }
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < BS; ++u)
+            if (u == o) { cd[u][0] = cc[k][0]; cd[u][1] = cc[k][1]; }
+          hi_written = max(hi_written, o);
         }
       }
     }
     if (other != 0) break;
   }
+  // the same words back for the tokens up to the last one written (a V pair whose
+  // second token is past it stores that token's codes as they were loaded)
+  auto b8 = [](int c) { return (uint32_t)(uint8_t)(int8_t)c; };
+  if constexpr (IS_V) {
 #pragma unroll
-  for (int u = 0; u < BS; ++u) {
-    if (din && u <= hi_written) {
-      lp0[tile_elem<IS_V>(u, 0, 1, D)] = (uint8_t)(int8_t)cd[u][0];
-      lp1[tile_elem<IS_V>(u, 0, 1, D)] = (uint8_t)(int8_t)cd[u][1];
-    }
+    for (int p = 0; p < BS / 2; ++p)
+      if (din && 2 * p <= hi_written)
+        *reinterpret_cast<uint32_t*>(lp0 + tile_elem<true>(2 * p, 0, 1, D)) =
+            b8(cd[2 * p][0]) | (b8(cd[2 * p + 1][0]) << 8) | (b8(cd[2 * p][1]) << 16) | (b8(cd[2 * p + 1][1]) << 24);
+  } else {
+#pragma unroll
+    for (int u = 0; u < BS; ++u)
+      if (din && u <= hi_written)
+        *reinterpret_cast<uint16_t*>(lp0 + tile_elem<false>(u, 0, 1, D)) = (uint16_t)(b8(cd[u][0]) | (b8(cd[u][1]) << 8));
   }
   if (lane == 0) *sp = s_bits;
 }
@@ -2917,15 +2979,16 @@ DEV void append_blk(const AppendParams& P, const void* src, uint8_t* codes, uint
     const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)ms, j);
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)ms >> 32), j);
     const int64_t slot = (int64_t)(((uint64_t)hi << 32) | lo);
-    if (!IS_V && h == 0 && lane == 0 && P.claim) {
-      // one run per block and call: a second run of this call on the same block
-      // (its tokens not adjacent in the call) would requantize it concurrently
-      const unsigned long long me = ((unsigned long long)P.epoch << 32) | (uint32_t)(w0 + j);
-      const unsigned long long old =
-          __hip_atomic_exchange(&P.claim[slot / BS], me, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((uint32_t)(old >> 32) == P.epoch && old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
-    }
+    // one run per block and call: a second run of this call on the same block
+    // (its tokens not adjacent in the call) would requantize it concurrently.
+    // The claim's old value is checked after the run, so that the exchange's
+    // round trip overlaps the run's loads instead of preceding them.
+    const bool claim = !IS_V && h == 0 && lane == 0 && P.claim;
+    const unsigned long long me = ((unsigned long long)P.epoch << 32) | (uint32_t)(w0 + j);
+    unsigned long long old = 0;
+    if (claim) old = __hip_atomic_exchange(&P.claim[slot / BS], me, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     append_blk_run<IS_V, D>(P, src, codes, scales, w0, j, slot, ms64, h);
+    if (claim && (uint32_t)(old >> 32) == P.epoch && old != me) flag_misuse(P.err, MISUSE_BLK_SPLIT_RUN);
   }
 }
 
