@@ -77,7 +77,7 @@ def parse():
     ap.add_argument("--kv-heads", type=int, default=8)
     ap.add_argument("--pool-blocks", type=int, default=40000, help="pool capacity in 16-token blocks")
     ap.add_argument("--page", type=int, default=16, help="decode workload: tokens per page (16 k, k = 1..16)")
-    ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128], help="decode workload: head_dim")
+    ap.add_argument("--head-dim", type=int, default=128, choices=[64, 128], help="decode and tree workloads: head_dim")
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = auto)")
     ap.add_argument("--q-dtype", choices=["fp16", "fp32"], default="fp16",
                     help="decode query dtype (fp32: the reference kernels' float q)")
@@ -400,6 +400,7 @@ def run_tree(ctx, args):
     block of every sequence (all layers), then per layer the append of the N draft
     tokens of every sequence and one tree-verify call."""
     S, H, Hkv, NL, N = args.seqs, args.heads, args.kv_heads, args.layers, args.nodes
+    D = args.head_dim  # 128, or 64 (the 64-dim tree kernels)
     kv = velokv.KV_I8_BLK if args.kv == "int8" else velokv.KV_F16
     prefix = args.prefix
     if prefix % BS:
@@ -444,7 +445,7 @@ def run_tree(ctx, args):
     perm = synth.rng(5).permutation(n_blocks).astype(np.int32)  # scatter pages over the pool
     tables, fill_tables = perm[tables], perm[fill_tables]
     pairs = perm[np.array(pairs, np.int64)] if pairs else np.zeros((0, 2), np.int32)
-    pool = velokv.Pool(ctx, NL, n_blocks, BS, Hkv, HD, kv)
+    pool = velokv.Pool(ctx, NL, n_blocks, BS, Hkv, D, kv)
 
     # ---- fill: prefix once through sequence 0's row, then every suffix ----
     outlier = 8.0 if kv == velokv.KV_I8_BLK else 1.0
@@ -452,10 +453,10 @@ def run_tree(ctx, args):
     pos = np.concatenate([np.arange(prefix)] + [np.arange(prefix, int(c)) for c in committed])
     fill_slots = ctx.upload(synth.slots_for_positions(fill_tables, pos, BS, rows))
     n_fill = len(pos)
-    kbuf, vbuf = ctx.alloc(n_fill * Hkv * HD * 2), ctx.alloc(n_fill * Hkv * HD * 2)
+    kbuf, vbuf = ctx.alloc(n_fill * Hkv * D * 2), ctx.alloc(n_fill * Hkv * D * 2)
     for layer in range(NL):
-        ctx.fill_normal_f16(kbuf, n_fill * Hkv * HD, 3000 + 2 * layer, Hkv * HD, outlier)
-        ctx.fill_normal_f16(vbuf, n_fill * Hkv * HD, 3001 + 2 * layer, Hkv * HD, outlier)
+        ctx.fill_normal_f16(kbuf, n_fill * Hkv * D, 3000 + 2 * layer, Hkv * D, outlier)
+        ctx.fill_normal_f16(vbuf, n_fill * Hkv * D, 3001 + 2 * layer, Hkv * D, outlier)
         ctx.append(pool, layer, kbuf, vbuf, velokv.DT_F16, fill_slots, n_fill)
     ctx.sync()
     kbuf.free()
@@ -472,16 +473,16 @@ def run_tree(ctx, args):
     qdt = velokv.DT_F32 if args.q_dtype == "fp32" else velokv.DT_F16
     for r in range(R):
         if qdt == velokv.DT_F32:  # seeded normals made on the host
-            q = ctx.upload(synth.rng(7100 + r).standard_normal(S * N * H * HD).astype(np.float32))
+            q = ctx.upload(synth.rng(7100 + r).standard_normal(S * N * H * D).astype(np.float32))
         else:
-            q = ctx.alloc(S * N * H * HD * 2)
-            ctx.fill_normal_f16(q, S * N * H * HD, 7100 + r, H * HD)
-        k = ctx.alloc(S * N * Hkv * HD * 2)
-        ctx.fill_normal_f16(k, S * N * Hkv * HD, 8100 + r, Hkv * HD, outlier)
-        v = ctx.alloc(S * N * Hkv * HD * 2)
-        ctx.fill_normal_f16(v, S * N * Hkv * HD, 9100 + r, Hkv * HD, outlier)
+            q = ctx.alloc(S * N * H * D * 2)
+            ctx.fill_normal_f16(q, S * N * H * D, 7100 + r, H * D)
+        k = ctx.alloc(S * N * Hkv * D * 2)
+        ctx.fill_normal_f16(k, S * N * Hkv * D, 8100 + r, Hkv * D, outlier)
+        v = ctx.alloc(S * N * Hkv * D * 2)
+        ctx.fill_normal_f16(v, S * N * Hkv * D, 9100 + r, Hkv * D, outlier)
         qs.append(q); ks.append(k); vs.append(v)
-    out = ctx.alloc(S * N * H * HD * 4)
+    out = ctx.alloc(S * N * H * D * 4)
     d_committed, d_mask, d_bt = ctx.upload(committed), ctx.upload(mask.astype(np.uint32)), ctx.upload(tables)
     # accepted path per sequence: root to node s % N (what find_best_path returns
     # when the target agrees along that branch)
@@ -542,31 +543,32 @@ def run_tree(ctx, args):
 
     esz = 1 if kv == velokv.KV_I8_BLK else 2
     sc = 2 if kv == velokv.KV_I8_BLK else 0
-    tile = BS * HD * esz
+    tile = BS * D * esz
     uniq_tok = prefix + int((total - prefix).sum())
     uniq_blk = pblocks + int(sum(-(-int(t) // BS) - pblocks for t in total))
     logical_tok = int(total.sum())
     logical_blk = int(sum(-(-int(t) // BS) for t in total))
-    qo = S * N * H * HD * ((4 if qdt == velokv.DT_F32 else 2) + 4) + S * N * 4 + S * 4 + logical_blk * 4
-    uniq = 2 * uniq_tok * Hkv * HD * esz + 2 * uniq_blk * Hkv * sc + qo
-    logical = 2 * logical_tok * Hkv * HD * esz + 2 * logical_blk * Hkv * sc + qo
+    qo = S * N * H * D * ((4 if qdt == velokv.DT_F32 else 2) + 4) + S * N * 4 + S * 4 + logical_blk * 4
+    uniq = 2 * uniq_tok * Hkv * D * esz + 2 * uniq_blk * Hkv * sc + qo
+    logical = 2 * logical_tok * Hkv * D * esz + 2 * logical_blk * Hkv * sc + qo
     G = H // Hkv
     rows = -(-N * G // 16) * 16
-    flops = 4 * rows * HD * logical_tok * Hkv  # QK and PV over every visible-or-not row of each unit
+    flops = 4 * rows * D * logical_tok * Hkv  # QK and PV over every visible-or-not row of each unit
     cow_bytes = 2 * len(pairs) * NL * 2 * Hkv * (tile + sc)
     # commit: each moved token's K and V rows read and written once per layer
-    commit_bytes = NL * moved_tok * 2 * 2 * Hkv * (HD * esz + sc)
-    step_bytes = cow_bytes + commit_bytes + NL * (uniq + append_bytes(kv, S * N, Hkv))
+    commit_bytes = NL * moved_tok * 2 * 2 * Hkv * (D * esz + sc)
+    step_bytes = cow_bytes + commit_bytes + NL * (uniq + append_bytes(kv, S * N, Hkv, D))
     ms_step = total_ms / args.steps
     ach = uniq / (tv_mean * 1e-3) / 1e9
     rt = 2 if N * G > 16 else 1
     qsfx = 0 if qdt == velokv.DT_F32 else 1
-    kname = "vk_tree_kv%d_g%d_r%d_q%d" % (kv, G, rt, qsfx)
+    gtag = "gx_d64" if D == 64 else "g%d" % G
+    kname = "vk_tree_kv%d_%s_r%d_q%d" % (kv, gtag, rt, qsfx)
     call_kernels = [kname, "vk_decode_merge"]
     if shared_blocks and kv in (velokv.KV_I8_BLK, velokv.KV_F16):
         # the rest of each context runs in one partition (no merge) while it fits 4096 tokens
         rest = max(int(committed.max()) - shared_blocks * BS, BS - 1) + N
-        call_kernels = ["vk_tree_pfx_kv%d_g%d_q%d" % (kv, G, qsfx), kname] + (["vk_decode_merge"] if rest > 4096 else [])
+        call_kernels = ["vk_tree_pfx_kv%d_%s_q%d" % (kv, gtag, qsfx), kname] + (["vk_decode_merge"] if rest > 4096 else [])
     tflops = flops / (tv_mean * 1e-3) / 1e12
     return {
         "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 2),
@@ -598,9 +600,9 @@ def run_tree(ctx, args):
         "roofline_hbm": {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach / HBM_PEAK_GBS, 4), "bytes_per_launch": uniq},
         "pool_gb": round(pool.nbytes / 1e9, 2),
-        "workload": "S=%d, prefix %d (aliased%s), suffix U[0,%d], %d-node tree, H=%d/Hkv=%d, %s KV, %d layers" %
+        "workload": "S=%d, prefix %d (aliased%s), suffix U[0,%d], %d-node tree, H=%d/Hkv=%d, D=%d, %s KV, %d layers" %
                     (S, prefix, ", shared_blocks %d" % shared_blocks if shared_blocks else "", args.max_suffix, N, H,
-                     Hkv, args.kv, NL),
+                     Hkv, D, args.kv, NL),
     }
 
 
